@@ -1,0 +1,145 @@
+/*
+ * dspark_amd.h - C ABI of the MI355X (gfx950) DSpark attention hot path.
+ *
+ * Every pointer is a device pointer the caller owns (torch tensors in the
+ * Python host layer); the library allocates nothing.  Every call is
+ * asynchronous on `stream` (a hipStream_t) and never synchronises the host.
+ * Return value: 0 on success, -1 for an invalid argument (nothing was
+ * launched), -2 for a HIP launch failure; dspark_last_error() then returns a
+ * thread-local message.
+ *
+ * Attention entry points are specialised to the Qwen3-0.6B geometry:
+ * 16 query heads, 8 KV heads, head dim 128, bf16 in and out, FP32 softmax.
+ * K/V token rows are [8][128] bf16 (2 KiB); query/output rows [16][128].
+ */
+#ifndef DSPARK_AMD_H
+#define DSPARK_AMD_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Thread-local message for the last failing call on this thread. */
+const char* dspark_last_error(void);
+
+/* ABI revision of this header (currently 1). */
+int dspark_abi_version(void);
+
+/*
+ * Bytes of split-K workspace (FP32 partial max/sum/output) needed by an
+ * attention call over `n_req` requests whose key rows total at most
+ * `key_rows_bound`, with `row_tiles` 16-row tiles per (request, KV head):
+ * ceil(max_q/8) for varlen/verify, max blocks per request for draft.
+ * Returns -1 on invalid input.
+ */
+int64_t dspark_attn_workspace_bytes(int n_req, int64_t key_rows_bound, int row_tiles, int chunk);
+
+/*
+ * Packed varlen attention, bottom-right causal (causal=1) or noncausal.
+ * q [q_rows,16,128], k/v [k_rows,8,128], cu_q/cu_k int32 [n_req+1].
+ * Request r attends queries cu_q[r]..cu_q[r+1] to keys cu_k[r]..cu_k[r+1];
+ * causal query i of a request with q queries and k keys sees keys j <= k-q+i.
+ * Key rows beyond cu_k[n_req] (a capacity tail) are never read.
+ * Replaces aten::_flash_attention_forward as called by
+ *   dspark_qwen/rocm_varlen.py:278-281          (PinnedRocmVarlenKernel.__call__, causal)
+ *   dspark_qwen/packed_draft.py:26-29           (PinnedRocmDraftKernel.__call__, noncausal)
+ *   dspark_qwen/persistent_qwen_target.py:231-234 (_native_attention, capacity tail)
+ */
+int dspark_varlen_attn_fwd(const void* q, const void* k, const void* v,
+                           const int32_t* cu_q, const int32_t* cu_k, int n_req,
+                           int64_t q_rows, int64_t k_rows, int max_q, int causal,
+                           float scale, int chunk, void* out,
+                           void* workspace, int64_t workspace_bytes, void* stream);
+
+/*
+ * Fused verification attention over the persistent KV store.
+ * k_res/v_res: one layer of the resident store, [slots, ctx_capacity, 8, 128];
+ * k_scr/v_scr: the same layer of the scratch, [max_q, 8, 128].
+ * cu_q/cu_k: int32 [n_req+1] as built by dspark_txn_metadata; slots: int32 [n_req].
+ * Request r sees its committed context (resident rows slot*cap .. +c) followed
+ * by its staged rows (scratch rows cu_q[r] ..), bottom-right causal.
+ * Replaces the per-layer pair prepare_attention + kernel call:
+ *   dspark_qwen/persistent_target_kv.py:441-460 (capacity gather, fused here)
+ *   dspark_qwen/persistent_qwen_target.py:223-234 (_native_attention)
+ * key_rows_bound >= cu_k[n_req] (the bucket key capacity) fixes the grid.
+ */
+int dspark_verify_attn_fwd(const void* q, const void* k_res, const void* v_res,
+                           const void* k_scr, const void* v_scr,
+                           const int32_t* cu_q, const int32_t* cu_k, const int32_t* slots,
+                           int n_req, int64_t ctx_capacity, int64_t key_rows_bound, int max_q,
+                           float scale, int chunk, void* out,
+                           void* workspace, int64_t workspace_bytes, void* stream);
+
+/*
+ * Multi-block DSpark draft attention.  Request r owns blocks
+ * cu_blocks[r]..cu_blocks[r+1] (1..8 blocks), each 7 query rows; block b
+ * sees context positions j < anchors[b] of its request plus its own 7 rows
+ * (bidirectional), never another block.  Context row j of request r lives at
+ *   k_ctx + phys*tok_stride + head*head_stride,
+ *   phys = ctx_idx ? ctx_idx[ctx_off[r] + j] : ctx_off[r] + j,
+ * so both a slotted pool ([slots*cap, 8, 128]) and the append-order pool of
+ * dspark_qwen/packed_draft.py ([1, 8, N, 128] with gather indices) are read
+ * in place.  q/out [7*n_blocks,16,128]; k_blk/v_blk [7*n_blocks,8,128].
+ * Replaces the cat + index_select + cast + noncausal kernel sequence of
+ *   dspark_qwen/packed_draft.py:219-236 (PackedDraft.backbone)
+ * with the block_mask semantics of dspark_qwen/model.py:12-19.
+ */
+int dspark_draft_attn_fwd(const void* q, const void* k_ctx, const void* v_ctx,
+                          const int64_t* ctx_idx, const int64_t* ctx_off, const int32_t* ctx_len,
+                          int64_t tok_stride, int64_t head_stride,
+                          const void* k_blk, const void* v_blk,
+                          const int32_t* cu_blocks, const int32_t* anchors,
+                          int n_req, int64_t ctx_rows_bound, int max_blocks, float scale, int chunk,
+                          void* out, void* workspace, int64_t workspace_bytes, void* stream);
+
+/*
+ * Transaction metadata of PersistentTargetKV.begin
+ * (dspark_qwen/persistent_target_kv.py:392-411), built on the device from
+ * req = int32 [3][n_req] (slot, committed context, query length per request):
+ * committed_idx/scratch_idx int64 [key_capacity], from_scratch/valid
+ * uint8 [key_capacity], positions int64 [query_tokens], cu_q/cu_k int32
+ * [n_req+1].  Bit-exact with the reference lists, capacity tail included.
+ */
+int dspark_txn_metadata(const int32_t* req, int n_req, int64_t ctx_capacity,
+                        int64_t key_capacity, int64_t query_tokens,
+                        int64_t* committed_idx, int64_t* scratch_idx,
+                        uint8_t* from_scratch, uint8_t* valid, int64_t* positions,
+                        int32_t* cu_q, int32_t* cu_k, void* stream);
+
+/*
+ * Stage one layer's new K/V rows into scratch
+ * (dspark_qwen/persistent_target_kv.py:436-437, stage_layer).
+ */
+int dspark_kv_stage(const void* k_new, const void* v_new, void* k_scr_layer, void* v_scr_layer,
+                    int64_t rows, int64_t row_bytes, void* stream);
+
+/*
+ * Commit the accepted prefix n_accepted[r] of every request for all layers
+ * in one launch: scratch rows cu_q[r]..+n -> resident rows slot*cap+c..+n
+ * (dspark_qwen/persistent_target_kv.py:479-483).  Rows n..q-1 are rolled
+ * back by omission.  req as for dspark_txn_metadata (pre-commit context).
+ */
+int dspark_kv_commit(void* k_res, void* v_res, const void* k_scr, const void* v_scr,
+                     const int32_t* req, const int32_t* cu_q, const int32_t* n_accepted,
+                     int n_req, int max_q, int layers, int64_t slots, int64_t ctx_capacity,
+                     int64_t scratch_rows, int64_t row_bytes, void* stream);
+
+/*
+ * Materialised capacity-length K/V of prepare_attention
+ * (dspark_qwen/persistent_target_kv.py:452-459): row j = valid[j] ?
+ * (from_scratch[j] ? scratch[scratch_idx[j]] : resident[committed_idx[j]]) : 0.
+ */
+int dspark_kv_gather(const void* k_res_layer, const void* v_res_layer,
+                     const void* k_scr_layer, const void* v_scr_layer,
+                     const int64_t* committed_idx, const int64_t* scratch_idx,
+                     const uint8_t* from_scratch, const uint8_t* valid,
+                     int64_t key_capacity, int64_t res_rows, int64_t scr_rows, int64_t row_bytes,
+                     void* k_out, void* v_out, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* DSPARK_AMD_H */

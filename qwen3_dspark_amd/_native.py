@@ -1,0 +1,76 @@
+"""ctypes binding of the C ABI declared in include/dspark_amd.h.
+
+Loading never falls back: a missing library raises, and every non-zero
+return code is raised as NativeError with the library's message.
+"""
+import ctypes
+import os
+import threading
+
+from .build import LIB_PATH
+
+_lock = threading.Lock()
+_lib = None
+
+_P = ctypes.c_void_p
+_I = ctypes.c_int
+_L = ctypes.c_int64
+_F = ctypes.c_float
+
+# name -> (restype, argtypes); mirrors include/dspark_amd.h exactly.
+SIGNATURES = {
+    'dspark_last_error': (ctypes.c_char_p, []),
+    'dspark_abi_version': (_I, []),
+    'dspark_attn_workspace_bytes': (_L, [_I, _L, _I, _I]),
+    'dspark_varlen_attn_fwd': (_I, [_P, _P, _P, _P, _P, _I, _L, _L, _I, _I, _F, _I, _P, _P, _L, _P]),
+    'dspark_verify_attn_fwd': (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _I, _L, _L, _I, _F, _I, _P, _P, _L, _P]),
+    'dspark_draft_attn_fwd': (_I, [_P, _P, _P, _P, _P, _P, _L, _L, _P, _P, _P, _P, _I, _L, _I, _F, _I, _P, _P, _L, _P]),
+    'dspark_txn_metadata': (_I, [_P, _I, _L, _L, _L, _P, _P, _P, _P, _P, _P, _P, _P]),
+    'dspark_kv_stage': (_I, [_P, _P, _P, _P, _L, _L, _P]),
+    'dspark_kv_commit': (_I, [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _L, _L, _L, _L, _P]),
+    'dspark_kv_gather': (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _L, _L, _L, _L, _P, _P, _P]),
+}
+
+ABI_VERSION = 1
+
+
+class NativeError(RuntimeError):
+    """A C-ABI call returned a non-zero status."""
+
+
+def load():
+    """Load (once) and return the HIP extension; raise if it is not built."""
+    global _lib
+    with _lock:
+        if _lib is None:
+            if not os.path.exists(LIB_PATH):
+                raise RuntimeError(f'HIP extension not built ({LIB_PATH}); run __graft_entry__.build(). '
+                                   'There is no CPU or fallback implementation.')
+            lib = ctypes.CDLL(LIB_PATH)
+            for name, (res, args) in SIGNATURES.items():
+                fn = getattr(lib, name)
+                fn.restype = res
+                fn.argtypes = args
+            if lib.dspark_abi_version() != ABI_VERSION:
+                raise RuntimeError('HIP extension ABI version mismatch; rebuild it')
+            _lib = lib
+    return _lib
+
+
+def call(name, *args):
+    """Invoke an entry point and raise NativeError on a non-zero status."""
+    lib = load()
+    rc = getattr(lib, name)(*args)
+    if rc != 0:
+        raise NativeError(f'{name}: {lib.dspark_last_error().decode(errors="replace")}')
+    return rc
+
+
+def ptr(t):
+    """Device address of a tensor (None -> NULL)."""
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def stream_handle(device):
+    import torch
+    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)

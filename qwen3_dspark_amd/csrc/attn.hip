@@ -1,0 +1,831 @@
+// DSpark attention kernels for gfx950 (MI355X).
+//
+// Three entry points share one MFMA inner loop:
+//   * varlen    - packed THD attention over cu_seqlens (exact-K or
+//                 capacity-tail K/V), bottom-right causal or noncausal.
+//                 Replaces aten::_flash_attention_forward as called by
+//                 dspark_qwen/rocm_varlen.py:111-114 (causal),
+//                 dspark_qwen/packed_draft.py:26-29 (noncausal) and
+//                 dspark_qwen/persistent_qwen_target.py:231-234 (capacity).
+//   * verify    - the same causal attention, but K/V are read straight from
+//                 the persistent resident store (committed context) and the
+//                 per-layer scratch (new rows), i.e. the gather of
+//                 dspark_qwen/persistent_target_kv.py:441-460 is fused into
+//                 the load path and never materialised.
+//   * draft     - multi-block DSpark draft attention: each 7-row block sees
+//                 context positions j < anchor plus its own 7 rows
+//                 (dspark_qwen/model.py:12-19); context is streamed once per
+//                 request for all of its blocks.
+//
+// MFMA mapping (v_mfma_f32_16x16x32_bf16, wave64):
+//   S^T[key][row] = K[key][:] . Q[row][:]   A = K (16 keys), B = Q^T
+//   O^T[d][row]  += V^T[d][key] P^T[key][row]  A = V^T (via LDS), B = P^T
+// A 16-row tile holds 8 query tokens x the 2 query heads of one KV head
+// (row = 2*token + head_in_group).  The S^T accumulator leaves every lane
+// with the 8 scores of ONE query row (keys 8*grp .. 8*grp+7 of a 32-key
+// tile), which is exactly the B operand layout the PV MFMA needs, and the
+// O^T accumulator again leaves every lane with values of its own row, so
+// the online softmax (FlashAttention-2, Dao 2023) needs only two cross-lane
+// shuffles per tile for the row maximum.  The reduction order inside an MFMA
+// is irrelevant as long as A and B use the same (lane group, slot) -> k
+// assignment, which both operands here do by construction.
+//
+// Long contexts are split into fixed chunks of keys (flash-decoding, Dao et
+// al. 2023); every (request, chunk, KV head) is one workgroup and partial
+// (max, sum, unnormalised O) triples are merged in FP32 by merge_kernel.
+#include "common.h"
+
+namespace dspark {
+
+constexpr int KT = 32;                 // keys per wave iteration
+constexpr int ROWB = HD * 2;           // bytes per LDS K/V row (256)
+constexpr int OPITCH = HD + 4;         // floats per row in the merge buffer
+
+// XOR swizzle of the 16-byte chunk index of LDS row k.  Chosen so that
+//  - the V^T gather (row 8*grp+s, dims 16*nb+col) hits 8 distinct chunks
+//    per 8-lane phase, and
+//  - the K fragment read (rows 8q+4j+e, chunk 4ks+grp) does as well.
+__device__ __forceinline__ int swz(int k) {
+  return (((k >> 3) & 3) << 1) ^ ((k & 1) | ((k & 2) << 1));
+}
+
+__device__ __forceinline__ int lds_chunk_off(int k, int chunk16) {
+  return k * ROWB + ((chunk16 ^ swz(k)) << 4);
+}
+
+__device__ __forceinline__ int lds_elem_off(int k, int d) {
+  return k * ROWB + ((((d >> 3) ^ swz(k))) << 4) + ((d & 7) << 1);
+}
+
+// Read the V^T A-operand for dims 16*nb + col from an LDS tile whose row r
+// holds key r; lane group grp covers keys 8*grp .. 8*grp+7.
+__device__ __forceinline__ bf16x8 lds_vt(const unsigned char* tile, int nb, int col, int grp) {
+  union { bf16x8 v; unsigned short u[8]; } t;
+  const int d = 16 * nb + col;
+  #pragma unroll
+  for (int s = 0; s < 8; ++s) {
+    const int k = 8 * grp + s;
+    t.u[s] = *reinterpret_cast<const unsigned short*>(tile + lds_elem_off(k, d));
+  }
+  return t.v;
+}
+
+__device__ __forceinline__ void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// One online-softmax + PV update for a 32-key tile.
+//   s0/s1  : S^T accumulators (keys kbase+4j+e for j=0/1, e=0..3)
+//   vis    : keys < vis are visible for this lane's row
+//   vt     : V^T A-operands for the 8 dim blocks
+struct RowState {
+  float m;       // running max (log2 domain, already scaled)
+  float l;       // per-lane partial denominator
+  f32x4 o[8];    // O^T accumulators: o[nb][e] = O[row][16nb+4grp+e]
+};
+
+__device__ __forceinline__ void row_init(RowState& st) {
+  st.m = -INFINITY;
+  st.l = 0.f;
+  #pragma unroll
+  for (int nb = 0; nb < 8; ++nb) st.o[nb] = f32x4{0.f, 0.f, 0.f, 0.f};
+}
+
+__device__ __forceinline__ bf16x8 softmax_update(RowState& st, const f32x4& s0, const f32x4& s1,
+                                                 int kbase, int vis, float scale_log2) {
+  float x[8];
+  #pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    x[e] = (kbase + e < vis) ? s0[e] * scale_log2 : -INFINITY;
+    x[4 + e] = (kbase + 4 + e < vis) ? s1[e] * scale_log2 : -INFINITY;
+  }
+  float mx = x[0];
+  #pragma unroll
+  for (int i = 1; i < 8; ++i) mx = fmaxf(mx, x[i]);
+  mx = wave_max_across_groups(mx);
+  const float m_new = fmaxf(st.m, mx);
+  const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
+  const float alpha = fast_exp2(st.m - m_use);
+  bf16x8 pb;
+  float ps = 0.f;
+  #pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const float p = fast_exp2(x[i] - m_use);
+    ps += p;
+    pb[i] = (bf16)p;
+  }
+  st.l = st.l * alpha + ps;
+  st.m = m_new;
+  #pragma unroll
+  for (int nb = 0; nb < 8; ++nb) st.o[nb] *= alpha;
+  return pb;
+}
+
+__device__ __forceinline__ void pv_update(RowState& st, const bf16x8& pb, const bf16x8* vt) {
+  #pragma unroll
+  for (int nb = 0; nb < 8; ++nb)
+    st.o[nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vt[nb], pb, st.o[nb], 0, 0, 0);
+}
+
+__device__ __forceinline__ void qk_tile(const bf16x8 (&kf)[2][4], const bf16x8 (&qf)[4], f32x4& s0, f32x4& s1) {
+  s0 = f32x4{0.f, 0.f, 0.f, 0.f};
+  s1 = f32x4{0.f, 0.f, 0.f, 0.f};
+  #pragma unroll
+  for (int ks = 0; ks < 4; ++ks) {
+    s0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf[0][ks], qf[ks], s0, 0, 0, 0);
+    s1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf[1][ks], qf[ks], s1, 0, 0, 0);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// varlen / verify
+// ---------------------------------------------------------------------------
+struct VarlenArgs {
+  const bf16* q;          // [nq, 16, 128]
+  const bf16* k_a;        // segment A: [rows, 8, 128]
+  const bf16* v_a;
+  const bf16* k_b;        // segment B (verify: scratch layer [max_q, 8, 128])
+  const bf16* v_b;
+  const int32_t* cu_q;    // [B+1]
+  const int32_t* cu_k;    // [B+1]
+  const int32_t* slots;   // verify: resident slot per request
+  int64_t slot_rows;      // verify: context capacity (rows per slot)
+  bf16* out;              // [nq, 16, 128]
+  float* part_o;          // [n_cl*8*tmax][16][128]
+  float* part_ml;         // [n_cl*8*tmax][16][2]
+  int n_req;
+  int causal;
+  int chunk;
+  int tmax;
+  float scale_log2;
+};
+
+constexpr int VARLEN_SMEM = 4 * 16 * OPITCH * 4 + 4 * 16 * 2 * 4;   // 34304 B (>= 4*32*256)
+static_assert(VARLEN_SMEM >= 4 * KT * ROWB, "merge buffer must cover the V tiles");
+
+template <bool VERIFY>
+__global__ __launch_bounds__(256) void varlen_attn_kernel(VarlenArgs a) {
+  __shared__ __attribute__((aligned(16))) unsigned char smem[VARLEN_SMEM];
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int col = lane & 15;
+  const int grp = lane >> 4;
+  const int g = blockIdx.x & 7;
+  const int cl = blockIdx.x >> 3;
+  const int t = blockIdx.y;
+
+  int r, first;
+  locate_chunk(a.cu_k, nullptr, a.n_req, a.chunk, cl, r, first);
+  if (r < 0) return;
+  const int q0 = a.cu_q[r];
+  const int ql = a.cu_q[r + 1] - q0;
+  if (8 * t >= ql) return;
+  const int kbeg = a.cu_k[r];
+  const int kl = a.cu_k[r + 1] - kbeg;
+  const int c = cl - first;
+  const int nch = chunks_for(kl, a.chunk);
+  const int k0 = c * a.chunk;
+  const int k1 = min(k0 + a.chunk, kl);
+
+  // Key j of this request lives in segment A for j < a_len, else segment B.
+  const bf16* kA;
+  const bf16* vA;
+  const bf16* kB;
+  const bf16* vB;
+  int a_len;
+  if (VERIFY) {
+    a_len = kl - ql;
+    const size_t abase = (size_t)a.slots[r] * (size_t)a.slot_rows * KV_ROW + (size_t)g * HD;
+    kA = a.k_a + abase;
+    vA = a.v_a + abase;
+    const size_t bbase = (size_t)q0 * KV_ROW + (size_t)g * HD;
+    kB = a.k_b + bbase;
+    vB = a.v_b + bbase;
+  } else {
+    a_len = kl;
+    const size_t abase = (size_t)kbeg * KV_ROW + (size_t)g * HD;
+    kA = a.k_a + abase;
+    vA = a.v_a + abase;
+    kB = kA;
+    vB = vA;
+  }
+
+  // This lane's query row.
+  const int tok = 8 * t + (col >> 1);
+  const int head = 2 * g + (col & 1);
+  const bool row_ok = tok < ql;
+  const int lim = row_ok ? (a.causal ? kl - ql + tok + 1 : kl) : 0;
+  const int last_tok = min(8 * t + 7, ql - 1);
+  const int tile_lim = a.causal ? kl - ql + last_tok + 1 : kl;
+  const int kend = min(k1, tile_lim);
+  const int vis = min(lim, kend);
+
+  bf16x8 qf[4];
+  {
+    const bf16* qp = a.q + (size_t)(q0 + (row_ok ? tok : 0)) * Q_ROW + (size_t)head * HD + 8 * grp;
+    #pragma unroll
+    for (int ks = 0; ks < 4; ++ks) qf[ks] = row_ok ? ld8(qp + 32 * ks) : zero8();
+  }
+
+  RowState st;
+  row_init(st);
+  unsigned char* vs = smem + wave * KT * ROWB;
+
+  for (int kt = k0 + KT * wave; kt < kend; kt += KT * 4) {
+    bf16x8 kf[2][4];
+    #pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int kk = kt + 8 * (col >> 2) + 4 * j + (col & 3);
+      if (kk < kend) {
+        const bf16* p = (kk < a_len ? kA + (size_t)kk * KV_ROW : kB + (size_t)(kk - a_len) * KV_ROW) + 8 * grp;
+        #pragma unroll
+        for (int ks = 0; ks < 4; ++ks) kf[j][ks] = ld8(p + 32 * ks);
+      } else {
+        #pragma unroll
+        for (int ks = 0; ks < 4; ++ks) kf[j][ks] = zero8();
+      }
+    }
+    bf16x8 vf[8];
+    #pragma unroll
+    for (int i2 = 0; i2 < 8; ++i2) {
+      const int kk = kt + 4 * i2 + grp;
+      if (kk < kend) {
+        const bf16* p = (kk < a_len ? vA + (size_t)kk * KV_ROW : vB + (size_t)(kk - a_len) * KV_ROW) + 8 * col;
+        vf[i2] = ld8(p);
+      } else {
+        vf[i2] = zero8();
+      }
+    }
+    f32x4 s0, s1;
+    qk_tile(kf, qf, s0, s1);
+    #pragma unroll
+    for (int i2 = 0; i2 < 8; ++i2) {
+      const int k = 4 * i2 + grp;
+      *reinterpret_cast<bf16x8*>(vs + lds_chunk_off(k, col)) = vf[i2];
+    }
+    const bf16x8 pb = softmax_update(st, s0, s1, kt + 8 * grp, vis, a.scale_log2);
+    wave_lds_sync();
+    bf16x8 vt[8];
+    #pragma unroll
+    for (int nb = 0; nb < 8; ++nb) vt[nb] = lds_vt(vs, nb, col, grp);
+    pv_update(st, pb, vt);
+    wave_lds_sync();
+  }
+
+  st.l = wave_sum_across_groups(st.l);
+  __syncthreads();
+  float* ob = reinterpret_cast<float*>(smem);
+  float* mlb = reinterpret_cast<float*>(smem + 4 * 16 * OPITCH * 4);
+  #pragma unroll
+  for (int nb = 0; nb < 8; ++nb)
+    *reinterpret_cast<f32x4*>(ob + (wave * 16 + col) * OPITCH + 16 * nb + 4 * grp) = st.o[nb];
+  if (grp == 0) {
+    mlb[(wave * 16 + col) * 2 + 0] = st.m;
+    mlb[(wave * 16 + col) * 2 + 1] = st.l;
+  }
+  __syncthreads();
+
+  const int tid = threadIdx.x;
+  const int row = tid >> 4;
+  const int d0 = (tid & 15) * 8;
+  float M = -INFINITY;
+  #pragma unroll
+  for (int w = 0; w < 4; ++w) M = fmaxf(M, mlb[(w * 16 + row) * 2]);
+  float L = 0.f;
+  float acc[8];
+  #pragma unroll
+  for (int i = 0; i < 8; ++i) acc[i] = 0.f;
+  #pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    const float mw = mlb[(w * 16 + row) * 2];
+    const float sc = (mw == -INFINITY) ? 0.f : fast_exp2(mw - M);
+    L += sc * mlb[(w * 16 + row) * 2 + 1];
+    const float* src = ob + (w * 16 + row) * OPITCH + d0;
+    #pragma unroll
+    for (int i = 0; i < 8; ++i) acc[i] += sc * src[i];
+  }
+  const int tok_r = 8 * t + (row >> 1);
+  const int head_r = 2 * g + (row & 1);
+  if (nch == 1) {
+    if (tok_r < ql) {
+      bf16x8 ov;
+      #pragma unroll
+      for (int i = 0; i < 8; ++i) ov[i] = (bf16)(acc[i] / L);
+      *reinterpret_cast<bf16x8*>(a.out + (size_t)(q0 + tok_r) * Q_ROW + (size_t)head_r * HD + d0) = ov;
+    }
+  } else {
+    const size_t p = (size_t)(cl * 8 + g) * a.tmax + t;
+    float* po = a.part_o + (p * 16 + row) * HD + d0;
+    *reinterpret_cast<f32x4*>(po) = f32x4{acc[0], acc[1], acc[2], acc[3]};
+    *reinterpret_cast<f32x4*>(po + 4) = f32x4{acc[4], acc[5], acc[6], acc[7]};
+    if ((tid & 15) == 0) {
+      a.part_ml[(p * 16 + row) * 2 + 0] = M;
+      a.part_ml[(p * 16 + row) * 2 + 1] = L;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// draft (multi-block, context streamed once per request)
+// ---------------------------------------------------------------------------
+struct DraftArgs {
+  const bf16* q;            // [7*n_blocks, 16, 128], request-major, block-major
+  const bf16* k_ctx;        // context pool, element (row, head, d) at
+  const bf16* v_ctx;        //   row*tok_stride + head*head_stride + d
+  const int64_t* ctx_idx;   // optional physical row per (request, position)
+  const int64_t* ctx_off;   // [B] first row (or first ctx_idx entry) of request r
+  const int32_t* ctx_len;   // [B] committed context rows of request r
+  const bf16* k_blk;        // [7*n_blocks, 8, 128] projected block K/V
+  const bf16* v_blk;
+  const int32_t* cu_b;      // [B+1] block offsets
+  const int32_t* anchors;   // [n_blocks] context rows visible to each block
+  bf16* out;                // [7*n_blocks, 16, 128]
+  float* part_o;
+  float* part_ml;
+  int64_t tok_stride;
+  int64_t head_stride;
+  int n_req;
+  int chunk;
+  int tmax;                 // max blocks per request (<= 8)
+  float scale_log2;
+};
+
+constexpr int BLOCK_ROWS = 7;
+constexpr int DSTEP = 64;                        // context keys per LDS step
+constexpr int DRAFT_SMEM = 2 * DSTEP * ROWB;     // K + V tiles (32 KiB)
+constexpr int DRAFT_TILES_PER_WAVE = 2;
+
+__global__ __launch_bounds__(256) void draft_attn_kernel(DraftArgs a) {
+  __shared__ __attribute__((aligned(16))) unsigned char smem[DRAFT_SMEM];
+  unsigned char* ks_tile = smem;
+  unsigned char* vs_tile = smem + DSTEP * ROWB;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int col = lane & 15;
+  const int grp = lane >> 4;
+  const int g = blockIdx.x & 7;
+  const int cl = blockIdx.x >> 3;
+
+  int r, first;
+  locate_chunk(nullptr, a.ctx_len, a.n_req, a.chunk, cl, r, first);
+  if (r < 0) return;
+  const int ctx = a.ctx_len[r];
+  const int c = cl - first;
+  const int nch = chunks_for(ctx, a.chunk);
+  const int k0 = c * a.chunk;
+  const int k1 = min(k0 + a.chunk, ctx);
+  const int b0 = a.cu_b[r];
+  const int nb = a.cu_b[r + 1] - b0;
+
+  // Tiles owned by this wave: blocks wave and wave+4.
+  bool has[DRAFT_TILES_PER_WAVE];
+  int vis[DRAFT_TILES_PER_WAVE];
+  int tile_anchor[DRAFT_TILES_PER_WAVE];
+  bf16x8 qf[DRAFT_TILES_PER_WAVE][4];
+  RowState st[DRAFT_TILES_PER_WAVE];
+  const int tok = col >> 1;
+  const bool row_ok = tok < BLOCK_ROWS;
+  int amax = 0;
+  for (int b = 0; b < nb; ++b) amax = max(amax, a.anchors[b0 + b]);
+  #pragma unroll
+  for (int i = 0; i < DRAFT_TILES_PER_WAVE; ++i) {
+    const int b = wave + 4 * i;
+    has[i] = b < nb;
+    tile_anchor[i] = has[i] ? min(a.anchors[b0 + b], k1) : 0;
+    vis[i] = row_ok ? tile_anchor[i] : 0;
+    row_init(st[i]);
+    const bf16* qp = a.q + (size_t)(BLOCK_ROWS * (b0 + (has[i] ? b : 0)) + (row_ok ? tok : 0)) * Q_ROW +
+                     (size_t)(2 * g + (col & 1)) * HD + 8 * grp;
+    #pragma unroll
+    for (int ks = 0; ks < 4; ++ks) qf[i][ks] = (has[i] && row_ok) ? ld8(qp + 32 * ks) : zero8();
+  }
+  const int kend = min(k1, amax);
+
+  // Context pointer of row j of this request (head g).
+  const size_t hoff = (size_t)g * a.head_stride;
+  const int64_t coff = a.ctx_off[r];
+  auto ctx_row = [&](int j) -> size_t {
+    const int64_t phys = a.ctx_idx ? a.ctx_idx[coff + j] : coff + j;
+    return (size_t)phys * (size_t)a.tok_stride + hoff;
+  };
+
+  // Cooperative staging: thread tid covers chunk (tid&15) of keys
+  // step + 16*it + (tid>>4), it = 0..3, for both K and V.
+  bf16x8 pk[4], pv[4];
+  auto prefetch = [&](int step) {
+    #pragma unroll
+    for (int it = 0; it < 4; ++it) {
+      const int kk = step + 16 * it + (tid >> 4);
+      if (kk < kend) {
+        const size_t off = ctx_row(kk) + 8 * (tid & 15);
+        pk[it] = ld8(a.k_ctx + off);
+        pv[it] = ld8(a.v_ctx + off);
+      } else {
+        pk[it] = zero8();
+        pv[it] = zero8();
+      }
+    }
+  };
+
+  if (k0 < kend) prefetch(k0);
+  for (int step = k0; step < kend; step += DSTEP) {
+    #pragma unroll
+    for (int it = 0; it < 4; ++it) {
+      const int k = 16 * it + (tid >> 4);
+      *reinterpret_cast<bf16x8*>(ks_tile + lds_chunk_off(k, tid & 15)) = pk[it];
+      *reinterpret_cast<bf16x8*>(vs_tile + lds_chunk_off(k, tid & 15)) = pv[it];
+    }
+    __syncthreads();
+    if (step + DSTEP < kend) prefetch(step + DSTEP);
+    #pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int kt = step + KT * h;
+      bool any = false;
+      #pragma unroll
+      for (int i = 0; i < DRAFT_TILES_PER_WAVE; ++i) any |= has[i] && (tile_anchor[i] > kt);
+      if (!any) continue;
+      bf16x8 kf[2][4];
+      #pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int k = KT * h + 8 * (col >> 2) + 4 * j + (col & 3);
+        #pragma unroll
+        for (int ks = 0; ks < 4; ++ks)
+          kf[j][ks] = *reinterpret_cast<const bf16x8*>(ks_tile + lds_chunk_off(k, 4 * ks + grp));
+      }
+      bf16x8 vt[8];
+      #pragma unroll
+      for (int nbk = 0; nbk < 8; ++nbk) vt[nbk] = lds_vt(vs_tile + KT * h * ROWB, nbk, col, grp);
+      #pragma unroll
+      for (int i = 0; i < DRAFT_TILES_PER_WAVE; ++i) {
+        if (!(has[i] && tile_anchor[i] > kt)) continue;
+        f32x4 s0, s1;
+        qk_tile(kf, qf[i], s0, s1);
+        const bf16x8 pb = softmax_update(st[i], s0, s1, kt + 8 * grp, vis[i], a.scale_log2);
+        pv_update(st[i], pb, vt);
+      }
+    }
+    __syncthreads();
+  }
+
+  // Own-block keys (bidirectional within the block), once per request.
+  if (c == nch - 1) {
+    unsigned char* wv = smem + wave * 8 * ROWB;   // 8 rows per wave
+    #pragma unroll
+    for (int i = 0; i < DRAFT_TILES_PER_WAVE; ++i) {
+      if (!has[i]) continue;
+      const int b = wave + 4 * i;
+      const size_t rb = (size_t)BLOCK_ROWS * (b0 + b);
+      bf16x8 kf[2][4];
+      #pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int kk = 8 * (col >> 2) + 4 * j + (col & 3);
+        if (kk < BLOCK_ROWS) {
+          const bf16* p = a.k_blk + (rb + kk) * KV_ROW + (size_t)g * HD + 8 * grp;
+          #pragma unroll
+          for (int ks = 0; ks < 4; ++ks) kf[j][ks] = ld8(p + 32 * ks);
+        } else {
+          #pragma unroll
+          for (int ks = 0; ks < 4; ++ks) kf[j][ks] = zero8();
+        }
+      }
+      #pragma unroll
+      for (int i2 = 0; i2 < 2; ++i2) {
+        const int kk = 4 * i2 + grp;
+        const bf16x8 v = (kk < BLOCK_ROWS) ? ld8(a.v_blk + (rb + kk) * KV_ROW + (size_t)g * HD + 8 * col) : zero8();
+        *reinterpret_cast<bf16x8*>(wv + lds_chunk_off(kk, col)) = v;
+      }
+      f32x4 s0, s1;
+      qk_tile(kf, qf[i], s0, s1);
+      const bf16x8 pb = softmax_update(st[i], s0, s1, 8 * grp, row_ok ? BLOCK_ROWS : 0, a.scale_log2);
+      wave_lds_sync();
+      bf16x8 vt[8];
+      #pragma unroll
+      for (int nbk = 0; nbk < 8; ++nbk) vt[nbk] = grp == 0 ? lds_vt(wv, nbk, col, 0) : zero8();
+      pv_update(st[i], pb, vt);
+      wave_lds_sync();
+    }
+  }
+
+  #pragma unroll
+  for (int i = 0; i < DRAFT_TILES_PER_WAVE; ++i) {
+    if (!has[i]) continue;
+    const int b = wave + 4 * i;
+    const float l = wave_sum_across_groups(st[i].l);
+    if (nch == 1) {
+      if (row_ok) {
+        bf16* op = a.out + (size_t)(BLOCK_ROWS * (b0 + b) + tok) * Q_ROW + (size_t)(2 * g + (col & 1)) * HD + 4 * grp;
+        #pragma unroll
+        for (int nbk = 0; nbk < 8; ++nbk) {
+          bf16x4 ov;
+          #pragma unroll
+          for (int e = 0; e < 4; ++e) ov[e] = (bf16)(st[i].o[nbk][e] / l);
+          *reinterpret_cast<bf16x4*>(op + 16 * nbk) = ov;
+        }
+      }
+    } else {
+      const size_t p = (size_t)(cl * 8 + g) * a.tmax + b;
+      float* po = a.part_o + (p * 16 + col) * HD + 4 * grp;
+      #pragma unroll
+      for (int nbk = 0; nbk < 8; ++nbk) *reinterpret_cast<f32x4*>(po + 16 * nbk) = st[i].o[nbk];
+      if (grp == 0) {
+        a.part_ml[(p * 16 + col) * 2 + 0] = st[i].m;
+        a.part_ml[(p * 16 + col) * 2 + 1] = l;
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// split-K merge
+// ---------------------------------------------------------------------------
+struct MergeArgs {
+  const int32_t* cu_q;     // varlen/verify
+  const int32_t* cu_k;     // varlen/verify chunk counts
+  const int32_t* ctx_len;  // draft chunk counts
+  const int32_t* cu_b;     // draft block offsets
+  const float* part_o;
+  const float* part_ml;
+  bf16* out;
+  int n_req;
+  int chunk;
+  int tmax;
+  int draft;
+};
+
+// Sum of chunks_for() over requests [0, r): executed by each wave.
+__device__ __forceinline__ int chunk_base(const int32_t* cu, const int32_t* lens, int r, int chunk) {
+  const int lane = threadIdx.x & 63;
+  int acc = 0;
+  for (int r0 = 0; r0 < r; r0 += WAVE) {
+    const int rr = r0 + lane;
+    int n = 0;
+    if (rr < r) n = chunks_for(cu ? (cu[rr + 1] - cu[rr]) : lens[rr], chunk);
+    #pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) n += __shfl_xor(n, off);
+    acc += n;
+  }
+  return acc;
+}
+
+__global__ __launch_bounds__(256) void merge_kernel(MergeArgs a) {
+  const int r = blockIdx.x;
+  const int g = blockIdx.y;
+  const int t = blockIdx.z;
+  int len, out_row0, rows_valid;
+  if (a.draft) {
+    const int b0 = a.cu_b[r];
+    if (t >= a.cu_b[r + 1] - b0) return;
+    len = a.ctx_len[r];
+    out_row0 = BLOCK_ROWS * (b0 + t);
+    rows_valid = BLOCK_ROWS;
+  } else {
+    const int q0 = a.cu_q[r];
+    const int ql = a.cu_q[r + 1] - q0;
+    if (8 * t >= ql) return;
+    len = a.cu_k[r + 1] - a.cu_k[r];
+    out_row0 = q0 + 8 * t;
+    rows_valid = min(8, ql - 8 * t);
+  }
+  const int nch = chunks_for(len, a.chunk);
+  if (nch == 1) return;
+  const int first = chunk_base(a.draft ? nullptr : a.cu_k, a.draft ? a.ctx_len : nullptr, r, a.chunk);
+  const int tid = threadIdx.x;
+  const int row = tid >> 4;
+  const int d0 = (tid & 15) * 8;
+  const int tok = row >> 1;
+  if (tok >= rows_valid) return;
+  float M = -INFINITY;
+  for (int c = 0; c < nch; ++c) {
+    const size_t p = (size_t)((first + c) * 8 + g) * a.tmax + t;
+    M = fmaxf(M, a.part_ml[(p * 16 + row) * 2]);
+  }
+  float L = 0.f;
+  float acc[8];
+  #pragma unroll
+  for (int i = 0; i < 8; ++i) acc[i] = 0.f;
+  for (int c = 0; c < nch; ++c) {
+    const size_t p = (size_t)((first + c) * 8 + g) * a.tmax + t;
+    const float mc = a.part_ml[(p * 16 + row) * 2];
+    const float sc = (mc == -INFINITY) ? 0.f : fast_exp2(mc - M);
+    L += sc * a.part_ml[(p * 16 + row) * 2 + 1];
+    const float* po = a.part_o + (p * 16 + row) * HD + d0;
+    const f32x4 x0 = *reinterpret_cast<const f32x4*>(po);
+    const f32x4 x1 = *reinterpret_cast<const f32x4*>(po + 4);
+    #pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      acc[i] += sc * x0[i];
+      acc[4 + i] += sc * x1[i];
+    }
+  }
+  bf16x8 ov;
+  #pragma unroll
+  for (int i = 0; i < 8; ++i) ov[i] = (bf16)(acc[i] / L);
+  *reinterpret_cast<bf16x8*>(a.out + (size_t)(out_row0 + tok) * Q_ROW + (size_t)(2 * g + (row & 1)) * HD + d0) = ov;
+}
+
+}  // namespace dspark
+
+// ---------------------------------------------------------------------------
+// C ABI
+// ---------------------------------------------------------------------------
+namespace {
+
+using namespace dspark;
+
+constexpr float LOG2E = 1.4426950408889634f;
+
+int64_t n_chunk_items(int n_req, int64_t rows_bound, int chunk) {
+  return (rows_bound + chunk - 1) / chunk + n_req;
+}
+
+int64_t workspace_bytes(int n_req, int64_t rows_bound, int tiles, int chunk) {
+  const int64_t items = n_chunk_items(n_req, rows_bound, chunk) * HKV * tiles;
+  return items * 16 * (HD + 2) * (int64_t)sizeof(float);
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+int check_common(int n_req, int64_t rows_bound, int tiles, int chunk, float scale,
+                 int64_t ws_bytes, const void* ws) {
+  DSPARK_REQUIRE(n_req >= 1, "n_req must be >= 1 (got %d)", n_req);
+  DSPARK_REQUIRE(rows_bound >= 0, "key row bound must be >= 0");
+  DSPARK_REQUIRE(tiles >= 1 && tiles <= 65535, "row tiles out of range (%d)", tiles);
+  DSPARK_REQUIRE(chunk >= 32 && chunk % 32 == 0 && chunk <= (1 << 20), "chunk must be a multiple of 32 in [32, 2^20] (got %d)", chunk);
+  DSPARK_REQUIRE(scale > 0.f && scale < 1e30f, "scale must be positive and finite");
+  const int64_t items = n_chunk_items(n_req, rows_bound, chunk) * HKV;
+  DSPARK_REQUIRE(items <= 0x7fffffffLL, "too many chunk work items (%lld)", (long long)items);
+  const int64_t need = workspace_bytes(n_req, rows_bound, tiles, chunk);
+  DSPARK_REQUIRE(ws_bytes >= need, "workspace too small: %lld < %lld bytes", (long long)ws_bytes, (long long)need);
+  DSPARK_REQUIRE(need == 0 || (ws != nullptr && aligned16(ws)), "workspace must be a 16-byte aligned device pointer");
+  return OK;
+}
+
+}  // namespace
+
+extern "C" int64_t dspark_attn_workspace_bytes(int n_req, int64_t key_rows_bound, int row_tiles, int chunk) {
+  if (n_req < 1 || key_rows_bound < 0 || row_tiles < 1 || chunk < 32) return -1;
+  return workspace_bytes(n_req, key_rows_bound, row_tiles, chunk);
+}
+
+extern "C" int dspark_varlen_attn_fwd(const void* q, const void* k, const void* v,
+                                      const int32_t* cu_q, const int32_t* cu_k, int n_req,
+                                      int64_t q_rows, int64_t k_rows, int max_q, int causal,
+                                      float scale, int chunk, void* out, void* workspace,
+                                      int64_t workspace_bytes_, void* stream) {
+  clear_error();
+  DSPARK_REQUIRE(q && k && v && cu_q && cu_k && out, "null pointer argument");
+  DSPARK_REQUIRE(aligned16(q) && aligned16(k) && aligned16(v) && aligned16(out), "Q/K/V/out must be 16-byte aligned");
+  DSPARK_REQUIRE(q_rows >= 1 && k_rows >= 1, "Q and K must be nonempty");
+  DSPARK_REQUIRE(max_q >= 1 && max_q <= q_rows, "max_q must be in [1, q_rows]");
+  const int tiles = (max_q + 7) / 8;
+  int rc = check_common(n_req, k_rows, tiles, chunk, scale, workspace_bytes_, workspace);
+  if (rc != OK) return rc;
+  const int64_t n_cl = n_chunk_items(n_req, k_rows, chunk);
+  VarlenArgs a{};
+  a.q = static_cast<const bf16*>(q);
+  a.k_a = static_cast<const bf16*>(k);
+  a.v_a = static_cast<const bf16*>(v);
+  a.k_b = a.k_a;
+  a.v_b = a.v_a;
+  a.cu_q = cu_q;
+  a.cu_k = cu_k;
+  a.slots = nullptr;
+  a.slot_rows = 0;
+  a.out = static_cast<bf16*>(out);
+  a.part_o = static_cast<float*>(workspace);
+  a.part_ml = a.part_o + n_cl * HKV * tiles * 16 * HD;
+  a.n_req = n_req;
+  a.causal = causal ? 1 : 0;
+  a.chunk = chunk;
+  a.tmax = tiles;
+  a.scale_log2 = scale * LOG2E;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  hipLaunchKernelGGL(varlen_attn_kernel<false>, dim3((unsigned)(n_cl * HKV), tiles), dim3(256), 0, s, a);
+  rc = launch_status("varlen_attn_kernel");
+  if (rc != OK) return rc;
+  MergeArgs m{};
+  m.cu_q = cu_q;
+  m.cu_k = cu_k;
+  m.part_o = a.part_o;
+  m.part_ml = a.part_ml;
+  m.out = a.out;
+  m.n_req = n_req;
+  m.chunk = chunk;
+  m.tmax = tiles;
+  m.draft = 0;
+  hipLaunchKernelGGL(merge_kernel, dim3(n_req, HKV, tiles), dim3(256), 0, s, m);
+  return launch_status("merge_kernel");
+}
+
+extern "C" int dspark_verify_attn_fwd(const void* q, const void* k_res, const void* v_res,
+                                      const void* k_scr, const void* v_scr,
+                                      const int32_t* cu_q, const int32_t* cu_k, const int32_t* slots,
+                                      int n_req, int64_t ctx_capacity, int64_t key_rows_bound, int max_q,
+                                      float scale, int chunk, void* out, void* workspace,
+                                      int64_t workspace_bytes_, void* stream) {
+  clear_error();
+  DSPARK_REQUIRE(q && k_res && v_res && k_scr && v_scr && cu_q && cu_k && slots && out, "null pointer argument");
+  DSPARK_REQUIRE(aligned16(q) && aligned16(k_res) && aligned16(v_res) && aligned16(k_scr) && aligned16(v_scr) && aligned16(out),
+                 "Q/K/V/out must be 16-byte aligned");
+  DSPARK_REQUIRE(ctx_capacity >= 1, "context capacity must be >= 1");
+  DSPARK_REQUIRE(max_q >= 1, "max_q must be >= 1");
+  const int tiles = (max_q + 7) / 8;
+  int rc = check_common(n_req, key_rows_bound, tiles, chunk, scale, workspace_bytes_, workspace);
+  if (rc != OK) return rc;
+  const int64_t n_cl = n_chunk_items(n_req, key_rows_bound, chunk);
+  VarlenArgs a{};
+  a.q = static_cast<const bf16*>(q);
+  a.k_a = static_cast<const bf16*>(k_res);
+  a.v_a = static_cast<const bf16*>(v_res);
+  a.k_b = static_cast<const bf16*>(k_scr);
+  a.v_b = static_cast<const bf16*>(v_scr);
+  a.cu_q = cu_q;
+  a.cu_k = cu_k;
+  a.slots = slots;
+  a.slot_rows = ctx_capacity;
+  a.out = static_cast<bf16*>(out);
+  a.part_o = static_cast<float*>(workspace);
+  a.part_ml = a.part_o + n_cl * HKV * tiles * 16 * HD;
+  a.n_req = n_req;
+  a.causal = 1;
+  a.chunk = chunk;
+  a.tmax = tiles;
+  a.scale_log2 = scale * LOG2E;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  hipLaunchKernelGGL(varlen_attn_kernel<true>, dim3((unsigned)(n_cl * HKV), tiles), dim3(256), 0, s, a);
+  rc = launch_status("verify_attn_kernel");
+  if (rc != OK) return rc;
+  MergeArgs m{};
+  m.cu_q = cu_q;
+  m.cu_k = cu_k;
+  m.part_o = a.part_o;
+  m.part_ml = a.part_ml;
+  m.out = a.out;
+  m.n_req = n_req;
+  m.chunk = chunk;
+  m.tmax = tiles;
+  m.draft = 0;
+  hipLaunchKernelGGL(merge_kernel, dim3(n_req, HKV, tiles), dim3(256), 0, s, m);
+  return launch_status("merge_kernel");
+}
+
+extern "C" int dspark_draft_attn_fwd(const void* q, const void* k_ctx, const void* v_ctx,
+                                     const int64_t* ctx_idx, const int64_t* ctx_off, const int32_t* ctx_len,
+                                     int64_t tok_stride, int64_t head_stride,
+                                     const void* k_blk, const void* v_blk,
+                                     const int32_t* cu_blocks, const int32_t* anchors,
+                                     int n_req, int64_t ctx_rows_bound, int max_blocks, float scale, int chunk,
+                                     void* out, void* workspace, int64_t workspace_bytes_, void* stream) {
+  clear_error();
+  DSPARK_REQUIRE(q && k_ctx && v_ctx && ctx_off && ctx_len && k_blk && v_blk && cu_blocks && anchors && out,
+                 "null pointer argument");
+  DSPARK_REQUIRE(aligned16(q) && aligned16(k_ctx) && aligned16(v_ctx) && aligned16(k_blk) && aligned16(v_blk) && aligned16(out),
+                 "Q/K/V/out must be 16-byte aligned");
+  DSPARK_REQUIRE(tok_stride >= HD && tok_stride % 8 == 0 && head_stride >= HD && head_stride % 8 == 0,
+                 "context strides must be multiples of 8 elements and >= 128");
+  DSPARK_REQUIRE(max_blocks >= 1 && max_blocks <= 4 * DRAFT_TILES_PER_WAVE,
+                 "max_blocks must be in [1, %d] (got %d)", 4 * DRAFT_TILES_PER_WAVE, max_blocks);
+  DSPARK_REQUIRE(chunk % DSTEP == 0, "draft chunk must be a multiple of %d", DSTEP);
+  int rc = check_common(n_req, ctx_rows_bound, max_blocks, chunk, scale, workspace_bytes_, workspace);
+  if (rc != OK) return rc;
+  const int64_t n_cl = n_chunk_items(n_req, ctx_rows_bound, chunk);
+  DraftArgs a{};
+  a.q = static_cast<const bf16*>(q);
+  a.k_ctx = static_cast<const bf16*>(k_ctx);
+  a.v_ctx = static_cast<const bf16*>(v_ctx);
+  a.ctx_idx = ctx_idx;
+  a.ctx_off = ctx_off;
+  a.ctx_len = ctx_len;
+  a.k_blk = static_cast<const bf16*>(k_blk);
+  a.v_blk = static_cast<const bf16*>(v_blk);
+  a.cu_b = cu_blocks;
+  a.anchors = anchors;
+  a.out = static_cast<bf16*>(out);
+  a.part_o = static_cast<float*>(workspace);
+  a.part_ml = a.part_o + n_cl * HKV * max_blocks * 16 * HD;
+  a.tok_stride = tok_stride;
+  a.head_stride = head_stride;
+  a.n_req = n_req;
+  a.chunk = chunk;
+  a.tmax = max_blocks;
+  a.scale_log2 = scale * LOG2E;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  hipLaunchKernelGGL(draft_attn_kernel, dim3((unsigned)(n_cl * HKV)), dim3(256), 0, s, a);
+  rc = launch_status("draft_attn_kernel");
+  if (rc != OK) return rc;
+  MergeArgs m{};
+  m.ctx_len = ctx_len;
+  m.cu_b = cu_blocks;
+  m.part_o = a.part_o;
+  m.part_ml = a.part_ml;
+  m.out = a.out;
+  m.n_req = n_req;
+  m.chunk = chunk;
+  m.tmax = max_blocks;
+  m.draft = 1;
+  hipLaunchKernelGGL(merge_kernel, dim3(n_req, HKV, max_blocks), dim3(256), 0, s, m);
+  return launch_status("merge_kernel(draft)");
+}

@@ -1,0 +1,114 @@
+// Shared device helpers for the DSpark attention hot path on gfx950 (CDNA4).
+//
+// Shapes are fixed to the Qwen3-0.6B attention geometry used by the DSpark
+// target and draft: 16 query heads, 8 KV heads, head dim 128 (GQA group 2).
+// Every K/V tensor is addressed as rows of [8 KV heads][128] bf16, i.e. one
+// 2 KiB "token row" per position, which is the layout of the persistent
+// resident store [layers, slots, capacity, 8, 128], its scratch
+// [layers, max_q, 8, 128] and of packed THD tensors [tokens, 8, 128].
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace dspark {
+
+typedef __bf16 bf16;
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int HQ = 16;              // query heads
+constexpr int HKV = 8;              // KV heads
+constexpr int HD = 128;             // head dim
+constexpr int KV_ROW = HKV * HD;    // elements per K or V token row
+constexpr int Q_ROW = HQ * HD;      // elements per Q/O token row
+constexpr int WAVE = 64;
+
+__device__ __forceinline__ bf16x8 zero8() {
+  bf16x8 z;
+  #pragma unroll
+  for (int i = 0; i < 8; ++i) z[i] = (bf16)0.0f;
+  return z;
+}
+
+__device__ __forceinline__ bf16x8 ld8(const bf16* p) {
+  return *reinterpret_cast<const bf16x8*>(p);
+}
+
+__device__ __forceinline__ float wave_max_across_groups(float x) {
+  // The 4 lanes {n, n+16, n+32, n+48} hold the same MFMA column (query row).
+  x = fmaxf(x, __shfl_xor(x, 16));
+  x = fmaxf(x, __shfl_xor(x, 32));
+  return x;
+}
+
+__device__ __forceinline__ float wave_sum_across_groups(float x) {
+  x += __shfl_xor(x, 16);
+  x += __shfl_xor(x, 32);
+  return x;
+}
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// Number of key chunks a request of `len` keys is split into (at least one,
+// so that requests with no keys still own a work item).
+__device__ __forceinline__ int chunks_for(int len, int chunk) {
+  return len <= 0 ? 1 : (len + chunk - 1) / chunk;
+}
+
+// Locate the request that owns linear chunk index `cl`.  Per-request key
+// counts come from a cumulative array `cu` (len = cu[r+1]-cu[r]) or a plain
+// length array `lens`.  Executed redundantly by every wave of a workgroup;
+// all lanes return the same (request, first-chunk) pair, or request -1 when
+// `cl` lies beyond the last request's chunks.
+__device__ __forceinline__ void locate_chunk(const int32_t* __restrict__ cu,
+                                             const int32_t* __restrict__ lens,
+                                             int n_req, int chunk, int cl,
+                                             int& req, int& first) {
+  const int lane = threadIdx.x & (WAVE - 1);
+  int running = 0;
+  for (int r0 = 0; r0 < n_req; r0 += WAVE) {
+    const int r = r0 + lane;
+    int n = 0;
+    if (r < n_req) n = chunks_for(cu ? (cu[r + 1] - cu[r]) : lens[r], chunk);
+    int incl = n;
+    #pragma unroll
+    for (int off = 1; off < WAVE; off <<= 1) {
+      const int t = __shfl_up(incl, off);
+      if (lane >= off) incl += t;
+    }
+    const int total = __shfl(incl, WAVE - 1);
+    if (cl < running + total) {
+      const unsigned long long hit = __ballot(r < n_req && running + incl > cl);
+      const int L = __ffsll((long long)hit) - 1;
+      const int excl = incl - n;
+      req = r0 + L;
+      first = running + __shfl(excl, L);
+      return;
+    }
+    running += total;
+  }
+  req = -1;
+  first = running;
+}
+
+}  // namespace dspark
+
+// ---------------------------------------------------------------------------
+// Host-side error reporting shared by the C-ABI entry points.
+// ---------------------------------------------------------------------------
+namespace dspark {
+enum Status : int { OK = 0, INVALID_ARGUMENT = -1, HIP_FAILURE = -2 };
+void set_error(const char* fmt, ...) __attribute__((format(printf, 1, 2)));
+void clear_error();
+// Returns OK if the last launch succeeded, else records `what` and the HIP error.
+int launch_status(const char* what);
+}  // namespace dspark
+
+#define DSPARK_REQUIRE(cond, ...)                 \
+  do {                                            \
+    if (!(cond)) {                                \
+      ::dspark::set_error(__VA_ARGS__);           \
+      return ::dspark::INVALID_ARGUMENT;          \
+    }                                             \
+  } while (0)

@@ -1,0 +1,319 @@
+// Persistent target KV transaction kernels for gfx950.
+//
+//   txn_metadata : device restatement of PersistentTargetKV.begin's host
+//                  list building (dspark_qwen/persistent_target_kv.py:392-411)
+//                  from per-request (slot, context, query) triples.  Produces
+//                  the seven workspace arrays bit-exactly, tail included.
+//   kv_stage     : copy a layer's new K/V rows into scratch
+//                  (persistent_target_kv.py:436-437).
+//   kv_commit    : copy every layer's accepted prefix scratch rows into the
+//                  resident slots in one launch (persistent_target_kv.py:479-483);
+//                  rows beyond the accepted prefix are never copied (rollback).
+//   kv_gather    : the capacity-length K/V of prepare_attention
+//                  (persistent_target_kv.py:452-459) in one pass: committed
+//                  rows from resident, new rows from scratch, tail zeroed.
+//
+// The copy kernels move rows of any multiple of 16 bytes (a Qwen3 token row
+// is [8 KV heads][128] bf16 = 2 KiB) with 16-byte vector accesses.
+#include "common.h"
+
+namespace dspark {
+
+constexpr int MAX_SCAN = 4096;   // requests per transaction handled by the block scan
+
+// Exclusive block scan of a[0..n) (n <= MAX_SCAN) into out[0..n] (out[n] = total),
+// executed by all 256 threads of the workgroup.
+__device__ void block_exclusive_scan(const int32_t* vals, int n, int32_t* out, int32_t* tmp) {
+  const int tid = threadIdx.x;
+  const int per = (n + 255) / 256;
+  const int beg = min(n, tid * per);
+  const int end = min(n, beg + per);
+  int s = 0;
+  for (int i = beg; i < end; ++i) s += vals[i];
+  tmp[tid] = s;
+  __syncthreads();
+  if (tid == 0) {
+    int run = 0;
+    for (int i = 0; i < 256; ++i) {
+      const int v = tmp[i];
+      tmp[i] = run;
+      run += v;
+    }
+    out[n] = run;
+  }
+  __syncthreads();
+  int run = tmp[tid];
+  for (int i = beg; i < end; ++i) {
+    out[i] = run;
+    run += vals[i];
+  }
+  __syncthreads();
+}
+
+struct TxnArgs {
+  const int32_t* req;        // [3][B]: slot, context, query per request
+  int64_t* committed_idx;    // [kcap]
+  int64_t* scratch_idx;      // [kcap]
+  uint8_t* from_scratch;     // [kcap]
+  uint8_t* valid;            // [kcap]
+  int64_t* positions;        // [nq]
+  int32_t* cu_q;             // [B+1]
+  int32_t* cu_k;             // [B+1]
+  int64_t ctx_capacity;
+  int64_t kcap;
+  int64_t nq;
+  int n_req;
+};
+
+__global__ __launch_bounds__(256) void txn_metadata_kernel(TxnArgs a) {
+  __shared__ int32_t s_len[MAX_SCAN];
+  __shared__ int32_t s_cuk[MAX_SCAN + 1];
+  __shared__ int32_t s_cuq[MAX_SCAN + 1];
+  __shared__ int32_t s_tmp[256];
+  const int B = a.n_req;
+  const int32_t* slot = a.req;
+  const int32_t* ctx = a.req + B;
+  const int32_t* ql = a.req + 2 * B;
+  for (int i = threadIdx.x; i < B; i += 256) s_len[i] = ctx[i] + ql[i];
+  __syncthreads();
+  block_exclusive_scan(s_len, B, s_cuk, s_tmp);
+  for (int i = threadIdx.x; i < B; i += 256) s_len[i] = ql[i];
+  __syncthreads();
+  block_exclusive_scan(s_len, B, s_cuq, s_tmp);
+
+  const int64_t gid = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (blockIdx.x == 0) {
+    for (int i = threadIdx.x; i <= B; i += 256) {
+      a.cu_q[i] = s_cuq[i];
+      a.cu_k[i] = s_cuk[i];
+    }
+  }
+  if (gid < a.kcap) {
+    const int64_t j = gid;
+    const int32_t logical = s_cuk[B];
+    int64_t old = 0, nw = 0;
+    uint8_t choose = 0, ok = 0;
+    if (j < logical) {
+      // request r with s_cuk[r] <= j < s_cuk[r+1]
+      int lo = 0, hi = B - 1;
+      while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (s_cuk[mid] <= j) lo = mid; else hi = mid - 1;
+      }
+      const int r = lo;
+      const int64_t off = j - s_cuk[r];
+      const int c = ctx[r];
+      ok = 1;
+      if (off < c) {
+        old = (int64_t)slot[r] * a.ctx_capacity + off;
+      } else {
+        nw = (int64_t)s_cuq[r] + (off - c);
+        choose = 1;
+      }
+    }
+    a.committed_idx[j] = old;
+    a.scratch_idx[j] = nw;
+    a.from_scratch[j] = choose;
+    a.valid[j] = ok;
+  }
+  if (gid < a.nq) {
+    const int64_t i = gid;
+    int lo = 0, hi = B - 1;
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (s_cuq[mid] <= i) lo = mid; else hi = mid - 1;
+    }
+    a.positions[i] = (int64_t)ctx[lo] + (i - s_cuq[lo]);
+  }
+}
+
+// Row copy kernels.  A row is `row_vecs` 16-byte vectors (2 KiB for the
+// Qwen3 [8][128] bf16 token row); every thread moves one vector.
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
+struct StageArgs {
+  const u32x4* k_new;   // [rows][row_vecs]
+  const u32x4* v_new;
+  u32x4* k_scr;         // scratch layer base
+  u32x4* v_scr;
+  int64_t n_vec;        // rows * row_vecs
+};
+
+__global__ __launch_bounds__(256) void kv_stage_kernel(StageArgs a) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i < a.n_vec) {
+    a.k_scr[i] = a.k_new[i];
+    a.v_scr[i] = a.v_new[i];
+  }
+}
+
+struct CommitArgs {
+  u32x4* k_res;           // [L, slots, cap, row]
+  u32x4* v_res;
+  const u32x4* k_scr;     // [L, max_q, row]
+  const u32x4* v_scr;
+  const int32_t* req;     // [3][B]: slot, context, query (pre-commit)
+  const int32_t* cu_q;    // [B+1] scratch row offset of each request
+  const int32_t* n_acc;   // [B] accepted prefix
+  int64_t layer_res;      // vectors per resident layer
+  int64_t layer_scr;      // vectors per scratch layer
+  int64_t ctx_capacity;
+  int64_t row_vecs;
+  int64_t total;          // n_req * max_q * row_vecs
+  int n_req;
+  int max_q;
+};
+
+// grid: (ceil(n_req*max_q*row_vecs / 256), layers)
+__global__ __launch_bounds__(256) void kv_commit_kernel(CommitArgs a) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= a.total) return;
+  const int64_t rowi = i / a.row_vecs;
+  const int64_t v = i - rowi * a.row_vecs;
+  const int r = (int)(rowi / a.max_q);
+  const int t = (int)(rowi - (int64_t)r * a.max_q);
+  const int layer = blockIdx.y;
+  if (t >= a.n_acc[r]) return;
+  const int32_t slot = a.req[r];
+  const int32_t c = a.req[a.n_req + r];
+  const int64_t src = layer * a.layer_scr + ((int64_t)a.cu_q[r] + t) * a.row_vecs + v;
+  const int64_t dst = layer * a.layer_res + ((int64_t)slot * a.ctx_capacity + c + t) * a.row_vecs + v;
+  a.k_res[dst] = a.k_scr[src];
+  a.v_res[dst] = a.v_scr[src];
+}
+
+struct GatherArgs {
+  const u32x4* k_res;           // resident layer base, rows [slots*cap]
+  const u32x4* v_res;
+  const u32x4* k_scr;           // scratch layer base, rows [max_q]
+  const u32x4* v_scr;
+  const int64_t* committed_idx; // [kcap]
+  const int64_t* scratch_idx;
+  const uint8_t* from_scratch;
+  const uint8_t* valid;
+  u32x4* k_out;                 // [kcap][row]
+  u32x4* v_out;
+  int64_t total;                // kcap * row_vecs
+  int64_t row_vecs;
+  int64_t res_rows;             // bound for committed_idx
+  int64_t scr_rows;             // bound for scratch_idx
+};
+
+__global__ __launch_bounds__(256) void kv_gather_kernel(GatherArgs a) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= a.total) return;
+  const int64_t j = i / a.row_vecs;
+  const int64_t v = i - j * a.row_vecs;
+  u32x4 kx = {0u, 0u, 0u, 0u}, vx = {0u, 0u, 0u, 0u};
+  if (a.valid[j]) {
+    if (a.from_scratch[j]) {
+      const int64_t s = a.scratch_idx[j];
+      if (s >= 0 && s < a.scr_rows) {
+        kx = a.k_scr[s * a.row_vecs + v];
+        vx = a.v_scr[s * a.row_vecs + v];
+      }
+    } else {
+      const int64_t s = a.committed_idx[j];
+      if (s >= 0 && s < a.res_rows) {
+        kx = a.k_res[s * a.row_vecs + v];
+        vx = a.v_res[s * a.row_vecs + v];
+      }
+    }
+  }
+  a.k_out[i] = kx;
+  a.v_out[i] = vx;
+}
+
+}  // namespace dspark
+
+// ---------------------------------------------------------------------------
+// C ABI
+// ---------------------------------------------------------------------------
+namespace {
+using namespace dspark;
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+}  // namespace
+
+extern "C" int dspark_txn_metadata(const int32_t* req, int n_req, int64_t ctx_capacity,
+                                   int64_t key_capacity, int64_t query_tokens,
+                                   int64_t* committed_idx, int64_t* scratch_idx,
+                                   uint8_t* from_scratch, uint8_t* valid, int64_t* positions,
+                                   int32_t* cu_q, int32_t* cu_k, void* stream) {
+  clear_error();
+  DSPARK_REQUIRE(req && committed_idx && scratch_idx && from_scratch && valid && positions && cu_q && cu_k,
+                 "null pointer argument");
+  DSPARK_REQUIRE(n_req >= 1 && n_req <= MAX_SCAN, "n_req must be in [1, %d]", MAX_SCAN);
+  DSPARK_REQUIRE(ctx_capacity >= 1 && key_capacity >= 1 && query_tokens >= 1, "capacities must be positive");
+  const int64_t work = key_capacity > query_tokens ? key_capacity : query_tokens;
+  const int64_t blocks = (work + 255) / 256;
+  DSPARK_REQUIRE(blocks <= 0x7fffffffLL, "key capacity too large");
+  TxnArgs a{req, committed_idx, scratch_idx, from_scratch, valid, positions, cu_q, cu_k,
+            ctx_capacity, key_capacity, query_tokens, n_req};
+  hipLaunchKernelGGL(txn_metadata_kernel, dim3((unsigned)blocks), dim3(256), 0, static_cast<hipStream_t>(stream), a);
+  return launch_status("txn_metadata_kernel");
+}
+
+extern "C" int dspark_kv_stage(const void* k_new, const void* v_new, void* k_scr_layer, void* v_scr_layer,
+                               int64_t rows, int64_t row_bytes, void* stream) {
+  clear_error();
+  DSPARK_REQUIRE(k_new && v_new && k_scr_layer && v_scr_layer, "null pointer argument");
+  DSPARK_REQUIRE(aligned16(k_new) && aligned16(v_new) && aligned16(k_scr_layer) && aligned16(v_scr_layer),
+                 "buffers must be 16-byte aligned");
+  DSPARK_REQUIRE(rows >= 1, "rows must be >= 1");
+  DSPARK_REQUIRE(row_bytes >= 16 && row_bytes % 16 == 0, "row bytes must be a positive multiple of 16");
+  StageArgs a{static_cast<const u32x4*>(k_new), static_cast<const u32x4*>(v_new),
+              static_cast<u32x4*>(k_scr_layer), static_cast<u32x4*>(v_scr_layer), rows * (row_bytes / 16)};
+  const int64_t blocks = (a.n_vec + 255) / 256;
+  DSPARK_REQUIRE(blocks <= 0x7fffffffLL, "stage too large");
+  hipLaunchKernelGGL(kv_stage_kernel, dim3((unsigned)blocks), dim3(256), 0, static_cast<hipStream_t>(stream), a);
+  return launch_status("kv_stage_kernel");
+}
+
+extern "C" int dspark_kv_commit(void* k_res, void* v_res, const void* k_scr, const void* v_scr,
+                                const int32_t* req, const int32_t* cu_q, const int32_t* n_accepted,
+                                int n_req, int max_q, int layers, int64_t slots, int64_t ctx_capacity,
+                                int64_t scratch_rows, int64_t row_bytes, void* stream) {
+  clear_error();
+  DSPARK_REQUIRE(k_res && v_res && k_scr && v_scr && req && cu_q && n_accepted, "null pointer argument");
+  DSPARK_REQUIRE(aligned16(k_res) && aligned16(v_res) && aligned16(k_scr) && aligned16(v_scr),
+                 "buffers must be 16-byte aligned");
+  DSPARK_REQUIRE(n_req >= 1 && max_q >= 1 && layers >= 1 && slots >= 1 && ctx_capacity >= 1 && scratch_rows >= 1,
+                 "sizes must be positive");
+  DSPARK_REQUIRE(row_bytes >= 16 && row_bytes % 16 == 0, "row bytes must be a positive multiple of 16");
+  DSPARK_REQUIRE(layers <= 65535, "too many layers");
+  const int64_t rv = row_bytes / 16;
+  const int64_t total = (int64_t)n_req * max_q * rv;
+  const int64_t blocks = (total + 255) / 256;
+  DSPARK_REQUIRE(blocks <= 0x7fffffffLL, "commit grid too large");
+  CommitArgs a{static_cast<u32x4*>(k_res), static_cast<u32x4*>(v_res),
+               static_cast<const u32x4*>(k_scr), static_cast<const u32x4*>(v_scr),
+               req, cu_q, n_accepted, slots * ctx_capacity * rv, scratch_rows * rv,
+               ctx_capacity, rv, total, n_req, max_q};
+  hipLaunchKernelGGL(kv_commit_kernel, dim3((unsigned)blocks, layers), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), a);
+  return launch_status("kv_commit_kernel");
+}
+
+extern "C" int dspark_kv_gather(const void* k_res_layer, const void* v_res_layer,
+                                const void* k_scr_layer, const void* v_scr_layer,
+                                const int64_t* committed_idx, const int64_t* scratch_idx,
+                                const uint8_t* from_scratch, const uint8_t* valid,
+                                int64_t key_capacity, int64_t res_rows, int64_t scr_rows, int64_t row_bytes,
+                                void* k_out, void* v_out, void* stream) {
+  clear_error();
+  DSPARK_REQUIRE(k_res_layer && v_res_layer && k_scr_layer && v_scr_layer && committed_idx && scratch_idx &&
+                 from_scratch && valid && k_out && v_out, "null pointer argument");
+  DSPARK_REQUIRE(aligned16(k_res_layer) && aligned16(v_res_layer) && aligned16(k_scr_layer) && aligned16(v_scr_layer) &&
+                 aligned16(k_out) && aligned16(v_out), "buffers must be 16-byte aligned");
+  DSPARK_REQUIRE(key_capacity >= 1 && res_rows >= 1 && scr_rows >= 1, "sizes must be positive");
+  DSPARK_REQUIRE(row_bytes >= 16 && row_bytes % 16 == 0, "row bytes must be a positive multiple of 16");
+  const int64_t rv = row_bytes / 16;
+  GatherArgs a{static_cast<const u32x4*>(k_res_layer), static_cast<const u32x4*>(v_res_layer),
+               static_cast<const u32x4*>(k_scr_layer), static_cast<const u32x4*>(v_scr_layer),
+               committed_idx, scratch_idx, from_scratch, valid,
+               static_cast<u32x4*>(k_out), static_cast<u32x4*>(v_out), key_capacity * rv, rv, res_rows, scr_rows};
+  const int64_t blocks = (a.total + 255) / 256;
+  DSPARK_REQUIRE(blocks <= 0x7fffffffLL, "key capacity too large");
+  hipLaunchKernelGGL(kv_gather_kernel, dim3((unsigned)blocks), dim3(256), 0, static_cast<hipStream_t>(stream), a);
+  return launch_status("kv_gather_kernel");
+}

@@ -1,0 +1,71 @@
+"""The C-ABI library loads and exports exactly what include/dspark_amd.h
+declares; argument validation runs on the host (no GPU work is launched)."""
+import ctypes
+import os
+import re
+import subprocess
+
+import pytest
+
+from qwen3_dspark_amd import _native
+from qwen3_dspark_amd.build import LIB_PATH
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def header_functions():
+    text = open(os.path.join(ROOT, 'include', 'dspark_amd.h')).read()
+    text = re.sub(r'/\*.*?\*/', '', text, flags=re.S)
+    return sorted(set(re.findall(r'\b(dspark_[a-z0-9_]+)\s*\(', text)))
+
+
+def test_header_and_binding_agree():
+    assert header_functions() == sorted(_native.SIGNATURES)
+
+
+def test_library_exports_every_declared_symbol():
+    assert os.path.exists(LIB_PATH), 'run __graft_entry__.build() first'
+    out = subprocess.run(['nm', '-D', '--defined-only', LIB_PATH], capture_output=True, text=True, check=True).stdout
+    exported = set(re.findall(r'\sT\s(dspark_[a-z0-9_]+)', out))
+    assert set(header_functions()) <= exported
+    lib = _native.load()
+    for name in header_functions():
+        assert getattr(lib, name) is not None
+    assert lib.dspark_abi_version() == _native.ABI_VERSION
+
+
+def test_workspace_size_formula():
+    lib = _native.load()
+    # (ceil(rows/chunk) + n_req) items * 8 KV heads * tiles * 16 rows * (128 + 2) floats
+    assert lib.dspark_attn_workspace_bytes(4, 1000, 1, 512) == (2 + 4) * 8 * 1 * 16 * 130 * 4
+    assert lib.dspark_attn_workspace_bytes(64, 524288 + 448, 1, 512) == (1025 + 64) * 8 * 16 * 130 * 4
+    assert lib.dspark_attn_workspace_bytes(0, 10, 1, 512) == -1
+
+
+@pytest.mark.parametrize('name', ['dspark_varlen_attn_fwd', 'dspark_verify_attn_fwd', 'dspark_draft_attn_fwd',
+                                  'dspark_txn_metadata', 'dspark_kv_stage', 'dspark_kv_commit', 'dspark_kv_gather'])
+def test_null_arguments_are_rejected_before_any_launch(name):
+    lib = _native.load()
+    fn = getattr(lib, name)
+    args = []
+    for t in fn.argtypes:
+        args.append(None if t is ctypes.c_void_p else 1)
+    rc = fn(*args)
+    assert rc == -1
+    assert 'null pointer' in lib.dspark_last_error().decode()
+
+
+def test_invalid_sizes_are_rejected_before_any_launch():
+    lib = _native.load()
+    fake = ctypes.c_void_p(1 << 20)  # never dereferenced: validation fails first
+    rc = lib.dspark_varlen_attn_fwd(fake, fake, fake, fake, fake, 0, 8, 8, 1, 1, 0.088, 512, fake, fake, 1 << 20, None)
+    assert rc == -1 and 'n_req' in lib.dspark_last_error().decode()
+    rc = lib.dspark_varlen_attn_fwd(fake, fake, fake, fake, fake, 2, 8, 8, 1, 1, 0.088, 500, fake, fake, 1 << 20, None)
+    assert rc == -1 and 'chunk' in lib.dspark_last_error().decode()
+    rc = lib.dspark_varlen_attn_fwd(fake, fake, fake, fake, fake, 2, 8, 8, 1, 1, 0.088, 512, fake, fake, 16, None)
+    assert rc == -1 and 'workspace too small' in lib.dspark_last_error().decode()
+    rc = lib.dspark_draft_attn_fwd(fake, fake, fake, None, fake, fake, 1024, 128, fake, fake, fake, fake,
+                                   2, 100, 9, 0.088, 512, fake, fake, 1 << 24, None)
+    assert rc == -1 and 'max_blocks' in lib.dspark_last_error().decode()
+    rc = lib.dspark_kv_stage(fake, fake, fake, fake, 4, 24, None)
+    assert rc == -1 and 'multiple of 16' in lib.dspark_last_error().decode()
