@@ -1,0 +1,316 @@
+#!/usr/bin/env python3
+"""Benchmark of the DSpark attention hot path on one MI355X.
+
+Workload (64-request stress shape, Qwen3-0.6B attention geometry: 16 query
+heads, 8 KV heads, head dim 128, bf16):
+  * 64 requests, committed contexts c = floor(exp(U(ln 256, ln 8192))),
+    KV cache preallocated at capacity 8192 rows per request (28 layers);
+  * draft: 5 layers, 1..8 blocks of 7 rows per request, one block anchored
+    at c and the others at U[0, c], context streamed from a slotted pool;
+  * verify: 7 appended rows per request (448 query tokens), 28 layers.
+One step = one speculative round of the hot path:
+  draft attention x5 -> begin (transaction metadata) ->
+  28 x (stage new K/V + fused verification attention) -> commit of a
+  seeded accepted prefix 0..7 per request (the rest rolled back).
+Inputs are seeded N(0,1) bf16 already resident in HBM; the timed region
+contains only the round itself.
+
+value = verified tokens per second = 448 / round time.
+
+    python bench.py [--gpus 1] [--steps 20] [--warmup 5]
+"""
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+METRIC = 'attn tokens/s + HBM GB/s (% roofline), 64 ragged reqs, Qwen3-0.6B shapes'
+SEED = 20261009
+B, Q_LEN, CAPACITY = 64, 7, 8192
+VERIFY_LAYERS, DRAFT_LAYERS, BLOCK = 28, 5, 7
+ROW_BYTES = 8 * 128 * 2            # one K (or V) token row, all 8 KV heads
+Q_ROW_BYTES = 16 * 128 * 2         # one Q (or O) token row, all 16 query heads
+HBM_PEAK_GBS = 8000.0              # MI355X HBM3E, published
+CPU_THREADS_CAP = 16               # host CPU share of one GPU on the box
+
+
+def log(msg):
+    print(msg, file=sys.stderr, flush=True)
+
+
+def parse():
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument('--gpus', type=int, default=1)
+    ap.add_argument('--steps', type=int, default=20)
+    ap.add_argument('--warmup', type=int, default=5)
+    ap.add_argument('--chunk', type=int, default=None, help='keys per split-K work item')
+    ap.add_argument('--no-cpu-baseline', action='store_true', help='skip the CPU oracle leg (profiling runs)')
+    ap.add_argument('--cpu-verify-layers', type=int, default=2, help='verify layers in the CPU sample')
+    return ap.parse_args()
+
+
+def workload(steps_total):
+    """Seeded integer draws: contexts, draft blocks/anchors, accepted prefixes."""
+    import numpy as np
+    rng = np.random.default_rng(SEED)
+    contexts = np.floor(np.exp(rng.uniform(math.log(256), math.log(8192), size=B))).astype(int)
+    # leave room for every round's commit (<= 7 rows per round)
+    contexts = np.minimum(contexts, CAPACITY - Q_LEN * (steps_total + 1))
+    blocks = rng.integers(1, 9, size=B)
+    anchors = []
+    for c, n in zip(contexts, blocks):
+        a = [int(c)] + [int(x) for x in rng.integers(0, c + 1, size=n - 1)]
+        anchors.append(a)
+    accepted = rng.integers(0, Q_LEN + 1, size=(steps_total, B))
+    return [int(c) for c in contexts], anchors, accepted
+
+
+def verify_bytes(contexts):
+    """Algorithmic HBM bytes of one verification-attention layer: every key
+    row (committed + staged) read once, Q read once, O written once."""
+    return sum(c + Q_LEN for c in contexts) * 2 * ROW_BYTES + 2 * B * Q_LEN * Q_ROW_BYTES
+
+
+def draft_bytes(anchors):
+    """Algorithmic bytes of one draft-attention layer: context rows up to the
+    largest anchor read once per request, block K/V, Q and O."""
+    rows = sum(max(a) for a in anchors)
+    q = BLOCK * sum(len(a) for a in anchors)
+    return rows * 2 * ROW_BYTES + q * 2 * ROW_BYTES + 2 * q * Q_ROW_BYTES
+
+
+def main():
+    args = parse()
+    world = int(os.environ.get('WORLD_SIZE', '1'))
+    if args.gpus != 1 or world != 1:
+        print(json.dumps({'error': 'this build measures one GPU only; the attention path has no cross-GPU '
+                                   'exchange (requests shard across GPUs, see DESIGN.md); run with --gpus 1'}))
+        sys.exit(2)
+    import numpy as np
+    import torch
+
+    from qwen3_dspark_amd.draft import DraftBatch, HipDraftAttention
+    from qwen3_dspark_amd.kernels import DEFAULT_CHUNK, SCALE
+    from qwen3_dspark_amd.persistent_kv import Bucket, PersistentTargetKV
+
+    chunk = args.chunk or DEFAULT_CHUNK
+    dev = torch.device('cuda:0')
+    torch.cuda.set_device(dev)
+    steps_total = args.warmup + args.steps
+    contexts, anchors, accepted = workload(steps_total)
+    log(f'[bench] contexts sum={sum(contexts)} min={min(contexts)} max={max(contexts)}; '
+        f'draft blocks={sum(len(a) for a in anchors)}')
+
+    gen = torch.Generator(device=dev).manual_seed(SEED)
+    # -- target store: resident [28, 64, 8192, 8, 128] K and V --------------
+    pool = PersistentTargetKV(layers=VERIFY_LAYERS, slots=B, context_capacity=CAPACITY,
+                              max_query_tokens=B * Q_LEN, heads=8, dim=128, device=dev, chunk=chunk)
+    handles = [pool.add_request(f'req{i}') for i in range(B)]
+    for layer in range(VERIFY_LAYERS):
+        pool.keys[layer].normal_(generator=gen)
+        pool.values[layer].normal_(generator=gen)
+    for h, c in zip(handles, contexts):
+        # the resident rows already hold the seeded prefix; adopt them in place
+        pool.load_prefix(h, pool.keys[:, h.index, :c], pool.values[:, h.index, :c])
+    bucket = Bucket((Q_LEN,) * B, (CAPACITY - Q_LEN,) * B, '64-request stress shape')
+    pool.register_bucket(bucket)
+    qv = torch.randn(VERIFY_LAYERS, B * Q_LEN, 16, 128, generator=gen, device=dev).to(torch.bfloat16)
+    kn = torch.randn(VERIFY_LAYERS, B * Q_LEN, 8, 128, generator=gen, device=dev).to(torch.bfloat16)
+    vn = torch.randn(VERIFY_LAYERS, B * Q_LEN, 8, 128, generator=gen, device=dev).to(torch.bfloat16)
+    # -- draft: slotted context pool [5, 64*8192, 8, 128] -----------------
+    dctx_k = torch.empty(DRAFT_LAYERS, B * CAPACITY, 8, 128, dtype=torch.bfloat16, device=dev)
+    dctx_v = torch.empty_like(dctx_k)
+    for layer in range(DRAFT_LAYERS):
+        dctx_k[layer].normal_(generator=gen)
+        dctx_v[layer].normal_(generator=gen)
+    nq_d = BLOCK * sum(len(a) for a in anchors)
+    qd = torch.randn(DRAFT_LAYERS, nq_d, 16, 128, generator=gen, device=dev).to(torch.bfloat16)
+    bkd = torch.randn(DRAFT_LAYERS, nq_d, 8, 128, generator=gen, device=dev).to(torch.bfloat16)
+    bvd = torch.randn(DRAFT_LAYERS, nq_d, 8, 128, generator=gen, device=dev).to(torch.bfloat16)
+    draft = HipDraftAttention(dev, chunk=chunk)
+    draft_offsets = [h.index * CAPACITY for h in handles]
+    torch.cuda.synchronize()
+
+    ev_v = []
+    ev_d = []
+    step_stats = []
+
+    def round_(step, timed):
+        ctx_now = [pool.length(h) for h in handles]
+        batch = DraftBatch(dev, draft_offsets, contexts, anchors)
+        outs = []
+        for layer in range(DRAFT_LAYERS):
+            if timed:
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                e0.record()
+            outs.append(draft(qd[layer], bkd[layer], bvd[layer], dctx_k[layer], dctx_v[layer], batch, scale=SCALE))
+            if timed:
+                e1.record()
+                ev_d.append((e0, e1))
+        tx = pool.begin(handles, bucket)
+        for layer in range(VERIFY_LAYERS):
+            pool.stage_layer(tx, layer, kn[layer], vn[layer])
+            if timed:
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                e0.record()
+            outs.append(pool.attend(tx, layer, qv[layer]))
+            if timed:
+                e1.record()
+                ev_v.append((e0, e1, verify_bytes(ctx_now)))
+        counts = [int(x) for x in accepted[step]]
+        pool.commit(tx, dict(zip(handles, counts)))
+        step_stats.append((ctx_now, counts))
+        return outs
+
+    log(f'[bench] warmup {args.warmup} steps')
+    for s in range(args.warmup):
+        round_(s, False)
+    torch.cuda.synchronize()
+    log(f'[bench] timing {args.steps} steps')
+    step_stats.clear()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for s in range(args.warmup, steps_total):
+        round_(s, True)
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    ms_step = 1e3 * elapsed / args.steps
+
+    v_ms = [a.elapsed_time(b) for a, b, _ in ev_v]
+    v_bytes = [n for _, _, n in ev_v]
+    d_ms = [a.elapsed_time(b) for a, b in ev_d]
+    v_avg_ms = sum(v_ms) / len(v_ms)
+    v_avg_bytes = sum(v_bytes) / len(v_bytes)
+    d_avg_ms = sum(d_ms) / len(d_ms)
+    d_b = draft_bytes(anchors)
+    v_gbs = v_avg_bytes / (v_avg_ms * 1e-3) / 1e9
+    d_gbs = d_b / (d_avg_ms * 1e-3) / 1e9
+    round_bytes = sum(VERIFY_LAYERS * verify_bytes(c) + DRAFT_LAYERS * d_b
+                      + VERIFY_LAYERS * 2 * B * Q_LEN * ROW_BYTES * 2     # stage: read + write new K/V rows
+                      + VERIFY_LAYERS * 2 * sum(n) * ROW_BYTES * 2       # commit: read + write accepted rows
+                      for c, n in step_stats) / len(step_stats)
+    round_gbs = round_bytes / (ms_step * 1e-3) / 1e9
+    value = B * Q_LEN / (ms_step * 1e-3)
+
+    traffic = None
+    tpath = os.path.join(ROOT, 'profiles', 'verify_attn_traffic.json')
+    if os.path.exists(tpath):
+        with open(tpath) as f:
+            traffic = json.load(f).get('hbm_bytes_per_launch')
+
+    result = {
+        'metric': METRIC, 'value': round(value, 1), 'unit': 'tokens/s', 'n_gpus': 1,
+        'steps': args.steps, 'warmup': args.warmup, 'ms_per_step': round(ms_step, 4),
+        'higher_is_better': True, 'scaling': 'weak', 'vs_baseline': None, 'dtype': 'bf16',
+        'data': 'synthetic (seeded N(0,1) bf16 Q/K/V resident in HBM)',
+        'config': {
+            'workload': 'one speculative round: 5 draft attention layers + 28 verify attention layers '
+                        '(stage + fused KV gather + attention) + commit/rollback, 64 ragged requests, '
+                        'contexts log-uniform [256, 8192], KV capacity 8192 per request, 16q/8kv heads, d128',
+            'requests': B, 'query_rows_per_request': Q_LEN, 'verify_layers': VERIFY_LAYERS,
+            'draft_layers': DRAFT_LAYERS, 'draft_blocks': sum(len(a) for a in anchors),
+            'context_rows': sum(contexts), 'chunk': chunk,
+        },
+        'roofline': {
+            'bound': 'hbm', 'achieved': round(v_gbs, 1), 'peak': HBM_PEAK_GBS, 'unit': 'GB/s',
+            'frac': round(v_gbs / HBM_PEAK_GBS, 4), 'traffic': traffic,
+            'kernel': 'varlen_attn_kernel<true> (fused verification attention)',
+            'avg_launch_ms': round(v_avg_ms, 5), 'algorithmic_bytes_per_launch': int(v_avg_bytes),
+        },
+        'breakdown': {
+            'verify_layer_ms': round(v_avg_ms, 5), 'verify_gbs': round(v_gbs, 1),
+            'verify_attn_tokens_per_s': round(B * Q_LEN / (v_avg_ms * 1e-3), 1),
+            'draft_layer_ms': round(d_avg_ms, 5), 'draft_gbs': round(d_gbs, 1),
+            'draft_frac': round(d_gbs / HBM_PEAK_GBS, 4),
+            'draft_attn_tokens_per_s': round(nq_d / (d_avg_ms * 1e-3), 1),
+            'round_algorithmic_bytes': int(round_bytes), 'round_gbs': round(round_gbs, 1),
+            'round_frac': round(round_gbs / HBM_PEAK_GBS, 4),
+        },
+    }
+
+    if not args.no_cpu_baseline:
+        result['cpu_baseline'], result['parity'] = cpu_leg(args, pool, bucket, handles, contexts, anchors, qv, qd,
+                                                           bkd, bvd, dctx_k, dctx_v, draft, draft_offsets)
+    print(json.dumps(result), flush=True)
+
+
+def cpu_leg(args, pool, bucket, handles, contexts, anchors, qv, qd, bkd, bvd, dctx_k, dctx_v, draft, draft_offsets):
+    """Time the C oracle (OpenMP, host cores) on a bounded sample of the same
+    workload and check the GPU outputs of the sampled layers against it."""
+    import numpy as np
+    import torch
+
+    from oracle import cref
+    from qwen3_dspark_amd.draft import DraftBatch
+    from qwen3_dspark_amd.kernels import SCALE
+
+    threads = max(1, min(CPU_THREADS_CAP, os.cpu_count() or 1))
+    dev = pool.device
+
+    def bits(t):
+        return t.detach().cpu().contiguous().view(torch.int16).numpy().view(np.uint16)
+
+    # One more (untimed) round's inputs: transaction on the current lengths.
+    ctx = [pool.length(h) for h in handles]
+    tx = pool.begin(handles, bucket)
+    kn = torch.randn(args.cpu_verify_layers, B * Q_LEN, 8, 128, device=dev).to(torch.bfloat16)
+    vn = torch.randn_like(kn)
+    stats = {'verify_max_abs': 0.0, 'verify_mean_abs': 0.0, 'draft_max_abs': 0.0, 'draft_mean_abs': 0.0}
+    cu_q = [Q_LEN * i for i in range(B + 1)]
+    slots = [h.index for h in handles]
+    t_verify = []
+    for layer in range(args.cpu_verify_layers):
+        pool.stage_layer(tx, layer, kn[layer], vn[layer])
+        out = pool.attend(tx, layer, qv[layer]).float().cpu().numpy()
+        # host copy of the active rows only: slot-major [64, max c, 8, 128]
+        cmax = max(ctx)
+        kres = bits(pool.keys[layer, :, :cmax])
+        vres = bits(pool.values[layer, :, :cmax])
+        ks, vs, q = bits(pool.scratch_keys[layer]), bits(pool.scratch_values[layer]), bits(qv[layer])
+        t0 = time.perf_counter()
+        ref = cref.verify_attention(q, kres, vres, ks, vs, slots, ctx, cu_q, scale=SCALE, threads=threads)
+        t_verify.append(time.perf_counter() - t0)
+        d = np.abs(out.astype(np.float64) - ref)
+        stats['verify_max_abs'] = max(stats['verify_max_abs'], float(d.max()))
+        stats['verify_mean_abs'] = max(stats['verify_mean_abs'], float(d.mean()))
+    pool.abort(tx)
+    batch = DraftBatch(dev, draft_offsets, contexts, anchors)
+    dout = draft(qd[0], bkd[0], bvd[0], dctx_k[0], dctx_v[0], batch, scale=SCALE).float().cpu().numpy()
+    offs_host, rows = [], []
+    base = 0
+    for o, c in zip(draft_offsets, contexts):
+        rows.append(dctx_k[0, o:o + c])
+        offs_host.append(base)
+        base += c
+    ck = bits(torch.cat(rows))
+    cv = bits(torch.cat([dctx_v[0, o:o + c] for o, c in zip(draft_offsets, contexts)]))
+    cu_b = np.cumsum([0] + [len(a) for a in anchors])
+    flat = [x for a in anchors for x in a]
+    t0 = time.perf_counter()
+    dref = cref.draft_attention(bits(qd[0]), ck, cv, offs_host, contexts, bits(bkd[0]), bits(bvd[0]), cu_b, flat,
+                                scale=SCALE, threads=threads)
+    t_draft = time.perf_counter() - t0
+    d = np.abs(dout.astype(np.float64) - dref)
+    stats['draft_max_abs'] = float(d.max())
+    stats['draft_mean_abs'] = float(d.mean())
+    stats['within_tolerance'] = bool(stats['verify_max_abs'] <= 2e-2 and stats['verify_mean_abs'] <= 2e-3
+                                     and stats['draft_max_abs'] <= 2e-2 and stats['draft_mean_abs'] <= 2e-3)
+    per_verify = sum(t_verify) / len(t_verify)
+    round_s = VERIFY_LAYERS * per_verify + DRAFT_LAYERS * t_draft
+    cpu = {
+        'value': round(B * Q_LEN / round_s, 3), 'unit': 'tokens/s', 'cores': threads, 'kind': 'port',
+        'sample': f'C oracle (oracle/attn_ref.c, FP32, OpenMP) on {len(t_verify)} of 28 verify layers '
+                  f'({per_verify:.3f} s/layer) and 1 of 5 draft layers ({t_draft:.3f} s/layer) of the same '
+                  f'64-request round; round time scaled as 28 verify + 5 draft layers = {round_s:.2f} s',
+    }
+    return cpu, stats
+
+
+if __name__ == '__main__':
+    main()

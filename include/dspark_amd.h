@@ -28,11 +28,14 @@ const char* dspark_last_error(void);
 int dspark_abi_version(void);
 
 /*
- * Bytes of split-K workspace (FP32 partial max/sum/output) needed by an
- * attention call over `n_req` requests whose key rows total at most
- * `key_rows_bound`, with `row_tiles` 16-row tiles per (request, KV head):
- * ceil(max_q/8) for varlen/verify, max blocks per request for draft.
- * Returns -1 on invalid input.
+ * Bytes of split-K workspace needed by an attention call over `n_req`
+ * requests whose key rows total at most `key_rows_bound`, with `row_tiles`
+ * 16-row tiles per (request, KV head): ceil(max_q/8) for varlen/verify, max
+ * blocks per request for draft.  Layout: FP32 partial outputs and (max, sum)
+ * pairs, then one int32 arrival counter per (request, KV head, tile).  The
+ * counters must be zero before the first call (allocate the workspace
+ * zero-filled); every call leaves them zero.  Calls that share a workspace
+ * must not overlap in time.  Returns -1 on invalid input.
  */
 int64_t dspark_attn_workspace_bytes(int n_req, int64_t key_rows_bound, int row_tiles, int chunk);
 

@@ -21,7 +21,12 @@ def require_gfx950(device):
 
 
 class Workspace:
-    """Grow-only device scratch (uint8) reused across calls on one device."""
+    """Grow-only device scratch (uint8) reused across calls on one device.
+
+    Allocated zero-filled: the attention kernels keep their split-K arrival
+    counters in the workspace tail, need them zero before the first call and
+    leave them zero after every call.
+    """
 
     def __init__(self, device):
         self.device = device
@@ -30,7 +35,7 @@ class Workspace:
     def get(self, nbytes):
         nbytes = max(int(nbytes), 16)
         if self._buf is None or self._buf.numel() < nbytes:
-            self._buf = torch.empty(nbytes, dtype=torch.uint8, device=self.device)
+            self._buf = torch.zeros(nbytes, dtype=torch.uint8, device=self.device)
         return self._buf
 
     @property

@@ -31,8 +31,12 @@
 // assignment, which both operands here do by construction.
 //
 // Long contexts are split into fixed chunks of keys (flash-decoding, Dao et
-// al. 2023); every (request, chunk, KV head) is one workgroup and partial
-// (max, sum, unnormalised O) triples are merged in FP32 by merge_kernel.
+// al. 2023); every (request, chunk, KV head) is one workgroup.  A request
+// with more than one chunk writes FP32 partial (max, sum, unnormalised O)
+// triples; the last workgroup of that (request, KV head, tile) to finish -
+// decided by a per-tile arrival counter - merges them and writes the bf16
+// output, then resets the counter to zero.  One launch per attention call,
+// no second merge kernel.
 #include "common.h"
 
 namespace dspark {
@@ -139,6 +143,47 @@ __device__ __forceinline__ void qk_tile(const bf16x8 (&kf)[2][4], const bf16x8 (
   }
 }
 
+
+// ---------------------------------------------------------------------------
+// split-K partials
+// ---------------------------------------------------------------------------
+// Work item p owns part_o[p][16][128] (unnormalised O) and part_ml[p][16][2]
+// (running max in the log2 domain, running sum).  The partials of one
+// (request, KV head, tile) are p0 + c*pstride for its chunks c = 0..nch-1.
+template <int ND>
+__device__ __forceinline__ void merge_partials(const float* __restrict__ part_o, const float* __restrict__ part_ml,
+                                               size_t p0, size_t pstride, int nch, int row, int d0,
+                                               float (&acc)[ND], float& L) {
+  float M = -INFINITY;
+  for (int c = 0; c < nch; ++c) M = fmaxf(M, part_ml[((p0 + c * pstride) * 16 + row) * 2]);
+  L = 0.f;
+  #pragma unroll
+  for (int i = 0; i < ND; ++i) acc[i] = 0.f;
+  for (int c = 0; c < nch; ++c) {
+    const size_t p = p0 + c * pstride;
+    const float mc = part_ml[(p * 16 + row) * 2];
+    const float sc = (mc == -INFINITY) ? 0.f : fast_exp2(mc - M);
+    L += sc * part_ml[(p * 16 + row) * 2 + 1];
+    const float* po = part_o + (p * 16 + row) * HD + d0;
+    #pragma unroll
+    for (int i = 0; i < ND; i += 4) {
+      const f32x4 x = *reinterpret_cast<const f32x4*>(po + i);
+      acc[i] += sc * x[0];
+      acc[i + 1] += sc * x[1];
+      acc[i + 2] += sc * x[2];
+      acc[i + 3] += sc * x[3];
+    }
+  }
+}
+
+// Publish this work item's partial and count its arrival; returns true in
+// exactly one caller per (request, KV head, tile): the last to arrive, which
+// then sees every other partial.  Called by one lane.
+__device__ __forceinline__ bool arrive_last(int* counter, int nch) {
+  const int prev = atomicAdd(counter, 1);
+  return prev == nch - 1;
+}
+
 // ---------------------------------------------------------------------------
 // varlen / verify
 // ---------------------------------------------------------------------------
@@ -155,6 +200,7 @@ struct VarlenArgs {
   bf16* out;              // [nq, 16, 128]
   float* part_o;          // [n_cl*8*tmax][16][128]
   float* part_ml;         // [n_cl*8*tmax][16][2]
+  int* counters;          // [n_req*8*tmax] arrival counters, zero between calls
   int n_req;
   int causal;
   int chunk;
@@ -308,14 +354,8 @@ __global__ __launch_bounds__(256) void varlen_attn_kernel(VarlenArgs a) {
   }
   const int tok_r = 8 * t + (row >> 1);
   const int head_r = 2 * g + (row & 1);
-  if (nch == 1) {
-    if (tok_r < ql) {
-      bf16x8 ov;
-      #pragma unroll
-      for (int i = 0; i < 8; ++i) ov[i] = (bf16)(acc[i] / L);
-      *reinterpret_cast<bf16x8*>(a.out + (size_t)(q0 + tok_r) * Q_ROW + (size_t)head_r * HD + d0) = ov;
-    }
-  } else {
+  bf16* orow = a.out + (size_t)(q0 + tok_r) * Q_ROW + (size_t)head_r * HD + d0;
+  if (nch > 1) {
     const size_t p = (size_t)(cl * 8 + g) * a.tmax + t;
     float* po = a.part_o + (p * 16 + row) * HD + d0;
     *reinterpret_cast<f32x4*>(po) = f32x4{acc[0], acc[1], acc[2], acc[3]};
@@ -324,6 +364,22 @@ __global__ __launch_bounds__(256) void varlen_attn_kernel(VarlenArgs a) {
       a.part_ml[(p * 16 + row) * 2 + 0] = M;
       a.part_ml[(p * 16 + row) * 2 + 1] = L;
     }
+    __threadfence();
+    __syncthreads();
+    __shared__ int s_last;
+    int* counter = a.counters + ((size_t)r * 8 + g) * a.tmax + t;
+    if (tid == 0) s_last = arrive_last(counter, nch);
+    __syncthreads();
+    if (!s_last) return;
+    __threadfence();
+    merge_partials<8>(a.part_o, a.part_ml, (size_t)(first * 8 + g) * a.tmax + t, (size_t)8 * a.tmax, nch, row, d0, acc, L);
+    if (tid == 0) *counter = 0;
+  }
+  if (tok_r < ql) {
+    bf16x8 ov;
+    #pragma unroll
+    for (int i = 0; i < 8; ++i) ov[i] = (bf16)(acc[i] / L);
+    *reinterpret_cast<bf16x8*>(orow) = ov;
   }
 }
 
@@ -344,6 +400,7 @@ struct DraftArgs {
   bf16* out;                // [7*n_blocks, 16, 128]
   float* part_o;
   float* part_ml;
+  int* counters;            // [n_req*8*tmax] arrival counters, zero between calls
   int64_t tok_stride;
   int64_t head_stride;
   int n_req;
@@ -514,9 +571,10 @@ __global__ __launch_bounds__(256) void draft_attn_kernel(DraftArgs a) {
     if (!has[i]) continue;
     const int b = wave + 4 * i;
     const float l = wave_sum_across_groups(st[i].l);
+    const size_t orow0 = (size_t)BLOCK_ROWS * (b0 + b);
     if (nch == 1) {
       if (row_ok) {
-        bf16* op = a.out + (size_t)(BLOCK_ROWS * (b0 + b) + tok) * Q_ROW + (size_t)(2 * g + (col & 1)) * HD + 4 * grp;
+        bf16* op = a.out + (orow0 + tok) * Q_ROW + (size_t)(2 * g + (col & 1)) * HD + 4 * grp;
         #pragma unroll
         for (int nbk = 0; nbk < 8; ++nbk) {
           bf16x4 ov;
@@ -525,105 +583,43 @@ __global__ __launch_bounds__(256) void draft_attn_kernel(DraftArgs a) {
           *reinterpret_cast<bf16x4*>(op + 16 * nbk) = ov;
         }
       }
-    } else {
-      const size_t p = (size_t)(cl * 8 + g) * a.tmax + b;
-      float* po = a.part_o + (p * 16 + col) * HD + 4 * grp;
+      continue;
+    }
+    const size_t p = (size_t)(cl * 8 + g) * a.tmax + b;
+    float* po = a.part_o + (p * 16 + col) * HD + 4 * grp;
+    #pragma unroll
+    for (int nbk = 0; nbk < 8; ++nbk) *reinterpret_cast<f32x4*>(po + 16 * nbk) = st[i].o[nbk];
+    if (grp == 0) {
+      a.part_ml[(p * 16 + col) * 2 + 0] = st[i].m;
+      a.part_ml[(p * 16 + col) * 2 + 1] = l;
+    }
+    __threadfence();
+    __builtin_amdgcn_wave_barrier();
+    int* counter = a.counters + ((size_t)r * 8 + g) * a.tmax + b;
+    int last = 0;
+    if (lane == 0) last = arrive_last(counter, nch) ? 1 : 0;
+    last = __shfl(last, 0);
+    if (!last) continue;
+    __threadfence();
+    // Lane -> (row = lane/4, dims 32*(lane%4) .. +32).
+    const int mrow = lane >> 2;
+    const int md0 = (lane & 3) * 32;
+    float acc[32];
+    float L;
+    merge_partials<32>(a.part_o, a.part_ml, (size_t)(first * 8 + g) * a.tmax + b, (size_t)8 * a.tmax, nch,
+                       mrow, md0, acc, L);
+    if (lane == 0) *counter = 0;
+    if ((mrow >> 1) < BLOCK_ROWS) {
+      bf16* op = a.out + (orow0 + (mrow >> 1)) * Q_ROW + (size_t)(2 * g + (mrow & 1)) * HD + md0;
       #pragma unroll
-      for (int nbk = 0; nbk < 8; ++nbk) *reinterpret_cast<f32x4*>(po + 16 * nbk) = st[i].o[nbk];
-      if (grp == 0) {
-        a.part_ml[(p * 16 + col) * 2 + 0] = st[i].m;
-        a.part_ml[(p * 16 + col) * 2 + 1] = l;
+      for (int v = 0; v < 4; ++v) {
+        bf16x8 ov;
+        #pragma unroll
+        for (int e = 0; e < 8; ++e) ov[e] = (bf16)(acc[8 * v + e] / L);
+        *reinterpret_cast<bf16x8*>(op + 8 * v) = ov;
       }
     }
   }
-}
-
-// ---------------------------------------------------------------------------
-// split-K merge
-// ---------------------------------------------------------------------------
-struct MergeArgs {
-  const int32_t* cu_q;     // varlen/verify
-  const int32_t* cu_k;     // varlen/verify chunk counts
-  const int32_t* ctx_len;  // draft chunk counts
-  const int32_t* cu_b;     // draft block offsets
-  const float* part_o;
-  const float* part_ml;
-  bf16* out;
-  int n_req;
-  int chunk;
-  int tmax;
-  int draft;
-};
-
-// Sum of chunks_for() over requests [0, r): executed by each wave.
-__device__ __forceinline__ int chunk_base(const int32_t* cu, const int32_t* lens, int r, int chunk) {
-  const int lane = threadIdx.x & 63;
-  int acc = 0;
-  for (int r0 = 0; r0 < r; r0 += WAVE) {
-    const int rr = r0 + lane;
-    int n = 0;
-    if (rr < r) n = chunks_for(cu ? (cu[rr + 1] - cu[rr]) : lens[rr], chunk);
-    #pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) n += __shfl_xor(n, off);
-    acc += n;
-  }
-  return acc;
-}
-
-__global__ __launch_bounds__(256) void merge_kernel(MergeArgs a) {
-  const int r = blockIdx.x;
-  const int g = blockIdx.y;
-  const int t = blockIdx.z;
-  int len, out_row0, rows_valid;
-  if (a.draft) {
-    const int b0 = a.cu_b[r];
-    if (t >= a.cu_b[r + 1] - b0) return;
-    len = a.ctx_len[r];
-    out_row0 = BLOCK_ROWS * (b0 + t);
-    rows_valid = BLOCK_ROWS;
-  } else {
-    const int q0 = a.cu_q[r];
-    const int ql = a.cu_q[r + 1] - q0;
-    if (8 * t >= ql) return;
-    len = a.cu_k[r + 1] - a.cu_k[r];
-    out_row0 = q0 + 8 * t;
-    rows_valid = min(8, ql - 8 * t);
-  }
-  const int nch = chunks_for(len, a.chunk);
-  if (nch == 1) return;
-  const int first = chunk_base(a.draft ? nullptr : a.cu_k, a.draft ? a.ctx_len : nullptr, r, a.chunk);
-  const int tid = threadIdx.x;
-  const int row = tid >> 4;
-  const int d0 = (tid & 15) * 8;
-  const int tok = row >> 1;
-  if (tok >= rows_valid) return;
-  float M = -INFINITY;
-  for (int c = 0; c < nch; ++c) {
-    const size_t p = (size_t)((first + c) * 8 + g) * a.tmax + t;
-    M = fmaxf(M, a.part_ml[(p * 16 + row) * 2]);
-  }
-  float L = 0.f;
-  float acc[8];
-  #pragma unroll
-  for (int i = 0; i < 8; ++i) acc[i] = 0.f;
-  for (int c = 0; c < nch; ++c) {
-    const size_t p = (size_t)((first + c) * 8 + g) * a.tmax + t;
-    const float mc = a.part_ml[(p * 16 + row) * 2];
-    const float sc = (mc == -INFINITY) ? 0.f : fast_exp2(mc - M);
-    L += sc * a.part_ml[(p * 16 + row) * 2 + 1];
-    const float* po = a.part_o + (p * 16 + row) * HD + d0;
-    const f32x4 x0 = *reinterpret_cast<const f32x4*>(po);
-    const f32x4 x1 = *reinterpret_cast<const f32x4*>(po + 4);
-    #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      acc[i] += sc * x0[i];
-      acc[4 + i] += sc * x1[i];
-    }
-  }
-  bf16x8 ov;
-  #pragma unroll
-  for (int i = 0; i < 8; ++i) ov[i] = (bf16)(acc[i] / L);
-  *reinterpret_cast<bf16x8*>(a.out + (size_t)(out_row0 + tok) * Q_ROW + (size_t)(2 * g + (row & 1)) * HD + d0) = ov;
 }
 
 }  // namespace dspark
@@ -641,9 +637,14 @@ int64_t n_chunk_items(int n_req, int64_t rows_bound, int chunk) {
   return (rows_bound + chunk - 1) / chunk + n_req;
 }
 
+// [part_o: items x 16 x 128 f32][part_ml: items x 16 x 2 f32][counters: n_req x 8 x tiles i32]
 int64_t workspace_bytes(int n_req, int64_t rows_bound, int tiles, int chunk) {
   const int64_t items = n_chunk_items(n_req, rows_bound, chunk) * HKV * tiles;
-  return items * 16 * (HD + 2) * (int64_t)sizeof(float);
+  return items * 16 * (HD + 2) * (int64_t)sizeof(float) + (int64_t)n_req * HKV * tiles * (int64_t)sizeof(int);
+}
+
+int* counters_of(void* ws, int64_t items) {
+  return reinterpret_cast<int*>(static_cast<float*>(ws) + items * 16 * (HD + 2));
 }
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
@@ -697,27 +698,15 @@ extern "C" int dspark_varlen_attn_fwd(const void* q, const void* k, const void* 
   a.out = static_cast<bf16*>(out);
   a.part_o = static_cast<float*>(workspace);
   a.part_ml = a.part_o + n_cl * HKV * tiles * 16 * HD;
+  a.counters = counters_of(workspace, n_cl * HKV * tiles);
   a.n_req = n_req;
   a.causal = causal ? 1 : 0;
   a.chunk = chunk;
   a.tmax = tiles;
   a.scale_log2 = scale * LOG2E;
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  hipLaunchKernelGGL(varlen_attn_kernel<false>, dim3((unsigned)(n_cl * HKV), tiles), dim3(256), 0, s, a);
-  rc = launch_status("varlen_attn_kernel");
-  if (rc != OK) return rc;
-  MergeArgs m{};
-  m.cu_q = cu_q;
-  m.cu_k = cu_k;
-  m.part_o = a.part_o;
-  m.part_ml = a.part_ml;
-  m.out = a.out;
-  m.n_req = n_req;
-  m.chunk = chunk;
-  m.tmax = tiles;
-  m.draft = 0;
-  hipLaunchKernelGGL(merge_kernel, dim3(n_req, HKV, tiles), dim3(256), 0, s, m);
-  return launch_status("merge_kernel");
+  hipLaunchKernelGGL(varlen_attn_kernel<false>, dim3((unsigned)(n_cl * HKV), tiles), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), a);
+  return launch_status("varlen_attn_kernel");
 }
 
 extern "C" int dspark_verify_attn_fwd(const void* q, const void* k_res, const void* v_res,
@@ -749,27 +738,15 @@ extern "C" int dspark_verify_attn_fwd(const void* q, const void* k_res, const vo
   a.out = static_cast<bf16*>(out);
   a.part_o = static_cast<float*>(workspace);
   a.part_ml = a.part_o + n_cl * HKV * tiles * 16 * HD;
+  a.counters = counters_of(workspace, n_cl * HKV * tiles);
   a.n_req = n_req;
   a.causal = 1;
   a.chunk = chunk;
   a.tmax = tiles;
   a.scale_log2 = scale * LOG2E;
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  hipLaunchKernelGGL(varlen_attn_kernel<true>, dim3((unsigned)(n_cl * HKV), tiles), dim3(256), 0, s, a);
-  rc = launch_status("verify_attn_kernel");
-  if (rc != OK) return rc;
-  MergeArgs m{};
-  m.cu_q = cu_q;
-  m.cu_k = cu_k;
-  m.part_o = a.part_o;
-  m.part_ml = a.part_ml;
-  m.out = a.out;
-  m.n_req = n_req;
-  m.chunk = chunk;
-  m.tmax = tiles;
-  m.draft = 0;
-  hipLaunchKernelGGL(merge_kernel, dim3(n_req, HKV, tiles), dim3(256), 0, s, m);
-  return launch_status("merge_kernel");
+  hipLaunchKernelGGL(varlen_attn_kernel<true>, dim3((unsigned)(n_cl * HKV), tiles), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), a);
+  return launch_status("verify_attn_kernel");
 }
 
 extern "C" int dspark_draft_attn_fwd(const void* q, const void* k_ctx, const void* v_ctx,
@@ -806,26 +783,14 @@ extern "C" int dspark_draft_attn_fwd(const void* q, const void* k_ctx, const voi
   a.out = static_cast<bf16*>(out);
   a.part_o = static_cast<float*>(workspace);
   a.part_ml = a.part_o + n_cl * HKV * max_blocks * 16 * HD;
+  a.counters = counters_of(workspace, n_cl * HKV * max_blocks);
   a.tok_stride = tok_stride;
   a.head_stride = head_stride;
   a.n_req = n_req;
   a.chunk = chunk;
   a.tmax = max_blocks;
   a.scale_log2 = scale * LOG2E;
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  hipLaunchKernelGGL(draft_attn_kernel, dim3((unsigned)(n_cl * HKV)), dim3(256), 0, s, a);
-  rc = launch_status("draft_attn_kernel");
-  if (rc != OK) return rc;
-  MergeArgs m{};
-  m.ctx_len = ctx_len;
-  m.cu_b = cu_blocks;
-  m.part_o = a.part_o;
-  m.part_ml = a.part_ml;
-  m.out = a.out;
-  m.n_req = n_req;
-  m.chunk = chunk;
-  m.tmax = max_blocks;
-  m.draft = 1;
-  hipLaunchKernelGGL(merge_kernel, dim3(n_req, HKV, max_blocks), dim3(256), 0, s, m);
-  return launch_status("merge_kernel(draft)");
+  hipLaunchKernelGGL(draft_attn_kernel, dim3((unsigned)(n_cl * HKV)), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), a);
+  return launch_status("draft_attn_kernel");
 }

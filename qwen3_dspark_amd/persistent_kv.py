@@ -171,7 +171,7 @@ class _Workspace:
         self.req = torch.zeros(3 * r, dtype=torch.int32, device=device)
         self.keys = torch.empty((n, heads, dim), dtype=dtype, device=device)
         self.values = torch.empty_like(self.keys)
-        self.attn = torch.empty(_attn_workspace_bytes(bucket, chunk), dtype=torch.uint8, device=device)
+        self.attn = torch.zeros(_attn_workspace_bytes(bucket, chunk), dtype=torch.uint8, device=device)
 
     def pointers(self):
         return {k: v.data_ptr() for k, v in vars(self).items() if isinstance(v, torch.Tensor) and v.is_cuda}

@@ -37,8 +37,9 @@ def test_library_exports_every_declared_symbol():
 def test_workspace_size_formula():
     lib = _native.load()
     # (ceil(rows/chunk) + n_req) items * 8 KV heads * tiles * 16 rows * (128 + 2) floats
-    assert lib.dspark_attn_workspace_bytes(4, 1000, 1, 512) == (2 + 4) * 8 * 1 * 16 * 130 * 4
-    assert lib.dspark_attn_workspace_bytes(64, 524288 + 448, 1, 512) == (1025 + 64) * 8 * 16 * 130 * 4
+    # + one int32 arrival counter per (request, KV head, tile)
+    assert lib.dspark_attn_workspace_bytes(4, 1000, 1, 512) == (2 + 4) * 8 * 1 * 16 * 130 * 4 + 4 * 8 * 4
+    assert lib.dspark_attn_workspace_bytes(64, 524288 + 448, 1, 512) == (1025 + 64) * 8 * 16 * 130 * 4 + 64 * 8 * 4
     assert lib.dspark_attn_workspace_bytes(0, 10, 1, 512) == -1
 
 
