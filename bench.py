@@ -123,8 +123,8 @@ def main():
     qv = torch.randn(VERIFY_LAYERS, B * Q_LEN, 16, 128, generator=gen, device=dev).to(torch.bfloat16)
     kn = torch.randn(VERIFY_LAYERS, B * Q_LEN, 8, 128, generator=gen, device=dev).to(torch.bfloat16)
     vn = torch.randn(VERIFY_LAYERS, B * Q_LEN, 8, 128, generator=gen, device=dev).to(torch.bfloat16)
-    # -- draft: slotted context pool [5, 64*8192, 8, 128] -----------------
-    dctx_k = torch.empty(DRAFT_LAYERS, B * CAPACITY, 8, 128, dtype=torch.bfloat16, device=dev)
+    # -- draft: head-major slotted context pool [5, 64, 8, 8192, 128] ----
+    dctx_k = torch.empty(DRAFT_LAYERS, B, 8, CAPACITY, 128, dtype=torch.bfloat16, device=dev)
     dctx_v = torch.empty_like(dctx_k)
     for layer in range(DRAFT_LAYERS):
         dctx_k[layer].normal_(generator=gen)
@@ -134,7 +134,7 @@ def main():
     bkd = torch.randn(DRAFT_LAYERS, nq_d, 8, 128, generator=gen, device=dev).to(torch.bfloat16)
     bvd = torch.randn(DRAFT_LAYERS, nq_d, 8, 128, generator=gen, device=dev).to(torch.bfloat16)
     draft = HipDraftAttention(dev, chunk=chunk)
-    draft_offsets = [h.index * CAPACITY for h in handles]
+    draft_offsets = [h.index * CAPACITY for h in handles]   # slot * capacity + first position
     torch.cuda.synchronize()
 
     ev_v = []
@@ -282,14 +282,14 @@ def cpu_leg(args, pool, bucket, handles, contexts, anchors, qv, qd, bkd, bvd, dc
     pool.abort(tx)
     batch = DraftBatch(dev, draft_offsets, contexts, anchors)
     dout = draft(qd[0], bkd[0], bvd[0], dctx_k[0], dctx_v[0], batch, scale=SCALE).float().cpu().numpy()
-    offs_host, rows = [], []
+    offs_host = []
     base = 0
-    for o, c in zip(draft_offsets, contexts):
-        rows.append(dctx_k[0, o:o + c])
+    for c in contexts:
         offs_host.append(base)
         base += c
-    ck = bits(torch.cat(rows))
-    cv = bits(torch.cat([dctx_v[0, o:o + c] for o, c in zip(draft_offsets, contexts)]))
+    # token-major host copies of each request's context rows
+    ck = bits(torch.cat([dctx_k[0, o // CAPACITY, :, :c].transpose(0, 1) for o, c in zip(draft_offsets, contexts)]))
+    cv = bits(torch.cat([dctx_v[0, o // CAPACITY, :, :c].transpose(0, 1) for o, c in zip(draft_offsets, contexts)]))
     cu_b = np.cumsum([0] + [len(a) for a in anchors])
     flat = [x for a in anchors for x in a]
     t0 = time.perf_counter()

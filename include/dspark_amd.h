@@ -31,15 +31,22 @@ int dspark_abi_version(void);
  * Bytes of split-K workspace needed by an attention call over `n_req`
  * requests whose key rows total at most `key_rows_bound`, with `row_tiles`
  * 16-row tiles per (request, KV head): ceil(max_q/8) for varlen/verify, max
- * blocks per request for draft.  Layout: FP32 partial outputs and (max, sum)
- * pairs, then one int32 arrival counter per (request, KV head, tile).  The
- * counters must be zero before the first call (allocate the workspace
- * zero-filled); every call leaves them zero.  Calls that share a workspace
- * must not overlap in time.  Returns -1 on invalid input.
+ * blocks per request for draft.  Layout: FP32 partial outputs, then FP32
+ * (max, sum) pairs.  Each attention call is a chunk kernel plus a merge
+ * kernel on `stream`; calls that share a workspace must not overlap in time.
+ * Returns -1 on invalid input.
  */
 int64_t dspark_attn_workspace_bytes(int n_req, int64_t key_rows_bound, int row_tiles, int chunk);
 
 /*
+ * Work lists.  Every attention entry point splits request r's keys into
+ * ceil(len_r / chunk) chunks (at least one) and runs one workgroup per
+ * (chunk, KV head).  With work == NULL the chunks are dispatched in request
+ * order over a grid sized from the row bound; otherwise work = int32
+ * [n_work][2] lists (request, chunk) pairs - every chunk exactly once - in
+ * the order they should be dispatched (longest first balances ragged
+ * lengths).  The list is not validated on the device.
+ *
  * Packed varlen attention, bottom-right causal (causal=1) or noncausal.
  * q [q_rows,16,128], k/v [k_rows,8,128], cu_q/cu_k int32 [n_req+1].
  * Request r attends queries cu_q[r]..cu_q[r+1] to keys cu_k[r]..cu_k[r+1];
@@ -53,12 +60,14 @@ int64_t dspark_attn_workspace_bytes(int n_req, int64_t key_rows_bound, int row_t
 int dspark_varlen_attn_fwd(const void* q, const void* k, const void* v,
                            const int32_t* cu_q, const int32_t* cu_k, int n_req,
                            int64_t q_rows, int64_t k_rows, int max_q, int causal,
-                           float scale, int chunk, void* out,
-                           void* workspace, int64_t workspace_bytes, void* stream);
+                           float scale, int chunk, const int32_t* work, int n_work,
+                           void* out, void* workspace, int64_t workspace_bytes, void* stream);
 
 /*
  * Fused verification attention over the persistent KV store.
- * k_res/v_res: one layer of the resident store, [slots, ctx_capacity, 8, 128];
+ * k_res/v_res: one layer of the resident store; element (slot, head, pos, d)
+ * at slot*slot_stride + head*head_stride + pos*tok_stride + d (elements;
+ * head-major [slots, 8, cap, 128] is 8*cap*128, cap*128, 128).
  * k_scr/v_scr: the same layer of the scratch, [max_q, 8, 128].
  * cu_q/cu_k: int32 [n_req+1] as built by dspark_txn_metadata; slots: int32 [n_req].
  * Request r sees its committed context (resident rows slot*cap .. +c) followed
@@ -71,8 +80,9 @@ int dspark_varlen_attn_fwd(const void* q, const void* k, const void* v,
 int dspark_verify_attn_fwd(const void* q, const void* k_res, const void* v_res,
                            const void* k_scr, const void* v_scr,
                            const int32_t* cu_q, const int32_t* cu_k, const int32_t* slots,
-                           int n_req, int64_t ctx_capacity, int64_t key_rows_bound, int max_q,
-                           float scale, int chunk, void* out,
+                           int n_req, int64_t slot_stride, int64_t tok_stride, int64_t head_stride,
+                           int64_t key_rows_bound, int max_q, float scale, int chunk,
+                           const int32_t* work, int n_work, void* out,
                            void* workspace, int64_t workspace_bytes, void* stream);
 
 /*
@@ -95,6 +105,7 @@ int dspark_draft_attn_fwd(const void* q, const void* k_ctx, const void* v_ctx,
                           const void* k_blk, const void* v_blk,
                           const int32_t* cu_blocks, const int32_t* anchors,
                           int n_req, int64_t ctx_rows_bound, int max_blocks, float scale, int chunk,
+                          const int32_t* work, int n_work,
                           void* out, void* workspace, int64_t workspace_bytes, void* stream);
 
 /*
@@ -120,26 +131,34 @@ int dspark_kv_stage(const void* k_new, const void* v_new, void* k_scr_layer, voi
 
 /*
  * Commit the accepted prefix n_accepted[r] of every request for all layers
- * in one launch: scratch rows cu_q[r]..+n -> resident rows slot*cap+c..+n
- * (dspark_qwen/persistent_target_kv.py:479-483).  Rows n..q-1 are rolled
- * back by omission.  req as for dspark_txn_metadata (pre-commit context).
+ * in one launch: scratch rows cu_q[r]..+n -> resident positions c..c+n of
+ * the request's slot (dspark_qwen/persistent_target_kv.py:479-483).  Rows
+ * n..q-1 are rolled back by omission.  req as for dspark_txn_metadata
+ * (pre-commit context).  Resident piece (layer, slot, head, pos) of
+ * piece_bytes starts at layer*layer_stride + slot*slot_stride +
+ * head*head_stride + pos*tok_stride (bytes); scratch is [L, scratch_rows,
+ * heads * piece_bytes].
  */
 int dspark_kv_commit(void* k_res, void* v_res, const void* k_scr, const void* v_scr,
                      const int32_t* req, const int32_t* cu_q, const int32_t* n_accepted,
-                     int n_req, int max_q, int layers, int64_t slots, int64_t ctx_capacity,
-                     int64_t scratch_rows, int64_t row_bytes, void* stream);
+                     int n_req, int max_q, int layers, int64_t layer_stride, int64_t slot_stride,
+                     int64_t head_stride, int64_t tok_stride, int64_t ctx_capacity, int heads,
+                     int64_t piece_bytes, int64_t scratch_rows, void* stream);
 
 /*
  * Materialised capacity-length K/V of prepare_attention
- * (dspark_qwen/persistent_target_kv.py:452-459): row j = valid[j] ?
- * (from_scratch[j] ? scratch[scratch_idx[j]] : resident[committed_idx[j]]) : 0.
+ * (dspark_qwen/persistent_target_kv.py:452-459), token-major out:
+ * row j = valid[j] ? (from_scratch[j] ? scratch[scratch_idx[j]]
+ *                                     : resident(slot, pos) with committed_idx[j] = slot*cap+pos) : 0.
+ * Resident geometry (bytes) as for dspark_kv_commit, one layer.
  */
 int dspark_kv_gather(const void* k_res_layer, const void* v_res_layer,
                      const void* k_scr_layer, const void* v_scr_layer,
                      const int64_t* committed_idx, const int64_t* scratch_idx,
                      const uint8_t* from_scratch, const uint8_t* valid,
-                     int64_t key_capacity, int64_t res_rows, int64_t scr_rows, int64_t row_bytes,
-                     void* k_out, void* v_out, void* stream);
+                     int64_t key_capacity, int64_t slots, int64_t slot_stride, int64_t head_stride,
+                     int64_t tok_stride, int64_t ctx_capacity, int heads, int64_t piece_bytes,
+                     int64_t scr_rows, void* k_out, void* v_out, void* stream);
 
 #ifdef __cplusplus
 }

@@ -21,12 +21,7 @@ def require_gfx950(device):
 
 
 class Workspace:
-    """Grow-only device scratch (uint8) reused across calls on one device.
-
-    Allocated zero-filled: the attention kernels keep their split-K arrival
-    counters in the workspace tail, need them zero before the first call and
-    leave them zero after every call.
-    """
+    """Grow-only device scratch (uint8) reused across calls on one device."""
 
     def __init__(self, device):
         self.device = device

@@ -22,13 +22,15 @@ SIGNATURES = {
     'dspark_last_error': (ctypes.c_char_p, []),
     'dspark_abi_version': (_I, []),
     'dspark_attn_workspace_bytes': (_L, [_I, _L, _I, _I]),
-    'dspark_varlen_attn_fwd': (_I, [_P, _P, _P, _P, _P, _I, _L, _L, _I, _I, _F, _I, _P, _P, _L, _P]),
-    'dspark_verify_attn_fwd': (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _I, _L, _L, _I, _F, _I, _P, _P, _L, _P]),
-    'dspark_draft_attn_fwd': (_I, [_P, _P, _P, _P, _P, _P, _L, _L, _P, _P, _P, _P, _I, _L, _I, _F, _I, _P, _P, _L, _P]),
+    'dspark_varlen_attn_fwd': (_I, [_P, _P, _P, _P, _P, _I, _L, _L, _I, _I, _F, _I, _P, _I, _P, _P, _L, _P]),
+    'dspark_verify_attn_fwd': (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _I, _L, _L, _L, _L, _I, _F, _I, _P, _I,
+                                    _P, _P, _L, _P]),
+    'dspark_draft_attn_fwd': (_I, [_P, _P, _P, _P, _P, _P, _L, _L, _P, _P, _P, _P, _I, _L, _I, _F, _I, _P, _I,
+                                   _P, _P, _L, _P]),
     'dspark_txn_metadata': (_I, [_P, _I, _L, _L, _L, _P, _P, _P, _P, _P, _P, _P, _P]),
     'dspark_kv_stage': (_I, [_P, _P, _P, _P, _L, _L, _P]),
-    'dspark_kv_commit': (_I, [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _L, _L, _L, _L, _P]),
-    'dspark_kv_gather': (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _L, _L, _L, _L, _P, _P, _P]),
+    'dspark_kv_commit': (_I, [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _L, _L, _L, _L, _L, _I, _L, _L, _P]),
+    'dspark_kv_gather': (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _L, _L, _L, _L, _L, _L, _I, _L, _L, _P, _P, _P]),
 }
 
 ABI_VERSION = 1

@@ -30,13 +30,11 @@
 // is irrelevant as long as A and B use the same (lane group, slot) -> k
 // assignment, which both operands here do by construction.
 //
-// Long contexts are split into fixed chunks of keys (flash-decoding, Dao et
-// al. 2023); every (request, chunk, KV head) is one workgroup.  A request
-// with more than one chunk writes FP32 partial (max, sum, unnormalised O)
-// triples; the last workgroup of that (request, KV head, tile) to finish -
-// decided by a per-tile arrival counter - merges them and writes the bf16
-// output, then resets the counter to zero.  One launch per attention call,
-// no second merge kernel.
+// Long contexts are split into chunks of keys (flash-decoding, Dao et al.
+// 2023); every (request, chunk, KV head) is one workgroup.  A request with
+// more than one chunk writes FP32 partial (max, sum, unnormalised O) triples
+// that merge_kernel combines; the kernel boundary makes them visible without
+// any per-workgroup cache flush.
 #include "common.h"
 
 namespace dspark {
@@ -45,33 +43,46 @@ constexpr int KT = 32;                 // keys per wave iteration
 constexpr int ROWB = HD * 2;           // bytes per LDS K/V row (256)
 constexpr int OPITCH = HD + 4;         // floats per row in the merge buffer
 
-// XOR swizzle of the 16-byte chunk index of LDS row k.  Chosen so that
-//  - the V^T gather (row 8*grp+s, dims 16*nb+col) hits 8 distinct chunks
-//    per 8-lane phase, and
-//  - the K fragment read (rows 8q+4j+e, chunk 4ks+grp) does as well.
+// XOR swizzle of the 16-byte chunk index of LDS row k (rows are 256 B).
+// Conflict-free for the three access patterns on a K/V tile:
+//  - row writes: 8 lanes write chunks 0..7 (or 8..15) of one row;
+//  - transpose reads (V^T): a 16-lane group reads 4 rows r=0..3, chunks
+//    2nb and 2nb+1; swz's bits 2:1 = r keep the 8 (row, chunk) pairs apart;
+//  - K fragment reads: 8 lanes read rows 8q+4j+e (q<2, e<4), one chunk;
+//    (k&3, (k>>3)&1) takes all 8 values.
 __device__ __forceinline__ int swz(int k) {
-  return (((k >> 3) & 3) << 1) ^ ((k & 1) | ((k & 2) << 1));
+  return ((k & 3) << 1) | ((k >> 3) & 1);
 }
 
 __device__ __forceinline__ int lds_chunk_off(int k, int chunk16) {
   return k * ROWB + ((chunk16 ^ swz(k)) << 4);
 }
 
-__device__ __forceinline__ int lds_elem_off(int k, int d) {
-  return k * ROWB + ((((d >> 3) ^ swz(k))) << 4) + ((d & 7) << 1);
-}
+typedef __attribute__((address_space(3))) bf16x4 lds_bf16x4;
 
-// Read the V^T A-operand for dims 16*nb + col from an LDS tile whose row r
-// holds key r; lane group grp covers keys 8*grp .. 8*grp+7.
-__device__ __forceinline__ bf16x8 lds_vt(const unsigned char* tile, int nb, int col, int grp) {
-  union { bf16x8 v; unsigned short u[8]; } t;
-  const int d = 16 * nb + col;
+// V^T A-operand for dims 16*nb .. 16*nb+15 from an LDS tile whose row k holds
+// key k: lane (j, grp) receives V[8*grp + s][16*nb + j] for s = 0..7, via two
+// transpose reads (ds_read_b64_tr_b16: within each 16-lane group, lane
+// 4*r+c supplies row r, dims 4c..4c+3 of a 4x16 tile; lane j receives
+// column j of the 4 rows).
+__device__ __forceinline__ bf16x8 lds_vt(const unsigned char* tile, int nb, int lane) {
+  const int grp = lane >> 4;
+  const int r = (lane >> 2) & 3;
+  const int c4 = lane & 3;
+  const int chunk = 2 * nb + (c4 >> 1);
+  const int k0 = 8 * grp + r;
+  const int k1 = k0 + 4;
+  const unsigned char* p0 = tile + k0 * ROWB + ((chunk ^ swz(k0)) << 4) + ((c4 & 1) << 3);
+  const unsigned char* p1 = tile + k1 * ROWB + ((chunk ^ swz(k1)) << 4) + ((c4 & 1) << 3);
+  const bf16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)p0);
+  const bf16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)p1);
+  bf16x8 v;
   #pragma unroll
-  for (int s = 0; s < 8; ++s) {
-    const int k = 8 * grp + s;
-    t.u[s] = *reinterpret_cast<const unsigned short*>(tile + lds_elem_off(k, d));
+  for (int i = 0; i < 4; ++i) {
+    v[i] = lo[i];
+    v[4 + i] = hi[i];
   }
-  return t.v;
+  return v;
 }
 
 __device__ __forceinline__ void wave_lds_sync() {
@@ -176,12 +187,20 @@ __device__ __forceinline__ void merge_partials(const float* __restrict__ part_o,
   }
 }
 
-// Publish this work item's partial and count its arrival; returns true in
-// exactly one caller per (request, KV head, tile): the last to arrive, which
-// then sees every other partial.  Called by one lane.
-__device__ __forceinline__ bool arrive_last(int* counter, int nch) {
-  const int prev = atomicAdd(counter, 1);
-  return prev == nch - 1;
+
+// Sum of chunks_for() over requests [0, r), executed by each wave.
+__device__ __forceinline__ int chunk_base(const int32_t* cu, const int32_t* lens, int r, int chunk) {
+  const int lane = threadIdx.x & 63;
+  int acc = 0;
+  for (int r0 = 0; r0 < r; r0 += WAVE) {
+    const int rr = r0 + lane;
+    int n = 0;
+    if (rr < r) n = chunks_for(cu ? (cu[rr + 1] - cu[rr]) : lens[rr], chunk);
+    #pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) n += __shfl_xor(n, off);
+    acc += n;
+  }
+  return acc;
 }
 
 // ---------------------------------------------------------------------------
@@ -196,11 +215,13 @@ struct VarlenArgs {
   const int32_t* cu_q;    // [B+1]
   const int32_t* cu_k;    // [B+1]
   const int32_t* slots;   // verify: resident slot per request
-  int64_t slot_rows;      // verify: context capacity (rows per slot)
+  int64_t slot_stride;    // verify: elements between resident slots
+  int64_t a_tok_stride;   // segment A elements between token rows
+  int64_t a_head_stride;  // segment A elements between KV heads
+  const int32_t* work;    // optional [n_items][2] (request, chunk) dispatch order
   bf16* out;              // [nq, 16, 128]
   float* part_o;          // [n_cl*8*tmax][16][128]
   float* part_ml;         // [n_cl*8*tmax][16][2]
-  int* counters;          // [n_req*8*tmax] arrival counters, zero between calls
   int n_req;
   int causal;
   int chunk;
@@ -222,15 +243,22 @@ __global__ __launch_bounds__(256) void varlen_attn_kernel(VarlenArgs a) {
   const int cl = blockIdx.x >> 3;
   const int t = blockIdx.y;
 
-  int r, first;
-  locate_chunk(a.cu_k, nullptr, a.n_req, a.chunk, cl, r, first);
-  if (r < 0) return;
+  int r, first, c;
+  if (a.work) {
+    r = a.work[2 * cl];
+    c = a.work[2 * cl + 1];
+    first = chunk_base(a.cu_k, nullptr, r, a.chunk);
+  } else {
+    locate_chunk(a.cu_k, nullptr, a.n_req, a.chunk, cl, r, first);
+    if (r < 0) return;
+    c = cl - first;
+  }
+  const int item = first + c;   // partial slot (request-major chunk numbering)
   const int q0 = a.cu_q[r];
   const int ql = a.cu_q[r + 1] - q0;
   if (8 * t >= ql) return;
   const int kbeg = a.cu_k[r];
   const int kl = a.cu_k[r + 1] - kbeg;
-  const int c = cl - first;
   const int nch = chunks_for(kl, a.chunk);
   const int k0 = c * a.chunk;
   const int k1 = min(k0 + a.chunk, kl);
@@ -243,7 +271,7 @@ __global__ __launch_bounds__(256) void varlen_attn_kernel(VarlenArgs a) {
   int a_len;
   if (VERIFY) {
     a_len = kl - ql;
-    const size_t abase = (size_t)a.slots[r] * (size_t)a.slot_rows * KV_ROW + (size_t)g * HD;
+    const size_t abase = (size_t)a.slots[r] * (size_t)a.slot_stride + (size_t)g * a.a_head_stride;
     kA = a.k_a + abase;
     vA = a.v_a + abase;
     const size_t bbase = (size_t)q0 * KV_ROW + (size_t)g * HD;
@@ -279,45 +307,56 @@ __global__ __launch_bounds__(256) void varlen_attn_kernel(VarlenArgs a) {
   row_init(st);
   unsigned char* vs = smem + wave * KT * ROWB;
 
-  for (int kt = k0 + KT * wave; kt < kend; kt += KT * 4) {
-    bf16x8 kf[2][4];
+  // Row kk of this request, clamped to kend-1 so that every load is in
+  // range; rows past kend are masked out of the softmax and zeroed in V.
+  auto krow = [&](int kk) -> const bf16* {
+    kk = min(kk, kend - 1);
+    return kk < a_len ? kA + (size_t)kk * a.a_tok_stride : kB + (size_t)(kk - a_len) * KV_ROW;
+  };
+  auto vrow = [&](int kk) -> const bf16* {
+    kk = min(kk, kend - 1);
+    return kk < a_len ? vA + (size_t)kk * a.a_tok_stride : vB + (size_t)(kk - a_len) * KV_ROW;
+  };
+  // One 32-key tile: K as the S^T A-operand (lane (m, grp) holds key
+  // 8*(m/4)+4j+m%4, dims 32ks+8grp..+8), V as 4 full rows per load.
+  struct Tile {
+    bf16x8 k[2][4];
+    bf16x8 v[8];
+  };
+  auto load_tile = [&](int kt, Tile& T) {
     #pragma unroll
     for (int j = 0; j < 2; ++j) {
-      const int kk = kt + 8 * (col >> 2) + 4 * j + (col & 3);
-      if (kk < kend) {
-        const bf16* p = (kk < a_len ? kA + (size_t)kk * KV_ROW : kB + (size_t)(kk - a_len) * KV_ROW) + 8 * grp;
-        #pragma unroll
-        for (int ks = 0; ks < 4; ++ks) kf[j][ks] = ld8(p + 32 * ks);
-      } else {
-        #pragma unroll
-        for (int ks = 0; ks < 4; ++ks) kf[j][ks] = zero8();
-      }
+      const bf16* p = krow(kt + 8 * (col >> 2) + 4 * j + (col & 3)) + 8 * grp;
+      #pragma unroll
+      for (int ks = 0; ks < 4; ++ks) T.k[j][ks] = ld8(p + 32 * ks);
     }
-    bf16x8 vf[8];
     #pragma unroll
-    for (int i2 = 0; i2 < 8; ++i2) {
-      const int kk = kt + 4 * i2 + grp;
-      if (kk < kend) {
-        const bf16* p = (kk < a_len ? vA + (size_t)kk * KV_ROW : vB + (size_t)(kk - a_len) * KV_ROW) + 8 * col;
-        vf[i2] = ld8(p);
-      } else {
-        vf[i2] = zero8();
-      }
+    for (int i2 = 0; i2 < 8; ++i2) T.v[i2] = ld8(vrow(kt + 4 * i2 + grp) + 8 * col);
+  };
+  auto compute_tile = [&](int kt, Tile& T) {
+    if (kt + KT > kend) {
+      #pragma unroll
+      for (int i2 = 0; i2 < 8; ++i2)
+        if (kt + 4 * i2 + grp >= kend) T.v[i2] = zero8();
     }
     f32x4 s0, s1;
-    qk_tile(kf, qf, s0, s1);
+    qk_tile(T.k, qf, s0, s1);
     #pragma unroll
-    for (int i2 = 0; i2 < 8; ++i2) {
-      const int k = 4 * i2 + grp;
-      *reinterpret_cast<bf16x8*>(vs + lds_chunk_off(k, col)) = vf[i2];
-    }
+    for (int i2 = 0; i2 < 8; ++i2)
+      *reinterpret_cast<bf16x8*>(vs + lds_chunk_off(4 * i2 + grp, col)) = T.v[i2];
     const bf16x8 pb = softmax_update(st, s0, s1, kt + 8 * grp, vis, a.scale_log2);
     wave_lds_sync();
     bf16x8 vt[8];
     #pragma unroll
-    for (int nb = 0; nb < 8; ++nb) vt[nb] = lds_vt(vs, nb, col, grp);
+    for (int nb = 0; nb < 8; ++nb) vt[nb] = lds_vt(vs, nb, lane);
     pv_update(st, pb, vt);
     wave_lds_sync();
+  };
+
+  for (int kt = k0 + KT * wave; kt < kend; kt += KT * 4) {
+    Tile T;
+    load_tile(kt, T);
+    compute_tile(kt, T);
   }
 
   st.l = wave_sum_across_groups(st.l);
@@ -356,7 +395,7 @@ __global__ __launch_bounds__(256) void varlen_attn_kernel(VarlenArgs a) {
   const int head_r = 2 * g + (row & 1);
   bf16* orow = a.out + (size_t)(q0 + tok_r) * Q_ROW + (size_t)head_r * HD + d0;
   if (nch > 1) {
-    const size_t p = (size_t)(cl * 8 + g) * a.tmax + t;
+    const size_t p = (size_t)(item * 8 + g) * a.tmax + t;
     float* po = a.part_o + (p * 16 + row) * HD + d0;
     *reinterpret_cast<f32x4*>(po) = f32x4{acc[0], acc[1], acc[2], acc[3]};
     *reinterpret_cast<f32x4*>(po + 4) = f32x4{acc[4], acc[5], acc[6], acc[7]};
@@ -364,16 +403,7 @@ __global__ __launch_bounds__(256) void varlen_attn_kernel(VarlenArgs a) {
       a.part_ml[(p * 16 + row) * 2 + 0] = M;
       a.part_ml[(p * 16 + row) * 2 + 1] = L;
     }
-    __threadfence();
-    __syncthreads();
-    __shared__ int s_last;
-    int* counter = a.counters + ((size_t)r * 8 + g) * a.tmax + t;
-    if (tid == 0) s_last = arrive_last(counter, nch);
-    __syncthreads();
-    if (!s_last) return;
-    __threadfence();
-    merge_partials<8>(a.part_o, a.part_ml, (size_t)(first * 8 + g) * a.tmax + t, (size_t)8 * a.tmax, nch, row, d0, acc, L);
-    if (tid == 0) *counter = 0;
+    return;
   }
   if (tok_r < ql) {
     bf16x8 ov;
@@ -400,9 +430,9 @@ struct DraftArgs {
   bf16* out;                // [7*n_blocks, 16, 128]
   float* part_o;
   float* part_ml;
-  int* counters;            // [n_req*8*tmax] arrival counters, zero between calls
   int64_t tok_stride;
   int64_t head_stride;
+  const int32_t* work;      // optional [n_items][2] (request, chunk) dispatch order
   int n_req;
   int chunk;
   int tmax;                 // max blocks per request (<= 8)
@@ -426,11 +456,18 @@ __global__ __launch_bounds__(256) void draft_attn_kernel(DraftArgs a) {
   const int g = blockIdx.x & 7;
   const int cl = blockIdx.x >> 3;
 
-  int r, first;
-  locate_chunk(nullptr, a.ctx_len, a.n_req, a.chunk, cl, r, first);
-  if (r < 0) return;
+  int r, first, c;
+  if (a.work) {
+    r = a.work[2 * cl];
+    c = a.work[2 * cl + 1];
+    first = chunk_base(nullptr, a.ctx_len, r, a.chunk);
+  } else {
+    locate_chunk(nullptr, a.ctx_len, a.n_req, a.chunk, cl, r, first);
+    if (r < 0) return;
+    c = cl - first;
+  }
+  const int item = first + c;
   const int ctx = a.ctx_len[r];
-  const int c = cl - first;
   const int nch = chunks_for(ctx, a.chunk);
   const int k0 = c * a.chunk;
   const int k1 = min(k0 + a.chunk, ctx);
@@ -514,7 +551,7 @@ __global__ __launch_bounds__(256) void draft_attn_kernel(DraftArgs a) {
       }
       bf16x8 vt[8];
       #pragma unroll
-      for (int nbk = 0; nbk < 8; ++nbk) vt[nbk] = lds_vt(vs_tile + KT * h * ROWB, nbk, col, grp);
+      for (int nbk = 0; nbk < 8; ++nbk) vt[nbk] = lds_vt(vs_tile + KT * h * ROWB, nbk, lane);
       #pragma unroll
       for (int i = 0; i < DRAFT_TILES_PER_WAVE; ++i) {
         if (!(has[i] && tile_anchor[i] > kt)) continue;
@@ -560,7 +597,11 @@ __global__ __launch_bounds__(256) void draft_attn_kernel(DraftArgs a) {
       wave_lds_sync();
       bf16x8 vt[8];
       #pragma unroll
-      for (int nbk = 0; nbk < 8; ++nbk) vt[nbk] = grp == 0 ? lds_vt(wv, nbk, col, 0) : zero8();
+      for (int nbk = 0; nbk < 8; ++nbk) {
+        // keys 8*grp+s >= 8 do not exist in a 7-row block
+        vt[nbk] = lds_vt(wv, nbk, lane);
+        if (grp != 0) vt[nbk] = zero8();
+      }
       pv_update(st[i], pb, vt);
       wave_lds_sync();
     }
@@ -585,7 +626,7 @@ __global__ __launch_bounds__(256) void draft_attn_kernel(DraftArgs a) {
       }
       continue;
     }
-    const size_t p = (size_t)(cl * 8 + g) * a.tmax + b;
+    const size_t p = (size_t)(item * 8 + g) * a.tmax + b;
     float* po = a.part_o + (p * 16 + col) * HD + 4 * grp;
     #pragma unroll
     for (int nbk = 0; nbk < 8; ++nbk) *reinterpret_cast<f32x4*>(po + 16 * nbk) = st[i].o[nbk];
@@ -593,33 +634,59 @@ __global__ __launch_bounds__(256) void draft_attn_kernel(DraftArgs a) {
       a.part_ml[(p * 16 + col) * 2 + 0] = st[i].m;
       a.part_ml[(p * 16 + col) * 2 + 1] = l;
     }
-    __threadfence();
-    __builtin_amdgcn_wave_barrier();
-    int* counter = a.counters + ((size_t)r * 8 + g) * a.tmax + b;
-    int last = 0;
-    if (lane == 0) last = arrive_last(counter, nch) ? 1 : 0;
-    last = __shfl(last, 0);
-    if (!last) continue;
-    __threadfence();
-    // Lane -> (row = lane/4, dims 32*(lane%4) .. +32).
-    const int mrow = lane >> 2;
-    const int md0 = (lane & 3) * 32;
-    float acc[32];
-    float L;
-    merge_partials<32>(a.part_o, a.part_ml, (size_t)(first * 8 + g) * a.tmax + b, (size_t)8 * a.tmax, nch,
-                       mrow, md0, acc, L);
-    if (lane == 0) *counter = 0;
-    if ((mrow >> 1) < BLOCK_ROWS) {
-      bf16* op = a.out + (orow0 + (mrow >> 1)) * Q_ROW + (size_t)(2 * g + (mrow & 1)) * HD + md0;
-      #pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        bf16x8 ov;
-        #pragma unroll
-        for (int e = 0; e < 8; ++e) ov[e] = (bf16)(acc[8 * v + e] / L);
-        *reinterpret_cast<bf16x8*>(op + 8 * v) = ov;
-      }
-    }
   }
+}
+
+// ---------------------------------------------------------------------------
+// split-K merge: one workgroup per (request, KV head, tile) with >1 chunk
+// ---------------------------------------------------------------------------
+struct MergeArgs {
+  const int32_t* cu_q;     // varlen/verify
+  const int32_t* cu_k;     // varlen/verify chunk counts
+  const int32_t* ctx_len;  // draft chunk counts
+  const int32_t* cu_b;     // draft block offsets
+  const float* part_o;
+  const float* part_ml;
+  bf16* out;
+  int n_req;
+  int chunk;
+  int tmax;
+  int draft;
+};
+
+__global__ __launch_bounds__(256) void merge_kernel(MergeArgs a) {
+  const int r = blockIdx.x;
+  const int g = blockIdx.y;
+  const int t = blockIdx.z;
+  int len, out_row0, rows_valid;
+  if (a.draft) {
+    const int b0 = a.cu_b[r];
+    if (t >= a.cu_b[r + 1] - b0) return;
+    len = a.ctx_len[r];
+    out_row0 = BLOCK_ROWS * (b0 + t);
+    rows_valid = BLOCK_ROWS;
+  } else {
+    const int q0 = a.cu_q[r];
+    const int ql = a.cu_q[r + 1] - q0;
+    if (8 * t >= ql) return;
+    len = a.cu_k[r + 1] - a.cu_k[r];
+    out_row0 = q0 + 8 * t;
+    rows_valid = min(8, ql - 8 * t);
+  }
+  const int nch = chunks_for(len, a.chunk);
+  if (nch == 1) return;
+  const int first = chunk_base(a.draft ? nullptr : a.cu_k, a.draft ? a.ctx_len : nullptr, r, a.chunk);
+  const int tid = threadIdx.x;
+  const int row = tid >> 4;
+  const int d0 = (tid & 15) * 8;
+  if ((row >> 1) >= rows_valid) return;
+  float acc[8];
+  float L;
+  merge_partials<8>(a.part_o, a.part_ml, (size_t)(first * 8 + g) * a.tmax + t, (size_t)8 * a.tmax, nch, row, d0, acc, L);
+  bf16x8 ov;
+  #pragma unroll
+  for (int i = 0; i < 8; ++i) ov[i] = (bf16)(acc[i] / L);
+  *reinterpret_cast<bf16x8*>(a.out + (size_t)(out_row0 + (row >> 1)) * Q_ROW + (size_t)(2 * g + (row & 1)) * HD + d0) = ov;
 }
 
 }  // namespace dspark
@@ -637,14 +704,15 @@ int64_t n_chunk_items(int n_req, int64_t rows_bound, int chunk) {
   return (rows_bound + chunk - 1) / chunk + n_req;
 }
 
-// [part_o: items x 16 x 128 f32][part_ml: items x 16 x 2 f32][counters: n_req x 8 x tiles i32]
+// [part_o: items x 16 x 128 f32][part_ml: items x 16 x 2 f32]
 int64_t workspace_bytes(int n_req, int64_t rows_bound, int tiles, int chunk) {
   const int64_t items = n_chunk_items(n_req, rows_bound, chunk) * HKV * tiles;
-  return items * 16 * (HD + 2) * (int64_t)sizeof(float) + (int64_t)n_req * HKV * tiles * (int64_t)sizeof(int);
+  return items * 16 * (HD + 2) * (int64_t)sizeof(float);
 }
 
-int* counters_of(void* ws, int64_t items) {
-  return reinterpret_cast<int*>(static_cast<float*>(ws) + items * 16 * (HD + 2));
+int launch_merge(const MergeArgs& m, int n_req, int tiles, hipStream_t s) {
+  hipLaunchKernelGGL(merge_kernel, dim3(n_req, HKV, tiles), dim3(256), 0, s, m);
+  return launch_status("merge_kernel");
 }
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
@@ -674,17 +742,20 @@ extern "C" int64_t dspark_attn_workspace_bytes(int n_req, int64_t key_rows_bound
 extern "C" int dspark_varlen_attn_fwd(const void* q, const void* k, const void* v,
                                       const int32_t* cu_q, const int32_t* cu_k, int n_req,
                                       int64_t q_rows, int64_t k_rows, int max_q, int causal,
-                                      float scale, int chunk, void* out, void* workspace,
+                                      float scale, int chunk, const int32_t* work, int n_work,
+                                      void* out, void* workspace,
                                       int64_t workspace_bytes_, void* stream) {
   clear_error();
   DSPARK_REQUIRE(q && k && v && cu_q && cu_k && out, "null pointer argument");
   DSPARK_REQUIRE(aligned16(q) && aligned16(k) && aligned16(v) && aligned16(out), "Q/K/V/out must be 16-byte aligned");
   DSPARK_REQUIRE(q_rows >= 1 && k_rows >= 1, "Q and K must be nonempty");
   DSPARK_REQUIRE(max_q >= 1 && max_q <= q_rows, "max_q must be in [1, q_rows]");
+  DSPARK_REQUIRE(!work || n_work >= 1, "n_work must be >= 1 with a work list");
   const int tiles = (max_q + 7) / 8;
   int rc = check_common(n_req, k_rows, tiles, chunk, scale, workspace_bytes_, workspace);
   if (rc != OK) return rc;
   const int64_t n_cl = n_chunk_items(n_req, k_rows, chunk);
+  DSPARK_REQUIRE(!work || n_work <= n_cl, "work list longer than the chunk bound");
   VarlenArgs a{};
   a.q = static_cast<const bf16*>(q);
   a.k_a = static_cast<const bf16*>(k);
@@ -694,37 +765,47 @@ extern "C" int dspark_varlen_attn_fwd(const void* q, const void* k, const void* 
   a.cu_q = cu_q;
   a.cu_k = cu_k;
   a.slots = nullptr;
-  a.slot_rows = 0;
+  a.slot_stride = 0;
+  a.a_tok_stride = KV_ROW;
+  a.a_head_stride = HD;
+  a.work = work;
   a.out = static_cast<bf16*>(out);
   a.part_o = static_cast<float*>(workspace);
   a.part_ml = a.part_o + n_cl * HKV * tiles * 16 * HD;
-  a.counters = counters_of(workspace, n_cl * HKV * tiles);
   a.n_req = n_req;
   a.causal = causal ? 1 : 0;
   a.chunk = chunk;
   a.tmax = tiles;
   a.scale_log2 = scale * LOG2E;
-  hipLaunchKernelGGL(varlen_attn_kernel<false>, dim3((unsigned)(n_cl * HKV), tiles), dim3(256), 0,
-                     static_cast<hipStream_t>(stream), a);
-  return launch_status("varlen_attn_kernel");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int64_t grid = work ? (int64_t)n_work * HKV : n_cl * HKV;
+  hipLaunchKernelGGL(varlen_attn_kernel<false>, dim3((unsigned)grid, tiles), dim3(256), 0, s, a);
+  rc = launch_status("varlen_attn_kernel");
+  if (rc != OK) return rc;
+  MergeArgs m{cu_q, cu_k, nullptr, nullptr, a.part_o, a.part_ml, a.out, n_req, chunk, tiles, 0};
+  return launch_merge(m, n_req, tiles, s);
 }
 
 extern "C" int dspark_verify_attn_fwd(const void* q, const void* k_res, const void* v_res,
                                       const void* k_scr, const void* v_scr,
                                       const int32_t* cu_q, const int32_t* cu_k, const int32_t* slots,
-                                      int n_req, int64_t ctx_capacity, int64_t key_rows_bound, int max_q,
-                                      float scale, int chunk, void* out, void* workspace,
+                                      int n_req, int64_t slot_stride, int64_t tok_stride, int64_t head_stride,
+                                      int64_t key_rows_bound, int max_q, float scale, int chunk,
+                                      const int32_t* work, int n_work, void* out, void* workspace,
                                       int64_t workspace_bytes_, void* stream) {
   clear_error();
   DSPARK_REQUIRE(q && k_res && v_res && k_scr && v_scr && cu_q && cu_k && slots && out, "null pointer argument");
   DSPARK_REQUIRE(aligned16(q) && aligned16(k_res) && aligned16(v_res) && aligned16(k_scr) && aligned16(v_scr) && aligned16(out),
                  "Q/K/V/out must be 16-byte aligned");
-  DSPARK_REQUIRE(ctx_capacity >= 1, "context capacity must be >= 1");
+  DSPARK_REQUIRE(slot_stride >= 0 && tok_stride >= HD && tok_stride % 8 == 0 && head_stride >= HD && head_stride % 8 == 0,
+                 "resident strides must be multiples of 8 elements (token/head strides >= 128)");
   DSPARK_REQUIRE(max_q >= 1, "max_q must be >= 1");
+  DSPARK_REQUIRE(!work || n_work >= 1, "n_work must be >= 1 with a work list");
   const int tiles = (max_q + 7) / 8;
   int rc = check_common(n_req, key_rows_bound, tiles, chunk, scale, workspace_bytes_, workspace);
   if (rc != OK) return rc;
   const int64_t n_cl = n_chunk_items(n_req, key_rows_bound, chunk);
+  DSPARK_REQUIRE(!work || n_work <= n_cl, "work list longer than the chunk bound");
   VarlenArgs a{};
   a.q = static_cast<const bf16*>(q);
   a.k_a = static_cast<const bf16*>(k_res);
@@ -734,19 +815,25 @@ extern "C" int dspark_verify_attn_fwd(const void* q, const void* k_res, const vo
   a.cu_q = cu_q;
   a.cu_k = cu_k;
   a.slots = slots;
-  a.slot_rows = ctx_capacity;
+  a.slot_stride = slot_stride;
+  a.a_tok_stride = tok_stride;
+  a.a_head_stride = head_stride;
+  a.work = work;
   a.out = static_cast<bf16*>(out);
   a.part_o = static_cast<float*>(workspace);
   a.part_ml = a.part_o + n_cl * HKV * tiles * 16 * HD;
-  a.counters = counters_of(workspace, n_cl * HKV * tiles);
   a.n_req = n_req;
   a.causal = 1;
   a.chunk = chunk;
   a.tmax = tiles;
   a.scale_log2 = scale * LOG2E;
-  hipLaunchKernelGGL(varlen_attn_kernel<true>, dim3((unsigned)(n_cl * HKV), tiles), dim3(256), 0,
-                     static_cast<hipStream_t>(stream), a);
-  return launch_status("verify_attn_kernel");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int64_t grid = work ? (int64_t)n_work * HKV : n_cl * HKV;
+  hipLaunchKernelGGL(varlen_attn_kernel<true>, dim3((unsigned)grid, tiles), dim3(256), 0, s, a);
+  rc = launch_status("verify_attn_kernel");
+  if (rc != OK) return rc;
+  MergeArgs m{cu_q, cu_k, nullptr, nullptr, a.part_o, a.part_ml, a.out, n_req, chunk, tiles, 0};
+  return launch_merge(m, n_req, tiles, s);
 }
 
 extern "C" int dspark_draft_attn_fwd(const void* q, const void* k_ctx, const void* v_ctx,
@@ -755,6 +842,7 @@ extern "C" int dspark_draft_attn_fwd(const void* q, const void* k_ctx, const voi
                                      const void* k_blk, const void* v_blk,
                                      const int32_t* cu_blocks, const int32_t* anchors,
                                      int n_req, int64_t ctx_rows_bound, int max_blocks, float scale, int chunk,
+                                     const int32_t* work, int n_work,
                                      void* out, void* workspace, int64_t workspace_bytes_, void* stream) {
   clear_error();
   DSPARK_REQUIRE(q && k_ctx && v_ctx && ctx_off && ctx_len && k_blk && v_blk && cu_blocks && anchors && out,
@@ -783,14 +871,19 @@ extern "C" int dspark_draft_attn_fwd(const void* q, const void* k_ctx, const voi
   a.out = static_cast<bf16*>(out);
   a.part_o = static_cast<float*>(workspace);
   a.part_ml = a.part_o + n_cl * HKV * max_blocks * 16 * HD;
-  a.counters = counters_of(workspace, n_cl * HKV * max_blocks);
   a.tok_stride = tok_stride;
   a.head_stride = head_stride;
+  a.work = work;
   a.n_req = n_req;
   a.chunk = chunk;
   a.tmax = max_blocks;
   a.scale_log2 = scale * LOG2E;
-  hipLaunchKernelGGL(draft_attn_kernel, dim3((unsigned)(n_cl * HKV)), dim3(256), 0,
-                     static_cast<hipStream_t>(stream), a);
-  return launch_status("draft_attn_kernel");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  DSPARK_REQUIRE(!work || (n_work >= 1 && n_work <= n_cl), "work list length out of range");
+  const int64_t grid = work ? (int64_t)n_work * HKV : n_cl * HKV;
+  hipLaunchKernelGGL(draft_attn_kernel, dim3((unsigned)grid), dim3(256), 0, s, a);
+  rc = launch_status("draft_attn_kernel");
+  if (rc != OK) return rc;
+  MergeArgs m{nullptr, nullptr, ctx_len, cu_blocks, a.part_o, a.part_ml, a.out, n_req, chunk, max_blocks, 1};
+  return launch_merge(m, n_req, max_blocks, s);
 }

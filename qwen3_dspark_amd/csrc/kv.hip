@@ -13,8 +13,10 @@
 //                  (persistent_target_kv.py:452-459) in one pass: committed
 //                  rows from resident, new rows from scratch, tail zeroed.
 //
-// The copy kernels move rows of any multiple of 16 bytes (a Qwen3 token row
-// is [8 KV heads][128] bf16 = 2 KiB) with 16-byte vector accesses.
+// The copy kernels move 16-byte vectors.  The resident store is addressed
+// through byte strides, so both its head-major layout [slots, H, cap, D]
+// (what this build uses: one contiguous stream per (slot, KV head)) and a
+// token-major layout work; scratch and outputs are token-major rows.
 #include "common.h"
 
 namespace dspark {
@@ -147,76 +149,102 @@ __global__ __launch_bounds__(256) void kv_stage_kernel(StageArgs a) {
   }
 }
 
+// Resident addressing (bytes): piece (slot, head, pos) of `piece_vecs`
+// 16-byte vectors starts at slot*slot_stride + head*head_stride +
+// pos*tok_stride within a layer.  Token-major [slots, cap, H, D] and
+// head-major [slots, H, cap, D] stores are both expressed this way.
+// Scratch and materialised outputs are token-major rows of H pieces.
+struct ResidentGeometry {
+  int64_t layer_stride;   // bytes per resident layer
+  int64_t slot_stride;
+  int64_t head_stride;
+  int64_t tok_stride;
+  int64_t ctx_capacity;   // positions per slot
+  int heads;
+  int piece_vecs;         // 16-byte vectors per (token, head) piece
+};
+
+__device__ __forceinline__ u32x4* resident_vec(char* base, const ResidentGeometry& g, int64_t layer, int64_t slot,
+                                              int64_t head, int64_t pos, int64_t v) {
+  return reinterpret_cast<u32x4*>(base + layer * g.layer_stride + slot * g.slot_stride + head * g.head_stride +
+                                  pos * g.tok_stride) + v;
+}
+
 struct CommitArgs {
-  u32x4* k_res;           // [L, slots, cap, row]
-  u32x4* v_res;
-  const u32x4* k_scr;     // [L, max_q, row]
+  char* k_res;
+  char* v_res;
+  const u32x4* k_scr;     // [L, max_q, H*piece_vecs]
   const u32x4* v_scr;
   const int32_t* req;     // [3][B]: slot, context, query (pre-commit)
   const int32_t* cu_q;    // [B+1] scratch row offset of each request
   const int32_t* n_acc;   // [B] accepted prefix
-  int64_t layer_res;      // vectors per resident layer
+  ResidentGeometry geo;
   int64_t layer_scr;      // vectors per scratch layer
-  int64_t ctx_capacity;
-  int64_t row_vecs;
-  int64_t total;          // n_req * max_q * row_vecs
+  int64_t total;          // n_req * max_q * heads * piece_vecs
   int n_req;
   int max_q;
 };
 
-// grid: (ceil(n_req*max_q*row_vecs / 256), layers)
+// grid: (ceil(total / 256), layers); one 16-byte vector per thread.
 __global__ __launch_bounds__(256) void kv_commit_kernel(CommitArgs a) {
   const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (i >= a.total) return;
-  const int64_t rowi = i / a.row_vecs;
-  const int64_t v = i - rowi * a.row_vecs;
+  const int64_t row_vecs = (int64_t)a.geo.heads * a.geo.piece_vecs;
+  const int64_t rowi = i / row_vecs;
+  const int64_t within = i - rowi * row_vecs;
+  const int64_t h = within / a.geo.piece_vecs;
+  const int64_t v = within - h * a.geo.piece_vecs;
   const int r = (int)(rowi / a.max_q);
   const int t = (int)(rowi - (int64_t)r * a.max_q);
   const int layer = blockIdx.y;
   if (t >= a.n_acc[r]) return;
   const int32_t slot = a.req[r];
   const int32_t c = a.req[a.n_req + r];
-  const int64_t src = layer * a.layer_scr + ((int64_t)a.cu_q[r] + t) * a.row_vecs + v;
-  const int64_t dst = layer * a.layer_res + ((int64_t)slot * a.ctx_capacity + c + t) * a.row_vecs + v;
-  a.k_res[dst] = a.k_scr[src];
-  a.v_res[dst] = a.v_scr[src];
+  const int64_t src = layer * a.layer_scr + ((int64_t)a.cu_q[r] + t) * row_vecs + within;
+  *resident_vec(a.k_res, a.geo, layer, slot, h, c + t, v) = a.k_scr[src];
+  *resident_vec(a.v_res, a.geo, layer, slot, h, c + t, v) = a.v_scr[src];
 }
 
 struct GatherArgs {
-  const u32x4* k_res;           // resident layer base, rows [slots*cap]
-  const u32x4* v_res;
+  const char* k_res;            // resident layer base
+  const char* v_res;
   const u32x4* k_scr;           // scratch layer base, rows [max_q]
   const u32x4* v_scr;
-  const int64_t* committed_idx; // [kcap]
+  const int64_t* committed_idx; // [kcap]: slot * capacity + position
   const int64_t* scratch_idx;
   const uint8_t* from_scratch;
   const uint8_t* valid;
-  u32x4* k_out;                 // [kcap][row]
+  u32x4* k_out;                 // [kcap][H*piece_vecs]
   u32x4* v_out;
-  int64_t total;                // kcap * row_vecs
-  int64_t row_vecs;
-  int64_t res_rows;             // bound for committed_idx
+  ResidentGeometry geo;
+  int64_t total;                // kcap * heads * piece_vecs
+  int64_t res_rows;             // slots * capacity (bound for committed_idx)
   int64_t scr_rows;             // bound for scratch_idx
 };
 
 __global__ __launch_bounds__(256) void kv_gather_kernel(GatherArgs a) {
   const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (i >= a.total) return;
-  const int64_t j = i / a.row_vecs;
-  const int64_t v = i - j * a.row_vecs;
+  const int64_t row_vecs = (int64_t)a.geo.heads * a.geo.piece_vecs;
+  const int64_t j = i / row_vecs;
+  const int64_t within = i - j * row_vecs;
   u32x4 kx = {0u, 0u, 0u, 0u}, vx = {0u, 0u, 0u, 0u};
   if (a.valid[j]) {
     if (a.from_scratch[j]) {
       const int64_t s = a.scratch_idx[j];
       if (s >= 0 && s < a.scr_rows) {
-        kx = a.k_scr[s * a.row_vecs + v];
-        vx = a.v_scr[s * a.row_vecs + v];
+        kx = a.k_scr[s * row_vecs + within];
+        vx = a.v_scr[s * row_vecs + within];
       }
     } else {
       const int64_t s = a.committed_idx[j];
       if (s >= 0 && s < a.res_rows) {
-        kx = a.k_res[s * a.row_vecs + v];
-        vx = a.v_res[s * a.row_vecs + v];
+        const int64_t slot = s / a.geo.ctx_capacity;
+        const int64_t pos = s - slot * a.geo.ctx_capacity;
+        const int64_t h = within / a.geo.piece_vecs;
+        const int64_t v = within - h * a.geo.piece_vecs;
+        kx = *resident_vec(const_cast<char*>(a.k_res), a.geo, 0, slot, h, pos, v);
+        vx = *resident_vec(const_cast<char*>(a.v_res), a.geo, 0, slot, h, pos, v);
       }
     }
   }
@@ -269,26 +297,37 @@ extern "C" int dspark_kv_stage(const void* k_new, const void* v_new, void* k_scr
   return launch_status("kv_stage_kernel");
 }
 
+namespace {
+int check_geometry(const ResidentGeometry& g) {
+  DSPARK_REQUIRE(g.heads >= 1 && g.piece_vecs >= 1 && g.ctx_capacity >= 1, "resident geometry sizes must be positive");
+  DSPARK_REQUIRE(g.layer_stride % 16 == 0 && g.slot_stride % 16 == 0 && g.head_stride % 16 == 0 && g.tok_stride % 16 == 0,
+                 "resident strides must be multiples of 16 bytes");
+  return OK;
+}
+}  // namespace
+
 extern "C" int dspark_kv_commit(void* k_res, void* v_res, const void* k_scr, const void* v_scr,
                                 const int32_t* req, const int32_t* cu_q, const int32_t* n_accepted,
-                                int n_req, int max_q, int layers, int64_t slots, int64_t ctx_capacity,
-                                int64_t scratch_rows, int64_t row_bytes, void* stream) {
+                                int n_req, int max_q, int layers, int64_t layer_stride, int64_t slot_stride,
+                                int64_t head_stride, int64_t tok_stride, int64_t ctx_capacity, int heads,
+                                int64_t piece_bytes, int64_t scratch_rows, void* stream) {
   clear_error();
   DSPARK_REQUIRE(k_res && v_res && k_scr && v_scr && req && cu_q && n_accepted, "null pointer argument");
   DSPARK_REQUIRE(aligned16(k_res) && aligned16(v_res) && aligned16(k_scr) && aligned16(v_scr),
                  "buffers must be 16-byte aligned");
-  DSPARK_REQUIRE(n_req >= 1 && max_q >= 1 && layers >= 1 && slots >= 1 && ctx_capacity >= 1 && scratch_rows >= 1,
-                 "sizes must be positive");
-  DSPARK_REQUIRE(row_bytes >= 16 && row_bytes % 16 == 0, "row bytes must be a positive multiple of 16");
+  DSPARK_REQUIRE(n_req >= 1 && max_q >= 1 && layers >= 1 && scratch_rows >= 1, "sizes must be positive");
+  DSPARK_REQUIRE(piece_bytes >= 16 && piece_bytes % 16 == 0, "piece bytes must be a positive multiple of 16");
   DSPARK_REQUIRE(layers <= 65535, "too many layers");
-  const int64_t rv = row_bytes / 16;
-  const int64_t total = (int64_t)n_req * max_q * rv;
+  ResidentGeometry geo{layer_stride, slot_stride, head_stride, tok_stride, ctx_capacity, heads, (int)(piece_bytes / 16)};
+  int rc = check_geometry(geo);
+  if (rc != OK) return rc;
+  const int64_t row_vecs = (int64_t)heads * geo.piece_vecs;
+  const int64_t total = (int64_t)n_req * max_q * row_vecs;
   const int64_t blocks = (total + 255) / 256;
   DSPARK_REQUIRE(blocks <= 0x7fffffffLL, "commit grid too large");
-  CommitArgs a{static_cast<u32x4*>(k_res), static_cast<u32x4*>(v_res),
+  CommitArgs a{static_cast<char*>(k_res), static_cast<char*>(v_res),
                static_cast<const u32x4*>(k_scr), static_cast<const u32x4*>(v_scr),
-               req, cu_q, n_accepted, slots * ctx_capacity * rv, scratch_rows * rv,
-               ctx_capacity, rv, total, n_req, max_q};
+               req, cu_q, n_accepted, geo, scratch_rows * row_vecs, total, n_req, max_q};
   hipLaunchKernelGGL(kv_commit_kernel, dim3((unsigned)blocks, layers), dim3(256), 0,
                      static_cast<hipStream_t>(stream), a);
   return launch_status("kv_commit_kernel");
@@ -298,20 +337,25 @@ extern "C" int dspark_kv_gather(const void* k_res_layer, const void* v_res_layer
                                 const void* k_scr_layer, const void* v_scr_layer,
                                 const int64_t* committed_idx, const int64_t* scratch_idx,
                                 const uint8_t* from_scratch, const uint8_t* valid,
-                                int64_t key_capacity, int64_t res_rows, int64_t scr_rows, int64_t row_bytes,
-                                void* k_out, void* v_out, void* stream) {
+                                int64_t key_capacity, int64_t slots, int64_t slot_stride, int64_t head_stride,
+                                int64_t tok_stride, int64_t ctx_capacity, int heads, int64_t piece_bytes,
+                                int64_t scr_rows, void* k_out, void* v_out, void* stream) {
   clear_error();
   DSPARK_REQUIRE(k_res_layer && v_res_layer && k_scr_layer && v_scr_layer && committed_idx && scratch_idx &&
                  from_scratch && valid && k_out && v_out, "null pointer argument");
   DSPARK_REQUIRE(aligned16(k_res_layer) && aligned16(v_res_layer) && aligned16(k_scr_layer) && aligned16(v_scr_layer) &&
                  aligned16(k_out) && aligned16(v_out), "buffers must be 16-byte aligned");
-  DSPARK_REQUIRE(key_capacity >= 1 && res_rows >= 1 && scr_rows >= 1, "sizes must be positive");
-  DSPARK_REQUIRE(row_bytes >= 16 && row_bytes % 16 == 0, "row bytes must be a positive multiple of 16");
-  const int64_t rv = row_bytes / 16;
-  GatherArgs a{static_cast<const u32x4*>(k_res_layer), static_cast<const u32x4*>(v_res_layer),
+  DSPARK_REQUIRE(key_capacity >= 1 && slots >= 1 && scr_rows >= 1, "sizes must be positive");
+  DSPARK_REQUIRE(piece_bytes >= 16 && piece_bytes % 16 == 0, "piece bytes must be a positive multiple of 16");
+  ResidentGeometry geo{0, slot_stride, head_stride, tok_stride, ctx_capacity, heads, (int)(piece_bytes / 16)};
+  int rc = check_geometry(geo);
+  if (rc != OK) return rc;
+  const int64_t row_vecs = (int64_t)heads * geo.piece_vecs;
+  GatherArgs a{static_cast<const char*>(k_res_layer), static_cast<const char*>(v_res_layer),
                static_cast<const u32x4*>(k_scr_layer), static_cast<const u32x4*>(v_scr_layer),
                committed_idx, scratch_idx, from_scratch, valid,
-               static_cast<u32x4*>(k_out), static_cast<u32x4*>(v_out), key_capacity * rv, rv, res_rows, scr_rows};
+               static_cast<u32x4*>(k_out), static_cast<u32x4*>(v_out), geo, key_capacity * row_vecs,
+               slots * ctx_capacity, scr_rows};
   const int64_t blocks = (a.total + 255) / 256;
   DSPARK_REQUIRE(blocks <= 0x7fffffffLL, "key capacity too large");
   hipLaunchKernelGGL(kv_gather_kernel, dim3((unsigned)blocks), dim3(256), 0, static_cast<hipStream_t>(stream), a);

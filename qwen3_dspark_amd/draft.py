@@ -10,17 +10,21 @@ dspark_qwen/packed_draft.py:205-236, without the whole-pool cat, the gather
 and the copies: context rows are read in place, once per request for all of
 its blocks.
 
-The context may live in
-  * a row store [rows, 8, 128] (e.g. a slotted pool layer viewed as
-    [slots * capacity, 8, 128]); request r uses rows off_r .. off_r + c_r, or
-  * the reference's append-order pool layer [1, 8, N, 128] together with the
-    per-request physical indices (PackedLayout.gather_indices order).
+The context K/V of one draft layer may live in
+  * a row store [rows, 8, 128]: request r uses rows off_r .. off_r + c_r;
+  * a head-major slotted pool [slots, 8, capacity, 128] (one contiguous run
+    per (slot, KV head), the layout this build streams fastest): off_r =
+    slot * capacity + first position;
+  * the reference's append-order pool layer [1, 8, N, 128] with per-request
+    physical indices (PackedLayout.gather_indices order): off_r indexes the
+    index vector.
 """
 import torch
 
 from . import _native
 from ._device import Workspace, require_gfx950
-from .kernels import DEFAULT_CHUNK, HEAD_DIM, KV_HEADS, Q_HEADS, SCALE, _check_scale
+from .kernels import HEAD_DIM, KV_HEADS, Q_HEADS, SCALE, _check_scale
+from .schedule import DEFAULT_CHUNK, chunk_items, upload_items
 
 BLOCK_SIZE = 7
 MAX_BLOCKS = 8
@@ -30,8 +34,7 @@ class DraftBatch:
     """Host-validated per-round draft metadata, uploaded once and reused by
     every draft layer.
 
-    context_offsets[r]: first context row (row store) or first entry of
-        context_indices (indexed pool) of request r.
+    context_offsets[r]: see the module docstring for each pool form.
     context_lengths[r]: committed context rows c_r.
     anchors[r]: sequence of block anchors, each in [0, c_r], 1..8 blocks.
     context_indices: optional int64 device tensor of physical pool rows.
@@ -50,9 +53,17 @@ class DraftBatch:
             raise ValueError(f'Each request needs 1..{MAX_BLOCKS} draft blocks')
         if any(not 0 <= a <= c for b, c in zip(blocks, lens) for a in b):
             raise ValueError('Every anchor must lie in [0, context length]')
+        if context_indices is not None:
+            if (not isinstance(context_indices, torch.Tensor) or context_indices.dtype != torch.long
+                    or context_indices.ndim != 1 or context_indices.device != self.device
+                    or not context_indices.is_contiguous()):
+                raise ValueError('context_indices must be a contiguous int64 vector on the draft device')
+            if any(o + c > context_indices.numel() for o, c in zip(offs, lens)):
+                raise ValueError('Context index ranges exceed context_indices')
         self.context_offsets = tuple(offs)
         self.context_lengths = tuple(lens)
         self.anchors = tuple(blocks)
+        self.context_indices = context_indices
         self.request_count = len(offs)
         self.block_count = sum(len(b) for b in blocks)
         self.max_blocks = max(len(b) for b in blocks)
@@ -61,46 +72,52 @@ class DraftBatch:
         cu_b = [0]
         for b in blocks:
             cu_b.append(cu_b[-1] + len(b))
-        flat_anchors = [a for b in blocks for a in b]
         self.cu_blocks_host = tuple(cu_b)
-        if context_indices is not None:
-            if (not isinstance(context_indices, torch.Tensor) or context_indices.dtype != torch.long
-                    or context_indices.ndim != 1 or context_indices.device != self.device
-                    or not context_indices.is_contiguous()):
-                raise ValueError('context_indices must be a contiguous int64 vector on the draft device')
-            if any(o + c > context_indices.numel() for o, c in zip(offs, lens)):
-                raise ValueError('Context index ranges exceed context_indices')
-        self.context_indices = context_indices
+        pinned = torch.tensor(lens + cu_b + [a for b in blocks for a in b], dtype=torch.int32).pin_memory()
+        meta = pinned.to(self.device, non_blocking=True)
+        n = self.request_count
+        self.ctx_len = meta[:n]
+        self.cu_blocks = meta[n:2 * n + 1]
+        self.anchor_rows = meta[2 * n + 1:]
+        self._offsets = {}
+        self._work = {}
         self._index_max = None
-        pinned64 = torch.tensor(offs, dtype=torch.int64).pin_memory()
-        pinned32 = torch.tensor(lens + cu_b + flat_anchors, dtype=torch.int32).pin_memory()
-        self.ctx_off = pinned64.to(self.device, non_blocking=True)
-        meta = pinned32.to(self.device, non_blocking=True)
-        b = self.request_count
-        self.ctx_len = meta[:b]
-        self.cu_blocks = meta[b:2 * b + 1]
-        self.anchor_rows = meta[2 * b + 1:]
+
+    def device_offsets(self, capacity):
+        """int64 per-request first kernel row: offsets as given, or - for a
+        head-major slotted pool of `capacity` positions - slot*8*capacity +
+        position, the row index in units of 128 elements."""
+        if capacity not in self._offsets:
+            offs = list(self.context_offsets)
+            if capacity:
+                offs = [o + (KV_HEADS - 1) * capacity * (o // capacity) for o in offs]
+            self._offsets[capacity] = torch.tensor(offs, dtype=torch.int64).pin_memory().to(self.device, non_blocking=True)
+        return self._offsets[capacity]
+
+    def work(self, chunk):
+        if chunk not in self._work:
+            items = chunk_items(self.context_lengths, chunk)
+            self._work[chunk] = (upload_items(items, self.device), len(items))
+        return self._work[chunk]
 
     def index_max(self):
-        """Largest physical context row addressed (one device sync, cached)."""
-        if self.context_indices is None:
-            return max((o + c for o, c in zip(self.context_offsets, self.context_lengths)), default=0) - 1
+        """Largest physical index addressed through context_indices (one
+        device sync, cached)."""
         if self._index_max is None:
             used = [self.context_indices[o:o + c] for o, c in zip(self.context_offsets, self.context_lengths) if c]
             if used:
                 cat = torch.cat(used)
-                lo, hi = int(cat.min()), int(cat.max())
-                if lo < 0:
+                if int(cat.min()) < 0:
                     raise ValueError('Negative context index')
-                self._index_max = hi
+                self._index_max = int(cat.max())
             else:
                 self._index_max = -1
         return self._index_max
 
 
 class HipDraftAttention:
-    """Multi-block draft attention kernel object (one launch per layer, plus a
-    split-K merge for contexts longer than one chunk)."""
+    """Multi-block draft attention kernel object (one chunk launch per layer
+    plus a split-K merge launch)."""
     backend_name = 'mi355x_hip_draft_blocks_v1'
     native_varlen_calls_per_layer = 1
 
@@ -111,6 +128,27 @@ class HipDraftAttention:
             raise ValueError('Draft chunk must be a multiple of 64')
         self.chunk = int(chunk)
         self._workspace = Workspace(self.device)
+
+    def _context_geometry(self, keys, batch):
+        """(kernel offsets, token stride, head stride) for the pool form."""
+        if keys.ndim == 3 and tuple(keys.shape[1:]) == (KV_HEADS, HEAD_DIM):
+            if batch.context_indices is not None:
+                if batch.index_max() >= keys.shape[0]:
+                    raise ValueError('Context rows addressed beyond the context tensor')
+            elif any(o + c > keys.shape[0] for o, c in zip(batch.context_offsets, batch.context_lengths)):
+                raise ValueError('Context rows addressed beyond the context tensor')
+            return batch.device_offsets(0), KV_HEADS * HEAD_DIM, HEAD_DIM
+        if keys.ndim == 4 and keys.shape[1] == KV_HEADS and keys.shape[3] == HEAD_DIM:
+            slots, cap = keys.shape[0], keys.shape[2]
+            if batch.context_indices is not None:
+                if slots != 1 or batch.index_max() >= cap:
+                    raise ValueError('An indexed pool must be [1,8,N,128] with indices < N')
+                return batch.device_offsets(0), HEAD_DIM, cap * HEAD_DIM
+            for o, c in zip(batch.context_offsets, batch.context_lengths):
+                if o // cap >= slots or (o % cap) + c > cap:
+                    raise ValueError('Context rows addressed beyond their pool slot')
+            return batch.device_offsets(cap), HEAD_DIM, cap * HEAD_DIM
+        raise ValueError('Context K/V must be [rows,8,128], [slots,8,capacity,128] or [1,8,N,128]')
 
     def __call__(self, query, block_keys, block_values, context_keys, context_values, batch, *, scale):
         if not isinstance(batch, DraftBatch) or batch.device != self.device:
@@ -128,25 +166,16 @@ class HipDraftAttention:
                 or context_values.device != self.device
                 or not context_keys.is_contiguous() or not context_values.is_contiguous()):
             raise ValueError('Context K/V must be matching contiguous bf16 tensors on the GPU')
-        if context_keys.ndim == 3 and tuple(context_keys.shape[1:]) == (KV_HEADS, HEAD_DIM):
-            rows, tok_stride, head_stride = context_keys.shape[0], KV_HEADS * HEAD_DIM, HEAD_DIM
-        elif context_keys.ndim == 4 and context_keys.shape[0] == 1 and context_keys.shape[1] == KV_HEADS \
-                and context_keys.shape[3] == HEAD_DIM:
-            rows, tok_stride, head_stride = context_keys.shape[2], HEAD_DIM, context_keys.shape[2] * HEAD_DIM
-            if batch.context_indices is None:
-                raise ValueError('A [1,8,N,128] pool needs per-request context indices')
-        else:
-            raise ValueError('Context K/V must be [rows,8,128] or [1,8,N,128]')
-        if batch.index_max() >= rows:
-            raise ValueError('Context rows addressed beyond the context tensor')
+        offsets, tok_stride, head_stride = self._context_geometry(context_keys, batch)
         out = torch.empty_like(query)
         bound = max(batch.context_rows, 1)
         need = _native.load().dspark_attn_workspace_bytes(batch.request_count, bound, batch.max_blocks, self.chunk)
         ws = self._workspace.get(need)
+        work, n_work = batch.work(self.chunk)
         _native.call('dspark_draft_attn_fwd', _native.ptr(query), _native.ptr(context_keys), _native.ptr(context_values),
-                     _native.ptr(batch.context_indices), _native.ptr(batch.ctx_off), _native.ptr(batch.ctx_len),
+                     _native.ptr(batch.context_indices), _native.ptr(offsets), _native.ptr(batch.ctx_len),
                      tok_stride, head_stride, _native.ptr(block_keys), _native.ptr(block_values),
                      _native.ptr(batch.cu_blocks), _native.ptr(batch.anchor_rows), batch.request_count, bound,
-                     batch.max_blocks, float(SCALE), self.chunk, _native.ptr(out), _native.ptr(ws), ws.numel(),
-                     _native.stream_handle(self.device))
+                     batch.max_blocks, float(SCALE), self.chunk, _native.ptr(work), n_work,
+                     _native.ptr(out), _native.ptr(ws), ws.numel(), _native.stream_handle(self.device))
         return out

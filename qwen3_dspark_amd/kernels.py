@@ -16,10 +16,10 @@ import torch
 
 from . import _native
 from ._device import Workspace, require_gfx950
+from .schedule import DEFAULT_CHUNK, chunk_items, upload_items
 
 Q_HEADS, KV_HEADS, HEAD_DIM = 16, 8, 128
 SCALE = 128 ** -0.5
-DEFAULT_CHUNK = 512
 
 
 def _check_scale(scale, what):
@@ -40,6 +40,8 @@ class HipVarlenKernel:
         self._workspace = Workspace(self.device)
         self._validated_layout = None
         self._layout_versions = None
+        self._work_for = None
+        self._work = None
 
     # Same contract and error classes as rocm_varlen.py:232-273.
     def _validate_inputs(self, query, key, value, layout, scale):
@@ -87,21 +89,32 @@ class HipVarlenKernel:
             raise ValueError('Cumulative lengths differ from packed metadata')
         self._validated_layout, self._layout_versions = layout, versions
 
-    def _launch(self, query, key, value, cu_q, cu_k, n_req, max_q, key_rows):
+    def _work_list(self, layout):
+        # One longest-first item list per layout object (its lengths are
+        # immutable host tuples), uploaded once and reused by every layer.
+        key = (id(layout), layout.key_lengths, self.chunk)
+        if self._work_for != key:
+            self._work = upload_items(chunk_items(layout.key_lengths, self.chunk), self.device)
+            self._work_for = key
+        return self._work
+
+    def _launch(self, query, key, value, layout, max_q, key_rows):
         out = torch.empty_like(query)
+        n_req = len(layout.query_lengths)
         tiles = (max_q + 7) // 8
         need = _native.load().dspark_attn_workspace_bytes(n_req, key_rows, tiles, self.chunk)
         ws = self._workspace.get(need)
+        work = self._work_list(layout)
         _native.call('dspark_varlen_attn_fwd', _native.ptr(query), _native.ptr(key), _native.ptr(value),
-                     _native.ptr(cu_q), _native.ptr(cu_k), n_req, query.shape[0], key_rows, max_q,
-                     int(self.causal), float(SCALE), self.chunk, _native.ptr(out), _native.ptr(ws),
-                     ws.numel(), _native.stream_handle(self.device))
+                     _native.ptr(layout.cu_query), _native.ptr(layout.cu_key), n_req, query.shape[0], key_rows,
+                     max_q, int(self.causal), float(SCALE), self.chunk, _native.ptr(work),
+                     0 if work is None else work.numel() // 2,
+                     _native.ptr(out), _native.ptr(ws), ws.numel(), _native.stream_handle(self.device))
         return out
 
     def __call__(self, query, key, value, layout, *, scale):
         self._validate_inputs(query, key, value, layout, scale)
-        output = self._launch(query, key, value, layout.cu_query, layout.cu_key, len(layout.query_lengths),
-                              max(layout.query_lengths), key.shape[0])
+        output = self._launch(query, key, value, layout, max(layout.query_lengths), key.shape[0])
         if output.shape != query.shape or output.dtype != query.dtype or output.device != query.device:
             raise RuntimeError('HIP varlen returned incompatible output')
         return output
@@ -124,6 +137,11 @@ class HipCapacityKernel(HipVarlenKernel):
     """
     backend_name = 'mi355x_hip_capacity_causal_v1'
 
+    def _work_list(self, layout):
+        # Request-order dispatch over a grid sized from the capacity: the
+        # same launch for every transaction of a bucket.
+        return None
+
     def __call__(self, query, key, value, layout, *, scale):
         if (not all(isinstance(t, torch.Tensor) for t in (query, key, value))
                 or query.dtype != torch.bfloat16 or key.dtype != query.dtype or value.dtype != query.dtype
@@ -141,5 +159,4 @@ class HipCapacityKernel(HipVarlenKernel):
         if max_q < max(layout.query_lengths):
             raise ValueError('Bucket maximum query length below an actual query length')
         self._validate_layout(layout, markers=False)
-        return self._launch(query, key, value, layout.cu_query, layout.cu_key, len(layout.query_lengths),
-                            max_q, layout.physical_key_capacity)
+        return self._launch(query, key, value, layout, max_q, layout.physical_key_capacity)

@@ -15,9 +15,12 @@ poisoning.  The device work is HIP:
                        resident rows and staged scratch rows in place; the
                        capacity-length K/V is never materialised.
 
-Layout in HBM: resident K and V [layers, slots, context_capacity, heads, dim],
-scratch K and V [layers, max_query_tokens, heads, dim] - one contiguous
-heads*dim row per token, so every row move is a run of 16-byte vectors.
+Layout in HBM: resident K and V are stored head-major,
+[layers, slots, heads, context_capacity, dim], so the attention of one
+(request, KV head) streams one contiguous run of 256-byte rows; `keys` /
+`values` are [layers, slots, context_capacity, heads, dim] views of that
+storage (the reference's shape).  Scratch K and V are token-major
+[layers, max_query_tokens, heads, dim], the shape the model produces.
 """
 from dataclasses import dataclass
 from typing import Mapping
@@ -26,7 +29,8 @@ import torch
 
 from . import _native
 from ._device import require_gfx950
-from .kernels import DEFAULT_CHUNK, HEAD_DIM, KV_HEADS, Q_HEADS, SCALE, _check_scale
+from .kernels import HEAD_DIM, KV_HEADS, Q_HEADS, SCALE, _check_scale
+from .schedule import DEFAULT_CHUNK, chunk_bound, chunk_items
 
 
 @dataclass(frozen=True)
@@ -141,7 +145,7 @@ class _Workspace:
     directly.  `req` holds the per-request (slot, context, query) triples the
     kernels consume and `attn` the split-K partials of attend().
     """
-    _COUNTS = {'cu_query': 'r1', 'cu_key': 'r1', 'positions': 'q', 'req': 'r3'}
+    _COUNTS = {'cu_query': 'r1', 'cu_key': 'r1', 'positions': 'q', 'req': 'r3', 'work': 'full', 'attn': 'full'}
 
     def __init__(self, bucket, heads, dim, dtype, device, chunk, arena=None):
         self.bucket = bucket
@@ -150,7 +154,7 @@ class _Workspace:
             for name, value in vars(arena).items():
                 if isinstance(value, torch.Tensor):
                     kind = self._COUNTS.get(name)
-                    if name == 'attn':
+                    if kind == 'full':
                         setattr(self, name, value)
                     elif kind == 'r1':
                         setattr(self, name, value[:r + 1])
@@ -169,6 +173,7 @@ class _Workspace:
         self.cu_key = torch.zeros_like(self.cu_query)
         self.positions = torch.zeros(q, dtype=torch.long, device=device)
         self.req = torch.zeros(3 * r, dtype=torch.int32, device=device)
+        self.work = torch.zeros(2 * chunk_bound(r, n, chunk), dtype=torch.int32, device=device)
         self.keys = torch.empty((n, heads, dim), dtype=dtype, device=device)
         self.values = torch.empty_like(self.keys)
         self.attn = torch.zeros(_attn_workspace_bytes(bucket, chunk), dtype=torch.uint8, device=device)
@@ -203,18 +208,21 @@ class PersistentTargetKV:
             raise ValueError('All capacities and dimensions must be positive integers')
         if not dtype.is_floating_point:
             raise ValueError('Floating point KV dtype required')
-        row_bytes = heads * dim * torch.empty((), dtype=dtype).element_size()
-        if row_bytes % 16:
-            raise ValueError('A KV token row (heads*dim*element size) must be a multiple of 16 bytes')
+        elem = torch.empty((), dtype=dtype).element_size()
+        if (dim * elem) % 16:
+            raise ValueError('A KV head row (dim * element size) must be a multiple of 16 bytes')
         self.device = require_gfx950(device)
         _native.load()
         self.layers, self.slot_capacity, self.context_capacity = layers, slots, context_capacity
         self.max_query_tokens, self.heads, self.dim = max_query_tokens, heads, dim
         self.dtype = dtype
         self.chunk = int(chunk)
-        self._row_bytes = row_bytes
-        self.keys = torch.zeros((layers, slots, context_capacity, heads, dim), dtype=dtype, device=self.device)
-        self.values = torch.zeros_like(self.keys)
+        self._elem = elem
+        # Head-major storage; the public tensors are reference-shaped views.
+        self._keys = torch.zeros((layers, slots, heads, context_capacity, dim), dtype=dtype, device=self.device)
+        self._values = torch.zeros_like(self._keys)
+        self.keys = self._keys.permute(0, 1, 3, 2, 4)
+        self.values = self._values.permute(0, 1, 3, 2, 4)
         self.scratch_keys = torch.zeros((layers, max_query_tokens, heads, dim), dtype=dtype, device=self.device)
         self.scratch_values = torch.zeros_like(self.scratch_keys)
         self._owners = [None] * slots
@@ -230,7 +238,13 @@ class PersistentTargetKV:
         self._writers = {}
         self._external = None
         self._submission_generation = 0
+        self._n_work = 0
         self.failed = False
+
+    def _geometry(self):
+        """Resident byte strides: (layer, slot, head, token) and piece bytes."""
+        e, H, C, D = self._elem, self.heads, self.context_capacity, self.dim
+        return (self.slot_capacity * H * C * D * e, H * C * D * e, C * D * e, D * e, D * e)
 
     # -- state guards ------------------------------------------------------
     def _healthy(self):
@@ -318,7 +332,8 @@ class PersistentTargetKV:
         """Exact device allocation of a bucket workspace before registering it."""
         n, r, q = bucket.key_capacity, bucket.request_count, bucket.query_tokens
         kv = 2 * n * self.heads * self.dim * self.keys.element_size()
-        return kv + 18 * n + 8 * (r + 1) + 8 * q + 12 * r + _attn_workspace_bytes(bucket, self.chunk)
+        return (kv + 18 * n + 8 * (r + 1) + 8 * q + 12 * r + 8 * chunk_bound(r, n, self.chunk)
+                + _attn_workspace_bytes(bucket, self.chunk))
 
     def family_arena_shape(self, families):
         """Validate the complete finite declaration before allocating any storage."""
@@ -434,8 +449,13 @@ class PersistentTargetKV:
             raise ValueError('Varlen cumulative lengths exceed int32')
         ws = self._workspaces[bucket]
         r = len(handles)
-        host = torch.tensor(list(indices) + list(contexts) + list(query_lengths), dtype=torch.int32).pin_memory()
-        ws.req[:3 * r].copy_(host, non_blocking=True)
+        items = chunk_items([c + q for c, q in zip(contexts, query_lengths)], self.chunk)
+        if 2 * len(items) > ws.work.numel():
+            raise ValueError('Work list exceeds the bucket workspace')
+        host = torch.tensor(list(indices) + list(contexts) + list(query_lengths) + [x for it in items for x in it],
+                            dtype=torch.int32).pin_memory()
+        ws.req[:3 * r].copy_(host[:3 * r], non_blocking=True)
+        ws.work[:2 * len(items)].copy_(host[3 * r:], non_blocking=True)
         _native.call('dspark_txn_metadata', _native.ptr(ws.req), r, self.context_capacity,
                      bucket.key_capacity, bucket.query_tokens,
                      _native.ptr(ws.committed_indices), _native.ptr(ws.scratch_indices),
@@ -443,7 +463,7 @@ class PersistentTargetKV:
                      _native.ptr(ws.cu_query), _native.ptr(ws.cu_key), _native.stream_handle(self.device))
         self._sequence += 1
         tx = Transaction(self._sequence, handles, contexts, bucket, query_lengths)
-        self._pending, self._staged = tx, set()
+        self._pending, self._staged, self._n_work = tx, set(), len(items)
         return tx
 
     def _transaction(self, tx):
@@ -468,7 +488,7 @@ class PersistentTargetKV:
         keys, values = keys.contiguous(), values.contiguous()
         _native.call('dspark_kv_stage', _native.ptr(keys), _native.ptr(values),
                      _native.ptr(self.scratch_keys[layer]), _native.ptr(self.scratch_values[layer]),
-                     q, self._row_bytes, _native.stream_handle(self.device))
+                     q, self.heads * self.dim * self._elem, _native.stream_handle(self.device))
         self._staged.add(layer)
 
     @torch.no_grad()
@@ -479,12 +499,14 @@ class PersistentTargetKV:
         if layer not in self._staged:
             raise ValueError('Layer scratch missing')
         n = tx.bucket.key_capacity
-        _native.call('dspark_kv_gather', _native.ptr(self.keys[layer]), _native.ptr(self.values[layer]),
+        _, slot_b, head_b, tok_b, piece_b = self._geometry()
+        _native.call('dspark_kv_gather', _native.ptr(self._keys[layer]), _native.ptr(self._values[layer]),
                      _native.ptr(self.scratch_keys[layer]), _native.ptr(self.scratch_values[layer]),
                      _native.ptr(ws.committed_indices), _native.ptr(ws.scratch_indices),
                      _native.ptr(ws.from_scratch), _native.ptr(ws.valid), n,
-                     self.slot_capacity * self.context_capacity, self.max_query_tokens, self._row_bytes,
-                     _native.ptr(ws.keys), _native.ptr(ws.values), _native.stream_handle(self.device))
+                     self.slot_capacity, slot_b, head_b, tok_b, self.context_capacity, self.heads, piece_b,
+                     self.max_query_tokens, _native.ptr(ws.keys), _native.ptr(ws.values),
+                     _native.stream_handle(self.device))
         return ws.keys, ws.values, ws.cu_query, ws.cu_key, ws.positions
 
     @torch.no_grad()
@@ -504,12 +526,14 @@ class PersistentTargetKV:
         _check_scale(scale, 'Fused verification attention')
         out = torch.empty_like(query)
         bucket = tx.bucket
+        C = self.context_capacity
         _native.call('dspark_verify_attn_fwd', _native.ptr(query),
-                     _native.ptr(self.keys[layer]), _native.ptr(self.values[layer]),
+                     _native.ptr(self._keys[layer]), _native.ptr(self._values[layer]),
                      _native.ptr(self.scratch_keys[layer]), _native.ptr(self.scratch_values[layer]),
                      _native.ptr(ws.cu_query), _native.ptr(ws.cu_key), _native.ptr(ws.req),
-                     len(tx.slots), self.context_capacity, bucket.key_capacity, bucket.maximum_query_length,
-                     float(SCALE), self.chunk, _native.ptr(out), _native.ptr(ws.attn), ws.attn.numel(),
+                     len(tx.slots), KV_HEADS * C * HEAD_DIM, HEAD_DIM, C * HEAD_DIM,
+                     bucket.key_capacity, bucket.maximum_query_length, float(SCALE), self.chunk,
+                     _native.ptr(ws.work), self._n_work, _native.ptr(out), _native.ptr(ws.attn), ws.attn.numel(),
                      _native.stream_handle(self.device))
         return out
 
@@ -534,11 +558,13 @@ class PersistentTargetKV:
         try:
             if any(counts):
                 acc = torch.tensor(counts, dtype=torch.int32).pin_memory().to(self.device, non_blocking=True)
-                _native.call('dspark_kv_commit', _native.ptr(self.keys), _native.ptr(self.values),
+                layer_b, slot_b, head_b, tok_b, piece_b = self._geometry()
+                _native.call('dspark_kv_commit', _native.ptr(self._keys), _native.ptr(self._values),
                              _native.ptr(self.scratch_keys), _native.ptr(self.scratch_values),
                              _native.ptr(ws.req), _native.ptr(ws.cu_query), _native.ptr(acc),
-                             r, max(tx.query_lengths), self.layers, self.slot_capacity, self.context_capacity,
-                             self.max_query_tokens, self._row_bytes, _native.stream_handle(self.device))
+                             r, max(tx.query_lengths), self.layers, layer_b, slot_b, head_b, tok_b,
+                             self.context_capacity, self.heads, piece_b, self.max_query_tokens,
+                             _native.stream_handle(self.device))
             for h, n in zip(tx.slots, counts):
                 self._lengths[h.index] += n
         except Exception:
@@ -560,7 +586,8 @@ class PersistentTargetKV:
     def request_kv(self, handle):
         i = self._slot(handle)
         n = self._lengths[i]
-        return self.keys[:, i, :n].detach().clone(), self.values[:, i, :n].detach().clone()
+        return (self.keys[:, i, :n].detach().clone(memory_format=torch.contiguous_format),
+                self.values[:, i, :n].detach().clone(memory_format=torch.contiguous_format))
 
     def pointers(self, bucket):
         """Audit stable allocation identities."""

@@ -37,9 +37,8 @@ def test_library_exports_every_declared_symbol():
 def test_workspace_size_formula():
     lib = _native.load()
     # (ceil(rows/chunk) + n_req) items * 8 KV heads * tiles * 16 rows * (128 + 2) floats
-    # + one int32 arrival counter per (request, KV head, tile)
-    assert lib.dspark_attn_workspace_bytes(4, 1000, 1, 512) == (2 + 4) * 8 * 1 * 16 * 130 * 4 + 4 * 8 * 4
-    assert lib.dspark_attn_workspace_bytes(64, 524288 + 448, 1, 512) == (1025 + 64) * 8 * 16 * 130 * 4 + 64 * 8 * 4
+    assert lib.dspark_attn_workspace_bytes(4, 1000, 1, 512) == (2 + 4) * 8 * 1 * 16 * 130 * 4
+    assert lib.dspark_attn_workspace_bytes(64, 524288 + 448, 1, 512) == (1025 + 64) * 8 * 16 * 130 * 4
     assert lib.dspark_attn_workspace_bytes(0, 10, 1, 512) == -1
 
 
@@ -59,14 +58,26 @@ def test_null_arguments_are_rejected_before_any_launch(name):
 def test_invalid_sizes_are_rejected_before_any_launch():
     lib = _native.load()
     fake = ctypes.c_void_p(1 << 20)  # never dereferenced: validation fails first
-    rc = lib.dspark_varlen_attn_fwd(fake, fake, fake, fake, fake, 0, 8, 8, 1, 1, 0.088, 512, fake, fake, 1 << 20, None)
+    rc = lib.dspark_varlen_attn_fwd(fake, fake, fake, fake, fake, 0, 8, 8, 1, 1, 0.088, 512, None, 0, fake, fake,
+                                    1 << 20, None)
     assert rc == -1 and 'n_req' in lib.dspark_last_error().decode()
-    rc = lib.dspark_varlen_attn_fwd(fake, fake, fake, fake, fake, 2, 8, 8, 1, 1, 0.088, 500, fake, fake, 1 << 20, None)
+    rc = lib.dspark_varlen_attn_fwd(fake, fake, fake, fake, fake, 2, 8, 8, 1, 1, 0.088, 500, None, 0, fake, fake,
+                                    1 << 20, None)
     assert rc == -1 and 'chunk' in lib.dspark_last_error().decode()
-    rc = lib.dspark_varlen_attn_fwd(fake, fake, fake, fake, fake, 2, 8, 8, 1, 1, 0.088, 512, fake, fake, 16, None)
+    rc = lib.dspark_varlen_attn_fwd(fake, fake, fake, fake, fake, 2, 8, 8, 1, 1, 0.088, 512, None, 0, fake, fake,
+                                    16, None)
     assert rc == -1 and 'workspace too small' in lib.dspark_last_error().decode()
+    rc = lib.dspark_varlen_attn_fwd(fake, fake, fake, fake, fake, 2, 8, 8, 1, 1, 0.088, 512, fake, 0, fake, fake,
+                                    1 << 20, None)
+    assert rc == -1 and 'n_work' in lib.dspark_last_error().decode()
     rc = lib.dspark_draft_attn_fwd(fake, fake, fake, None, fake, fake, 1024, 128, fake, fake, fake, fake,
-                                   2, 100, 9, 0.088, 512, fake, fake, 1 << 24, None)
+                                   2, 100, 9, 0.088, 512, None, 0, fake, fake, 1 << 24, None)
     assert rc == -1 and 'max_blocks' in lib.dspark_last_error().decode()
+    rc = lib.dspark_verify_attn_fwd(fake, fake, fake, fake, fake, fake, fake, fake, 2, 1 << 20, 100, 128, 1000, 7,
+                                    0.088, 512, None, 0, fake, fake, 1 << 24, None)
+    assert rc == -1 and 'strides' in lib.dspark_last_error().decode()
     rc = lib.dspark_kv_stage(fake, fake, fake, fake, 4, 24, None)
     assert rc == -1 and 'multiple of 16' in lib.dspark_last_error().decode()
+    rc = lib.dspark_kv_commit(fake, fake, fake, fake, fake, fake, fake, 2, 7, 1, 1 << 20, 1 << 16, 1 << 12, 24, 16,
+                              8, 256, 14, None)
+    assert rc == -1 and '16 bytes' in lib.dspark_last_error().decode()

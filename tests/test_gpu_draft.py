@@ -110,11 +110,12 @@ def test_single_block_equals_packed_noncausal_path(dev):
     attention_gate(f64(packed), ref, seg)
 
 
-def test_indexed_append_order_pool_is_bit_identical(dev):
+def test_pool_forms_are_bit_identical(dev):
     """The reference pool layout [1,8,N,128] with interleaved requests and
-    per-request physical indices gives the same bits as the row store."""
+    per-request physical indices, and a head-major slotted pool with NaN
+    outside the used rows, give the same bits as the row store."""
     from qwen3_dspark_amd.draft import HipDraftAttention
-    say('[draft] indexed [1,8,N,128] pool')
+    say('[draft] pool forms')
     rng = np.random.default_rng(SEED + 5)
     gen = torch.Generator().manual_seed(SEED + 5)
     contexts, blocks = [300, 41, 900], [3, 2, 6]
@@ -136,6 +137,19 @@ def test_indexed_append_order_pool_is_bit_identical(dev):
         pool_v[0, :, idx] = c['ctx_v'][o:o + l].transpose(0, 1)
     idx_t = torch.tensor(indices, dtype=torch.long, device=dev)
     out = run(dev, kernel, c, ctx_k=pool_k, ctx_v=pool_v, indices=idx_t, offs=offs)
+    assert torch.equal(out, rows_out)
+    # Head-major slotted pool [slots, 8, capacity, 128]: request r in slot
+    # 2-r at position 5 (offset = slot * capacity + position).
+    cap = 1000
+    slot_k = torch.full((3, 8, cap, 128), float('nan'), dtype=torch.bfloat16)
+    slot_v = torch.full_like(slot_k, float('nan'))
+    soffs = []
+    for r, (o, l) in enumerate(zip(c['offs'], c['lens'])):
+        slot = 2 - r
+        slot_k[slot, :, 5:5 + l] = c['ctx_k'][o:o + l].transpose(0, 1)
+        slot_v[slot, :, 5:5 + l] = c['ctx_v'][o:o + l].transpose(0, 1)
+        soffs.append(slot * cap + 5)
+    out = run(dev, kernel, c, ctx_k=slot_k, ctx_v=slot_v, offs=soffs)
     assert torch.equal(out, rows_out)
 
 
