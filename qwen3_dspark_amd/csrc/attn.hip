@@ -440,14 +440,33 @@ struct DraftArgs {
 };
 
 constexpr int BLOCK_ROWS = 7;
-constexpr int DSTEP = 64;                        // context keys per LDS step
-constexpr int DRAFT_SMEM = 2 * DSTEP * ROWB;     // K + V tiles (32 KiB)
-constexpr int DRAFT_TILES_PER_WAVE = 2;
+constexpr int DWAVES = 8;                            // one draft block per wave
+constexpr int DSTEP = 64;                            // context keys per ring stage
+constexpr int DSTAGES = 4;                           // ring depth (3 stages in flight)
+constexpr int DSTAGE_BYTES = 2 * DSTEP * ROWB;       // K + V tiles (32 KiB)
+constexpr int DRAFT_SMEM = DSTAGES * DSTAGE_BYTES;   // 128 KiB
+constexpr int DRAFT_PIECES = 2 * DSTEP * ROWB / 1024;  // 1 KiB pieces per stage (32)
+static_assert(DRAFT_PIECES == DWAVES * 4, "each thread issues 4 direct loads per stage");
 
-__global__ __launch_bounds__(256) void draft_attn_kernel(DraftArgs a) {
+// Direct global->LDS load of 16 bytes per lane: lane L's data lands at LDS
+// byte address `lds` + 16*L.  Issued as inline assembly so that the
+// compiler neither waits on it nor reorders LDS reads around it; the kernel
+// orders it with explicit vmcnt waits and barriers.
+__device__ __forceinline__ void lds_dma16(const void* gptr, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(lds), "v"(gptr) : "memory");
+}
+
+__device__ __forceinline__ uint32_t lds_address(const void* p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
+}
+
+// INDEXED: context rows come through a per-request physical index vector
+// (the append-order pool); otherwise they are consecutive rows.  The
+// non-indexed instance has no ordinary global loads inside the stage loop,
+// so nothing forces a full vmcnt drain between ring stages.
+template <bool INDEXED>
+__global__ __launch_bounds__(512) void draft_attn_kernel(DraftArgs a) {
   __shared__ __attribute__((aligned(16))) unsigned char smem[DRAFT_SMEM];
-  unsigned char* ks_tile = smem;
-  unsigned char* vs_tile = smem + DSTEP * ROWB;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
@@ -473,167 +492,160 @@ __global__ __launch_bounds__(256) void draft_attn_kernel(DraftArgs a) {
   const int k1 = min(k0 + a.chunk, ctx);
   const int b0 = a.cu_b[r];
   const int nb = a.cu_b[r + 1] - b0;
-
-  // Tiles owned by this wave: blocks wave and wave+4.
-  bool has[DRAFT_TILES_PER_WAVE];
-  int vis[DRAFT_TILES_PER_WAVE];
-  int tile_anchor[DRAFT_TILES_PER_WAVE];
-  bf16x8 qf[DRAFT_TILES_PER_WAVE][4];
-  RowState st[DRAFT_TILES_PER_WAVE];
-  const int tok = col >> 1;
-  const bool row_ok = tok < BLOCK_ROWS;
   int amax = 0;
   for (int b = 0; b < nb; ++b) amax = max(amax, a.anchors[b0 + b]);
-  #pragma unroll
-  for (int i = 0; i < DRAFT_TILES_PER_WAVE; ++i) {
-    const int b = wave + 4 * i;
-    has[i] = b < nb;
-    tile_anchor[i] = has[i] ? min(a.anchors[b0 + b], k1) : 0;
-    vis[i] = row_ok ? tile_anchor[i] : 0;
-    row_init(st[i]);
-    const bf16* qp = a.q + (size_t)(BLOCK_ROWS * (b0 + (has[i] ? b : 0)) + (row_ok ? tok : 0)) * Q_ROW +
-                     (size_t)(2 * g + (col & 1)) * HD + 8 * grp;
-    #pragma unroll
-    for (int ks = 0; ks < 4; ++ks) qf[i][ks] = (has[i] && row_ok) ? ld8(qp + 32 * ks) : zero8();
-  }
   const int kend = min(k1, amax);
 
-  // Context pointer of row j of this request (head g).
-  const size_t hoff = (size_t)g * a.head_stride;
+  // This wave's block (if any): rows = 7 tokens x the 2 query heads of KV head g.
+  const int b = wave;
+  const bool active = b < nb;
+  const int tok = col >> 1;
+  const bool row_ok = tok < BLOCK_ROWS;
+  const int tile_anchor = active ? min(a.anchors[b0 + b], k1) : 0;
+  const int vis = row_ok ? tile_anchor : 0;
+  bf16x8 qf[4];
+  {
+    const bf16* qp = a.q + (size_t)(BLOCK_ROWS * (b0 + (active ? b : 0)) + (row_ok ? tok : 0)) * Q_ROW +
+                     (size_t)(2 * g + (col & 1)) * HD + 8 * grp;
+    #pragma unroll
+    for (int ks = 0; ks < 4; ++ks) qf[ks] = (active && row_ok) ? ld8(qp + 32 * ks) : zero8();
+  }
+  RowState st;
+  row_init(st);
+
+  // Context row kk of this request for KV head g (clamped into range).
   const int64_t coff = a.ctx_off[r];
-  auto ctx_row = [&](int j) -> size_t {
-    const int64_t phys = a.ctx_idx ? a.ctx_idx[coff + j] : coff + j;
-    return (size_t)phys * (size_t)a.tok_stride + hoff;
+  const bf16* kbase = a.k_ctx + (size_t)g * a.head_stride;
+  const bf16* vbase = a.v_ctx + (size_t)g * a.head_stride;
+  auto ctx_row = [&](const bf16* base, int kk) -> const bf16* {
+    kk = min(kk, kend - 1);
+    const int64_t phys = INDEXED ? a.ctx_idx[coff + kk] : coff + kk;
+    return base + (size_t)phys * (size_t)a.tok_stride;
   };
-
-  // Cooperative staging: thread tid covers chunk (tid&15) of keys
-  // step + 16*it + (tid>>4), it = 0..3, for both K and V.
-  bf16x8 pk[4], pv[4];
-  auto prefetch = [&](int step) {
+  const uint32_t smem_lds = lds_address(smem);
+  // Stage `step` of the ring: 32 pieces of 1 KiB (pieces 0-15: K rows,
+  // 16-31: V rows, 4 rows each); wave w issues pieces 4w..4w+3.  Lane L of a
+  // piece fetches row 4*piece + L/16, 16-byte chunk (L%16) ^ swz(row).
+  auto issue = [&](int step) {
+    const int ks = k0 + step * DSTEP;
+    const uint32_t stage = smem_lds + (uint32_t)((step % DSTAGES) * DSTAGE_BYTES);
     #pragma unroll
-    for (int it = 0; it < 4; ++it) {
-      const int kk = step + 16 * it + (tid >> 4);
-      if (kk < kend) {
-        const size_t off = ctx_row(kk) + 8 * (tid & 15);
-        pk[it] = ld8(a.k_ctx + off);
-        pv[it] = ld8(a.v_ctx + off);
-      } else {
-        pk[it] = zero8();
-        pv[it] = zero8();
-      }
+    for (int i = 0; i < 4; ++i) {
+      const int piece = wave * 4 + i;
+      const bool is_v = piece >= 16;
+      const int pr = piece & 15;
+      const int k = 4 * pr + grp;
+      const bf16* src = ctx_row(is_v ? vbase : kbase, ks + k) + 8 * (col ^ swz(k));
+      const uint32_t dst = stage + (uint32_t)((is_v ? DSTEP * ROWB : 0) + pr * 1024);
+      lds_dma16(src, __builtin_amdgcn_readfirstlane(dst));
     }
   };
-
-  if (k0 < kend) prefetch(k0);
-  for (int step = k0; step < kend; step += DSTEP) {
-    #pragma unroll
-    for (int it = 0; it < 4; ++it) {
-      const int k = 16 * it + (tid >> 4);
-      *reinterpret_cast<bf16x8*>(ks_tile + lds_chunk_off(k, tid & 15)) = pk[it];
-      *reinterpret_cast<bf16x8*>(vs_tile + lds_chunk_off(k, tid & 15)) = pv[it];
-    }
-    __syncthreads();
-    if (step + DSTEP < kend) prefetch(step + DSTEP);
+  auto compute = [&](int step) {
+    const unsigned char* kt_lds = smem + (step % DSTAGES) * DSTAGE_BYTES;
+    const unsigned char* vt_lds = kt_lds + DSTEP * ROWB;
     #pragma unroll
     for (int h = 0; h < 2; ++h) {
-      const int kt = step + KT * h;
-      bool any = false;
-      #pragma unroll
-      for (int i = 0; i < DRAFT_TILES_PER_WAVE; ++i) any |= has[i] && (tile_anchor[i] > kt);
-      if (!any) continue;
+      const int kt = k0 + step * DSTEP + KT * h;
+      if (tile_anchor <= kt) continue;
       bf16x8 kf[2][4];
       #pragma unroll
       for (int j = 0; j < 2; ++j) {
         const int k = KT * h + 8 * (col >> 2) + 4 * j + (col & 3);
         #pragma unroll
         for (int ks = 0; ks < 4; ++ks)
-          kf[j][ks] = *reinterpret_cast<const bf16x8*>(ks_tile + lds_chunk_off(k, 4 * ks + grp));
+          kf[j][ks] = *reinterpret_cast<const bf16x8*>(kt_lds + lds_chunk_off(k, 4 * ks + grp));
       }
+      f32x4 s0, s1;
+      qk_tile(kf, qf, s0, s1);
+      const bf16x8 pb = softmax_update(st, s0, s1, kt + 8 * grp, vis, a.scale_log2);
       bf16x8 vt[8];
       #pragma unroll
-      for (int nbk = 0; nbk < 8; ++nbk) vt[nbk] = lds_vt(vs_tile + KT * h * ROWB, nbk, lane);
-      #pragma unroll
-      for (int i = 0; i < DRAFT_TILES_PER_WAVE; ++i) {
-        if (!(has[i] && tile_anchor[i] > kt)) continue;
-        f32x4 s0, s1;
-        qk_tile(kf, qf[i], s0, s1);
-        const bf16x8 pb = softmax_update(st[i], s0, s1, kt + 8 * grp, vis[i], a.scale_log2);
-        pv_update(st[i], pb, vt);
+      for (int nbk = 0; nbk < 8; ++nbk) vt[nbk] = lds_vt(vt_lds + KT * h * ROWB, nbk, lane);
+      if (kt + KT > kend) {
+        // rows past kend hold clamped copies; their weights are 0, keep V finite-safe
+        #pragma unroll
+        for (int nbk = 0; nbk < 8; ++nbk)
+          #pragma unroll
+          for (int e = 0; e < 8; ++e)
+            if (kt + 8 * grp + e >= kend) vt[nbk][e] = (bf16)0.0f;
       }
+      pv_update(st, pb, vt);
     }
-    __syncthreads();
+  };
+
+  const int n_steps = kend > k0 ? (kend - k0 + DSTEP - 1) / DSTEP : 0;
+  if (n_steps > 0) {
+    // Every thread issues exactly 4 loads per stage (stages past the end
+    // re-read the clamped last row), so "stage s has landed" is always
+    // vmcnt(4 * (DSTAGES - 2)) at the top of step s.
+    #pragma unroll
+    for (int p = 0; p < DSTAGES - 1; ++p) issue(p);
+    for (int s = 0; s < n_steps; ++s) {
+      asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+      asm volatile("s_barrier" ::: "memory");
+      issue(s + DSTAGES - 1);
+      if (active) compute(s);
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    asm volatile("s_barrier" ::: "memory");
   }
 
   // Own-block keys (bidirectional within the block), once per request.
-  if (c == nch - 1) {
+  if (c == nch - 1 && active) {
     unsigned char* wv = smem + wave * 8 * ROWB;   // 8 rows per wave
+    const size_t rb = (size_t)BLOCK_ROWS * (b0 + b);
+    bf16x8 kf[2][4];
     #pragma unroll
-    for (int i = 0; i < DRAFT_TILES_PER_WAVE; ++i) {
-      if (!has[i]) continue;
-      const int b = wave + 4 * i;
-      const size_t rb = (size_t)BLOCK_ROWS * (b0 + b);
-      bf16x8 kf[2][4];
+    for (int j = 0; j < 2; ++j) {
+      const int kk = 8 * (col >> 2) + 4 * j + (col & 3);
+      const bf16* p = a.k_blk + (rb + min(kk, BLOCK_ROWS - 1)) * KV_ROW + (size_t)g * HD + 8 * grp;
       #pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        const int kk = 8 * (col >> 2) + 4 * j + (col & 3);
-        if (kk < BLOCK_ROWS) {
-          const bf16* p = a.k_blk + (rb + kk) * KV_ROW + (size_t)g * HD + 8 * grp;
-          #pragma unroll
-          for (int ks = 0; ks < 4; ++ks) kf[j][ks] = ld8(p + 32 * ks);
-        } else {
-          #pragma unroll
-          for (int ks = 0; ks < 4; ++ks) kf[j][ks] = zero8();
-        }
-      }
-      #pragma unroll
-      for (int i2 = 0; i2 < 2; ++i2) {
-        const int kk = 4 * i2 + grp;
-        const bf16x8 v = (kk < BLOCK_ROWS) ? ld8(a.v_blk + (rb + kk) * KV_ROW + (size_t)g * HD + 8 * col) : zero8();
-        *reinterpret_cast<bf16x8*>(wv + lds_chunk_off(kk, col)) = v;
-      }
-      f32x4 s0, s1;
-      qk_tile(kf, qf[i], s0, s1);
-      const bf16x8 pb = softmax_update(st[i], s0, s1, 8 * grp, row_ok ? BLOCK_ROWS : 0, a.scale_log2);
-      wave_lds_sync();
-      bf16x8 vt[8];
-      #pragma unroll
-      for (int nbk = 0; nbk < 8; ++nbk) {
-        // keys 8*grp+s >= 8 do not exist in a 7-row block
-        vt[nbk] = lds_vt(wv, nbk, lane);
-        if (grp != 0) vt[nbk] = zero8();
-      }
-      pv_update(st[i], pb, vt);
-      wave_lds_sync();
+      for (int ks = 0; ks < 4; ++ks) kf[j][ks] = ld8(p + 32 * ks);
     }
+    #pragma unroll
+    for (int i2 = 0; i2 < 2; ++i2) {
+      const int kk = 4 * i2 + grp;
+      const bf16x8 v = (kk < BLOCK_ROWS) ? ld8(a.v_blk + (rb + kk) * KV_ROW + (size_t)g * HD + 8 * col) : zero8();
+      *reinterpret_cast<bf16x8*>(wv + lds_chunk_off(kk, col)) = v;
+    }
+    f32x4 s0, s1;
+    qk_tile(kf, qf, s0, s1);
+    const bf16x8 pb = softmax_update(st, s0, s1, 8 * grp, row_ok ? BLOCK_ROWS : 0, a.scale_log2);
+    wave_lds_sync();
+    bf16x8 vt[8];
+    #pragma unroll
+    for (int nbk = 0; nbk < 8; ++nbk) {
+      // keys 8*grp+s >= 8 do not exist in a 7-row block
+      vt[nbk] = lds_vt(wv, nbk, lane);
+      if (grp != 0) vt[nbk] = zero8();
+    }
+    pv_update(st, pb, vt);
+    wave_lds_sync();
   }
 
-  #pragma unroll
-  for (int i = 0; i < DRAFT_TILES_PER_WAVE; ++i) {
-    if (!has[i]) continue;
-    const int b = wave + 4 * i;
-    const float l = wave_sum_across_groups(st[i].l);
-    const size_t orow0 = (size_t)BLOCK_ROWS * (b0 + b);
-    if (nch == 1) {
-      if (row_ok) {
-        bf16* op = a.out + (orow0 + tok) * Q_ROW + (size_t)(2 * g + (col & 1)) * HD + 4 * grp;
+  if (!active) return;
+  const float l = wave_sum_across_groups(st.l);
+  const size_t orow0 = (size_t)BLOCK_ROWS * (b0 + b);
+  if (nch == 1) {
+    if (row_ok) {
+      bf16* op = a.out + (orow0 + tok) * Q_ROW + (size_t)(2 * g + (col & 1)) * HD + 4 * grp;
+      #pragma unroll
+      for (int nbk = 0; nbk < 8; ++nbk) {
+        bf16x4 ov;
         #pragma unroll
-        for (int nbk = 0; nbk < 8; ++nbk) {
-          bf16x4 ov;
-          #pragma unroll
-          for (int e = 0; e < 4; ++e) ov[e] = (bf16)(st[i].o[nbk][e] / l);
-          *reinterpret_cast<bf16x4*>(op + 16 * nbk) = ov;
-        }
+        for (int e = 0; e < 4; ++e) ov[e] = (bf16)(st.o[nbk][e] / l);
+        *reinterpret_cast<bf16x4*>(op + 16 * nbk) = ov;
       }
-      continue;
     }
-    const size_t p = (size_t)(item * 8 + g) * a.tmax + b;
-    float* po = a.part_o + (p * 16 + col) * HD + 4 * grp;
-    #pragma unroll
-    for (int nbk = 0; nbk < 8; ++nbk) *reinterpret_cast<f32x4*>(po + 16 * nbk) = st[i].o[nbk];
-    if (grp == 0) {
-      a.part_ml[(p * 16 + col) * 2 + 0] = st[i].m;
-      a.part_ml[(p * 16 + col) * 2 + 1] = l;
-    }
+    return;
+  }
+  const size_t p = (size_t)(item * 8 + g) * a.tmax + b;
+  float* po = a.part_o + (p * 16 + col) * HD + 4 * grp;
+  #pragma unroll
+  for (int nbk = 0; nbk < 8; ++nbk) *reinterpret_cast<f32x4*>(po + 16 * nbk) = st.o[nbk];
+  if (grp == 0) {
+    a.part_ml[(p * 16 + col) * 2 + 0] = st.m;
+    a.part_ml[(p * 16 + col) * 2 + 1] = l;
   }
 }
 
@@ -851,8 +863,8 @@ extern "C" int dspark_draft_attn_fwd(const void* q, const void* k_ctx, const voi
                  "Q/K/V/out must be 16-byte aligned");
   DSPARK_REQUIRE(tok_stride >= HD && tok_stride % 8 == 0 && head_stride >= HD && head_stride % 8 == 0,
                  "context strides must be multiples of 8 elements and >= 128");
-  DSPARK_REQUIRE(max_blocks >= 1 && max_blocks <= 4 * DRAFT_TILES_PER_WAVE,
-                 "max_blocks must be in [1, %d] (got %d)", 4 * DRAFT_TILES_PER_WAVE, max_blocks);
+  DSPARK_REQUIRE(max_blocks >= 1 && max_blocks <= DWAVES,
+                 "max_blocks must be in [1, %d] (got %d)", DWAVES, max_blocks);
   DSPARK_REQUIRE(chunk % DSTEP == 0, "draft chunk must be a multiple of %d", DSTEP);
   int rc = check_common(n_req, ctx_rows_bound, max_blocks, chunk, scale, workspace_bytes_, workspace);
   if (rc != OK) return rc;
@@ -881,7 +893,10 @@ extern "C" int dspark_draft_attn_fwd(const void* q, const void* k_ctx, const voi
   hipStream_t s = static_cast<hipStream_t>(stream);
   DSPARK_REQUIRE(!work || (n_work >= 1 && n_work <= n_cl), "work list length out of range");
   const int64_t grid = work ? (int64_t)n_work * HKV : n_cl * HKV;
-  hipLaunchKernelGGL(draft_attn_kernel, dim3((unsigned)grid), dim3(256), 0, s, a);
+  if (ctx_idx)
+    hipLaunchKernelGGL(draft_attn_kernel<true>, dim3((unsigned)grid), dim3(DWAVES * WAVE), 0, s, a);
+  else
+    hipLaunchKernelGGL(draft_attn_kernel<false>, dim3((unsigned)grid), dim3(DWAVES * WAVE), 0, s, a);
   rc = launch_status("draft_attn_kernel");
   if (rc != OK) return rc;
   MergeArgs m{nullptr, nullptr, ctx_len, cu_blocks, a.part_o, a.part_ml, a.out, n_req, chunk, max_blocks, 1};
