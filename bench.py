@@ -13,13 +13,21 @@ One step = one speculative round of the hot path:
   28 x (stage new K/V + fused verification attention) -> commit of a
   seeded accepted prefix 0..7 per request (the rest rolled back).
 Inputs are seeded N(0,1) bf16 already resident in HBM; the timed region
-contains only the round itself.
+contains only the rounds themselves.
 
-value = verified tokens per second = 448 / round time.
+value = verified tokens per second = 448 / round time (wall clock between
+two device synchronisations around the K timed rounds).
+
+Per-launch durations come from HIP events recorded on the launch stream
+inside the timed rounds, around a rotating sample of launches (3 of the 28
+verification-attention calls and 1 of the 5 draft-attention calls per round;
+each call is a split-K chunk kernel followed by its merge kernel).  Events
+around every launch would add ~12 us of marker work each to the round.
 
     python bench.py [--gpus 1] [--steps 20] [--warmup 5]
 """
 import argparse
+import gc
 import json
 import math
 import os
@@ -34,6 +42,7 @@ METRIC = 'attn tokens/s + HBM GB/s (% roofline), 64 ragged reqs, Qwen3-0.6B shap
 SEED = 20261009
 B, Q_LEN, CAPACITY = 64, 7, 8192
 VERIFY_LAYERS, DRAFT_LAYERS, BLOCK = 28, 5, 7
+VERIFY_SAMPLES, DRAFT_SAMPLES = 3, 1  # event-timed launches per round
 ROW_BYTES = 8 * 128 * 2            # one K (or V) token row, all 8 KV heads
 Q_ROW_BYTES = 16 * 128 * 2         # one Q (or O) token row, all 16 query heads
 HBM_PEAK_GBS = 8000.0              # MI355X HBM3E, published
@@ -51,7 +60,11 @@ def parse():
     ap.add_argument('--warmup', type=int, default=5)
     ap.add_argument('--chunk', type=int, default=None, help='keys per split-K work item')
     ap.add_argument('--no-cpu-baseline', action='store_true', help='skip the CPU oracle leg (profiling runs)')
-    ap.add_argument('--cpu-verify-layers', type=int, default=2, help='verify layers in the CPU sample')
+    ap.add_argument('--traffic-probe', action='store_true',
+                    help='untimed run for hardware-counter passes: 3 verification-attention layers of the '
+                         'workload, then a 1 GiB device-to-device copy as the counter calibration')
+    ap.add_argument('--cpu-verify-layers', type=int, default=VERIFY_LAYERS, help='verify layers in the CPU sample')
+    ap.add_argument('--cpu-draft-layers', type=int, default=DRAFT_LAYERS, help='draft layers in the CPU sample')
     return ap.parse_args()
 
 
@@ -92,6 +105,8 @@ def main():
         print(json.dumps({'error': 'this build measures one GPU only; the attention path has no cross-GPU '
                                    'exchange (requests shard across GPUs, see DESIGN.md); run with --gpus 1'}))
         sys.exit(2)
+    if args.traffic_probe:
+        return traffic_probe(args)
     import numpy as np
     import torch
 
@@ -141,26 +156,32 @@ def main():
     ev_d = []
     step_stats = []
 
+    def events():
+        return torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+
     def round_(step, timed):
         ctx_now = [pool.length(h) for h in handles]
+        sampled_v = {(step * VERIFY_SAMPLES + j * (VERIFY_LAYERS // VERIFY_SAMPLES)) % VERIFY_LAYERS
+                     for j in range(VERIFY_SAMPLES)} if timed else ()
+        sampled_d = {(step * DRAFT_SAMPLES + j) % DRAFT_LAYERS for j in range(DRAFT_SAMPLES)} if timed else ()
         batch = DraftBatch(dev, draft_offsets, contexts, anchors)
         outs = []
         for layer in range(DRAFT_LAYERS):
-            if timed:
-                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            if layer in sampled_d:
+                e0, e1 = events()
                 e0.record()
             outs.append(draft(qd[layer], bkd[layer], bvd[layer], dctx_k[layer], dctx_v[layer], batch, scale=SCALE))
-            if timed:
+            if layer in sampled_d:
                 e1.record()
                 ev_d.append((e0, e1))
         tx = pool.begin(handles, bucket)
         for layer in range(VERIFY_LAYERS):
             pool.stage_layer(tx, layer, kn[layer], vn[layer])
-            if timed:
-                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            if layer in sampled_v:
+                e0, e1 = events()
                 e0.record()
             outs.append(pool.attend(tx, layer, qv[layer]))
-            if timed:
+            if layer in sampled_v:
                 e1.record()
                 ev_v.append((e0, e1, verify_bytes(ctx_now)))
         counts = [int(x) for x in accepted[step]]
@@ -168,6 +189,12 @@ def main():
         step_stats.append((ctx_now, counts))
         return outs
 
+    # Like a long-running server after start-up: move the set-up objects
+    # out of the cyclic collector's reach, so that a full collection during
+    # the rounds (tens of ms over torch/numpy internals) does not stall the
+    # launch stream.  The collector stays enabled.
+    gc.collect()
+    gc.freeze()
     log(f'[bench] warmup {args.warmup} steps')
     for s in range(args.warmup):
         round_(s, False)
@@ -182,12 +209,16 @@ def main():
     elapsed = time.perf_counter() - t0
     ms_step = 1e3 * elapsed / args.steps
 
-    v_ms = [a.elapsed_time(b) for a, b, _ in ev_v]
-    v_bytes = [n for _, _, n in ev_v]
-    d_ms = [a.elapsed_time(b) for a, b in ev_d]
-    v_avg_ms = sum(v_ms) / len(v_ms)
-    v_avg_bytes = sum(v_bytes) / len(v_bytes)
-    d_avg_ms = sum(d_ms) / len(d_ms)
+    v_ms = np.array([a.elapsed_time(b) for a, b, _ in ev_v])
+    v_bytes = np.array([n for _, _, n in ev_v], dtype=np.float64)
+    d_ms = np.array([a.elapsed_time(b) for a, b in ev_d])
+    v_avg_ms = float(v_ms.mean())
+    v_avg_bytes = float(v_bytes.mean())
+    d_avg_ms = float(d_ms.mean())
+
+    def pct(x):
+        return {'p10': round(float(np.percentile(x, 10)), 5), 'median': round(float(np.median(x)), 5),
+                'p90': round(float(np.percentile(x, 90)), 5), 'samples': int(len(x))}
     d_b = draft_bytes(anchors)
     v_gbs = v_avg_bytes / (v_avg_ms * 1e-3) / 1e9
     d_gbs = d_b / (d_avg_ms * 1e-3) / 1e9
@@ -198,11 +229,15 @@ def main():
     round_gbs = round_bytes / (ms_step * 1e-3) / 1e9
     value = B * Q_LEN / (ms_step * 1e-3)
 
-    traffic = None
+    # HBM bytes per call from the two counter passes of --traffic-probe
+    # (FETCH_SIZE, WRITE_SIZE, calibrated against a plain 1 GiB copy), for
+    # the first round of this workload; summarised in profiles/.
+    traffic, traffic_ratio = None, None
     tpath = os.path.join(ROOT, 'profiles', 'verify_attn_traffic.json')
     if os.path.exists(tpath):
         with open(tpath) as f:
-            traffic = json.load(f).get('hbm_bytes_per_launch')
+            tj = json.load(f)
+        traffic, traffic_ratio = tj.get('hbm_bytes_per_launch'), tj.get('ratio')
 
     result = {
         'metric': METRIC, 'value': round(value, 1), 'unit': 'tokens/s', 'n_gpus': 1,
@@ -219,16 +254,17 @@ def main():
         },
         'roofline': {
             'bound': 'hbm', 'achieved': round(v_gbs, 1), 'peak': HBM_PEAK_GBS, 'unit': 'GB/s',
-            'frac': round(v_gbs / HBM_PEAK_GBS, 4), 'traffic': traffic,
-            'kernel': 'varlen_attn_kernel<true> (fused verification attention)',
+            'frac': round(v_gbs / HBM_PEAK_GBS, 4), 'traffic': traffic, 'traffic_per_algorithmic_byte': traffic_ratio,
+            'kernel': 'fused verification attention: varlen_attn_kernel<true> + merge_kernel',
             'avg_launch_ms': round(v_avg_ms, 5), 'algorithmic_bytes_per_launch': int(v_avg_bytes),
         },
         'breakdown': {
-            'verify_layer_ms': round(v_avg_ms, 5), 'verify_gbs': round(v_gbs, 1),
-            'verify_attn_tokens_per_s': round(B * Q_LEN / (v_avg_ms * 1e-3), 1),
-            'draft_layer_ms': round(d_avg_ms, 5), 'draft_gbs': round(d_gbs, 1),
+            'verify_layer_ms': round(v_avg_ms, 5), 'verify_call_ms': pct(v_ms), 'verify_gbs': round(v_gbs, 1),
+            'verify_attn_tokens_per_s': round(B * Q_LEN / (float(np.median(v_ms)) * 1e-3), 1),
+            'draft_layer_ms': round(d_avg_ms, 5), 'draft_call_ms': pct(d_ms), 'draft_gbs': round(d_gbs, 1),
             'draft_frac': round(d_gbs / HBM_PEAK_GBS, 4),
-            'draft_attn_tokens_per_s': round(nq_d / (d_avg_ms * 1e-3), 1),
+            'draft_algorithmic_bytes_per_launch': int(d_b),
+            'draft_attn_tokens_per_s': round(nq_d / (float(np.median(d_ms)) * 1e-3), 1),
             'round_algorithmic_bytes': int(round_bytes), 'round_gbs': round(round_gbs, 1),
             'round_frac': round(round_gbs / HBM_PEAK_GBS, 4),
         },
@@ -240,9 +276,47 @@ def main():
     print(json.dumps(result), flush=True)
 
 
+def traffic_probe(args):
+    """Kernels for `rocprofv3 --pmc FETCH_SIZE` / `--pmc WRITE_SIZE` passes:
+    the verification-attention launches of the workload (store contents are
+    irrelevant to the bytes moved, so it stays zero-filled), then a plain
+    copy of exactly 2**30 bytes whose counter reading calibrates the
+    counters to bytes."""
+    import torch
+
+    from qwen3_dspark_amd.kernels import DEFAULT_CHUNK
+    from qwen3_dspark_amd.persistent_kv import Bucket, PersistentTargetKV
+
+    dev = torch.device('cuda:0')
+    contexts, _, _ = workload(args.warmup + args.steps)
+    pool = PersistentTargetKV(layers=3, slots=B, context_capacity=CAPACITY, max_query_tokens=B * Q_LEN,
+                              heads=8, dim=128, device=dev, chunk=args.chunk or DEFAULT_CHUNK)
+    handles = [pool.add_request(f'req{i}') for i in range(B)]
+    for h, c in zip(handles, contexts):
+        pool.load_prefix(h, pool.keys[:, h.index, :c], pool.values[:, h.index, :c])
+    bucket = Bucket((Q_LEN,) * B, (CAPACITY - Q_LEN,) * B, '64-request stress shape')
+    pool.register_bucket(bucket)
+    q = torch.zeros(B * Q_LEN, 16, 128, dtype=torch.bfloat16, device=dev)
+    kn = torch.zeros(B * Q_LEN, 8, 128, dtype=torch.bfloat16, device=dev)
+    tx = pool.begin(handles, bucket)
+    for layer in range(3):
+        pool.stage_layer(tx, layer, kn, kn)
+        pool.attend(tx, layer, q)
+    pool.abort(tx)
+    src = torch.ones(1 << 30, dtype=torch.uint8, device=dev)
+    dst = torch.empty_like(src)
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({'traffic_probe': 'done', 'verify_algorithmic_bytes_per_launch': verify_bytes(contexts),
+                      'context_rows': sum(contexts),
+                      'calibration_copy_bytes': 1 << 30}), flush=True)
+
+
 def cpu_leg(args, pool, bucket, handles, contexts, anchors, qv, qd, bkd, bvd, dctx_k, dctx_v, draft, draft_offsets):
-    """Time the C oracle (OpenMP, host cores) on a bounded sample of the same
-    workload and check the GPU outputs of the sampled layers against it."""
+    """Time the C oracle (FP32, OpenMP over the host cores) on one more round
+    of the same workload - by default all 28 verification and 5 draft layers,
+    nothing extrapolated - and check every GPU output of that round
+    against it."""
     import numpy as np
     import torch
 
@@ -252,62 +326,72 @@ def cpu_leg(args, pool, bucket, handles, contexts, anchors, qv, qd, bkd, bvd, dc
 
     threads = max(1, min(CPU_THREADS_CAP, os.cpu_count() or 1))
     dev = pool.device
+    n_verify = max(1, min(VERIFY_LAYERS, args.cpu_verify_layers))
+    n_draft = max(1, min(DRAFT_LAYERS, args.cpu_draft_layers))
 
     def bits(t):
-        return t.detach().cpu().contiguous().view(torch.int16).numpy().view(np.uint16)
+        # make the layout contiguous on the device, then one D2H copy
+        return t.detach().contiguous().cpu().view(torch.int16).numpy().view(np.uint16)
 
-    # One more (untimed) round's inputs: transaction on the current lengths.
+    stats = {'verify_max_abs': 0.0, 'verify_mean_abs': 0.0, 'draft_max_abs': 0.0, 'draft_mean_abs': 0.0}
+
+    def gate(out, ref, kind):
+        d = np.abs(out.astype(np.float64) - ref)
+        stats[kind + '_max_abs'] = max(stats[kind + '_max_abs'], float(d.max()))
+        stats[kind + '_mean_abs'] = max(stats[kind + '_mean_abs'], float(d.mean()))
+
+    # Verification: a transaction on the current lengths, fresh staged rows.
     ctx = [pool.length(h) for h in handles]
     tx = pool.begin(handles, bucket)
-    kn = torch.randn(args.cpu_verify_layers, B * Q_LEN, 8, 128, device=dev).to(torch.bfloat16)
-    vn = torch.randn_like(kn)
-    stats = {'verify_max_abs': 0.0, 'verify_mean_abs': 0.0, 'draft_max_abs': 0.0, 'draft_mean_abs': 0.0}
+    gen = torch.Generator(device=dev).manual_seed(SEED + 1)
     cu_q = [Q_LEN * i for i in range(B + 1)]
     slots = [h.index for h in handles]
-    t_verify = []
-    for layer in range(args.cpu_verify_layers):
-        pool.stage_layer(tx, layer, kn[layer], vn[layer])
+    cmax = max(ctx)
+    t_verify = 0.0
+    for layer in range(n_verify):
+        kn = torch.randn(B * Q_LEN, 8, 128, generator=gen, device=dev).to(torch.bfloat16)
+        vn = torch.randn(B * Q_LEN, 8, 128, generator=gen, device=dev).to(torch.bfloat16)
+        pool.stage_layer(tx, layer, kn, vn)
         out = pool.attend(tx, layer, qv[layer]).float().cpu().numpy()
-        # host copy of the active rows only: slot-major [64, max c, 8, 128]
-        cmax = max(ctx)
-        kres = bits(pool.keys[layer, :, :cmax])
-        vres = bits(pool.values[layer, :, :cmax])
+        # token-major host copy of the active rows: [64, max c, 8, 128]
+        kres, vres = bits(pool.keys[layer, :, :cmax]), bits(pool.values[layer, :, :cmax])
         ks, vs, q = bits(pool.scratch_keys[layer]), bits(pool.scratch_values[layer]), bits(qv[layer])
         t0 = time.perf_counter()
         ref = cref.verify_attention(q, kres, vres, ks, vs, slots, ctx, cu_q, scale=SCALE, threads=threads)
-        t_verify.append(time.perf_counter() - t0)
-        d = np.abs(out.astype(np.float64) - ref)
-        stats['verify_max_abs'] = max(stats['verify_max_abs'], float(d.max()))
-        stats['verify_mean_abs'] = max(stats['verify_mean_abs'], float(d.mean()))
+        t_verify += time.perf_counter() - t0
+        gate(out, ref, 'verify')
+        del kres, vres
     pool.abort(tx)
+
+    # Draft: the round's blocks over each layer's slotted context pool.
     batch = DraftBatch(dev, draft_offsets, contexts, anchors)
-    dout = draft(qd[0], bkd[0], bvd[0], dctx_k[0], dctx_v[0], batch, scale=SCALE).float().cpu().numpy()
-    offs_host = []
-    base = 0
-    for c in contexts:
-        offs_host.append(base)
-        base += c
-    # token-major host copies of each request's context rows
-    ck = bits(torch.cat([dctx_k[0, o // CAPACITY, :, :c].transpose(0, 1) for o, c in zip(draft_offsets, contexts)]))
-    cv = bits(torch.cat([dctx_v[0, o // CAPACITY, :, :c].transpose(0, 1) for o, c in zip(draft_offsets, contexts)]))
+    offs_host = np.concatenate([[0], np.cumsum(contexts)[:-1]]).tolist()
     cu_b = np.cumsum([0] + [len(a) for a in anchors])
     flat = [x for a in anchors for x in a]
-    t0 = time.perf_counter()
-    dref = cref.draft_attention(bits(qd[0]), ck, cv, offs_host, contexts, bits(bkd[0]), bits(bvd[0]), cu_b, flat,
-                                scale=SCALE, threads=threads)
-    t_draft = time.perf_counter() - t0
-    d = np.abs(dout.astype(np.float64) - dref)
-    stats['draft_max_abs'] = float(d.max())
-    stats['draft_mean_abs'] = float(d.mean())
+    t_draft = 0.0
+    for layer in range(n_draft):
+        dout = draft(qd[layer], bkd[layer], bvd[layer], dctx_k[layer], dctx_v[layer], batch,
+                     scale=SCALE).float().cpu().numpy()
+        # token-major host copies of each request's context rows
+        ck = bits(torch.cat([dctx_k[layer, o // CAPACITY, :, :c].transpose(0, 1)
+                             for o, c in zip(draft_offsets, contexts)]))
+        cv = bits(torch.cat([dctx_v[layer, o // CAPACITY, :, :c].transpose(0, 1)
+                             for o, c in zip(draft_offsets, contexts)]))
+        t0 = time.perf_counter()
+        dref = cref.draft_attention(bits(qd[layer]), ck, cv, offs_host, contexts, bits(bkd[layer]),
+                                    bits(bvd[layer]), cu_b, flat, scale=SCALE, threads=threads)
+        t_draft += time.perf_counter() - t0
+        gate(dout, dref, 'draft')
     stats['within_tolerance'] = bool(stats['verify_max_abs'] <= 2e-2 and stats['verify_mean_abs'] <= 2e-3
                                      and stats['draft_max_abs'] <= 2e-2 and stats['draft_mean_abs'] <= 2e-3)
-    per_verify = sum(t_verify) / len(t_verify)
-    round_s = VERIFY_LAYERS * per_verify + DRAFT_LAYERS * t_draft
+    stats['checked_layers'] = {'verify': n_verify, 'draft': n_draft}
+    round_s = VERIFY_LAYERS * t_verify / n_verify + DRAFT_LAYERS * t_draft / n_draft
+    scaled = '' if (n_verify, n_draft) == (VERIFY_LAYERS, DRAFT_LAYERS) else ', scaled to 28 + 5 layers'
     cpu = {
         'value': round(B * Q_LEN / round_s, 3), 'unit': 'tokens/s', 'cores': threads, 'kind': 'port',
-        'sample': f'C oracle (oracle/attn_ref.c, FP32, OpenMP) on {len(t_verify)} of 28 verify layers '
-                  f'({per_verify:.3f} s/layer) and 1 of 5 draft layers ({t_draft:.3f} s/layer) of the same '
-                  f'64-request round; round time scaled as 28 verify + 5 draft layers = {round_s:.2f} s',
+        'sample': f'C oracle (oracle/attn_ref.c, FP32, OpenMP, {threads} threads) over one round of the same '
+                  f'64-request workload: {n_verify} verification layers ({t_verify:.2f} s) and {n_draft} draft '
+                  f'layers ({t_draft:.2f} s){scaled}; round time {round_s:.2f} s',
     }
     return cpu, stats
 

@@ -1,4 +1,8 @@
 """Device selection and per-device reusable buffers for the HIP path."""
+import collections
+import threading
+
+import numpy as np
 import torch
 
 ARCH = 'gfx950'
@@ -36,3 +40,85 @@ class Workspace:
     @property
     def nbytes(self):
         return 0 if self._buf is None else self._buf.numel()
+
+
+class HostStaging:
+    """Pinned host ring for the small host-to-device metadata uploads of the
+    hot path (work lists, offsets, transaction requests, accepted counts).
+
+    The pinned buffer is allocated once.  Each upload writes the next
+    256-byte-aligned region, enqueues an asynchronous copy on the current
+    stream and records an event for the region; a region is rewritten only
+    after its event has completed.  Steady state therefore performs no
+    pinned allocation (which can stall the host for milliseconds) and never
+    synchronises the device.  One instance per device, guarded by a lock.
+    """
+
+    def __init__(self, device, nbytes=1 << 20):
+        self.device = device
+        self._buf = torch.empty(nbytes, dtype=torch.uint8, pin_memory=True)
+        self._head = 0
+        self._inflight = collections.deque()    # (start, end, event), oldest first
+        self._events = []
+        self._lock = threading.Lock()
+
+    def _retire(self, start, end):
+        # Uploads on one stream complete in order: drop finished ones first,
+        # then wait only for a still-pending region that the new one reuses.
+        q = self._inflight
+        while q and q[0][2].query():
+            self._events.append(q.popleft()[2])
+        pending = collections.deque()
+        for s, e, ev in q:
+            if s < end and start < e:
+                ev.synchronize()
+                self._events.append(ev)
+            else:
+                pending.append((s, e, ev))
+        self._inflight = pending
+
+    def upload(self, values, dtype=torch.int32, out=None):
+        """Copy `values` (ints or a numpy array) into a device tensor of
+        `dtype` (a new one unless `out`, a contiguous device tensor of the
+        same size and dtype, is given); returns it.  Asynchronous."""
+        arr = np.ascontiguousarray(np.asarray(values, dtype=torch.empty(0, dtype=dtype).numpy().dtype).reshape(-1))
+        n = arr.nbytes
+        if out is None:
+            out = torch.empty(arr.size, dtype=dtype, device=self.device)
+        elif out.dtype != dtype or out.numel() != arr.size or not out.is_contiguous() or out.device != self.device:
+            raise ValueError('Upload target must be a contiguous device tensor of matching size and dtype')
+        if n == 0:
+            return out
+        with self._lock:
+            span = (n + 255) & ~255
+            if span > self._buf.numel():
+                for _, _, ev in self._inflight:
+                    ev.synchronize()
+                self._inflight.clear()
+                self._buf = torch.empty(max(span, 2 * self._buf.numel()), dtype=torch.uint8, pin_memory=True)
+                self._head = 0
+            if self._head + span > self._buf.numel():
+                self._head = 0
+            start, end = self._head, self._head + span
+            self._retire(start, end)
+            self._head = end
+            host = self._buf[start:start + n].view(dtype)
+            host.copy_(torch.from_numpy(arr))
+            out.copy_(host, non_blocking=True)
+            ev = self._events.pop() if self._events else torch.cuda.Event()
+            ev.record(torch.cuda.current_stream(self.device))
+            self._inflight.append((start, end, ev))
+        return out
+
+
+_STAGING = {}
+_STAGING_LOCK = threading.Lock()
+
+
+def upload(device, values, dtype=torch.int32, out=None):
+    """Asynchronous host-to-device upload through the device's HostStaging."""
+    with _STAGING_LOCK:
+        staging = _STAGING.get(device)
+        if staging is None:
+            staging = _STAGING[device] = HostStaging(device)
+    return staging.upload(values, dtype, out)

@@ -61,7 +61,7 @@ def load():
 
 def call(name, *args):
     """Invoke an entry point and raise NativeError on a non-zero status."""
-    lib = load()
+    lib = _lib or load()
     rc = getattr(lib, name)(*args)
     if rc != 0:
         raise NativeError(f'{name}: {lib.dspark_last_error().decode(errors="replace")}')
@@ -70,9 +70,9 @@ def call(name, *args):
 
 def ptr(t):
     """Device address of a tensor (None -> NULL)."""
-    return None if t is None else ctypes.c_void_p(t.data_ptr())
+    return None if t is None else t.data_ptr()
 
 
 def stream_handle(device):
     import torch
-    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+    return torch.cuda.current_stream(device).cuda_stream

@@ -22,7 +22,7 @@ The context K/V of one draft layer may live in
 import torch
 
 from . import _native
-from ._device import Workspace, require_gfx950
+from ._device import Workspace, require_gfx950, upload
 from .kernels import HEAD_DIM, KV_HEADS, Q_HEADS, SCALE, _check_scale
 from .schedule import DEFAULT_CHUNK, chunk_items, upload_items
 
@@ -73,8 +73,7 @@ class DraftBatch:
         for b in blocks:
             cu_b.append(cu_b[-1] + len(b))
         self.cu_blocks_host = tuple(cu_b)
-        pinned = torch.tensor(lens + cu_b + [a for b in blocks for a in b], dtype=torch.int32).pin_memory()
-        meta = pinned.to(self.device, non_blocking=True)
+        meta = upload(self.device, lens + cu_b + [a for b in blocks for a in b])
         n = self.request_count
         self.ctx_len = meta[:n]
         self.cu_blocks = meta[n:2 * n + 1]
@@ -91,7 +90,7 @@ class DraftBatch:
             offs = list(self.context_offsets)
             if capacity:
                 offs = [o + (KV_HEADS - 1) * capacity * (o // capacity) for o in offs]
-            self._offsets[capacity] = torch.tensor(offs, dtype=torch.int64).pin_memory().to(self.device, non_blocking=True)
+            self._offsets[capacity] = upload(self.device, offs, torch.int64)
         return self._offsets[capacity]
 
     def work(self, chunk):
@@ -128,6 +127,8 @@ class HipDraftAttention:
             raise ValueError('Draft chunk must be a multiple of 64')
         self.chunk = int(chunk)
         self._workspace = Workspace(self.device)
+        self._geometry_for = None
+        self._geometry = None
 
     def _context_geometry(self, keys, batch):
         """(kernel offsets, token stride, head stride) for the pool form."""
@@ -166,7 +167,12 @@ class HipDraftAttention:
                 or context_values.device != self.device
                 or not context_keys.is_contiguous() or not context_values.is_contiguous()):
             raise ValueError('Context K/V must be matching contiguous bf16 tensors on the GPU')
-        offsets, tok_stride, head_stride = self._context_geometry(context_keys, batch)
+        # The batch is immutable: its pool bounds are checked once per pool shape.
+        key = (batch, context_keys.shape)
+        if self._geometry_for is None or self._geometry_for[0] is not batch or self._geometry_for[1] != key[1]:
+            self._geometry = self._context_geometry(context_keys, batch)
+            self._geometry_for = key
+        offsets, tok_stride, head_stride = self._geometry
         out = torch.empty_like(query)
         bound = max(batch.context_rows, 1)
         need = _native.load().dspark_attn_workspace_bytes(batch.request_count, bound, batch.max_blocks, self.chunk)

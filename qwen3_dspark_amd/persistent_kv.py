@@ -28,7 +28,7 @@ from typing import Mapping
 import torch
 
 from . import _native
-from ._device import require_gfx950
+from ._device import require_gfx950, upload
 from .kernels import HEAD_DIM, KV_HEADS, Q_HEADS, SCALE, _check_scale
 from .schedule import DEFAULT_CHUNK, chunk_bound, chunk_items
 
@@ -239,6 +239,17 @@ class PersistentTargetKV:
         self._external = None
         self._submission_generation = 0
         self._n_work = 0
+        # Committed-state generation: bumped by every mutation of slots or
+        # lengths; a transaction is valid only while it is unchanged, which
+        # replaces a per-call scan over the transaction's handles.
+        self._mutations = 0
+        self._tx_mutations = None
+        self._tx_shape = None
+        # Per-layer device addresses (the allocations never move).
+        lk, ls = self._keys[0].numel() * elem, self.scratch_keys[0].numel() * elem
+        self._layer_ptrs = tuple((self._keys.data_ptr() + l * lk, self._values.data_ptr() + l * lk,
+                                  self.scratch_keys.data_ptr() + l * ls, self.scratch_values.data_ptr() + l * ls)
+                                 for l in range(layers))
         self.failed = False
 
     def _geometry(self):
@@ -277,12 +288,14 @@ class PersistentTargetKV:
         self._owners[i], self._lengths[i] = request, 0
         handle = Slot(request, i, self._incarnations[i])
         self._handles[i] = handle
+        self._mutations += 1
         return handle
 
     def remove_request(self, handle):
         self._idle()
         i = self._slot(handle)
         self._owners[i], self._lengths[i], self._handles[i] = None, 0, None
+        self._mutations += 1
 
     def length(self, handle):
         return self._lengths[self._slot(handle)]
@@ -308,6 +321,7 @@ class PersistentTargetKV:
             self.keys[:, i, :n].copy_(keys)
             self.values[:, i, :n].copy_(values)
             self._lengths[i] = n
+            self._mutations += 1
         except Exception:
             self.failed = True
             raise
@@ -452,10 +466,8 @@ class PersistentTargetKV:
         items = chunk_items([c + q for c, q in zip(contexts, query_lengths)], self.chunk)
         if 2 * len(items) > ws.work.numel():
             raise ValueError('Work list exceeds the bucket workspace')
-        host = torch.tensor(list(indices) + list(contexts) + list(query_lengths) + [x for it in items for x in it],
-                            dtype=torch.int32).pin_memory()
-        ws.req[:3 * r].copy_(host[:3 * r], non_blocking=True)
-        ws.work[:2 * len(items)].copy_(host[3 * r:], non_blocking=True)
+        upload(self.device, list(indices) + list(contexts) + list(query_lengths), out=ws.req[:3 * r])
+        upload(self.device, [x for it in items for x in it], out=ws.work[:2 * len(items)])
         _native.call('dspark_txn_metadata', _native.ptr(ws.req), r, self.context_capacity,
                      bucket.key_capacity, bucket.query_tokens,
                      _native.ptr(ws.committed_indices), _native.ptr(ws.scratch_indices),
@@ -464,15 +476,17 @@ class PersistentTargetKV:
         self._sequence += 1
         tx = Transaction(self._sequence, handles, contexts, bucket, query_lengths)
         self._pending, self._staged, self._n_work = tx, set(), len(items)
+        self._tx_mutations = self._mutations
+        # (query tokens, launch maximum query length, bucket key capacity)
+        self._tx_shape = (sum(query_lengths), bucket.maximum_query_length, bucket.key_capacity)
         return tx
 
     def _transaction(self, tx):
         self._healthy()
         if tx is not self._pending:
             raise ValueError('Stale, copied or foreign transaction')
-        for h, c in zip(tx.slots, tx.context_lengths):
-            if self._lengths[self._slot(h)] != c:
-                raise RuntimeError('Committed state changed during verification')
+        if self._mutations != self._tx_mutations:
+            raise RuntimeError('Committed state changed during verification')
         return self._workspaces[tx.bucket]
 
     @torch.no_grad()
@@ -483,11 +497,11 @@ class PersistentTargetKV:
             raise ValueError('Cannot mix eager and registered external scratch writes')
         if type(layer) is not int or not 0 <= layer < self.layers or layer in self._staged:
             raise ValueError('Each model layer must stage exactly once')
-        q = sum(tx.query_lengths)
+        q = self._tx_shape[0]
         self._kv(keys, values, (q, self.heads, self.dim))
         keys, values = keys.contiguous(), values.contiguous()
-        _native.call('dspark_kv_stage', _native.ptr(keys), _native.ptr(values),
-                     _native.ptr(self.scratch_keys[layer]), _native.ptr(self.scratch_values[layer]),
+        _, _, sk, sv = self._layer_ptrs[layer]
+        _native.call('dspark_kv_stage', keys.data_ptr(), values.data_ptr(), sk, sv,
                      q, self.heads * self.dim * self._elem, _native.stream_handle(self.device))
         self._staged.add(layer)
 
@@ -519,21 +533,19 @@ class PersistentTargetKV:
             raise ValueError('Layer scratch missing')
         if (self.heads, self.dim, self.dtype) != (KV_HEADS, HEAD_DIM, torch.bfloat16):
             raise ValueError('Fused attention requires bf16 Hkv8/D128 storage')
-        q = sum(tx.query_lengths)
+        q, max_q, key_capacity = self._tx_shape
         if (not isinstance(query, torch.Tensor) or query.dtype != torch.bfloat16 or query.device != self.device
-                or tuple(query.shape) != (q, Q_HEADS, HEAD_DIM) or not query.is_contiguous() or query.requires_grad):
+                or query.shape != (q, Q_HEADS, HEAD_DIM) or not query.is_contiguous() or query.requires_grad):
             raise ValueError('Expected contiguous no-autograd bf16 [Q,16,128] queries on the store device')
         _check_scale(scale, 'Fused verification attention')
         out = torch.empty_like(query)
-        bucket = tx.bucket
         C = self.context_capacity
-        _native.call('dspark_verify_attn_fwd', _native.ptr(query),
-                     _native.ptr(self._keys[layer]), _native.ptr(self._values[layer]),
-                     _native.ptr(self.scratch_keys[layer]), _native.ptr(self.scratch_values[layer]),
-                     _native.ptr(ws.cu_query), _native.ptr(ws.cu_key), _native.ptr(ws.req),
+        k, v, sk, sv = self._layer_ptrs[layer]
+        _native.call('dspark_verify_attn_fwd', query.data_ptr(), k, v, sk, sv,
+                     ws.cu_query.data_ptr(), ws.cu_key.data_ptr(), ws.req.data_ptr(),
                      len(tx.slots), KV_HEADS * C * HEAD_DIM, HEAD_DIM, C * HEAD_DIM,
-                     bucket.key_capacity, bucket.maximum_query_length, float(SCALE), self.chunk,
-                     _native.ptr(ws.work), self._n_work, _native.ptr(out), _native.ptr(ws.attn), ws.attn.numel(),
+                     key_capacity, max_q, SCALE, self.chunk,
+                     ws.work.data_ptr(), self._n_work, out.data_ptr(), ws.attn.data_ptr(), ws.attn.numel(),
                      _native.stream_handle(self.device))
         return out
 
@@ -557,7 +569,7 @@ class PersistentTargetKV:
         r = len(tx.slots)
         try:
             if any(counts):
-                acc = torch.tensor(counts, dtype=torch.int32).pin_memory().to(self.device, non_blocking=True)
+                acc = upload(self.device, counts)
                 layer_b, slot_b, head_b, tok_b, piece_b = self._geometry()
                 _native.call('dspark_kv_commit', _native.ptr(self._keys), _native.ptr(self._values),
                              _native.ptr(self.scratch_keys), _native.ptr(self.scratch_values),
@@ -567,6 +579,7 @@ class PersistentTargetKV:
                              _native.stream_handle(self.device))
             for h, n in zip(tx.slots, counts):
                 self._lengths[h.index] += n
+            self._mutations += 1
         except Exception:
             self.failed = True
             raise

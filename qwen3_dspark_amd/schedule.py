@@ -5,7 +5,7 @@ short tail chunks of ragged requests fill the end of the grid (greedy
 longest-processing-time order); the partial-result slot of an item stays
 its request-major index, so the dispatch order does not affect results.
 """
-import torch
+from ._device import upload
 
 DEFAULT_CHUNK = 1024
 
@@ -29,6 +29,5 @@ def chunk_bound(n_req, rows_bound, chunk):
 
 
 def upload_items(items, device):
-    """int32 [n_items * 2] device tensor via a pinned staging copy."""
-    flat = [x for rc in items for x in rc]
-    return torch.tensor(flat, dtype=torch.int32).pin_memory().to(device, non_blocking=True)
+    """int32 [n_items * 2] device tensor via the pinned staging ring."""
+    return upload(device, [x for rc in items for x in rc])
