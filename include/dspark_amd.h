@@ -24,7 +24,7 @@ extern "C" {
 /* Thread-local message for the last failing call on this thread. */
 const char* dspark_last_error(void);
 
-/* ABI revision of this header (currently 1). */
+/* ABI revision of this header (currently 2). */
 int dspark_abi_version(void);
 
 /*
@@ -159,6 +159,38 @@ int dspark_kv_gather(const void* k_res_layer, const void* v_res_layer,
                      int64_t key_capacity, int64_t slots, int64_t slot_stride, int64_t head_stride,
                      int64_t tok_stride, int64_t ctx_capacity, int heads, int64_t piece_bytes,
                      int64_t scr_rows, void* k_out, void* v_out, void* stream);
+
+/*
+ * Packed varlen layout of PackedLayout.from_metadata
+ * (dspark_qwen/varlen_target.py:28-60), built on the device.
+ * Inputs: int64 query markers/positions [nq] and key markers/positions [nk].
+ * Requests are the runs of equal consecutive query markers (at most max_req,
+ * max_req <= 8192).  Outputs: cu_q/cu_k int32 [max_req+1] (first B+1 used),
+ * gather int64 [nk] (first sum-K used: every request's keys in physical
+ * order, requests in query order), and summary int64 [4 + 3*max_req]:
+ *   [0] 0 ok | 1 a request's queries are not one contiguous run |
+ *       2 keys are not the complete prefix 0..k-1 (or k < q) |
+ *       3 query positions are not k-q..k-1 | 4 more than max_req requests
+ *   [1] first failing request (query order; prefix checked before suffix)
+ *   [2] B, [3] sum K, [4+r] marker, [4+max_req+r] q_r, [4+2*max_req+r] k_r.
+ * The caller reads the summary once (the reference also synchronises) and
+ * raises the reference's ValueError for codes 1-3.
+ */
+int64_t dspark_layout_workspace_bytes(int64_t nq, int64_t nk, int max_req);
+int dspark_layout_build(const int64_t* query_requests, const int64_t* query_positions, int64_t nq,
+                        const int64_t* key_requests, const int64_t* key_positions, int64_t nk,
+                        int max_req, int32_t* cu_q, int32_t* cu_k, int64_t* gather,
+                        int64_t* summary, void* workspace, int64_t workspace_bytes, void* stream);
+
+/*
+ * PackedLayout.gather_kv (dspark_qwen/varlen_target.py:74-82): rows
+ * indices[0..n_rows) of a [heads, src_rows, piece] pool layer (byte strides
+ * head_stride, row_stride) into token-major [n_rows, heads, piece] outputs,
+ * K and V in one launch.  Indices outside [0, src_rows) produce zero rows.
+ */
+int dspark_pool_gather(const void* k_src, const void* v_src, int64_t src_rows, int64_t head_stride,
+                       int64_t row_stride, int heads, int64_t piece_bytes, const int64_t* indices,
+                       int64_t n_rows, void* k_dst, void* v_dst, void* stream);
 
 #ifdef __cplusplus
 }

@@ -31,9 +31,12 @@ SIGNATURES = {
     'dspark_kv_stage': (_I, [_P, _P, _P, _P, _L, _L, _P]),
     'dspark_kv_commit': (_I, [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _L, _L, _L, _L, _L, _I, _L, _L, _P]),
     'dspark_kv_gather': (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _L, _L, _L, _L, _L, _L, _I, _L, _L, _P, _P, _P]),
+    'dspark_layout_workspace_bytes': (_L, [_L, _L, _I]),
+    'dspark_layout_build': (_I, [_P, _P, _L, _P, _P, _L, _I, _P, _P, _P, _P, _P, _L, _P]),
+    'dspark_pool_gather': (_I, [_P, _P, _L, _L, _L, _I, _L, _P, _L, _P, _P, _P]),
 }
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 
 class NativeError(RuntimeError):

@@ -9,16 +9,16 @@ from dataclasses import dataclass
 
 import torch
 
+from . import _native
+from ._device import require_gfx950
+
 INT32_LIMIT = 2 ** 31
-
-
-def _cumulative(lengths, device):
-    ends = [0]
-    for n in lengths:
-        ends.append(ends[-1] + n)
-    if ends[-1] >= INT32_LIMIT:
-        raise ValueError('Varlen cumulative lengths exceed int32')
-    return torch.tensor(ends, device=device, dtype=torch.int32)
+MAX_LAYOUT_REQUESTS = 8192    # requests per layout built on the device
+_LAYOUT_ERRORS = {
+    1: 'Each request query must form one contiguous chunk',
+    2: 'Active keys must be a complete request-local prefix',
+    3: 'Queries must be the terminal suffix of their own key prefix',
+}
 
 
 @dataclass(frozen=True)
@@ -40,8 +40,11 @@ class PackedLayout:
         contiguous chunk; its keys (in physical order) are exactly positions
         0..k-1; its query positions are the terminal suffix k-q..k-1.
         gather_indices lists every request's keys in physical order, requests
-        in query order.  Validation runs on the tensors' device with a single
-        device-to-host transfer of the small per-request summary.
+        in query order.  Argument checks raise ValueError first, as in the
+        reference; the layout itself is derived and validated on the GPU by
+        dspark_layout_build, followed by one small device-to-host read of its
+        summary (the reference synchronises as well).  Metadata must live on
+        the gfx950 device: there is no CPU path.
         """
         arrays = (query_requests, query_positions, key_requests, key_positions)
         if any(not isinstance(x, torch.Tensor) or x.ndim != 1 or x.dtype != torch.long for x in arrays):
@@ -51,50 +54,29 @@ class PackedLayout:
         if (query_requests.numel() == 0 or query_requests.shape != query_positions.shape
                 or key_requests.shape != key_positions.shape):
             raise ValueError('Nonempty queries and matching marker/position lengths required')
-        dev = query_requests.device
-        nq = query_requests.numel()
-        nk = key_requests.numel()
-        # Runs of equal consecutive query markers are the requests.
-        starts = torch.ones(nq, dtype=torch.bool, device=dev)
-        starts[1:] = query_requests[1:] != query_requests[:-1]
-        seg_of_query = torch.cumsum(starts.to(torch.int64), 0) - 1
-        markers = query_requests[starts]
-        b = markers.numel()
-        q_counts = torch.bincount(seg_of_query, minlength=b)
-        sorted_markers, order = torch.sort(markers)
-        repeated = (sorted_markers[1:] == sorted_markers[:-1]).any().reshape(1).to(torch.long)
-        # Map every physical key to the request owning its marker (b = none).
-        slot = torch.searchsorted(sorted_markers, key_requests).clamp(max=b - 1)
-        hit = sorted_markers[slot] == key_requests
-        seg_of_key = torch.where(hit, order[slot], torch.full_like(slot, b))
-        k_counts = torch.bincount(seg_of_key, minlength=b + 1)[:b]
-        # Keys grouped by request in query order, physical order kept inside.
-        phys = torch.argsort(seg_of_key * (nk + 1) + torch.arange(nk, device=dev))
-        grouped_seg = seg_of_key[phys]
-        k_starts = torch.cat((torch.cumsum(k_counts, 0) - k_counts, k_counts.new_zeros(1)))
-        rank = torch.arange(nk, device=dev) - k_starts[grouped_seg]
-        wrong_pos = ((key_positions[phys] != rank) & (grouped_seg < b)).to(torch.long)
-        bad_prefix = torch.zeros(b + 1, dtype=torch.long, device=dev).index_add_(0, grouped_seg, wrong_pos)[:b]
-        bad_prefix = bad_prefix + (k_counts < q_counts).to(torch.long)
-        # Query positions must be k-q .. k-1 of their own request.
-        q_rank = torch.arange(nq, device=dev) - (torch.cumsum(q_counts, 0) - q_counts)[seg_of_query]
-        expected_q = (k_counts - q_counts)[seg_of_query] + q_rank
-        bad_suffix = torch.zeros(b, dtype=torch.long, device=dev).index_add_(
-            0, seg_of_query, (query_positions != expected_q).to(torch.long))
-        summary = torch.cat((repeated, markers, q_counts, k_counts, bad_prefix, bad_suffix)).tolist()
-        if summary[0]:
-            raise ValueError('Each request query must form one contiguous chunk')
-        host_markers = tuple(summary[1:1 + b])
-        q_lengths = tuple(summary[1 + b:1 + 2 * b])
-        k_lengths = tuple(summary[1 + 2 * b:1 + 3 * b])
-        for pre, suf in zip(summary[1 + 3 * b:1 + 4 * b], summary[1 + 4 * b:1 + 5 * b]):
-            if pre:
-                raise ValueError('Active keys must be a complete request-local prefix')
-            if suf:
-                raise ValueError('Queries must be the terminal suffix of their own key prefix')
-        gather = phys[:sum(k_lengths)]
-        return cls(host_markers, q_lengths, k_lengths,
-                   _cumulative(q_lengths, dev), _cumulative(k_lengths, dev), gather, nk)
+        dev = require_gfx950(query_requests.device)
+        nq, nk = query_requests.numel(), key_requests.numel()
+        if nq >= INT32_LIMIT or nk >= INT32_LIMIT:
+            raise ValueError('Varlen cumulative lengths exceed int32')
+        lib = _native.load()
+        m = min(nq, MAX_LAYOUT_REQUESTS)
+        ws = torch.empty(lib.dspark_layout_workspace_bytes(nq, nk, m), dtype=torch.uint8, device=dev)
+        cu = torch.empty(2, m + 1, dtype=torch.int32, device=dev)
+        gather = torch.empty(max(nk, 1), dtype=torch.long, device=dev)
+        summary = torch.empty(4 + 3 * m, dtype=torch.long, device=dev)
+        arrays = tuple(x.contiguous() for x in arrays)
+        _native.call('dspark_layout_build', arrays[0].data_ptr(), arrays[1].data_ptr(), nq,
+                     arrays[2].data_ptr(), arrays[3].data_ptr(), nk, m, cu[0].data_ptr(), cu[1].data_ptr(),
+                     gather.data_ptr(), summary.data_ptr(), ws.data_ptr(), ws.numel(),
+                     _native.stream_handle(dev))
+        host = summary.tolist()
+        error, b, total_k = host[0], host[2], host[3]
+        if error == 4:
+            raise ValueError(f'At most {MAX_LAYOUT_REQUESTS} requests per packed layout')
+        if error:
+            raise ValueError(_LAYOUT_ERRORS[error])
+        return cls(tuple(host[4:4 + b]), tuple(host[4 + m:4 + m + b]), tuple(host[4 + 2 * m:4 + 2 * m + b]),
+                   cu[0, :b + 1], cu[1, :b + 1], gather[:total_k], nk)
 
     @property
     def query_tokens(self):
@@ -109,13 +91,27 @@ class PackedLayout:
         return sum(q * k for q, k in zip(self.query_lengths, self.key_lengths))
 
     def gather_kv(self, key, value):
-        """[1,Hkv,physical_K,D] cache tensors -> packed [sum K, Hkv, D] (varlen_target.py:74-82)."""
+        """[1,Hkv,physical_K,D] cache tensors -> packed [sum K, Hkv, D]
+        (varlen_target.py:74-82), one dspark_pool_gather launch for K and V."""
         if (key.ndim != 4 or key.shape[0] != 1 or value.shape != key.shape
                 or key.shape[2] != self.physical_key_tokens or key.device != self.gather_indices.device
                 or value.device != key.device or value.dtype != key.dtype):
             raise ValueError('Expected matching [1,Hkv,physical_K,D] cache tensors')
-        return tuple(x.index_select(2, self.gather_indices).squeeze(0).transpose(0, 1).contiguous()
-                     for x in (key, value))
+        dev = require_gfx950(key.device)
+        _, heads, rows, dim = key.shape
+        elem = key.element_size()
+        if key.stride() != value.stride() or key.stride(3) != 1 or (dim * elem) % 16:
+            raise ValueError('gather_kv needs matching strides, contiguous rows and 16-byte head rows')
+        strides = (key.stride(1) * elem, key.stride(2) * elem)
+        if any(x % 16 for x in strides) or key.data_ptr() % 16 or value.data_ptr() % 16:
+            raise ValueError('gather_kv needs 16-byte aligned pool rows')
+        n = self.gather_indices.numel()
+        out_k = torch.empty((n, heads, dim), dtype=key.dtype, device=dev)
+        out_v = torch.empty_like(out_k)
+        _native.call('dspark_pool_gather', key.data_ptr(), value.data_ptr(), rows, strides[0], strides[1], heads,
+                     dim * elem, self.gather_indices.data_ptr(), n, out_k.data_ptr(), out_v.data_ptr(),
+                     _native.stream_handle(dev))
+        return out_k, out_v
 
 
 @dataclass(frozen=True)

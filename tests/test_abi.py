@@ -43,7 +43,8 @@ def test_workspace_size_formula():
 
 
 @pytest.mark.parametrize('name', ['dspark_varlen_attn_fwd', 'dspark_verify_attn_fwd', 'dspark_draft_attn_fwd',
-                                  'dspark_txn_metadata', 'dspark_kv_stage', 'dspark_kv_commit', 'dspark_kv_gather'])
+                                  'dspark_txn_metadata', 'dspark_kv_stage', 'dspark_kv_commit', 'dspark_kv_gather',
+                                  'dspark_layout_build', 'dspark_pool_gather'])
 def test_null_arguments_are_rejected_before_any_launch(name):
     lib = _native.load()
     fn = getattr(lib, name)
@@ -81,3 +82,11 @@ def test_invalid_sizes_are_rejected_before_any_launch():
     rc = lib.dspark_kv_commit(fake, fake, fake, fake, fake, fake, fake, 2, 7, 1, 1 << 20, 1 << 16, 1 << 12, 24, 16,
                               8, 256, 14, None)
     assert rc == -1 and '16 bytes' in lib.dspark_last_error().decode()
+    assert lib.dspark_layout_workspace_bytes(10, 10, 8193) == -1
+    assert lib.dspark_layout_workspace_bytes(0, 10, 1) == -1
+    rc = lib.dspark_layout_build(fake, fake, 4, fake, fake, 4, 9000, fake, fake, fake, fake, fake, 1 << 20, None)
+    assert rc == -1 and 'max_req' in lib.dspark_last_error().decode()
+    rc = lib.dspark_layout_build(fake, fake, 4, fake, fake, 4, 4, fake, fake, fake, fake, fake, 16, None)
+    assert rc == -1 and 'workspace too small' in lib.dspark_last_error().decode()
+    rc = lib.dspark_pool_gather(fake, fake, 8, 4096, 256, 8, 24, fake, 4, fake, fake, None)
+    assert rc == -1 and 'multiples of 16' in lib.dspark_last_error().decode()
