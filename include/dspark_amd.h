@@ -192,6 +192,27 @@ int dspark_pool_gather(const void* k_src, const void* v_src, int64_t src_rows, i
                        int64_t row_stride, int heads, int64_t piece_bytes, const int64_t* indices,
                        int64_t n_rows, void* k_dst, void* v_dst, void* stream);
 
+/*
+ * Draft context pool append (dspark_qwen/packed_draft.py:130-168
+ * append_committed: the cat of projected K/V onto the pool).  The pool is
+ * one tensor per K and V, [layers, slots, heads, capacity, piece] or any
+ * order expressed by the byte strides (as for dspark_kv_commit).  Per layer
+ * l, k_src[l]/v_src[l] (a host array of device pointers, layers <= 16) hold
+ * the new rows of all requests in chunk order, row i of head h at
+ * h*src_head_stride + i*src_row_stride bytes.  req = int32 [4][n_req]:
+ * slot, first position, first source row (ascending), row count.  Rows are
+ * written beyond the caller's committed lengths, so the append becomes
+ * visible only when the caller advances them.  nonfinite (optional, int32)
+ * is set to 1 if any appended element is Inf/NaN (elem_bytes 2 = bf16,
+ * 4 = fp32).
+ */
+int dspark_pool_append(void* k_pool, void* v_pool, int64_t layer_stride, int64_t slot_stride,
+                       int64_t head_stride, int64_t tok_stride, int64_t capacity, int heads,
+                       int64_t piece_bytes, int elem_bytes, int layers,
+                       const void* const* k_src, const void* const* v_src,
+                       int64_t src_head_stride, int64_t src_row_stride, int64_t src_rows,
+                       const int32_t* req, int n_req, int32_t* nonfinite, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

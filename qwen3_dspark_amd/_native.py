@@ -16,6 +16,7 @@ _P = ctypes.c_void_p
 _I = ctypes.c_int
 _L = ctypes.c_int64
 _F = ctypes.c_float
+_PP = ctypes.POINTER(ctypes.c_void_p)   # host array of device pointers
 
 # name -> (restype, argtypes); mirrors include/dspark_amd.h exactly.
 SIGNATURES = {
@@ -34,6 +35,7 @@ SIGNATURES = {
     'dspark_layout_workspace_bytes': (_L, [_L, _L, _I]),
     'dspark_layout_build': (_I, [_P, _P, _L, _P, _P, _L, _I, _P, _P, _P, _P, _P, _L, _P]),
     'dspark_pool_gather': (_I, [_P, _P, _L, _L, _L, _I, _L, _P, _L, _P, _P, _P]),
+    'dspark_pool_append': (_I, [_P, _P, _L, _L, _L, _L, _L, _I, _L, _I, _I, _PP, _PP, _L, _L, _L, _P, _I, _P, _P]),
 }
 
 ABI_VERSION = 2
@@ -69,6 +71,11 @@ def call(name, *args):
     if rc != 0:
         raise NativeError(f'{name}: {lib.dspark_last_error().decode(errors="replace")}')
     return rc
+
+
+def pointer_array(tensors):
+    """Host array of device pointers (for entry points taking one per layer)."""
+    return (ctypes.c_void_p * len(tensors))(*(t.data_ptr() for t in tensors))
 
 
 def ptr(t):

@@ -252,6 +252,69 @@ __global__ __launch_bounds__(256) void kv_gather_kernel(GatherArgs a) {
   a.v_out[i] = vx;
 }
 
+// Draft context pool append: new projected K/V rows of several requests
+// (source rows in chunk order, [heads, rows, piece] or [rows, heads, piece]
+// per layer through byte strides) into each request's slot at positions
+// start..start+count-1 of every layer, in one launch.  Rows land beyond the
+// pool's committed lengths, so nothing becomes visible until the host
+// advances the lengths; an optional flag reports any nonfinite element so
+// that the host can refuse the append without publishing it
+// (dspark_qwen/packed_draft.py:130-168 checks finiteness before the cat).
+constexpr int APPEND_MAX_LAYERS = 16;
+
+struct AppendArgs {
+  char* k_pool;
+  char* v_pool;
+  const char* k_src[APPEND_MAX_LAYERS];
+  const char* v_src[APPEND_MAX_LAYERS];
+  const int32_t* req;       // [4][B]: slot, start position, source row offset (ascending), count
+  int32_t* nonfinite;       // optional flag, set to 1 on any Inf/NaN
+  ResidentGeometry geo;
+  int64_t src_head_stride;  // bytes
+  int64_t src_row_stride;   // bytes
+  int64_t total;            // source rows * heads * piece_vecs
+  int n_req;
+  int elem_bytes;           // 2 (bf16) or 4 (fp32): finiteness test granularity
+};
+
+__device__ __forceinline__ bool vec_nonfinite(u32x4 x, int elem_bytes) {
+  bool bad = false;
+  #pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const unsigned w = x[i];
+    if (elem_bytes == 2) bad |= ((w & 0x7F80u) == 0x7F80u) || ((w & 0x7F800000u) == 0x7F800000u);
+    else bad |= (w & 0x7F800000u) == 0x7F800000u;
+  }
+  return bad;
+}
+
+// grid: (ceil(total / 256), layers)
+__global__ __launch_bounds__(256) void pool_append_kernel(AppendArgs a) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= a.total) return;
+  const int layer = blockIdx.y;
+  const int64_t row_vecs = (int64_t)a.geo.heads * a.geo.piece_vecs;
+  const int64_t row = i / row_vecs;
+  const int64_t within = i - row * row_vecs;
+  const int64_t h = within / a.geo.piece_vecs;
+  const int64_t v = within - h * a.geo.piece_vecs;
+  const int32_t* offs = a.req + 2 * a.n_req;
+  int lo = 0, hi = a.n_req - 1;   // last request whose source offset <= row
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (offs[mid] <= row) lo = mid; else hi = mid - 1;
+  }
+  const int64_t t = row - offs[lo];
+  if (t < 0 || t >= a.req[3 * a.n_req + lo]) return;
+  const int64_t slot = a.req[lo], pos = a.req[a.n_req + lo] + t;
+  const int64_t src = h * a.src_head_stride + row * a.src_row_stride + v * 16;
+  const u32x4 kx = *reinterpret_cast<const u32x4*>(a.k_src[layer] + src);
+  const u32x4 vx = *reinterpret_cast<const u32x4*>(a.v_src[layer] + src);
+  *resident_vec(a.k_pool, a.geo, layer, slot, h, pos, v) = kx;
+  *resident_vec(a.v_pool, a.geo, layer, slot, h, pos, v) = vx;
+  if (a.nonfinite && (vec_nonfinite(kx, a.elem_bytes) || vec_nonfinite(vx, a.elem_bytes))) atomicOr(a.nonfinite, 1);
+}
+
 }  // namespace dspark
 
 // ---------------------------------------------------------------------------
@@ -360,4 +423,45 @@ extern "C" int dspark_kv_gather(const void* k_res_layer, const void* v_res_layer
   DSPARK_REQUIRE(blocks <= 0x7fffffffLL, "key capacity too large");
   hipLaunchKernelGGL(kv_gather_kernel, dim3((unsigned)blocks), dim3(256), 0, static_cast<hipStream_t>(stream), a);
   return launch_status("kv_gather_kernel");
+}
+
+extern "C" int dspark_pool_append(void* k_pool, void* v_pool, int64_t layer_stride, int64_t slot_stride,
+                                  int64_t head_stride, int64_t tok_stride, int64_t capacity, int heads,
+                                  int64_t piece_bytes, int elem_bytes, int layers,
+                                  const void* const* k_src, const void* const* v_src,
+                                  int64_t src_head_stride, int64_t src_row_stride, int64_t src_rows,
+                                  const int32_t* req, int n_req, int32_t* nonfinite, void* stream) {
+  clear_error();
+  DSPARK_REQUIRE(k_pool && v_pool && k_src && v_src && req, "null pointer argument");
+  DSPARK_REQUIRE(layers >= 1 && layers <= APPEND_MAX_LAYERS, "layers must be in [1, %d]", APPEND_MAX_LAYERS);
+  DSPARK_REQUIRE(n_req >= 1 && src_rows >= 1, "sizes must be positive");
+  DSPARK_REQUIRE(elem_bytes == 2 || elem_bytes == 4, "element size must be 2 or 4 bytes");
+  DSPARK_REQUIRE(piece_bytes >= 16 && piece_bytes % 16 == 0, "piece bytes must be a positive multiple of 16");
+  DSPARK_REQUIRE(src_head_stride % 16 == 0 && src_row_stride % 16 == 0, "source strides must be multiples of 16 bytes");
+  DSPARK_REQUIRE(aligned16(k_pool) && aligned16(v_pool), "buffers must be 16-byte aligned");
+  AppendArgs a{};
+  for (int l = 0; l < layers; ++l) {
+    DSPARK_REQUIRE(k_src[l] && v_src[l], "null pointer argument");
+    DSPARK_REQUIRE(aligned16(k_src[l]) && aligned16(v_src[l]), "buffers must be 16-byte aligned");
+    a.k_src[l] = static_cast<const char*>(k_src[l]);
+    a.v_src[l] = static_cast<const char*>(v_src[l]);
+  }
+  ResidentGeometry geo{layer_stride, slot_stride, head_stride, tok_stride, capacity, heads, (int)(piece_bytes / 16)};
+  int rc = check_geometry(geo);
+  if (rc != OK) return rc;
+  a.k_pool = static_cast<char*>(k_pool);
+  a.v_pool = static_cast<char*>(v_pool);
+  a.req = req;
+  a.nonfinite = nonfinite;
+  a.geo = geo;
+  a.src_head_stride = src_head_stride;
+  a.src_row_stride = src_row_stride;
+  a.total = src_rows * heads * geo.piece_vecs;
+  a.n_req = n_req;
+  a.elem_bytes = elem_bytes;
+  const int64_t blocks = (a.total + 255) / 256;
+  DSPARK_REQUIRE(blocks <= 0x7fffffffLL, "append grid too large");
+  hipLaunchKernelGGL(pool_append_kernel, dim3((unsigned)blocks, layers), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), a);
+  return launch_status("pool_append_kernel");
 }

@@ -185,3 +185,184 @@ class HipDraftAttention:
                      batch.max_blocks, float(SCALE), self.chunk, _native.ptr(work), n_work,
                      _native.ptr(out), _native.ptr(ws), ws.numel(), _native.stream_handle(self.device))
         return out
+
+
+class DraftKVPool:
+    """Projected draft context per request: the cache state of PackedDraft
+    (dspark_qwen/packed_draft.py:63-185) without the model.
+
+    Storage: K and V are [layers, slots, 8, capacity, 128] head-major, one
+    contiguous run per (layer, slot, KV head), each request owning one slot.
+    Consequences against the reference's append-order pool [1, 8, N, 128]:
+      * append_projected writes the new rows in place (one launch for all
+        layers and requests); the reference concatenates the whole pool;
+      * crop / remove_request only change lengths; the reference compacts
+        every layer with a keep mask;
+      * draft attention streams each request's context as one linear run.
+    The projection that produces the rows (fc, context_norm, RoPE, k_proj,
+    k_norm, v_proj: packed_draft.py:147-158) stays with the caller.
+    Appends are transactional: rows land beyond the committed lengths and
+    become visible only when every check, including finiteness, passed.
+    """
+
+    def __init__(self, *, layers, slots, capacity, heads=KV_HEADS, dim=HEAD_DIM, dtype=torch.bfloat16,
+                 device='cuda', chunk=DEFAULT_CHUNK):
+        if any(type(n) is not int or n < 1 for n in (layers, slots, capacity, heads, dim)):
+            raise ValueError('All pool sizes must be positive integers')
+        if dtype not in (torch.bfloat16, torch.float32):
+            raise ValueError('Draft pool dtype must be bfloat16 or float32')
+        if layers > 16:
+            raise ValueError('At most 16 draft layers per pool')
+        self.device = require_gfx950(device)
+        _native.load()
+        self.layers, self.slot_capacity, self.capacity, self.heads, self.dim = layers, slots, capacity, heads, dim
+        self.dtype = dtype
+        self._elem = torch.empty((), dtype=dtype).element_size()
+        if (dim * self._elem) % 16:
+            raise ValueError('A KV head row must be a multiple of 16 bytes')
+        self.keys = torch.zeros((layers, slots, heads, capacity, dim), dtype=dtype, device=self.device)
+        self.values = torch.zeros_like(self.keys)
+        self._lengths = {}
+        self._slots = {}
+        self._free = list(range(slots))
+        self._attention = HipDraftAttention(self.device, chunk=chunk) if (heads, dim) == (KV_HEADS, HEAD_DIM) else None
+        self._flag = torch.zeros(1, dtype=torch.int32, device=self.device)
+        self.last_append_work = None
+
+    @property
+    def lengths(self):
+        return dict(self._lengths)
+
+    def slot(self, request):
+        self._request(request)
+        return self._slots[request]
+
+    def add_request(self, request):
+        if not isinstance(request, str) or not request or request in self._lengths:
+            raise ValueError('Require a fresh nonempty request name')
+        if not self._free:
+            raise ValueError('Draft pool slot capacity exhausted')
+        self._slots[request] = self._free.pop(0)
+        self._lengths[request] = 0
+
+    def _request(self, request):
+        if request not in self._lengths:
+            raise KeyError(request)
+
+    def validate_cache(self):
+        """Host state invariants (packed_draft.py:102-122 checks the same
+        prefix property on its append-order metadata)."""
+        if len(set(self._slots.values())) != len(self._slots) or set(self._slots) != set(self._lengths):
+            raise RuntimeError('Draft cache metadata length mismatch')
+        if any(not 0 <= n <= self.capacity for n in self._lengths.values()):
+            raise RuntimeError('Draft cache must be the complete request-local committed prefix')
+
+    def _source(self, t, rows):
+        """(head stride, row stride) in bytes of a [1, H, rows, D] or
+        [rows, H, D] tensor of new K or V rows."""
+        if not isinstance(t, torch.Tensor) or t.device != self.device:
+            raise ValueError('Projected K/V must be tensors on the pool device')
+        if t.dtype != self.dtype:
+            raise ValueError('Draft cache precision cannot change across appends')
+        e = self._elem
+        if t.ndim == 4 and tuple(t.shape) == (1, self.heads, rows, self.dim) and t.stride(3) == 1:
+            strides = (t.stride(1) * e, t.stride(2) * e)
+        elif t.ndim == 3 and tuple(t.shape) == (rows, self.heads, self.dim) and t.stride(2) == 1:
+            strides = (t.stride(1) * e, t.stride(0) * e)
+        else:
+            raise ValueError('Projected K/V must be [1, heads, rows, dim] or [rows, heads, dim]')
+        if any(x % 16 for x in strides) or t.data_ptr() % 16:
+            raise ValueError('Projected K/V rows must be 16-byte aligned')
+        return strides
+
+    @torch.no_grad()
+    def append_projected(self, chunks, projected, *, check_finite=True):
+        """Append committed context rows.  chunks: ordered {request: rows};
+        projected: per layer (keys, values) holding the rows of all chunks in
+        that order (what one projection over the concatenated features
+        yields, packed_draft.py:147-158).  With check_finite (the reference
+        always checks), one device read decides whether the append is
+        published; a nonfinite element raises and leaves the pool as it was."""
+        if not chunks:
+            raise ValueError('Require at least one committed feature chunk')
+        self.validate_cache()
+        order = list(chunks.items())
+        for request, n in order:
+            self._request(request)
+            if type(n) is not int or n < 1:
+                raise ValueError('Each committed chunk needs a positive row count')
+            if self._lengths[request] + n > self.capacity:
+                raise ValueError('Committed draft context exceeds the pool capacity')
+        rows = sum(n for _, n in order)
+        if len(projected) != self.layers:
+            raise ValueError('Draft cache layer count mismatch')
+        strides = None
+        for k, v in projected:
+            sk, sv = self._source(k, rows), self._source(v, rows)
+            if sk != sv or (strides is not None and sk != strides):
+                raise ValueError('Projected K/V must share one layout across layers')
+            strides = sk
+        req, offset = [[], [], [], []], 0
+        for request, n in order:
+            req[0].append(self._slots[request])
+            req[1].append(self._lengths[request])
+            req[2].append(offset)
+            req[3].append(n)
+            offset += n
+        dev_req = upload(self.device, [x for row in req for x in row])
+        if check_finite:
+            self._flag.zero_()
+        e, H, C, D = self._elem, self.heads, self.capacity, self.dim
+        _native.call('dspark_pool_append', self.keys.data_ptr(), self.values.data_ptr(),
+                     self.slot_capacity * H * C * D * e, H * C * D * e, C * D * e, D * e, C, H, D * e, e,
+                     self.layers, _native.pointer_array([k for k, _ in projected]),
+                     _native.pointer_array([v for _, v in projected]), strides[0], strides[1], rows,
+                     dev_req.data_ptr(), len(order), self._flag.data_ptr() if check_finite else None,
+                     _native.stream_handle(self.device))
+        if check_finite and int(self._flag.item()):
+            raise RuntimeError('Nonfinite projected draft context')
+        for request, n in order:
+            self._lengths[request] += n
+        self.last_append_work = dict(requests=len(order), new_context_tokens=rows, append_launches=1,
+                                     appended_kv_bytes=2 * self.layers * rows * H * D * e,
+                                     cache_concatenation_kv_bytes=0)
+        return self.last_append_work
+
+    def crop(self, request, length):
+        self._request(request)
+        if type(length) is not int or not 0 <= length <= self._lengths[request]:
+            raise ValueError('Invalid committed draft crop length')
+        self._lengths[request] = length
+
+    def remove_request(self, request):
+        self.crop(request, 0)
+        self._free.append(self._slots.pop(request))
+        del self._lengths[request]
+        self.validate_cache()
+
+    def request_kv(self, request):
+        """Per layer (keys, values) [1, heads, length, dim] copies of the
+        request's committed context (packed_draft.py:124-127)."""
+        i, n = self.slot(request), self._lengths[request]
+        return tuple((self.keys[l, i, :, :n][None].clone(), self.values[l, i, :, :n][None].clone())
+                     for l in range(self.layers))
+
+    def batch(self, anchors):
+        """DraftBatch over this pool for an ordered {request: anchors}
+        mapping (1..8 anchors in [0, length] each)."""
+        if not anchors:
+            raise ValueError('Require active anchor requests')
+        names = list(anchors)
+        for r in names:
+            self._request(r)
+        return DraftBatch(self.device, [self._slots[r] * self.capacity for r in names],
+                          [self._lengths[r] for r in names], [list(anchors[r]) for r in names])
+
+    def attention(self, layer, query, block_keys, block_values, batch, *, scale=SCALE):
+        """Multi-block draft attention of one layer over the pool."""
+        if self._attention is None:
+            raise ValueError('Draft attention requires the 8-head, 128-dim geometry')
+        if type(layer) is not int or not 0 <= layer < self.layers:
+            raise ValueError('Invalid draft layer')
+        return self._attention(query, block_keys, block_values, self.keys[layer], self.values[layer], batch,
+                               scale=scale)

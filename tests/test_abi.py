@@ -44,13 +44,13 @@ def test_workspace_size_formula():
 
 @pytest.mark.parametrize('name', ['dspark_varlen_attn_fwd', 'dspark_verify_attn_fwd', 'dspark_draft_attn_fwd',
                                   'dspark_txn_metadata', 'dspark_kv_stage', 'dspark_kv_commit', 'dspark_kv_gather',
-                                  'dspark_layout_build', 'dspark_pool_gather'])
+                                  'dspark_layout_build', 'dspark_pool_gather', 'dspark_pool_append'])
 def test_null_arguments_are_rejected_before_any_launch(name):
     lib = _native.load()
     fn = getattr(lib, name)
     args = []
     for t in fn.argtypes:
-        args.append(None if t is ctypes.c_void_p else 1)
+        args.append(None if t is ctypes.c_void_p or issubclass(t, ctypes._Pointer) else 1)
     rc = fn(*args)
     assert rc == -1
     assert 'null pointer' in lib.dspark_last_error().decode()
