@@ -213,6 +213,34 @@ int dspark_pool_append(void* k_pool, void* v_pool, int64_t layer_stride, int64_t
                        int64_t src_head_stride, int64_t src_row_stride, int64_t src_rows,
                        const int32_t* req, int n_req, int32_t* nonfinite, void* stream);
 
+/*
+ * Append-order KV cache of PackedTarget (dspark_qwen/packed_target.py:30-113):
+ * per layer K/V [1, H, N, piece] with rows in append order and int64
+ * key_requests / key_positions [N].
+ *
+ * dspark_crop_plan: the keep mask of crop (packed_target.py:99-108),
+ * keep = (request != marker) | (position < length), as a stable compaction:
+ * plan[j] = source row of kept row j, and the compacted markers/positions.
+ * The caller knows the kept count (N minus the cropped rows).
+ * Workspace: dspark_crop_plan_workspace_bytes(N).
+ */
+int64_t dspark_crop_plan_workspace_bytes(int64_t n);
+int dspark_crop_plan(const int64_t* key_requests, const int64_t* key_positions, int64_t n,
+                     int64_t marker, int64_t length, int64_t* plan, int64_t* out_requests,
+                     int64_t* out_positions, void* workspace, int64_t workspace_bytes, void* stream);
+
+/*
+ * Rebuild `tensors` (<= 64) row tensors [H, rows, piece] in one launch
+ * (src/add/dst: host arrays of device pointers).  With plan: output row j =
+ * src row plan[j] (crop / gather, n_out <= n_old).  Without: output rows are
+ * the n_old src rows then the n_add add rows (append: the reference's
+ * torch.cat along the row axis, packed_target.py:159-168 and
+ * packed_draft.py:159-161).
+ */
+int dspark_rows_rebuild(const void* const* src, const void* const* add, void* const* dst, int tensors,
+                        int heads, int64_t piece_bytes, int64_t n_old, int64_t n_add,
+                        const int64_t* plan, int64_t n_out, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

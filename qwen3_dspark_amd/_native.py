@@ -36,6 +36,9 @@ SIGNATURES = {
     'dspark_layout_build': (_I, [_P, _P, _L, _P, _P, _L, _I, _P, _P, _P, _P, _P, _L, _P]),
     'dspark_pool_gather': (_I, [_P, _P, _L, _L, _L, _I, _L, _P, _L, _P, _P, _P]),
     'dspark_pool_append': (_I, [_P, _P, _L, _L, _L, _L, _L, _I, _L, _I, _I, _PP, _PP, _L, _L, _L, _P, _I, _P, _P]),
+    'dspark_crop_plan_workspace_bytes': (_L, [_L]),
+    'dspark_crop_plan': (_I, [_P, _P, _L, _L, _L, _P, _P, _P, _P, _L, _P]),
+    'dspark_rows_rebuild': (_I, [_PP, _PP, _PP, _I, _I, _L, _L, _L, _P, _L, _P]),
 }
 
 ABI_VERSION = 2
@@ -74,8 +77,9 @@ def call(name, *args):
 
 
 def pointer_array(tensors):
-    """Host array of device pointers (for entry points taking one per layer)."""
-    return (ctypes.c_void_p * len(tensors))(*(t.data_ptr() for t in tensors))
+    """Host array of device pointers (for entry points taking one per layer);
+    None entries become NULL."""
+    return (ctypes.c_void_p * len(tensors))(*(None if t is None else t.data_ptr() for t in tensors))
 
 
 def ptr(t):

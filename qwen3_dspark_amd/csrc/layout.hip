@@ -423,3 +423,196 @@ extern "C" int dspark_pool_gather(const void* k_src, const void* v_src, int64_t 
   hipLaunchKernelGGL(pool_gather_kernel, dim3(grid, 2), dim3(256), 0, static_cast<hipStream_t>(stream), g);
   return launch_status("dspark_pool_gather");
 }
+
+// ---------------------------------------------------------------------------
+// Append-order KV cache of PackedTarget / VarlenPackedTarget
+// (dspark_qwen/packed_target.py:30-113): per layer K and V [1, H, N, piece]
+// with physical rows in append order (requests interleaved) and int64
+// key_requests / key_positions [N].
+//
+//   crop_plan    : keep = (request != marker) | (position < length)
+//                  (packed_target.py:99-108) as a stable compaction: the
+//                  source row of every kept output row, and the compacted
+//                  markers/positions.  Tile counts, a one-workgroup scan of
+//                  the tile totals, then a per-tile scan that scatters.
+//   rows_rebuild : every layer's K and V rebuilt in one launch, output row j
+//                  taken from plan[j] (crop) or, without a plan, from the old
+//                  rows then the appended rows (append: the reference's cat).
+// ---------------------------------------------------------------------------
+namespace dspark {
+
+constexpr int PLAN_TILE = 4096;            // rows per tile (256 threads x 16)
+constexpr int REBUILD_MAX_LAYERS = 64;
+
+struct CropPlanArgs {
+  const int64_t* kr;
+  const int64_t* kp;
+  int64_t n;
+  int64_t marker;
+  int64_t length;
+  int32_t* tile_kept;     // [tiles] kept rows per tile, then exclusive offsets
+  int64_t* plan;          // [n_kept] source row of each kept row
+  int64_t* out_kr;        // [n_kept]
+  int64_t* out_kp;        // [n_kept]
+  int64_t tiles;
+};
+
+__device__ __forceinline__ bool crop_keeps(const CropPlanArgs& a, int64_t i) {
+  return a.kr[i] != a.marker || a.kp[i] < a.length;
+}
+
+__global__ __launch_bounds__(256) void crop_count_kernel(CropPlanArgs a) {
+  __shared__ int s_sum;
+  if (threadIdx.x == 0) s_sum = 0;
+  __syncthreads();
+  const int64_t base = (int64_t)blockIdx.x * PLAN_TILE;
+  int kept = 0;
+  for (int k = threadIdx.x; k < PLAN_TILE; k += 256) {
+    const int64_t i = base + k;
+    if (i < a.n && crop_keeps(a, i)) ++kept;
+  }
+  atomicAdd(&s_sum, kept);
+  __syncthreads();
+  if (threadIdx.x == 0) a.tile_kept[blockIdx.x] = s_sum;
+}
+
+// One workgroup: exclusive scan of the tile totals in place.
+__global__ __launch_bounds__(LAYOUT_THREADS) void crop_scan_kernel(CropPlanArgs a) {
+  __shared__ int s_tmp[40];
+  int running = 0;
+  for (int64_t base = 0; base < a.tiles; base += LAYOUT_THREADS) {
+    const int64_t t = base + threadIdx.x;
+    const int v = t < a.tiles ? a.tile_kept[t] : 0;
+    const int incl = block_inclusive_scan_1024(v, s_tmp);
+    const int total = s_tmp[32];
+    if (t < a.tiles) a.tile_kept[t] = running + incl - v;
+    running += total;
+    __syncthreads();
+  }
+}
+
+// Per tile: rows in order, 16 consecutive rows per thread, block scan of the
+// per-thread counts; kept rows scatter to their output slot.
+__global__ __launch_bounds__(256) void crop_scatter_kernel(CropPlanArgs a) {
+  __shared__ int s_tmp[256];
+  const int64_t base = (int64_t)blockIdx.x * PLAN_TILE + (int64_t)threadIdx.x * 16;
+  int kept = 0;
+  for (int k = 0; k < 16; ++k) {
+    const int64_t i = base + k;
+    if (i < a.n && crop_keeps(a, i)) ++kept;
+  }
+  s_tmp[threadIdx.x] = kept;
+  __syncthreads();
+  for (int off = 1; off < 256; off <<= 1) {   // Hillis-Steele inclusive scan
+    const int v = threadIdx.x >= off ? s_tmp[threadIdx.x - off] : 0;
+    __syncthreads();
+    s_tmp[threadIdx.x] += v;
+    __syncthreads();
+  }
+  int64_t out = a.tile_kept[blockIdx.x] + s_tmp[threadIdx.x] - kept;
+  for (int k = 0; k < 16; ++k) {
+    const int64_t i = base + k;
+    if (i < a.n && crop_keeps(a, i)) {
+      a.plan[out] = i;
+      a.out_kr[out] = a.kr[i];
+      a.out_kp[out] = a.kp[i];
+      ++out;
+    }
+  }
+}
+
+struct RebuildArgs {
+  const char* src[REBUILD_MAX_LAYERS];     // per (layer, K|V): old rows [H, n_old, piece]
+  const char* add[REBUILD_MAX_LAYERS];     // appended rows [H, n_add, piece] (append only)
+  char* dst[REBUILD_MAX_LAYERS];           // new rows [H, n_out, piece]
+  const int64_t* plan;                     // crop: source row per output row; null for append
+  int64_t n_old;
+  int64_t n_add;
+  int64_t n_out;
+  int64_t piece_vecs;
+  int heads;
+};
+
+// grid: (ceil(n_out * heads * piece_vecs / 256), tensors)
+__global__ __launch_bounds__(256) void rows_rebuild_kernel(RebuildArgs a) {
+  typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int64_t per_head = a.n_out * a.piece_vecs;
+  if (i >= per_head * a.heads) return;
+  const int t = blockIdx.y;
+  const int64_t h = i / per_head;
+  const int64_t rem = i - h * per_head;
+  const int64_t row = rem / a.piece_vecs;
+  const int64_t e = rem - row * a.piece_vecs;
+  const u32x4_t* from;
+  if (a.plan) {
+    from = reinterpret_cast<const u32x4_t*>(a.src[t]) + (h * a.n_old + a.plan[row]) * a.piece_vecs + e;
+  } else if (row < a.n_old) {
+    from = reinterpret_cast<const u32x4_t*>(a.src[t]) + (h * a.n_old + row) * a.piece_vecs + e;
+  } else {
+    from = reinterpret_cast<const u32x4_t*>(a.add[t]) + (h * a.n_add + row - a.n_old) * a.piece_vecs + e;
+  }
+  reinterpret_cast<u32x4_t*>(a.dst[t])[i] = *from;
+}
+
+}  // namespace dspark
+
+extern "C" int64_t dspark_crop_plan_workspace_bytes(int64_t n) {
+  if (n < 0) return -1;
+  return 4 * std::max<int64_t>((n + PLAN_TILE - 1) / PLAN_TILE, 1);
+}
+
+extern "C" int dspark_crop_plan(const int64_t* key_requests, const int64_t* key_positions, int64_t n,
+                                int64_t marker, int64_t length, int64_t* plan, int64_t* out_requests,
+                                int64_t* out_positions, void* workspace, int64_t workspace_bytes, void* stream) {
+  clear_error();
+  DSPARK_REQUIRE(n >= 0 && n < (int64_t(1) << 40), "dspark_crop_plan: invalid row count");
+  if (n == 0) return OK;
+  DSPARK_REQUIRE(key_requests && key_positions && plan && out_requests && out_positions && workspace,
+                 "dspark_crop_plan: null pointer");
+  DSPARK_REQUIRE(workspace_bytes >= dspark_crop_plan_workspace_bytes(n), "dspark_crop_plan: workspace too small");
+  CropPlanArgs a{key_requests, key_positions, n, marker, length, static_cast<int32_t*>(workspace),
+                 plan, out_requests, out_positions, (n + PLAN_TILE - 1) / PLAN_TILE};
+  DSPARK_REQUIRE(a.tiles <= 0x7fffffffLL, "dspark_crop_plan: too many rows");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  hipLaunchKernelGGL(crop_count_kernel, dim3((unsigned)a.tiles), dim3(256), 0, s, a);
+  hipLaunchKernelGGL(crop_scan_kernel, dim3(1), dim3(LAYOUT_THREADS), 0, s, a);
+  hipLaunchKernelGGL(crop_scatter_kernel, dim3((unsigned)a.tiles), dim3(256), 0, s, a);
+  return launch_status("dspark_crop_plan");
+}
+
+extern "C" int dspark_rows_rebuild(const void* const* src, const void* const* add, void* const* dst, int tensors,
+                                   int heads, int64_t piece_bytes, int64_t n_old, int64_t n_add,
+                                   const int64_t* plan, int64_t n_out, void* stream) {
+  clear_error();
+  DSPARK_REQUIRE(src && dst, "dspark_rows_rebuild: null pointer");
+  DSPARK_REQUIRE(tensors >= 1 && tensors <= REBUILD_MAX_LAYERS, "dspark_rows_rebuild: tensors must be in [1, %d]",
+                 REBUILD_MAX_LAYERS);
+  DSPARK_REQUIRE(heads >= 1 && n_old >= 0 && n_add >= 0 && n_out >= 0, "dspark_rows_rebuild: invalid sizes");
+  DSPARK_REQUIRE(piece_bytes >= 16 && piece_bytes % 16 == 0, "dspark_rows_rebuild: piece bytes must be a multiple of 16");
+  DSPARK_REQUIRE(plan ? n_out <= n_old : n_out == n_old + n_add,
+                 "dspark_rows_rebuild: output rows must be n_old + n_add (append) or <= n_old (crop)");
+  if (n_out == 0) return OK;
+  DSPARK_REQUIRE(plan || n_add == 0 || add, "dspark_rows_rebuild: null pointer");
+  RebuildArgs a{};
+  for (int t = 0; t < tensors; ++t) {
+    DSPARK_REQUIRE(dst[t] && (n_old == 0 || src[t]) && (plan || n_add == 0 || add[t]),
+                   "dspark_rows_rebuild: null pointer");
+    DSPARK_REQUIRE(((uintptr_t)dst[t] | (uintptr_t)(src[t]) | (uintptr_t)(add ? add[t] : nullptr)) % 16 == 0,
+                   "dspark_rows_rebuild: pointers must be 16-byte aligned");
+    a.src[t] = static_cast<const char*>(src[t]);
+    a.add[t] = add ? static_cast<const char*>(add[t]) : nullptr;
+    a.dst[t] = static_cast<char*>(dst[t]);
+  }
+  a.plan = plan;
+  a.n_old = n_old;
+  a.n_add = n_add;
+  a.n_out = n_out;
+  a.piece_vecs = piece_bytes / 16;
+  a.heads = heads;
+  const int64_t blocks = (n_out * heads * a.piece_vecs + 255) / 256;
+  DSPARK_REQUIRE(blocks <= 0x7fffffffLL, "dspark_rows_rebuild: grid too large");
+  hipLaunchKernelGGL(rows_rebuild_kernel, dim3((unsigned)blocks, tensors), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), a);
+  return launch_status("dspark_rows_rebuild");
+}
