@@ -42,10 +42,20 @@ int64_t dspark_attn_workspace_bytes(int n_req, int64_t key_rows_bound, int row_t
  * Work lists.  Every attention entry point splits request r's keys into
  * ceil(len_r / chunk) chunks (at least one) and runs one workgroup per
  * (chunk, KV head).  With work == NULL the chunks are dispatched in request
- * order over a grid sized from the row bound; otherwise work = int32
- * [n_work][2] lists (request, chunk) pairs - every chunk exactly once - in
- * the order they should be dispatched (longest first balances ragged
- * lengths).  The list is not validated on the device.
+ * order over a grid sized from the row bound.  Otherwise work holds
+ * int32 [n_work][8] item records - every chunk exactly once, in dispatch
+ * order (longest first balances ragged lengths) - followed by int32
+ * [n_req][4] request records, so that a workgroup reads one record instead
+ * of walking the cumulative arrays:
+ *   varlen/verify item: request, chunk, chunk base (sum of the chunk counts
+ *     of earlier requests), first query row, query length, key length,
+ *     first key row (varlen) or resident slot (verify), chunk count;
+ *   draft item: request, chunk, chunk base, context length, first block,
+ *     block count, largest anchor, chunk count;
+ *   request: chunk base, chunk count, first query row (varlen/verify) or
+ *     first block (draft), query length or block count.
+ * The records must agree with the cumulative arrays; they are not
+ * validated on the device.
  *
  * Packed varlen attention, bottom-right causal (causal=1) or noncausal.
  * q [q_rows,16,128], k/v [k_rows,8,128], cu_q/cu_k int32 [n_req+1].

@@ -35,23 +35,30 @@
 // more than one chunk writes FP32 partial (max, sum, unnormalised O) triples
 // that merge_kernel combines; the kernel boundary makes them visible without
 // any per-workgroup cache flush.
+#include <type_traits>
+
 #include "common.h"
 
 namespace dspark {
 
 constexpr int KT = 32;                 // keys per wave iteration
+constexpr int WORK_INTS = 8;           // int32 per work record
+constexpr int REQ_INTS = 4;            // int32 per request record (merge)
 constexpr int ROWB = HD * 2;           // bytes per LDS K/V row (256)
 constexpr int OPITCH = HD + 4;         // floats per row in the merge buffer
 
-// XOR swizzle of the 16-byte chunk index of LDS row k (rows are 256 B).
-// Conflict-free for the three access patterns on a K/V tile:
-//  - row writes: 8 lanes write chunks 0..7 (or 8..15) of one row;
-//  - transpose reads (V^T): a 16-lane group reads 4 rows r=0..3, chunks
-//    2nb and 2nb+1; swz's bits 2:1 = r keep the 8 (row, chunk) pairs apart;
-//  - K fragment reads: 8 lanes read rows 8q+4j+e (q<2, e<4), one chunk;
-//    (k&3, (k>>3)&1) takes all 8 values.
+// XOR swizzle of the 16-byte chunk index of LDS row k (rows are 256 B,
+// i.e. 16 chunks spanning all banks).  Conflict-free for the three access
+// patterns on a K/V tile:
+//  - row writes (registers or direct loads): 16 lanes write the 16 chunks
+//    of one row, any per-row XOR keeps them distinct;
+//  - transpose reads (V^T): a 16-lane group reads rows 8grp+r (r<4), chunks
+//    2nb and 2nb+1; swz = 4r + grp moves the 4 rows to distinct chunk
+//    pairs;
+//  - K fragment reads (draft, from LDS): 16 lanes read rows 8q+4j+e (q<4,
+//    e<4), one chunk; (k&3, (k>>3)&3) takes all 16 values.
 __device__ __forceinline__ int swz(int k) {
-  return ((k & 3) << 1) | ((k >> 3) & 1);
+  return ((k & 3) << 2) | ((k >> 3) & 3);
 }
 
 __device__ __forceinline__ int lds_chunk_off(int k, int chunk16) {
@@ -108,21 +115,39 @@ __device__ __forceinline__ void row_init(RowState& st) {
   for (int nb = 0; nb < 8; ++nb) st.o[nb] = f32x4{0.f, 0.f, 0.f, 0.f};
 }
 
+// The running maximum only moves up when a tile's maximum exceeds it by more
+// than RESCALE_SLACK (log2 units), so O and l are rescaled rarely (once per
+// row for typical score distributions) instead of every tile.  Exact for
+// any reference value: O and l always share the same reference max, which
+// the split-K merges carry along; probabilities stay <= 2^RESCALE_SLACK,
+// far from FP32/bf16 overflow.  The rescale branch is wave-uniform.
+constexpr float RESCALE_SLACK = 8.0f;
+
+template <bool MASKED>
 __device__ __forceinline__ bf16x8 softmax_update(RowState& st, const f32x4& s0, const f32x4& s1,
                                                  int kbase, int vis, float scale_log2) {
   float x[8];
   #pragma unroll
   for (int e = 0; e < 4; ++e) {
-    x[e] = (kbase + e < vis) ? s0[e] * scale_log2 : -INFINITY;
-    x[4 + e] = (kbase + 4 + e < vis) ? s1[e] * scale_log2 : -INFINITY;
+    x[e] = s0[e] * scale_log2;
+    x[4 + e] = s1[e] * scale_log2;
+    if (MASKED) {
+      if (kbase + e >= vis) x[e] = -INFINITY;
+      if (kbase + 4 + e >= vis) x[4 + e] = -INFINITY;
+    }
   }
-  float mx = x[0];
-  #pragma unroll
-  for (int i = 1; i < 8; ++i) mx = fmaxf(mx, x[i]);
+  float mx = fmaxf(fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3])), fmaxf(fmaxf(x[4], x[5]), fmaxf(x[6], x[7])));
   mx = wave_max_across_groups(mx);
-  const float m_new = fmaxf(st.m, mx);
-  const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
-  const float alpha = fast_exp2(st.m - m_use);
+  const bool raise = mx > st.m + RESCALE_SLACK;
+  if (__builtin_amdgcn_ballot_w64(raise)) {
+    const float m_new = raise ? mx : st.m;
+    const float alpha = fast_exp2(st.m - m_new);
+    st.l *= alpha;
+    #pragma unroll
+    for (int nb = 0; nb < 8; ++nb) st.o[nb] *= alpha;
+    st.m = m_new;
+  }
+  const float m_use = (st.m == -INFINITY) ? 0.f : st.m;
   bf16x8 pb;
   float ps = 0.f;
   #pragma unroll
@@ -131,10 +156,7 @@ __device__ __forceinline__ bf16x8 softmax_update(RowState& st, const f32x4& s0, 
     ps += p;
     pb[i] = (bf16)p;
   }
-  st.l = st.l * alpha + ps;
-  st.m = m_new;
-  #pragma unroll
-  for (int nb = 0; nb < 8; ++nb) st.o[nb] *= alpha;
+  st.l += ps;
   return pb;
 }
 
@@ -165,24 +187,45 @@ template <int ND>
 __device__ __forceinline__ void merge_partials(const float* __restrict__ part_o, const float* __restrict__ part_ml,
                                                size_t p0, size_t pstride, int nch, int row, int d0,
                                                float (&acc)[ND], float& L) {
+  // One pass in groups of four chunks: every load of a group is issued
+  // before any use, then the (max, sum, O) triples are folded in with the
+  // online-softmax rule.  Chunks with no visible key (max = -inf) add
+  // nothing.
   float M = -INFINITY;
-  for (int c = 0; c < nch; ++c) M = fmaxf(M, part_ml[((p0 + c * pstride) * 16 + row) * 2]);
   L = 0.f;
   #pragma unroll
   for (int i = 0; i < ND; ++i) acc[i] = 0.f;
-  for (int c = 0; c < nch; ++c) {
-    const size_t p = p0 + c * pstride;
-    const float mc = part_ml[(p * 16 + row) * 2];
-    const float sc = (mc == -INFINITY) ? 0.f : fast_exp2(mc - M);
-    L += sc * part_ml[(p * 16 + row) * 2 + 1];
-    const float* po = part_o + (p * 16 + row) * HD + d0;
+  for (int c0 = 0; c0 < nch; c0 += 4) {
+    float mc[4], lc[4];
+    f32x4 x[4][ND / 4];
     #pragma unroll
-    for (int i = 0; i < ND; i += 4) {
-      const f32x4 x = *reinterpret_cast<const f32x4*>(po + i);
-      acc[i] += sc * x[0];
-      acc[i + 1] += sc * x[1];
-      acc[i + 2] += sc * x[2];
-      acc[i + 3] += sc * x[3];
+    for (int u = 0; u < 4; ++u) {
+      const size_t p = p0 + (size_t)min(c0 + u, nch - 1) * pstride;
+      mc[u] = part_ml[(p * 16 + row) * 2];
+      lc[u] = part_ml[(p * 16 + row) * 2 + 1];
+      const float* po = part_o + (p * 16 + row) * HD + d0;
+      #pragma unroll
+      for (int i = 0; i < ND / 4; ++i) x[u][i] = *reinterpret_cast<const f32x4*>(po + 4 * i);
+    }
+    #pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      if (c0 + u >= nch || mc[u] == -INFINITY) continue;
+      if (mc[u] > M) {
+        const float sc = fast_exp2(M - mc[u]);
+        L *= sc;
+        #pragma unroll
+        for (int i = 0; i < ND; ++i) acc[i] *= sc;
+        M = mc[u];
+      }
+      const float w = fast_exp2(mc[u] - M);
+      L += w * lc[u];
+      #pragma unroll
+      for (int i = 0; i < ND / 4; ++i) {
+        acc[4 * i] += w * x[u][i][0];
+        acc[4 * i + 1] += w * x[u][i][1];
+        acc[4 * i + 2] += w * x[u][i][2];
+        acc[4 * i + 3] += w * x[u][i][3];
+      }
     }
   }
 }
@@ -223,6 +266,7 @@ struct VarlenArgs {
   float* part_o;          // [n_cl*8*tmax][16][128]
   float* part_ml;         // [n_cl*8*tmax][16][2]
   int n_req;
+  int n_slots;            // (item, KV head) slots: 8 * items
   int causal;
   int chunk;
   int tmax;
@@ -232,34 +276,43 @@ struct VarlenArgs {
 constexpr int VARLEN_SMEM = 4 * 16 * OPITCH * 4 + 4 * 16 * 2 * 4;   // 34304 B (>= 4*32*256)
 static_assert(VARLEN_SMEM >= 4 * KT * ROWB, "merge buffer must cover the V tiles");
 
+// One (chunk item, KV head, row tile) of varlen / verify attention.  Every
+// early return is uniform across the workgroup.
 template <bool VERIFY>
-__global__ __launch_bounds__(256) void varlen_attn_kernel(VarlenArgs a) {
-  __shared__ __attribute__((aligned(16))) unsigned char smem[VARLEN_SMEM];
+__device__ __forceinline__ void varlen_item(const VarlenArgs& a, unsigned char* smem, int idx, int t) {
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int col = lane & 15;
   const int grp = lane >> 4;
-  const int g = blockIdx.x & 7;
-  const int cl = blockIdx.x >> 3;
-  const int t = blockIdx.y;
+  const int g = idx & 7;
+  const int cl = idx >> 3;
 
-  int r, first, c;
+  // Work record (one scalar load): request, chunk, chunk base, query start
+  // and length, key length, key start (varlen) or resident slot (verify),
+  // chunk count.  Without a list the grid walks the chunks in request order.
+  int r, first, c, q0, ql, kl, start, nch;
   if (a.work) {
-    r = a.work[2 * cl];
-    c = a.work[2 * cl + 1];
-    first = chunk_base(a.cu_k, nullptr, r, a.chunk);
+    const int32_t* w = a.work + WORK_INTS * cl;
+    r = w[0];
+    c = w[1];
+    first = w[2];
+    q0 = w[3];
+    ql = w[4];
+    kl = w[5];
+    start = w[6];
+    nch = w[7];
   } else {
     locate_chunk(a.cu_k, nullptr, a.n_req, a.chunk, cl, r, first);
     if (r < 0) return;
     c = cl - first;
+    q0 = a.cu_q[r];
+    ql = a.cu_q[r + 1] - q0;
+    kl = a.cu_k[r + 1] - a.cu_k[r];
+    start = VERIFY ? a.slots[r] : a.cu_k[r];
+    nch = chunks_for(kl, a.chunk);
   }
   const int item = first + c;   // partial slot (request-major chunk numbering)
-  const int q0 = a.cu_q[r];
-  const int ql = a.cu_q[r + 1] - q0;
   if (8 * t >= ql) return;
-  const int kbeg = a.cu_k[r];
-  const int kl = a.cu_k[r + 1] - kbeg;
-  const int nch = chunks_for(kl, a.chunk);
   const int k0 = c * a.chunk;
   const int k1 = min(k0 + a.chunk, kl);
 
@@ -271,7 +324,7 @@ __global__ __launch_bounds__(256) void varlen_attn_kernel(VarlenArgs a) {
   int a_len;
   if (VERIFY) {
     a_len = kl - ql;
-    const size_t abase = (size_t)a.slots[r] * (size_t)a.slot_stride + (size_t)g * a.a_head_stride;
+    const size_t abase = (size_t)start * (size_t)a.slot_stride + (size_t)g * a.a_head_stride;
     kA = a.k_a + abase;
     vA = a.v_a + abase;
     const size_t bbase = (size_t)q0 * KV_ROW + (size_t)g * HD;
@@ -279,7 +332,7 @@ __global__ __launch_bounds__(256) void varlen_attn_kernel(VarlenArgs a) {
     vB = a.v_b + bbase;
   } else {
     a_len = kl;
-    const size_t abase = (size_t)kbeg * KV_ROW + (size_t)g * HD;
+    const size_t abase = (size_t)start * KV_ROW + (size_t)g * HD;
     kA = a.k_a + abase;
     vA = a.v_a + abase;
     kB = kA;
@@ -333,8 +386,9 @@ __global__ __launch_bounds__(256) void varlen_attn_kernel(VarlenArgs a) {
     #pragma unroll
     for (int i2 = 0; i2 < 8; ++i2) T.v[i2] = ld8(vrow(kt + 4 * i2 + grp) + 8 * col);
   };
-  auto compute_tile = [&](int kt, Tile& T) {
-    if (kt + KT > kend) {
+  auto compute_tile = [&](int kt, Tile& T, auto masked) {
+    constexpr bool MASKED = decltype(masked)::value;
+    if (MASKED && kt + KT > kend) {
       #pragma unroll
       for (int i2 = 0; i2 < 8; ++i2)
         if (kt + 4 * i2 + grp >= kend) T.v[i2] = zero8();
@@ -344,7 +398,7 @@ __global__ __launch_bounds__(256) void varlen_attn_kernel(VarlenArgs a) {
     #pragma unroll
     for (int i2 = 0; i2 < 8; ++i2)
       *reinterpret_cast<bf16x8*>(vs + lds_chunk_off(4 * i2 + grp, col)) = T.v[i2];
-    const bf16x8 pb = softmax_update(st, s0, s1, kt + 8 * grp, vis, a.scale_log2);
+    const bf16x8 pb = softmax_update<MASKED>(st, s0, s1, kt + 8 * grp, vis, a.scale_log2);
     wave_lds_sync();
     bf16x8 vt[8];
     #pragma unroll
@@ -353,10 +407,37 @@ __global__ __launch_bounds__(256) void varlen_attn_kernel(VarlenArgs a) {
     wave_lds_sync();
   };
 
-  for (int kt = k0 + KT * wave; kt < kend; kt += KT * 4) {
+  // Keys below kfast come from segment A and are visible to every row of
+  // this tile (bottom-right causal: row tok sees keys <= kl - ql + tok), so
+  // their tiles need no clamping, source selection or masking.  The tile
+  // base is wave-uniform; each lane adds loop-invariant 32-bit offsets.
+  const int kfast = min(min(kend, a_len), a.causal ? kl - ql + 8 * t + 1 : kl);
+  const int wave_u = __builtin_amdgcn_readfirstlane(wave);
+  int kt = k0 + KT * wave_u;
+  {
+    const int64_t ts = a.a_tok_stride;
+    uint32_t koff[2], voff[8];
+    #pragma unroll
+    for (int j = 0; j < 2; ++j) koff[j] = (uint32_t)(((8 * (col >> 2) + 4 * j + (col & 3)) * ts + 8 * grp) * 2);
+    #pragma unroll
+    for (int i2 = 0; i2 < 8; ++i2) voff[i2] = (uint32_t)(((4 * i2 + grp) * ts + 8 * col) * 2);
+    for (; kt + KT <= kfast; kt += KT * 4) {
+      const char* kb = reinterpret_cast<const char*>(kA + (size_t)kt * ts);
+      const char* vb = reinterpret_cast<const char*>(vA + (size_t)kt * ts);
+      Tile T;
+      #pragma unroll
+      for (int j = 0; j < 2; ++j)
+        #pragma unroll
+        for (int ks = 0; ks < 4; ++ks) T.k[j][ks] = *reinterpret_cast<const bf16x8*>(kb + koff[j] + 64 * ks);
+      #pragma unroll
+      for (int i2 = 0; i2 < 8; ++i2) T.v[i2] = *reinterpret_cast<const bf16x8*>(vb + voff[i2]);
+      compute_tile(kt, T, std::false_type{});
+    }
+  }
+  for (; kt < kend; kt += KT * 4) {
     Tile T;
     load_tile(kt, T);
-    compute_tile(kt, T);
+    compute_tile(kt, T, std::true_type{});
   }
 
   st.l = wave_sum_across_groups(st.l);
@@ -410,6 +491,18 @@ __global__ __launch_bounds__(256) void varlen_attn_kernel(VarlenArgs a) {
     #pragma unroll
     for (int i = 0; i < 8; ++i) ov[i] = (bf16)(acc[i] / L);
     *reinterpret_cast<bf16x8*>(orow) = ov;
+  }
+}
+
+// Persistent grid: each workgroup walks (item, KV head) slots with a stride
+// of the grid size, so per-workgroup start-up is paid once per CU slot
+// rather than once per chunk.
+template <bool VERIFY>
+__global__ __launch_bounds__(256) void varlen_attn_kernel(VarlenArgs a) {
+  __shared__ __attribute__((aligned(16))) unsigned char smem[VARLEN_SMEM];
+  for (int idx = blockIdx.x; idx < a.n_slots; idx += gridDim.x) {
+    varlen_item<VERIFY>(a, smem, idx, blockIdx.y);
+    __syncthreads();   // the next item reuses the LDS tiles and merge buffer
   }
 }
 
@@ -475,25 +568,33 @@ __global__ __launch_bounds__(512) void draft_attn_kernel(DraftArgs a) {
   const int g = blockIdx.x & 7;
   const int cl = blockIdx.x >> 3;
 
-  int r, first, c;
+  // Work record (one scalar load): request, chunk, chunk base, context
+  // length, first block, block count, largest anchor, chunk count.
+  int r, first, c, ctx, b0, nb, amax, nch;
   if (a.work) {
-    r = a.work[2 * cl];
-    c = a.work[2 * cl + 1];
-    first = chunk_base(nullptr, a.ctx_len, r, a.chunk);
+    const int32_t* w = a.work + WORK_INTS * cl;
+    r = w[0];
+    c = w[1];
+    first = w[2];
+    ctx = w[3];
+    b0 = w[4];
+    nb = w[5];
+    amax = w[6];
+    nch = w[7];
   } else {
     locate_chunk(nullptr, a.ctx_len, a.n_req, a.chunk, cl, r, first);
     if (r < 0) return;
     c = cl - first;
+    ctx = a.ctx_len[r];
+    nch = chunks_for(ctx, a.chunk);
+    b0 = a.cu_b[r];
+    nb = a.cu_b[r + 1] - b0;
+    amax = 0;
+    for (int b = 0; b < nb; ++b) amax = max(amax, a.anchors[b0 + b]);
   }
   const int item = first + c;
-  const int ctx = a.ctx_len[r];
-  const int nch = chunks_for(ctx, a.chunk);
   const int k0 = c * a.chunk;
   const int k1 = min(k0 + a.chunk, ctx);
-  const int b0 = a.cu_b[r];
-  const int nb = a.cu_b[r + 1] - b0;
-  int amax = 0;
-  for (int b = 0; b < nb; ++b) amax = max(amax, a.anchors[b0 + b]);
   const int kend = min(k1, amax);
 
   // This wave's block (if any): rows = 7 tokens x the 2 query heads of KV head g.
@@ -540,6 +641,35 @@ __global__ __launch_bounds__(512) void draft_attn_kernel(DraftArgs a) {
       lds_dma16(src, __builtin_amdgcn_readfirstlane(dst));
     }
   };
+  // Keys below this wave's anchor (and the chunk's end) need no mask; the
+  // test is uniform across the wave.
+  const int full_lim = min(tile_anchor, kend);
+  auto compute_sub = [&](const unsigned char* kt_lds, const unsigned char* vt_lds, int h, int kt, auto masked) {
+    constexpr bool MASKED = decltype(masked)::value;
+    bf16x8 kf[2][4];
+    #pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int k = KT * h + 8 * (col >> 2) + 4 * j + (col & 3);
+      #pragma unroll
+      for (int ks = 0; ks < 4; ++ks)
+        kf[j][ks] = *reinterpret_cast<const bf16x8*>(kt_lds + lds_chunk_off(k, 4 * ks + grp));
+    }
+    f32x4 s0, s1;
+    qk_tile(kf, qf, s0, s1);
+    const bf16x8 pb = softmax_update<MASKED>(st, s0, s1, kt + 8 * grp, vis, a.scale_log2);
+    bf16x8 vt[8];
+    #pragma unroll
+    for (int nbk = 0; nbk < 8; ++nbk) vt[nbk] = lds_vt(vt_lds + KT * h * ROWB, nbk, lane);
+    if (MASKED && kt + KT > kend) {
+      // rows past kend hold clamped copies; their weights are 0, keep V finite-safe
+      #pragma unroll
+      for (int nbk = 0; nbk < 8; ++nbk)
+        #pragma unroll
+        for (int e = 0; e < 8; ++e)
+          if (kt + 8 * grp + e >= kend) vt[nbk][e] = (bf16)0.0f;
+    }
+    pv_update(st, pb, vt);
+  };
   auto compute = [&](int step) {
     const unsigned char* kt_lds = smem + (step % DSTAGES) * DSTAGE_BYTES;
     const unsigned char* vt_lds = kt_lds + DSTEP * ROWB;
@@ -547,32 +677,10 @@ __global__ __launch_bounds__(512) void draft_attn_kernel(DraftArgs a) {
     for (int h = 0; h < 2; ++h) {
       const int kt = k0 + step * DSTEP + KT * h;
       if (tile_anchor <= kt) continue;
-      bf16x8 kf[2][4];
-      #pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        const int k = KT * h + 8 * (col >> 2) + 4 * j + (col & 3);
-        #pragma unroll
-        for (int ks = 0; ks < 4; ++ks)
-          kf[j][ks] = *reinterpret_cast<const bf16x8*>(kt_lds + lds_chunk_off(k, 4 * ks + grp));
-      }
-      f32x4 s0, s1;
-      qk_tile(kf, qf, s0, s1);
-      const bf16x8 pb = softmax_update(st, s0, s1, kt + 8 * grp, vis, a.scale_log2);
-      bf16x8 vt[8];
-      #pragma unroll
-      for (int nbk = 0; nbk < 8; ++nbk) vt[nbk] = lds_vt(vt_lds + KT * h * ROWB, nbk, lane);
-      if (kt + KT > kend) {
-        // rows past kend hold clamped copies; their weights are 0, keep V finite-safe
-        #pragma unroll
-        for (int nbk = 0; nbk < 8; ++nbk)
-          #pragma unroll
-          for (int e = 0; e < 8; ++e)
-            if (kt + 8 * grp + e >= kend) vt[nbk][e] = (bf16)0.0f;
-      }
-      pv_update(st, pb, vt);
+      if (kt + KT <= full_lim) compute_sub(kt_lds, vt_lds, h, kt, std::false_type{});
+      else compute_sub(kt_lds, vt_lds, h, kt, std::true_type{});
     }
   };
-
   const int n_steps = kend > k0 ? (kend - k0 + DSTEP - 1) / DSTEP : 0;
   if (n_steps > 0) {
     // Every thread issues exactly 4 loads per stage (stages past the end
@@ -610,7 +718,7 @@ __global__ __launch_bounds__(512) void draft_attn_kernel(DraftArgs a) {
     }
     f32x4 s0, s1;
     qk_tile(kf, qf, s0, s1);
-    const bf16x8 pb = softmax_update(st, s0, s1, 8 * grp, row_ok ? BLOCK_ROWS : 0, a.scale_log2);
+    const bf16x8 pb = softmax_update<true>(st, s0, s1, 8 * grp, row_ok ? BLOCK_ROWS : 0, a.scale_log2);
     wave_lds_sync();
     bf16x8 vt[8];
     #pragma unroll
@@ -653,6 +761,7 @@ __global__ __launch_bounds__(512) void draft_attn_kernel(DraftArgs a) {
 // split-K merge: one workgroup per (request, KV head, tile) with >1 chunk
 // ---------------------------------------------------------------------------
 struct MergeArgs {
+  const int32_t* req;      // optional [B][4]: chunk base, chunk count, first output row / block, rows / blocks
   const int32_t* cu_q;     // varlen/verify
   const int32_t* cu_k;     // varlen/verify chunk counts
   const int32_t* ctx_len;  // draft chunk counts
@@ -671,6 +780,34 @@ __global__ __launch_bounds__(256) void merge_kernel(MergeArgs a) {
   const int g = blockIdx.y;
   const int t = blockIdx.z;
   int len, out_row0, rows_valid;
+  if (a.req) {
+    const int32_t* m = a.req + REQ_INTS * r;
+    const int nch = m[1];
+    if (nch == 1) return;
+    int row0, valid;
+    if (a.draft) {
+      if (t >= m[3]) return;
+      row0 = BLOCK_ROWS * (m[2] + t);
+      valid = BLOCK_ROWS;
+    } else {
+      if (8 * t >= m[3]) return;
+      row0 = m[2] + 8 * t;
+      valid = min(8, m[3] - 8 * t);
+    }
+    const int tid = threadIdx.x;
+    const int row = tid >> 4;
+    const int d0 = (tid & 15) * 8;
+    if ((row >> 1) >= valid) return;
+    float acc[8];
+    float L;
+    merge_partials<8>(a.part_o, a.part_ml, (size_t)(m[0] * 8 + g) * a.tmax + t, (size_t)8 * a.tmax, nch, row, d0,
+                      acc, L);
+    bf16x8 ov;
+    #pragma unroll
+    for (int i = 0; i < 8; ++i) ov[i] = (bf16)(acc[i] / L);
+    *reinterpret_cast<bf16x8*>(a.out + (size_t)(row0 + (row >> 1)) * Q_ROW + (size_t)(2 * g + (row & 1)) * HD + d0) = ov;
+    return;
+  }
   if (a.draft) {
     const int b0 = a.cu_b[r];
     if (t >= a.cu_b[r + 1] - b0) return;
@@ -711,6 +848,19 @@ namespace {
 using namespace dspark;
 
 constexpr float LOG2E = 1.4426950408889634f;
+
+// Workgroups resident at once for the varlen/verify kernel (2 per CU at its
+// register budget), times the number of row tiles sharing the machine.
+unsigned persistent_grid(int n_slots, int tiles) {
+  static int cus = 0;
+  if (!cus) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+      cus = 256;
+  }
+  const int64_t resident = std::max<int64_t>(8, (int64_t)cus * 2 / std::max(tiles, 1) / 8 * 8);
+  return (unsigned)std::min<int64_t>(n_slots, resident);
+}
 
 int64_t n_chunk_items(int n_req, int64_t rows_bound, int chunk) {
   return (rows_bound + chunk - 1) / chunk + n_req;
@@ -790,11 +940,12 @@ extern "C" int dspark_varlen_attn_fwd(const void* q, const void* k, const void* 
   a.tmax = tiles;
   a.scale_log2 = scale * LOG2E;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  const int64_t grid = work ? (int64_t)n_work * HKV : n_cl * HKV;
-  hipLaunchKernelGGL(varlen_attn_kernel<false>, dim3((unsigned)grid, tiles), dim3(256), 0, s, a);
+  a.n_slots = (int)(work ? (int64_t)n_work * HKV : n_cl * HKV);
+  hipLaunchKernelGGL(varlen_attn_kernel<false>, dim3(persistent_grid(a.n_slots, tiles), tiles), dim3(256), 0, s, a);
   rc = launch_status("varlen_attn_kernel");
   if (rc != OK) return rc;
-  MergeArgs m{cu_q, cu_k, nullptr, nullptr, a.part_o, a.part_ml, a.out, n_req, chunk, tiles, 0};
+  MergeArgs m{work ? work + WORK_INTS * n_work : nullptr, cu_q, cu_k, nullptr, nullptr, a.part_o, a.part_ml, a.out,
+              n_req, chunk, tiles, 0};
   return launch_merge(m, n_req, tiles, s);
 }
 
@@ -840,11 +991,12 @@ extern "C" int dspark_verify_attn_fwd(const void* q, const void* k_res, const vo
   a.tmax = tiles;
   a.scale_log2 = scale * LOG2E;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  const int64_t grid = work ? (int64_t)n_work * HKV : n_cl * HKV;
-  hipLaunchKernelGGL(varlen_attn_kernel<true>, dim3((unsigned)grid, tiles), dim3(256), 0, s, a);
+  a.n_slots = (int)(work ? (int64_t)n_work * HKV : n_cl * HKV);
+  hipLaunchKernelGGL(varlen_attn_kernel<true>, dim3(persistent_grid(a.n_slots, tiles), tiles), dim3(256), 0, s, a);
   rc = launch_status("verify_attn_kernel");
   if (rc != OK) return rc;
-  MergeArgs m{cu_q, cu_k, nullptr, nullptr, a.part_o, a.part_ml, a.out, n_req, chunk, tiles, 0};
+  MergeArgs m{work ? work + WORK_INTS * n_work : nullptr, cu_q, cu_k, nullptr, nullptr, a.part_o, a.part_ml, a.out,
+              n_req, chunk, tiles, 0};
   return launch_merge(m, n_req, tiles, s);
 }
 
@@ -899,6 +1051,7 @@ extern "C" int dspark_draft_attn_fwd(const void* q, const void* k_ctx, const voi
     hipLaunchKernelGGL(draft_attn_kernel<false>, dim3((unsigned)grid), dim3(DWAVES * WAVE), 0, s, a);
   rc = launch_status("draft_attn_kernel");
   if (rc != OK) return rc;
-  MergeArgs m{nullptr, nullptr, ctx_len, cu_blocks, a.part_o, a.part_ml, a.out, n_req, chunk, max_blocks, 1};
+  MergeArgs m{work ? work + WORK_INTS * n_work : nullptr, nullptr, nullptr, ctx_len, cu_blocks, a.part_o, a.part_ml,
+              a.out, n_req, chunk, max_blocks, 1};
   return launch_merge(m, n_req, max_blocks, s);
 }

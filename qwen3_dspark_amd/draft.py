@@ -24,7 +24,7 @@ import torch
 from . import _native
 from ._device import Workspace, require_gfx950, upload
 from .kernels import HEAD_DIM, KV_HEADS, Q_HEADS, SCALE, _check_scale
-from .schedule import DEFAULT_CHUNK, chunk_items, upload_items
+from .schedule import DEFAULT_CHUNK, draft_work, upload_work
 
 BLOCK_SIZE = 7
 MAX_BLOCKS = 8
@@ -95,8 +95,9 @@ class DraftBatch:
 
     def work(self, chunk):
         if chunk not in self._work:
-            items = chunk_items(self.context_lengths, chunk)
-            self._work[chunk] = (upload_items(items, self.device), len(items))
+            records, n_items = draft_work(self.context_lengths, self.cu_blocks_host,
+                                          [a for b in self.anchors for a in b], chunk)
+            self._work[chunk] = (upload_work(records, self.device), n_items)
         return self._work[chunk]
 
     def index_max(self):

@@ -16,7 +16,7 @@ import torch
 
 from . import _native
 from ._device import Workspace, require_gfx950
-from .schedule import DEFAULT_CHUNK, chunk_items, upload_items
+from .schedule import DEFAULT_CHUNK, upload_work, varlen_work
 
 Q_HEADS, KV_HEADS, HEAD_DIM = 16, 8, 128
 SCALE = 128 ** -0.5
@@ -90,11 +90,16 @@ class HipVarlenKernel:
         self._validated_layout, self._layout_versions = layout, versions
 
     def _work_list(self, layout):
-        # One longest-first item list per layout object (its lengths are
+        # One longest-first record list per layout shape (its lengths are
         # immutable host tuples), uploaded once and reused by every layer.
-        key = (id(layout), layout.key_lengths, self.chunk)
+        key = (layout.query_lengths, layout.key_lengths, self.chunk)
         if self._work_for != key:
-            self._work = upload_items(chunk_items(layout.key_lengths, self.chunk), self.device)
+            starts, acc = [], 0
+            for k in layout.key_lengths:
+                starts.append(acc)
+                acc += k
+            records, n_items = varlen_work(layout.query_lengths, layout.key_lengths, starts, self.chunk)
+            self._work = (upload_work(records, self.device), n_items)
             self._work_for = key
         return self._work
 
@@ -104,11 +109,11 @@ class HipVarlenKernel:
         tiles = (max_q + 7) // 8
         need = _native.load().dspark_attn_workspace_bytes(n_req, key_rows, tiles, self.chunk)
         ws = self._workspace.get(need)
-        work = self._work_list(layout)
+        work, n_work = self._work_list(layout) or (None, 0)
         _native.call('dspark_varlen_attn_fwd', _native.ptr(query), _native.ptr(key), _native.ptr(value),
                      _native.ptr(layout.cu_query), _native.ptr(layout.cu_key), n_req, query.shape[0], key_rows,
                      max_q, int(self.causal), float(SCALE), self.chunk, _native.ptr(work),
-                     0 if work is None else work.numel() // 2,
+                     n_work,
                      _native.ptr(out), _native.ptr(ws), ws.numel(), _native.stream_handle(self.device))
         return out
 

@@ -30,7 +30,7 @@ import torch
 from . import _native
 from ._device import require_gfx950, upload
 from .kernels import HEAD_DIM, KV_HEADS, Q_HEADS, SCALE, _check_scale
-from .schedule import DEFAULT_CHUNK, chunk_bound, chunk_items
+from .schedule import DEFAULT_CHUNK, REQ_INTS, WORK_INTS, chunk_bound, varlen_work
 
 
 @dataclass(frozen=True)
@@ -173,7 +173,7 @@ class _Workspace:
         self.cu_key = torch.zeros_like(self.cu_query)
         self.positions = torch.zeros(q, dtype=torch.long, device=device)
         self.req = torch.zeros(3 * r, dtype=torch.int32, device=device)
-        self.work = torch.zeros(2 * chunk_bound(r, n, chunk), dtype=torch.int32, device=device)
+        self.work = torch.zeros(WORK_INTS * chunk_bound(r, n, chunk) + REQ_INTS * r, dtype=torch.int32, device=device)
         self.keys = torch.empty((n, heads, dim), dtype=dtype, device=device)
         self.values = torch.empty_like(self.keys)
         self.attn = torch.zeros(_attn_workspace_bytes(bucket, chunk), dtype=torch.uint8, device=device)
@@ -463,11 +463,12 @@ class PersistentTargetKV:
             raise ValueError('Varlen cumulative lengths exceed int32')
         ws = self._workspaces[bucket]
         r = len(handles)
-        items = chunk_items([c + q for c, q in zip(contexts, query_lengths)], self.chunk)
-        if 2 * len(items) > ws.work.numel():
+        records, n_items = varlen_work(query_lengths, [c + q for c, q in zip(contexts, query_lengths)], indices,
+                                       self.chunk)
+        if len(records) > ws.work.numel():
             raise ValueError('Work list exceeds the bucket workspace')
         upload(self.device, list(indices) + list(contexts) + list(query_lengths), out=ws.req[:3 * r])
-        upload(self.device, [x for it in items for x in it], out=ws.work[:2 * len(items)])
+        upload(self.device, records, out=ws.work[:len(records)])
         _native.call('dspark_txn_metadata', _native.ptr(ws.req), r, self.context_capacity,
                      bucket.key_capacity, bucket.query_tokens,
                      _native.ptr(ws.committed_indices), _native.ptr(ws.scratch_indices),
@@ -475,7 +476,7 @@ class PersistentTargetKV:
                      _native.ptr(ws.cu_query), _native.ptr(ws.cu_key), _native.stream_handle(self.device))
         self._sequence += 1
         tx = Transaction(self._sequence, handles, contexts, bucket, query_lengths)
-        self._pending, self._staged, self._n_work = tx, set(), len(items)
+        self._pending, self._staged, self._n_work = tx, set(), n_items
         self._tx_mutations = self._mutations
         # (query tokens, launch maximum query length, bucket key capacity)
         self._tx_shape = (sum(query_lengths), bucket.maximum_query_length, bucket.key_capacity)
