@@ -96,6 +96,23 @@ int dspark_verify_attn_fwd(const void* q, const void* k_res, const void* v_res,
                            void* workspace, int64_t workspace_bytes, void* stream);
 
 /*
+ * dspark_verify_attn_fwd with the layer's staging fused in: the new rows are
+ * read from k_new/v_new ([q_rows, 8, 128], the model's projected K/V) and
+ * copied into k_scr/v_scr by the workgroups that read them, replacing the
+ * separate dspark_kv_stage launch of stage_layer
+ * (dspark_qwen/persistent_target_kv.py:427-438).  Scratch contents after the
+ * call equal those after dspark_kv_stage; outputs are bit-identical to the
+ * unfused pair.  k_new/v_new must not alias the scratch.
+ */
+int dspark_verify_attn_staged_fwd(const void* q, const void* k_res, const void* v_res,
+                                  const void* k_new, const void* v_new, void* k_scr, void* v_scr,
+                                  const int32_t* cu_q, const int32_t* cu_k, const int32_t* slots,
+                                  int n_req, int64_t slot_stride, int64_t tok_stride, int64_t head_stride,
+                                  int64_t key_rows_bound, int max_q, float scale, int chunk,
+                                  const int32_t* work, int n_work, void* out,
+                                  void* workspace, int64_t workspace_bytes, void* stream);
+
+/*
  * Multi-block DSpark draft attention.  Request r owns blocks
  * cu_blocks[r]..cu_blocks[r+1] (1..8 blocks), each 7 query rows; block b
  * sees context positions j < anchors[b] of its request plus its own 7 rows

@@ -261,7 +261,9 @@ struct VarlenArgs {
   int64_t slot_stride;    // verify: elements between resident slots
   int64_t a_tok_stride;   // segment A elements between token rows
   int64_t a_head_stride;  // segment A elements between KV heads
-  const int32_t* work;    // optional [n_items][2] (request, chunk) dispatch order
+  const int32_t* work;    // optional work records (see the C ABI)
+  bf16* stage_k;          // verify with staging: scratch written from segment B (k_b/v_b = new rows)
+  bf16* stage_v;
   bf16* out;              // [nq, 16, 128]
   float* part_o;          // [n_cl*8*tmax][16][128]
   float* part_ml;         // [n_cl*8*tmax][16][2]
@@ -330,6 +332,17 @@ __device__ __forceinline__ void varlen_item(const VarlenArgs& a, unsigned char* 
     const size_t bbase = (size_t)q0 * KV_ROW + (size_t)g * HD;
     kB = a.k_b + bbase;
     vB = a.v_b + bbase;
+    if (a.stage_k && c == nch - 1 && t == 0) {
+      // Fused stage: this workgroup is the only reader of the request's new
+      // rows for KV head g, so it also copies them into the scratch layer.
+      for (int i = threadIdx.x; i < 2 * ql * 16; i += 256) {
+        const int which = i / (ql * 16);
+        const int rem = i - which * ql * 16;
+        const size_t off = bbase + (size_t)(rem >> 4) * KV_ROW + (size_t)(rem & 15) * 8;
+        *reinterpret_cast<bf16x8*>((which ? a.stage_v : a.stage_k) + off) =
+            *reinterpret_cast<const bf16x8*>((which ? a.v_b : a.k_b) + off);
+      }
+    }
   } else {
     a_len = kl;
     const size_t abase = (size_t)start * KV_ROW + (size_t)g * HD;
@@ -949,16 +962,16 @@ extern "C" int dspark_varlen_attn_fwd(const void* q, const void* k, const void* 
   return launch_merge(m, n_req, tiles, s);
 }
 
-extern "C" int dspark_verify_attn_fwd(const void* q, const void* k_res, const void* v_res,
-                                      const void* k_scr, const void* v_scr,
-                                      const int32_t* cu_q, const int32_t* cu_k, const int32_t* slots,
-                                      int n_req, int64_t slot_stride, int64_t tok_stride, int64_t head_stride,
-                                      int64_t key_rows_bound, int max_q, float scale, int chunk,
-                                      const int32_t* work, int n_work, void* out, void* workspace,
-                                      int64_t workspace_bytes_, void* stream) {
-  clear_error();
-  DSPARK_REQUIRE(q && k_res && v_res && k_scr && v_scr && cu_q && cu_k && slots && out, "null pointer argument");
-  DSPARK_REQUIRE(aligned16(q) && aligned16(k_res) && aligned16(v_res) && aligned16(k_scr) && aligned16(v_scr) && aligned16(out),
+namespace {
+int verify_launch(const void* q, const void* k_res, const void* v_res, const void* k_b, const void* v_b,
+                  void* stage_k, void* stage_v, const int32_t* cu_q, const int32_t* cu_k, const int32_t* slots,
+                  int n_req, int64_t slot_stride, int64_t tok_stride, int64_t head_stride,
+                  int64_t key_rows_bound, int max_q, float scale, int chunk,
+                  const int32_t* work, int n_work, void* out, void* workspace,
+                  int64_t workspace_bytes_, void* stream) {
+  DSPARK_REQUIRE(q && k_res && v_res && k_b && v_b && cu_q && cu_k && slots && out, "null pointer argument");
+  DSPARK_REQUIRE(aligned16(q) && aligned16(k_res) && aligned16(v_res) && aligned16(k_b) && aligned16(v_b) && aligned16(out) &&
+                 aligned16(stage_k) && aligned16(stage_v),
                  "Q/K/V/out must be 16-byte aligned");
   DSPARK_REQUIRE(slot_stride >= 0 && tok_stride >= HD && tok_stride % 8 == 0 && head_stride >= HD && head_stride % 8 == 0,
                  "resident strides must be multiples of 8 elements (token/head strides >= 128)");
@@ -973,8 +986,10 @@ extern "C" int dspark_verify_attn_fwd(const void* q, const void* k_res, const vo
   a.q = static_cast<const bf16*>(q);
   a.k_a = static_cast<const bf16*>(k_res);
   a.v_a = static_cast<const bf16*>(v_res);
-  a.k_b = static_cast<const bf16*>(k_scr);
-  a.v_b = static_cast<const bf16*>(v_scr);
+  a.k_b = static_cast<const bf16*>(k_b);
+  a.v_b = static_cast<const bf16*>(v_b);
+  a.stage_k = static_cast<bf16*>(stage_k);
+  a.stage_v = static_cast<bf16*>(stage_v);
   a.cu_q = cu_q;
   a.cu_k = cu_k;
   a.slots = slots;
@@ -998,6 +1013,35 @@ extern "C" int dspark_verify_attn_fwd(const void* q, const void* k_res, const vo
   MergeArgs m{work ? work + WORK_INTS * n_work : nullptr, cu_q, cu_k, nullptr, nullptr, a.part_o, a.part_ml, a.out,
               n_req, chunk, tiles, 0};
   return launch_merge(m, n_req, tiles, s);
+}
+}  // namespace
+
+extern "C" int dspark_verify_attn_fwd(const void* q, const void* k_res, const void* v_res,
+                                      const void* k_scr, const void* v_scr,
+                                      const int32_t* cu_q, const int32_t* cu_k, const int32_t* slots,
+                                      int n_req, int64_t slot_stride, int64_t tok_stride, int64_t head_stride,
+                                      int64_t key_rows_bound, int max_q, float scale, int chunk,
+                                      const int32_t* work, int n_work, void* out, void* workspace,
+                                      int64_t workspace_bytes_, void* stream) {
+  clear_error();
+  return verify_launch(q, k_res, v_res, k_scr, v_scr, nullptr, nullptr, cu_q, cu_k, slots, n_req, slot_stride,
+                       tok_stride, head_stride, key_rows_bound, max_q, scale, chunk, work, n_work, out, workspace,
+                       workspace_bytes_, stream);
+}
+
+extern "C" int dspark_verify_attn_staged_fwd(const void* q, const void* k_res, const void* v_res,
+                                             const void* k_new, const void* v_new, void* k_scr, void* v_scr,
+                                             const int32_t* cu_q, const int32_t* cu_k, const int32_t* slots,
+                                             int n_req, int64_t slot_stride, int64_t tok_stride, int64_t head_stride,
+                                             int64_t key_rows_bound, int max_q, float scale, int chunk,
+                                             const int32_t* work, int n_work, void* out, void* workspace,
+                                             int64_t workspace_bytes_, void* stream) {
+  clear_error();
+  DSPARK_REQUIRE(k_scr && v_scr, "null pointer argument");
+  DSPARK_REQUIRE(k_new != k_scr && v_new != v_scr, "new rows and scratch must be distinct buffers");
+  return verify_launch(q, k_res, v_res, k_new, v_new, k_scr, v_scr, cu_q, cu_k, slots, n_req, slot_stride,
+                       tok_stride, head_stride, key_rows_bound, max_q, scale, chunk, work, n_work, out, workspace,
+                       workspace_bytes_, stream);
 }
 
 extern "C" int dspark_draft_attn_fwd(const void* q, const void* k_ctx, const void* v_ctx,

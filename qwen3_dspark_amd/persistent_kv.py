@@ -525,12 +525,26 @@ class PersistentTargetKV:
         return ws.keys, ws.values, ws.cu_query, ws.cu_key, ws.positions
 
     @torch.no_grad()
-    def attend(self, tx, layer, query, *, scale=SCALE):
-        """Bottom-right causal attention of the staged layer: request r's
-        queries see its committed rows (resident) then its staged rows
-        (scratch).  query [sum Q, 16, 128] bf16 -> output of the same shape."""
+    def attend(self, tx, layer, query, *, scale=SCALE, keys=None, values=None):
+        """Bottom-right causal attention of one layer: request r's queries see
+        its committed rows (resident) then its new rows, read in place.
+        query [sum Q, 16, 128] bf16 -> output of the same shape.
+
+        With keys/values (the layer's new [sum Q, 8, 128] rows) the layer is
+        staged in the same launch: the kernel reads the new rows from them
+        and copies them into scratch, exactly what stage_layer followed by
+        attend does, minus one launch and one pass over the new rows.
+        Otherwise the layer must have been staged with stage_layer."""
         ws = self._transaction(tx)
-        if layer not in self._staged:
+        fused = keys is not None or values is not None
+        if fused:
+            if self._external is not None:
+                raise ValueError('Cannot mix eager and registered external scratch writes')
+            if type(layer) is not int or not 0 <= layer < self.layers or layer in self._staged:
+                raise ValueError('Each model layer must stage exactly once')
+            self._kv(keys, values, (self._tx_shape[0], self.heads, self.dim))
+            keys, values = keys.contiguous(), values.contiguous()
+        elif layer not in self._staged:
             raise ValueError('Layer scratch missing')
         if (self.heads, self.dim, self.dtype) != (KV_HEADS, HEAD_DIM, torch.bfloat16):
             raise ValueError('Fused attention requires bf16 Hkv8/D128 storage')
@@ -542,12 +556,17 @@ class PersistentTargetKV:
         out = torch.empty_like(query)
         C = self.context_capacity
         k, v, sk, sv = self._layer_ptrs[layer]
-        _native.call('dspark_verify_attn_fwd', query.data_ptr(), k, v, sk, sv,
-                     ws.cu_query.data_ptr(), ws.cu_key.data_ptr(), ws.req.data_ptr(),
-                     len(tx.slots), KV_HEADS * C * HEAD_DIM, HEAD_DIM, C * HEAD_DIM,
-                     key_capacity, max_q, SCALE, self.chunk,
-                     ws.work.data_ptr(), self._n_work, out.data_ptr(), ws.attn.data_ptr(), ws.attn.numel(),
-                     _native.stream_handle(self.device))
+        tail = (ws.cu_query.data_ptr(), ws.cu_key.data_ptr(), ws.req.data_ptr(),
+                len(tx.slots), KV_HEADS * C * HEAD_DIM, HEAD_DIM, C * HEAD_DIM,
+                key_capacity, max_q, SCALE, self.chunk,
+                ws.work.data_ptr(), self._n_work, out.data_ptr(), ws.attn.data_ptr(), ws.attn.numel(),
+                _native.stream_handle(self.device))
+        if fused:
+            _native.call('dspark_verify_attn_staged_fwd', query.data_ptr(), k, v, keys.data_ptr(), values.data_ptr(),
+                         sk, sv, *tail)
+            self._staged.add(layer)
+        else:
+            _native.call('dspark_verify_attn_fwd', query.data_ptr(), k, v, sk, sv, *tail)
         return out
 
     @torch.no_grad()

@@ -42,7 +42,8 @@ def test_workspace_size_formula():
     assert lib.dspark_attn_workspace_bytes(0, 10, 1, 512) == -1
 
 
-@pytest.mark.parametrize('name', ['dspark_varlen_attn_fwd', 'dspark_verify_attn_fwd', 'dspark_draft_attn_fwd',
+@pytest.mark.parametrize('name', ['dspark_varlen_attn_fwd', 'dspark_verify_attn_fwd', 'dspark_verify_attn_staged_fwd',
+                                  'dspark_draft_attn_fwd',
                                   'dspark_txn_metadata', 'dspark_kv_stage', 'dspark_kv_commit', 'dspark_kv_gather',
                                   'dspark_layout_build', 'dspark_pool_gather', 'dspark_pool_append',
                                   'dspark_crop_plan', 'dspark_rows_rebuild'])

@@ -295,7 +295,8 @@ def test_metadata_gather_commit_bit_exact_against_oracle(dev):
 def test_fused_verify_attention_parity_commit_and_second_round(dev):
     """Config: 4 requests, cached contexts U[64,512], 7 appended rows, 1 layer
     (plus a second layer), seeded accepted prefix 0..7 committed, rest
-    rolled back; the next round attends over the committed rows."""
+    rolled back; the next round attends over the committed rows with the
+    staging fused into the attention launch."""
     from qwen3_dspark_amd.kernels import HipCapacityKernel
     from qwen3_dspark_amd.layout import PersistentAttentionLayout
     from qwen3_dspark_amd.persistent_kv import Bucket, PersistentTargetKV
@@ -324,9 +325,16 @@ def test_fused_verify_attention_parity_commit_and_second_round(dev):
         nk = randn_bf16(gen, L, 7 * B, 8, 128).to(dev)
         nv = randn_bf16(gen, L, 7 * B, 8, 128).to(dev)
         for layer in range(L):
-            pool.stage_layer(tx, layer, nk[layer], nv[layer])
-            out = pool.attend(tx, layer, q[layer])
+            if rnd == 0:
+                pool.stage_layer(tx, layer, nk[layer], nv[layer])
+                out = pool.attend(tx, layer, q[layer])
+            else:   # staging fused into the attention launch
+                out = pool.attend(tx, layer, q[layer], keys=nk[layer], values=nv[layer])
+                with pytest.raises(ValueError, match='exactly once'):
+                    pool.attend(tx, layer, q[layer], keys=nk[layer], values=nv[layer])
             torch.cuda.synchronize()
+            assert torch.equal(pool.scratch_keys[layer, :7 * B], nk[layer])
+            assert torch.equal(pool.scratch_values[layer, :7 * B], nv[layer])
             cu_q = list(range(0, 7 * B + 1, 7))
             ref = cref.verify_attention(bits(q[layer]), bits(pool.keys[layer]), bits(pool.values[layer]),
                                         bits(pool.scratch_keys[layer]), bits(pool.scratch_values[layer]),
