@@ -59,7 +59,8 @@ def parse():
     ap.add_argument('--gpus', type=int, default=1)
     ap.add_argument('--steps', type=int, default=20)
     ap.add_argument('--warmup', type=int, default=5)
-    ap.add_argument('--chunk', type=int, default=None, help='keys per split-K work item')
+    ap.add_argument('--chunk', type=int, default=None, help='keys per split-K verification work item')
+    ap.add_argument('--draft-chunk', type=int, default=None, help='keys per split-K draft work item')
     ap.add_argument('--no-cpu-baseline', action='store_true', help='skip the CPU oracle leg (profiling runs)')
     ap.add_argument('--traffic-probe', action='store_true',
                     help='untimed run for hardware-counter passes: 3 verification-attention layers of the '
@@ -113,6 +114,7 @@ def main():
 
     from qwen3_dspark_amd.draft import DraftBatch, HipDraftAttention
     from qwen3_dspark_amd.kernels import DEFAULT_CHUNK, SCALE
+    from qwen3_dspark_amd.schedule import DRAFT_CHUNK
     from qwen3_dspark_amd.persistent_kv import Bucket, PersistentTargetKV
 
     chunk = args.chunk or DEFAULT_CHUNK
@@ -149,7 +151,7 @@ def main():
     qd = torch.randn(DRAFT_LAYERS, nq_d, 16, 128, generator=gen, device=dev).to(torch.bfloat16)
     bkd = torch.randn(DRAFT_LAYERS, nq_d, 8, 128, generator=gen, device=dev).to(torch.bfloat16)
     bvd = torch.randn(DRAFT_LAYERS, nq_d, 8, 128, generator=gen, device=dev).to(torch.bfloat16)
-    draft = HipDraftAttention(dev, chunk=chunk)
+    draft = HipDraftAttention(dev, chunk=args.draft_chunk or DRAFT_CHUNK)
     draft_offsets = [h.index * CAPACITY for h in handles]   # slot * capacity + first position
     torch.cuda.synchronize()
 
@@ -252,7 +254,7 @@ def main():
                         'contexts log-uniform [256, 8192], KV capacity 8192 per request, 16q/8kv heads, d128',
             'requests': B, 'query_rows_per_request': Q_LEN, 'verify_layers': VERIFY_LAYERS,
             'draft_layers': DRAFT_LAYERS, 'draft_blocks': sum(len(a) for a in anchors),
-            'context_rows': sum(contexts), 'chunk': chunk,
+            'context_rows': sum(contexts), 'chunk': chunk, 'draft_chunk': draft.chunk,
         },
         'roofline': {
             'bound': 'hbm', 'achieved': round(v_gbs, 1), 'peak': HBM_PEAK_GBS, 'unit': 'GB/s',

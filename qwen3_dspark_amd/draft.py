@@ -24,7 +24,7 @@ import torch
 from . import _native
 from ._device import Workspace, require_gfx950, upload
 from .kernels import HEAD_DIM, KV_HEADS, Q_HEADS, SCALE, _check_scale
-from .schedule import DEFAULT_CHUNK, draft_work, upload_work
+from .schedule import DRAFT_CHUNK, draft_work, upload_work
 
 BLOCK_SIZE = 7
 MAX_BLOCKS = 8
@@ -121,7 +121,7 @@ class HipDraftAttention:
     backend_name = 'mi355x_hip_draft_blocks_v1'
     native_varlen_calls_per_layer = 1
 
-    def __init__(self, device, *, chunk=DEFAULT_CHUNK):
+    def __init__(self, device, *, chunk=DRAFT_CHUNK):
         self.device = require_gfx950(device)
         _native.load()
         if chunk % 64:
@@ -207,7 +207,7 @@ class DraftKVPool:
     """
 
     def __init__(self, *, layers, slots, capacity, heads=KV_HEADS, dim=HEAD_DIM, dtype=torch.bfloat16,
-                 device='cuda', chunk=DEFAULT_CHUNK):
+                 device='cuda', chunk=DRAFT_CHUNK):
         if any(type(n) is not int or n < 1 for n in (layers, slots, capacity, heads, dim)):
             raise ValueError('All pool sizes must be positive integers')
         if dtype not in (torch.bfloat16, torch.float32):

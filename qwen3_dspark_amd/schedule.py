@@ -22,7 +22,10 @@ kernel reads one record instead of walking the cumulative arrays.
 """
 from ._device import upload
 
-DEFAULT_CHUNK = 1024
+DEFAULT_CHUNK = 1024          # verification / varlen: one query tile per item
+# Draft items carry up to 8 blocks of FP32 partials each, so they are cut
+# more coarsely: only contexts longer than this are split.
+DRAFT_CHUNK = 4096
 WORK_INTS = 8
 REQ_INTS = 4
 

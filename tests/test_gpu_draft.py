@@ -72,13 +72,14 @@ def test_multi_block_against_oracle(dev, name, contexts, blocks):
     rng = np.random.default_rng(SEED + len(name))
     gen = torch.Generator().manual_seed(SEED + sum(contexts))
     c = draft_case(gen, rng, contexts, blocks)
-    kernel = HipDraftAttention(dev)
-    out = run(dev, kernel, c)
     ref, cu_b = oracle(c)
-    attention_gate(f64(out), ref, [(7 * cu_b[i], 7 * cu_b[i + 1]) for i in range(len(cu_b) - 1)])
-    # Linearity in V (context and block values together) is exact.
-    c2 = dict(c, ctx_v=2 * c['ctx_v'], bv=2 * c['bv'])
-    assert torch.equal(run(dev, kernel, c2), 2 * out)
+    # default chunking, and 1024-key chunks (more split-K partials and merges)
+    for kernel in (HipDraftAttention(dev), HipDraftAttention(dev, chunk=1024)):
+        out = run(dev, kernel, c)
+        attention_gate(f64(out), ref, [(7 * cu_b[i], 7 * cu_b[i + 1]) for i in range(len(cu_b) - 1)])
+        # Linearity in V (context and block values together) is exact.
+        c2 = dict(c, ctx_v=2 * c['ctx_v'], bv=2 * c['bv'])
+        assert torch.equal(run(dev, kernel, c2), 2 * out)
 
 
 def test_single_block_equals_packed_noncausal_path(dev):
