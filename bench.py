@@ -341,8 +341,9 @@ def cpu_leg(args, pool, bucket, handles, contexts, anchors, qv, qd, bkd, bvd, dc
 
     def gate(out, ref, kind):
         d = np.abs(out.astype(np.float64) - ref)
-        stats[kind + '_max_abs'] = max(stats[kind + '_max_abs'], float(d.max()))
-        stats[kind + '_mean_abs'] = max(stats[kind + '_mean_abs'], float(d.mean()))
+        finite = bool(np.isfinite(d).all())     # a NaN/Inf output fails the gate
+        stats[kind + '_max_abs'] = max(stats[kind + '_max_abs'], float(d.max()) if finite else float('inf'))
+        stats[kind + '_mean_abs'] = max(stats[kind + '_mean_abs'], float(d.mean()) if finite else float('inf'))
 
     # Verification: a transaction on the current lengths, fresh staged rows.
     ctx = [pool.length(h) for h in handles]

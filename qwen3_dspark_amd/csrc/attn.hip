@@ -140,12 +140,13 @@ __device__ __forceinline__ bf16x8 softmax_update(RowState& st, const f32x4& s0, 
   mx = wave_max_across_groups(mx);
   const bool raise = mx > st.m + RESCALE_SLACK;
   if (__builtin_amdgcn_ballot_w64(raise)) {
-    const float m_new = raise ? mx : st.m;
-    const float alpha = fast_exp2(st.m - m_new);
+    // Rows that do not raise keep factor 1 (their max may still be -inf,
+    // and -inf - -inf must not reach exp2).
+    const float alpha = raise ? fast_exp2(st.m - mx) : 1.0f;
     st.l *= alpha;
     #pragma unroll
     for (int nb = 0; nb < 8; ++nb) st.o[nb] *= alpha;
-    st.m = m_new;
+    if (raise) st.m = mx;
   }
   const float m_use = (st.m == -INFINITY) ? 0.f : st.m;
   bf16x8 pb;

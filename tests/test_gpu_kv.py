@@ -357,6 +357,42 @@ def test_fused_verify_attention_parity_commit_and_second_round(dev):
             assert torch.isnan(pool.keys[:, h.index, ctx[i] + n:]).all()
 
 
+def test_verify_rows_without_visible_keys_in_a_tile(dev):
+    """Contexts whose last key tile holds new rows visible to the later
+    query rows only (c + 7 just past a 32-key or chunk boundary): every
+    output stays finite and meets the oracle, fused staging or not."""
+    from qwen3_dspark_amd.persistent_kv import Bucket, PersistentTargetKV
+    gen = torch.Generator().manual_seed(SEED + 5)
+    contexts = [26, 31, 61, 90, 1050, 1051, 2045, 300]
+    B, C = len(contexts), 2112
+    say(f'[verify] partial-tile visibility contexts={contexts}')
+    pool = PersistentTargetKV(layers=1, slots=B, context_capacity=C, max_query_tokens=7 * B, heads=8, dim=128,
+                              device=dev)
+    handles = [pool.add_request(f'r{i}') for i in range(B)]
+    for h, c in zip(handles, contexts):
+        kv = randn_bf16(gen, 2, 1, c, 8, 128).to(dev)
+        pool.load_prefix(h, kv[0], kv[1])
+    bucket = Bucket((7,) * B, (C - 7,) * B, 'partial tiles')
+    pool.register_bucket(bucket)
+    cu_q = list(range(0, 7 * B + 1, 7))
+    for fused in (False, True):
+        tx = pool.begin(handles, bucket)
+        q = randn_bf16(gen, 7 * B, 16, 128).to(dev)
+        nk, nv = randn_bf16(gen, 7 * B, 8, 128).to(dev), randn_bf16(gen, 7 * B, 8, 128).to(dev)
+        if fused:
+            out = pool.attend(tx, 0, q, keys=nk, values=nv)
+        else:
+            pool.stage_layer(tx, 0, nk, nv)
+            out = pool.attend(tx, 0, q)
+        torch.cuda.synchronize()
+        assert torch.isfinite(out.float()).all()
+        ref = cref.verify_attention(bits(q), bits(pool.keys[0]), bits(pool.values[0]), bits(pool.scratch_keys[0]),
+                                    bits(pool.scratch_values[0]), [h.index for h in handles], contexts, cu_q,
+                                    scale=SCALE)
+        attention_gate(f64(out), ref, segments(cu_q))
+        pool.abort(tx)
+
+
 def test_fused_attention_contract(dev):
     from qwen3_dspark_amd.persistent_kv import Bucket, PersistentTargetKV
     say('[verify] contract errors')

@@ -128,6 +128,8 @@ def make_packed(gen, q_lens, k_lens):
     ('multi_tile_q20', [20, 9, 1], [700, 9, 1]),
     ('single_key', [1, 1], [1, 2]),
     ('chunk_boundary', [7, 7], [512, 1031]),
+    # the last 32-key tile of a wave is visible to some query rows only
+    ('partial_tile_visibility', [7] * 8, [33, 38, 68, 97, 129, 1057, 1058, 2081]),
 ])
 @pytest.mark.parametrize('causal', [True, False])
 def test_packed_shapes_against_oracle(dev, kernels, name, q_lens, k_lens, causal):
