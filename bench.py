@@ -274,10 +274,44 @@ def main():
         },
     }
 
+    result['next'] = {'qkv_prologue': prologue_leg(dev, B * Q_LEN)}
+
     if not args.no_cpu_baseline:
         result['cpu_baseline'], result['parity'] = cpu_leg(args, pool, bucket, handles, contexts, anchors, qv, qd,
                                                            bkd, bvd, dctx_k, dctx_v, draft, draft_offsets)
     print(json.dumps(result), flush=True)
+
+
+def prologue_leg(dev, tokens, reps=50):
+    """The verify-layer prologue (q/k/v projection + q/k RMSNorm + RoPE, K/V
+    written token-major as into scratch) for one layer of the round's
+    tokens, Qwen3-0.6B sizes (hidden 1024), random-init weights.  Median of
+    `reps` event-timed launches."""
+    import numpy as np
+    import torch
+
+    from qwen3_dspark_amd.prologue import QKVPrologue
+    g = torch.Generator(device=dev).manual_seed(SEED + 7)
+    w = [(torch.randn(n, 1024, generator=g, device=dev) * 0.03).to(torch.bfloat16) for n in (2048, 1024, 1024)]
+    norms = [torch.ones(128, device=dev, dtype=torch.bfloat16) for _ in range(2)]
+    pro = QKVPrologue(*w, *norms)
+    x = torch.randn(tokens, 1024, generator=g, device=dev).to(torch.bfloat16)
+    pos = torch.arange(tokens, device=dev, dtype=torch.long) * 13
+    for _ in range(5):
+        pro(x, pos)
+    times = []
+    for _ in range(reps):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        pro(x, pos)
+        e1.record()
+        times.append((e0, e1))
+    torch.cuda.synchronize()
+    ms = float(np.median([a.elapsed_time(b) for a, b in times]))
+    nbytes = (4096 * 1024 + tokens * 1024 + tokens * 4096) * 2
+    flops = 2 * tokens * 1024 * 4096
+    return {'tokens': tokens, 'median_ms': round(ms, 5), 'bytes': nbytes, 'gbs': round(nbytes / ms / 1e6, 1),
+            'tflops': round(flops / ms / 1e9, 2)}
 
 
 def traffic_probe(args):

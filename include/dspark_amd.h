@@ -136,6 +136,24 @@ int dspark_draft_attn_fwd(const void* q, const void* k_ctx, const void* v_ctx,
                           void* out, void* workspace, int64_t workspace_bytes, void* stream);
 
 /*
+ * Verify-layer prologue (the Qwen3 attention steps before the KV cache
+ * update, as run by dspark_qwen/persistent_qwen_target.py:45-95 through
+ * transformers' Qwen3Attention): for every token t of x [tokens, hidden]
+ *   q = RoPE(RMSNorm(x Wq^T, q_norm)), k = RoPE(RMSNorm(x Wk^T, k_norm)), v = x Wv^T
+ * per 128-dim head; W* in nn.Linear layout ([16*128 | 8*128, hidden]),
+ * RMSNorm y = w x / sqrt(mean(x^2) + eps), RoPE rotate-half with angle
+ * positions[t] * inv_freq[d] (float32 table of 64 entries).  q_out
+ * [tokens, 16, 128]; k_out/v_out token rows of 8*128 elements,
+ * kv_row_stride apart (1024 writes a [tokens, 8, 128] tensor, e.g. the
+ * transaction scratch layer, replacing stage_layer's copy).  hidden must be
+ * a multiple of 64.  FP32 accumulation, bf16 outputs.
+ */
+int dspark_qkv_prologue(const void* x, const void* wq, const void* wk, const void* wv,
+                        const void* q_norm, const void* k_norm, const float* inv_freq,
+                        const int64_t* positions, int tokens, int hidden, float eps,
+                        void* q_out, void* k_out, void* v_out, int64_t kv_row_stride, void* stream);
+
+/*
  * Transaction metadata of PersistentTargetKV.begin
  * (dspark_qwen/persistent_target_kv.py:392-411), built on the device from
  * req = int32 [3][n_req] (slot, committed context, query length per request):

@@ -555,18 +555,6 @@ constexpr int DRAFT_SMEM = DSTAGES * DSTAGE_BYTES;   // 128 KiB
 constexpr int DRAFT_PIECES = 2 * DSTEP * ROWB / 1024;  // 1 KiB pieces per stage (32)
 static_assert(DRAFT_PIECES == DWAVES * 4, "each thread issues 4 direct loads per stage");
 
-// Direct global->LDS load of 16 bytes per lane: lane L's data lands at LDS
-// byte address `lds` + 16*L.  Issued as inline assembly so that the
-// compiler neither waits on it nor reorders LDS reads around it; the kernel
-// orders it with explicit vmcnt waits and barriers.
-__device__ __forceinline__ void lds_dma16(const void* gptr, uint32_t lds) {
-  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(lds), "v"(gptr) : "memory");
-}
-
-__device__ __forceinline__ uint32_t lds_address(const void* p) {
-  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
-}
-
 // INDEXED: context rows come through a per-request physical index vector
 // (the append-order pool); otherwise they are consecutive rows.  The
 // non-indexed instance has no ordinary global loads inside the stage loop,

@@ -92,6 +92,20 @@ __device__ __forceinline__ void locate_chunk(const int32_t* __restrict__ cu,
   first = running;
 }
 
+// Direct global->LDS load of 16 bytes per lane: lane L's data lands at LDS
+// byte address `lds` + 16*L (`lds` must be wave-uniform).  Issued as inline
+// assembly so that the compiler neither waits on it nor reorders LDS reads
+// around it; kernels order it with explicit vmcnt waits and barriers, and
+// must then issue no compiler-visible global loads while such loads are in
+// flight (the compiler's own vmcnt waits would drain them).
+__device__ __forceinline__ void lds_dma16(const void* gptr, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(lds), "v"(gptr) : "memory");
+}
+
+__device__ __forceinline__ uint32_t lds_address(const void* p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
+}
+
 }  // namespace dspark
 
 // ---------------------------------------------------------------------------

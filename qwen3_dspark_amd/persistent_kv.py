@@ -507,6 +507,27 @@ class PersistentTargetKV:
         self._staged.add(layer)
 
     @torch.no_grad()
+    def stage_projected(self, tx, layer, hidden, prologue):
+        """Run the layer's attention prologue (QKVPrologue: q/k/v projection,
+        q/k RMSNorm, RoPE at each row's absolute position) on the packed
+        hidden states [sum Q, H] and write K/V straight into this layer's
+        scratch - stage_layer without the separate copy.  Returns the
+        queries [sum Q, 16, 128] for attend()."""
+        ws = self._transaction(tx)
+        if self._external is not None:
+            raise ValueError('Cannot mix eager and registered external scratch writes')
+        if type(layer) is not int or not 0 <= layer < self.layers or layer in self._staged:
+            raise ValueError('Each model layer must stage exactly once')
+        if (self.heads, self.dim, self.dtype) != (KV_HEADS, HEAD_DIM, torch.bfloat16):
+            raise ValueError('The fused prologue requires bf16 Hkv8/D128 storage')
+        q = self._tx_shape[0]
+        if not isinstance(hidden, torch.Tensor) or hidden.ndim != 2 or hidden.shape[0] != q:
+            raise ValueError('Hidden states must be [sum Q, hidden] for the transaction')
+        queries, _, _ = prologue(hidden, ws.positions, k_out=self.scratch_keys[layer], v_out=self.scratch_values[layer])
+        self._staged.add(layer)
+        return queries
+
+    @torch.no_grad()
     def prepare_attention(self, tx, layer):
         """Materialise the capacity-length K/V (parity mode); attend() is the
         fused path that never builds it."""

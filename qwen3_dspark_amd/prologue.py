@@ -1,0 +1,83 @@
+"""Verify-layer prologue on MI355X: the Qwen3 attention steps that produce
+the attention kernel's inputs (transformers' Qwen3Attention as driven by
+dspark_qwen/persistent_qwen_target.py:45-95, RoPE as dspark_qwen/model.py:22-24):
+
+    q = RoPE(RMSNorm_q(x Wq^T)),  k = RoPE(RMSNorm_k(x Wk^T)),  v = x Wv^T
+
+in one HIP launch per layer (dspark_qkv_prologue).  K/V can be written
+straight into a PersistentTargetKV transaction's scratch
+(PersistentTargetKV.stage_projected), which replaces stage_layer's copy.
+"""
+import torch
+
+from . import _native
+from ._device import require_gfx950
+from .kernels import HEAD_DIM, KV_HEADS, Q_HEADS
+
+
+def rope_inv_freq(theta=1e6, dim=HEAD_DIM):
+    """The model's float32 inverse frequencies, 1 / theta**(2j/dim), computed
+    with torch's float32 pow exactly as transformers' default RoPE does."""
+    return 1.0 / (theta ** (torch.arange(0, dim, 2, dtype=torch.float) / dim))
+
+
+class QKVPrologue:
+    """One layer's projection weights in nn.Linear layout: q_proj [16*128, H],
+    k_proj / v_proj [8*128, H], q_norm / k_norm [128]; bf16 on a gfx950 GPU."""
+
+    def __init__(self, q_proj, k_proj, v_proj, q_norm, k_norm, *, eps=1e-6, theta=1e6):
+        self.device = require_gfx950(q_proj.device)
+        _native.load()
+        hidden = q_proj.shape[-1] if q_proj.ndim == 2 else 0
+        shapes = ((q_proj, (Q_HEADS * HEAD_DIM, hidden)), (k_proj, (KV_HEADS * HEAD_DIM, hidden)),
+                  (v_proj, (KV_HEADS * HEAD_DIM, hidden)), (q_norm, (HEAD_DIM,)), (k_norm, (HEAD_DIM,)))
+        for t, shape in shapes:
+            if (not isinstance(t, torch.Tensor) or t.dtype != torch.bfloat16 or t.device != self.device
+                    or tuple(t.shape) != shape):
+                raise ValueError('Prologue weights must be bf16 q/k/v projections [Hq*128|Hkv*128, H] and '
+                                 '[128] norms on one gfx950 device')
+        if hidden < 64 or hidden % 64:
+            raise ValueError('Hidden size must be a positive multiple of 64')
+        if not (eps > 0 and theta > 0):
+            raise ValueError('eps and theta must be positive')
+        self.hidden = hidden
+        self.eps = float(eps)
+        self.weights = tuple(t.detach().contiguous() for t in (q_proj, k_proj, v_proj, q_norm, k_norm))
+        self.inv_freq = rope_inv_freq(theta).to(self.device)
+
+    @classmethod
+    def from_attention(cls, attn, *, theta=None):
+        """From a transformers Qwen3Attention module (its weights are used in
+        place when already bf16 and contiguous)."""
+        cfg = attn.config
+        theta = theta if theta is not None else (cfg.rope_parameters or {}).get('rope_theta', 1e6)
+        return cls(attn.q_proj.weight, attn.k_proj.weight, attn.v_proj.weight, attn.q_norm.weight,
+                   attn.k_norm.weight, eps=cfg.rms_norm_eps, theta=theta)
+
+    def __call__(self, hidden, positions, *, k_out=None, v_out=None):
+        """hidden [T, H] bf16, positions [T] int64 (device) -> (q [T,16,128],
+        k, v [T,8,128]).  k_out/v_out: optional destinations whose token rows
+        are 8*128 elements apart (e.g. a scratch layer); they are returned."""
+        t = hidden.shape[0] if isinstance(hidden, torch.Tensor) and hidden.ndim == 2 else 0
+        if (t < 1 or hidden.shape[1] != self.hidden or hidden.dtype != torch.bfloat16
+                or hidden.device != self.device or not hidden.is_contiguous()):
+            raise ValueError('Hidden states must be contiguous bf16 [T, hidden] on the prologue device')
+        if (not isinstance(positions, torch.Tensor) or positions.dtype != torch.long or positions.shape != (t,)
+                or positions.device != self.device or not positions.is_contiguous()):
+            raise ValueError('Positions must be a contiguous int64 [T] device tensor')
+        q = torch.empty((t, Q_HEADS, HEAD_DIM), dtype=torch.bfloat16, device=self.device)
+        outs = []
+        for o in (k_out, v_out):
+            if o is None:
+                o = torch.empty((t, KV_HEADS, HEAD_DIM), dtype=torch.bfloat16, device=self.device)
+            elif (o.dtype != torch.bfloat16 or o.device != self.device or o.shape[0] < t
+                  or tuple(o.shape[1:]) != (KV_HEADS, HEAD_DIM) or o.stride(0) != KV_HEADS * HEAD_DIM
+                  or o.stride(2) != 1 or o.stride(1) != HEAD_DIM):
+                raise ValueError('K/V destinations must be bf16 [>=T, 8, 128] token-major on the device')
+            outs.append(o)
+        wq, wk, wv, qn, kn = self.weights
+        _native.call('dspark_qkv_prologue', hidden.data_ptr(), wq.data_ptr(), wk.data_ptr(), wv.data_ptr(),
+                     qn.data_ptr(), kn.data_ptr(), self.inv_freq.data_ptr(), positions.data_ptr(), t, self.hidden,
+                     self.eps, q.data_ptr(), outs[0].data_ptr(), outs[1].data_ptr(), KV_HEADS * HEAD_DIM,
+                     _native.stream_handle(self.device))
+        return q, outs[0], outs[1]

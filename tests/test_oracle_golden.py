@@ -261,3 +261,41 @@ def test_c_oracle_matches_numpy_oracle():
                                       ctx_rows[1][offs[r]:offs[r] + lens[r]].double().numpy(),
                                       bk[rows].double().numpy(), bv[rows].double().numpy(), anchors[r], scale=SCALE)
         assert np.abs(a[rows] - b).max() < 1e-5
+
+
+def test_qkv_prologue_oracle_matches_transformers_qwen3_modules():
+    """The prologue oracle against transformers' own Qwen3 projection, q/k
+    RMSNorm and rotary modules (float32, CPU): a library routine pins the
+    formula, including the rotate-half pairing and the inverse frequencies."""
+    from transformers import Qwen3Config
+    from transformers.models.qwen3 import modeling_qwen3 as mq
+
+    from oracle import qkv
+    cfg = Qwen3Config(vocab_size=64, hidden_size=256, intermediate_size=256, num_hidden_layers=1,
+                      num_attention_heads=16, num_key_value_heads=8, head_dim=128, rope_theta=1e6)
+    torch.manual_seed(7)
+    attn = mq.Qwen3Attention(cfg, layer_idx=0).eval()
+    with torch.no_grad():
+        attn.q_norm.weight.uniform_(0.5, 1.5)
+        attn.k_norm.weight.uniform_(0.5, 1.5)
+    rot = mq.Qwen3RotaryEmbedding(cfg)
+    t = 13
+    x = torch.randn(1, t, 256)
+    pos = torch.tensor([[0, 1, 2, 7, 100, 511, 4095, 8191, 3, 3, 9000, 17, 6000]])
+    with torch.no_grad():
+        q = attn.q_norm(attn.q_proj(x).view(1, t, -1, 128)).transpose(1, 2)
+        k = attn.k_norm(attn.k_proj(x).view(1, t, -1, 128)).transpose(1, 2)
+        v = attn.v_proj(x).view(1, t, -1, 128)
+        cos, sin = rot(x, pos)
+        q, k = mq.apply_rotary_pos_emb(q, k, cos, sin)
+    w = {n: p.detach().numpy() for n, p in attn.named_parameters()}
+    oq, ok, ov = qkv.qkv_prologue(x[0].numpy(), w['q_proj.weight'], w['k_proj.weight'], w['v_proj.weight'],
+                                  w['q_norm.weight'], w['k_norm.weight'], pos[0].numpy(), eps=cfg.rms_norm_eps)
+    np.testing.assert_allclose(oq, q[0].transpose(0, 1).numpy(), rtol=1e-4, atol=2e-4)
+    np.testing.assert_allclose(ok, k[0].transpose(0, 1).numpy(), rtol=1e-4, atol=2e-4)
+    np.testing.assert_allclose(ov, v[0].numpy(), rtol=1e-5, atol=1e-5)
+    # Planted mistakes must fail: unrotated pairing and a missing norm weight.
+    bad = qkv.rope(qkv.rms_norm((x[0].numpy() @ w['q_proj.weight'].T).reshape(t, 16, 128),
+                                np.ones(128), cfg.rms_norm_eps), pos[0].numpy(), qkv.inv_freq())
+    assert not np.allclose(bad, q[0].transpose(0, 1).numpy(), atol=1e-3)
+    assert np.allclose(qkv.inv_freq(), rot.inv_freq.numpy(), rtol=0, atol=0)
