@@ -13,18 +13,24 @@
 * FusedVerifier - binds a PersistentTargetKV transaction to one model forward
   (the callback finds it through the `fused_verification` forward kwarg, as
   the reference passes `persistent_target`).
+* PersistentQwenTarget - the full-model transaction adapter of
+  dspark_qwen/persistent_qwen_target.py:100-473 (verify / commit / abort /
+  prefill / predict / request_kv, captured layer features) on that path.
 
 The callbacks keep the reference's contract: no attention mask or dropout,
 the module must belong to the bound model, ValueError otherwise.
 """
 import contextlib
+from collections.abc import Mapping
+from dataclasses import dataclass
 
 import torch
 from transformers import Cache
 from transformers.modeling_utils import ALL_ATTENTION_FUNCTIONS
 
 from .layout import PackedLayout
-from .persistent_kv import PersistentTargetKV
+from .persistent_kv import Bucket, PersistentTargetKV, QueryFamily
+from .schedule import DEFAULT_CHUNK
 
 VARLEN_BACKEND = 'dspark_mi355x_varlen'
 FUSED_BACKEND = 'dspark_mi355x_fused_verify'
@@ -146,3 +152,193 @@ class FusedVerifier:
             raise RuntimeError('Forward outside owned transaction')
         return self.model(input_ids=input_ids, position_ids=position_ids, attention_mask=None,
                           past_key_values=self.cache, use_cache=True, fused_verification=self)
+
+
+# ---------------------------------------------------------------------------
+# Full-model transaction adapter (dspark_qwen/persistent_qwen_target.py:100-473)
+# ---------------------------------------------------------------------------
+
+@dataclass(frozen=True)
+class CachedFeatures:
+    """One request's slice of a verification forward (cached_target.py:15-22)."""
+    start: int
+    last: torch.Tensor
+    context: torch.Tensor
+
+    @property
+    def end(self):
+        return self.start + self.last.shape[1]
+
+
+@dataclass(frozen=True)
+class PackedFeatures:
+    """Hidden states of one packed verification forward (packed_target.py:18-28):
+    last [1, sum Q, hidden], context = captured layer outputs concatenated on
+    the feature axis (or None), spans request -> (offset, count, start)."""
+    last: torch.Tensor
+    context: object
+    spans: dict
+    work: dict
+
+    def for_request(self, request_id):
+        offset, count, start = self.spans[request_id]
+        return CachedFeatures(start, self.last[:, offset:offset + count],
+                              None if self.context is None else self.context[:, offset:offset + count])
+
+
+class PersistentQwenTarget:
+    """HF Qwen3 target over a PersistentTargetKV with the fused MI355X
+    attention (the API of persistent_qwen_target.py:100-473, eager path).
+
+    verify() runs one packed forward whose layers stage their new K/V rows
+    into scratch and attend over resident + scratch rows in place; nothing is
+    committed until commit() keeps the caller's accepted prefixes (the rest
+    is rolled back by omission).  prefill() = verify + commit of every row.
+    Decoder outputs of `layer_ids` are captured as draft context features.
+    """
+    BACKEND_NAME = FUSED_BACKEND
+
+    def __init__(self, model, layer_ids=(), *, slots, context_capacity, max_query_tokens, chunk=DEFAULT_CHUNK):
+        cfg = model.config
+        if (cfg.model_type != 'qwen3' or getattr(cfg, 'use_sliding_window', False)
+                or any(kind != 'full_attention' for kind in cfg.layer_types)
+                or (cfg.rope_parameters or {}).get('rope_type', 'default') != 'default'):
+            raise ValueError('Owned dense Qwen3 with default RoPE required')
+        if (cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim) != (16, 8, 128):
+            raise ValueError('The MI355X attention path requires 16 query heads, 8 KV heads, head dim 128')
+        self.layer_ids = tuple(layer_ids)
+        if (tuple(sorted(set(self.layer_ids))) != self.layer_ids
+                or any(type(i) is not int or not 0 <= i < cfg.num_hidden_layers for i in self.layer_ids)):
+            raise ValueError('Unique increasing valid decoder layer IDs required')
+        device = model.get_input_embeddings().weight.device
+        dtype = model.get_input_embeddings().weight.dtype
+        if dtype != torch.bfloat16:
+            raise ValueError('The MI355X attention path requires a bf16 model')
+        self.store = PersistentTargetKV(layers=cfg.num_hidden_layers, slots=slots, context_capacity=context_capacity,
+                                        max_query_tokens=max_query_tokens, heads=cfg.num_key_value_heads,
+                                        dim=cfg.head_dim, dtype=dtype, device=device, chunk=chunk)
+        self.verifier = FusedVerifier(model, self.store)
+        self.model = self.verifier.model
+        self._handles = {}
+        self._pending = None
+        self._captured = {}
+        self._hooks = [self.model.model.layers[i].register_forward_hook(self._hook(i)) for i in self.layer_ids]
+
+    @property
+    def device(self):
+        return self.store.device
+
+    @property
+    def lengths(self):
+        return {r: self.store.length(h) for r, h in self._handles.items()}
+
+    def _hook(self, index):
+        def capture(_module, _inputs, output):
+            if self.verifier.transaction is None:
+                raise RuntimeError('Foreign model forward while the adapter owns the model')
+            self._captured[index] = output[0] if isinstance(output, tuple) else output
+        return capture
+
+    def add_request(self, request):
+        self._idle()
+        self._handles[request] = self.store.add_request(request)
+
+    def remove_request(self, request):
+        self._idle()
+        self.store.remove_request(self._handles.pop(request))
+
+    def register_bucket(self, bucket):
+        self._idle()
+        self.store.register_bucket(bucket)
+
+    def _idle(self):
+        if self._pending is not None:
+            raise RuntimeError('Finish existing verification transaction first')
+
+    def _validate_chunks(self, chunks, bucket):
+        if not isinstance(chunks, Mapping) or not chunks:
+            raise ValueError('Need a nonempty request-to-token mapping')
+        if not isinstance(bucket, (Bucket, QueryFamily)):
+            raise ValueError('Explicit Bucket or QueryFamily required')
+        for request, ids in chunks.items():
+            if request not in self._handles:
+                raise ValueError('Unknown request ID')
+            if (not isinstance(ids, torch.Tensor) or ids.ndim != 2 or ids.shape[0] != 1 or ids.shape[1] < 1
+                    or ids.dtype != torch.long or ids.device != self.device):
+                raise ValueError('Each chunk needs nonempty [1,q] long IDs on the model device')
+
+    @torch.no_grad()
+    def verify(self, chunks, *, bucket):
+        """One packed forward over {request: ids [1, q]} in bucket order;
+        returns PackedFeatures and leaves the transaction open."""
+        self._idle()
+        self._validate_chunks(chunks, bucket)
+        handles = tuple(self._handles[r] for r in chunks)
+        query_lengths = tuple(ids.shape[1] for ids in chunks.values())
+        self._captured = {}
+        with self.verifier.transaction_for(handles, bucket, query_lengths=query_lengths) as tx:
+            ws = self.store._workspaces[tx.bucket]
+            try:
+                out = self.model.model(input_ids=torch.cat(tuple(chunks.values()), dim=1),
+                                       position_ids=ws.positions[None], attention_mask=None,
+                                       past_key_values=self.verifier.cache, use_cache=True, return_dict=True,
+                                       fused_verification=self.verifier)
+                if len(self.store._staged) != self.store.layers or set(self._captured) != set(self.layer_ids):
+                    raise RuntimeError('Full layer cache update or selected feature capture missing')
+            except BaseException:
+                if self.store._pending is tx and not self.store.failed:
+                    self.store.abort(tx)
+                raise
+            finally:
+                captured, self._captured = self._captured, {}
+        spans, offset = {}, 0
+        for request, c, q in zip(chunks, tx.context_lengths, tx.query_lengths):
+            spans[request] = (offset, q, c)
+            offset += q
+        context = torch.cat([captured[i] for i in self.layer_ids], dim=-1) if self.layer_ids else None
+        work = self.store.work(tx)
+        work.update(model_forward_calls=1, layers=self.store.layers, selected_layer_ids=list(self.layer_ids),
+                    attention_backend=self.BACKEND_NAME,
+                    committed_write_policy='scratch_only_until_explicit_commit')
+        features = PackedFeatures(out.last_hidden_state.detach(), None if context is None else context.detach(),
+                                  spans, work)
+        self._pending = (features, tx)
+        return features
+
+    @torch.no_grad()
+    def commit(self, features, committed_query_lengths):
+        if self._pending is None or self._pending[0] is not features:
+            raise ValueError('Only the outstanding verification features can commit')
+        if not isinstance(committed_query_lengths, Mapping) or set(committed_query_lengths) != set(features.spans):
+            raise ValueError('One committed query prefix per verified request required')
+        _, tx = self._pending
+        result = self.store.commit(tx, {self._handles[r]: n for r, n in committed_query_lengths.items()})
+        self._pending = None
+        return result
+
+    def abort(self, features):
+        if self._pending is None or self._pending[0] is not features:
+            raise ValueError('Only outstanding verification features can abort')
+        self.store.abort(self._pending[1])
+        self._pending = None
+
+    @torch.no_grad()
+    def prefill(self, chunks, *, bucket):
+        self._idle()
+        if any(self.lengths.get(r) != 0 for r in chunks):
+            raise ValueError('Prefill is only for newly admitted empty requests')
+        features = self.verify(chunks, bucket=bucket)
+        self.commit(features, {r: ids.shape[1] for r, ids in chunks.items()})
+        return features
+
+    @torch.no_grad()
+    def predict(self, features, last_only=False):
+        """The model's LM head over the verified rows (after its final norm)."""
+        logits = self.model.get_output_embeddings()(features.last)
+        return {r: (logits[:, offset + count - 1] if last_only else logits[:, offset:offset + count])
+                for r, (offset, count, _) in features.spans.items()}
+
+    def request_kv(self, request):
+        """Per layer (keys, values) [1, Hkv, C, D] copies of a request's committed rows."""
+        keys, values = self.store.request_kv(self._handles[request])
+        return tuple((k.transpose(0, 1)[None], v.transpose(0, 1)[None]) for k, v in zip(keys, values))

@@ -119,3 +119,53 @@ def test_varlen_callback_matches_fused_path():
     with pytest.raises(ValueError, match='metadata-only'):
         varlen_attention_forward(None, query, key, value, torch.ones(1), packed_layout=layout,
                                  packed_varlen_kernel=kernel)
+
+
+def test_persistent_qwen_target_prefill_verify_commit_features():
+    """The full-model adapter (persistent_qwen_target.py:100-473 API):
+    prefill ragged prompts, verify 7 tokens per request, commit a prefix,
+    verify again; logits via predict() and captured layer features match the
+    CPU float32 model over each request's full sequence."""
+    from qwen3_dspark_amd.hf_hooks import PersistentQwenTarget
+    from qwen3_dspark_amd.persistent_kv import Bucket
+    cpu, gpu = tiny_qwen3()
+    rng = np.random.default_rng(11)
+    prompts = [rng.integers(0, 512, size=n).tolist() for n in (20, 65, 9)]
+    target = PersistentQwenTarget(gpu, layer_ids=(0, 1), slots=3, context_capacity=256, max_query_tokens=128)
+    names = ['a', 'b', 'c']
+    for n in names:
+        target.add_request(n)
+    pre = Bucket(tuple(len(p) for p in prompts), (0, 0, 0), 'prefill')
+    target.register_bucket(pre)
+    t = lambda ids: torch.tensor([ids], device=DEV)
+    target.prefill({n: t(p) for n, p in zip(names, prompts)}, bucket=pre)
+    assert target.lengths == {n: len(p) for n, p in zip(names, prompts)}
+    with pytest.raises(ValueError, match='newly admitted'):
+        target.prefill({'a': t([1])}, bucket=pre)
+    step = Bucket((NEW,) * 3, (256 - NEW,) * 3, 'verify')
+    target.register_bucket(step)
+    seqs = [list(p) for p in prompts]
+    for accepted in ([7, 2, 0], [4, 4, 4]):
+        new = [rng.integers(0, 512, size=NEW).tolist() for _ in seqs]
+        feats = target.verify({n: t(x) for n, x in zip(names, new)}, bucket=step)
+        logits = target.predict(feats)
+        outs = {}
+        hooks = [cpu.model.layers[i].register_forward_hook(
+            lambda m, a, o, i=i: outs.__setitem__(i, o[0] if isinstance(o, tuple) else o)) for i in (0, 1)]
+        try:
+            with torch.no_grad():
+                for r, (n, s) in enumerate(zip(names, seqs)):
+                    ref = cpu(input_ids=torch.tensor([s + new[r]]), use_cache=False)
+                    close(logits[n][0].float().cpu().numpy(), ref.logits[0, -NEW:].numpy(), (n, 'logits'))
+                    f = feats.for_request(n)
+                    assert f.start == len(s) and f.last.shape[1] == NEW
+                    want = torch.cat([outs[0][0, -NEW:], outs[1][0, -NEW:]], dim=-1)
+                    close(f.context[0].float().cpu().numpy(), want.numpy(), (n, 'features'))
+        finally:
+            for h in hooks:
+                h.remove()
+        target.commit(feats, dict(zip(names, accepted)))
+        seqs = [s + x[:a] for s, x, a in zip(seqs, new, accepted)]
+        assert target.lengths == {n: len(s) for n, s in zip(names, seqs)}
+    k, v = target.request_kv('b')[0]
+    assert k.shape == (1, 8, len(seqs[1]), 128)
