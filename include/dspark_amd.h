@@ -24,38 +24,55 @@ extern "C" {
 /* Thread-local message for the last failing call on this thread. */
 const char* dspark_last_error(void);
 
-/* ABI revision of this header (currently 2). */
+/* ABI revision of this header (currently 3). */
 int dspark_abi_version(void);
 
 /*
- * Bytes of split-K workspace needed by an attention call over `n_req`
- * requests whose key rows total at most `key_rows_bound`, with `row_tiles`
- * 16-row tiles per (request, KV head): ceil(max_q/8) for varlen/verify, max
- * blocks per request for draft.  Layout: FP32 partial outputs, then FP32
- * (max, sum) pairs.  Each attention call is a chunk kernel plus a merge
- * kernel on `stream`; calls that share a workspace must not overlap in time.
- * Returns -1 on invalid input.
+ * Bytes of split-K workspace needed by an attention call.  Layout: FP32
+ * partial outputs, then FP32 (max, sum) pairs, for `n` partial slots of 8 KV
+ * heads x `row_tiles` 16-row tiles (row_tiles = ceil(max_q/8) for
+ * varlen/verify, max blocks per request for draft), where
+ *   n = ceil(key_rows_bound / chunk) + n_req    (fixed chunks, no work list)
+ * A varlen/verify call with a work list of n_work segments needs
+ * dspark_attn_workspace_bytes(n_work, 0, row_tiles, chunk) bytes.  Each
+ * attention call is a chunk kernel plus a merge kernel on `stream`; calls
+ * that share a workspace must not overlap in time.  Returns -1 on invalid
+ * input.
  */
 int64_t dspark_attn_workspace_bytes(int n_req, int64_t key_rows_bound, int row_tiles, int chunk);
 
 /*
- * Work lists.  Every attention entry point splits request r's keys into
- * ceil(len_r / chunk) chunks (at least one) and runs one workgroup per
- * (chunk, KV head).  With work == NULL the chunks are dispatched in request
- * order over a grid sized from the row bound.  Otherwise work holds
- * int32 [n_work][8] item records - every chunk exactly once, in dispatch
- * order (longest first balances ragged lengths) - followed by int32
- * [n_req][4] request records, so that a workgroup reads one record instead
- * of walking the cumulative arrays:
- *   varlen/verify item: request, chunk, chunk base (sum of the chunk counts
- *     of earlier requests), first query row, query length, key length,
- *     first key row (varlen) or resident slot (verify), chunk count;
- *   draft item: request, chunk, chunk base, context length, first block,
- *     block count, largest anchor, chunk count;
- *   request: chunk base, chunk count, first query row (varlen/verify) or
- *     first block (draft), query length or block count.
- * The records must agree with the cumulative arrays; they are not
- * validated on the device.
+ * Work lists (int32, device memory, built by the caller; not validated on
+ * the device beyond clamping the run ranges to [0, n_work]).
+ *
+ * varlen / verify: segment lists.  A segment is keys [k0, k1) of one
+ * request.  Workgroup (run w, KV head g) processes the records of run w:
+ *   [n_work][8] segment records, grouped by run:
+ *       request, k0, k1, partial slot (-1 when the request has one segment,
+ *       which then writes the output), first query row, query length,
+ *       key length, first key row (varlen) or resident slot (verify)
+ *   [n_groups + 1] run ranges: run w holds records range[w] .. range[w+1]
+ *   [n_req][4] request records: first partial slot, segment count,
+ *       first query row, query length
+ * The segments of a request must cover its keys exactly once, and a split
+ * request's segments must use consecutive partial slots in key order (the
+ * merge folds them in slot order).  Cuts at the same key positions give
+ * bit-identical outputs; a balanced plan (equal keys per run) moves the cuts
+ * with the batch, a request-local plan (cuts at multiples of a fixed chunk)
+ * makes every request's output independent of the batch.
+ * Without a list (work == NULL) a persistent grid walks fixed chunks of
+ * `chunk` keys in request order: the launch depends only on n_req,
+ * key_rows_bound and max_q (the capacity-tail kernel relies on this).
+ *
+ * draft: item lists.  Request r's context is split into ceil(len_r / chunk)
+ * chunks (at least one) and one workgroup runs per (chunk, KV head); work
+ * holds int32 [n_work][8] item records, every chunk exactly once in dispatch
+ * order (longest first balances ragged lengths), then int32 [n_req][4]
+ * request records:
+ *   item: request, chunk, chunk base (sum of the chunk counts of earlier
+ *     requests), context length, first block, block count, largest anchor,
+ *     chunk count;
+ *   request: chunk base, chunk count, first block, block count.
  *
  * Packed varlen attention, bottom-right causal (causal=1) or noncausal.
  * q [q_rows,16,128], k/v [k_rows,8,128], cu_q/cu_k int32 [n_req+1].
@@ -70,7 +87,7 @@ int64_t dspark_attn_workspace_bytes(int n_req, int64_t key_rows_bound, int row_t
 int dspark_varlen_attn_fwd(const void* q, const void* k, const void* v,
                            const int32_t* cu_q, const int32_t* cu_k, int n_req,
                            int64_t q_rows, int64_t k_rows, int max_q, int causal,
-                           float scale, int chunk, const int32_t* work, int n_work,
+                           float scale, int chunk, const int32_t* work, int n_work, int n_groups,
                            void* out, void* workspace, int64_t workspace_bytes, void* stream);
 
 /*
@@ -92,7 +109,7 @@ int dspark_verify_attn_fwd(const void* q, const void* k_res, const void* v_res,
                            const int32_t* cu_q, const int32_t* cu_k, const int32_t* slots,
                            int n_req, int64_t slot_stride, int64_t tok_stride, int64_t head_stride,
                            int64_t key_rows_bound, int max_q, float scale, int chunk,
-                           const int32_t* work, int n_work, void* out,
+                           const int32_t* work, int n_work, int n_groups, void* out,
                            void* workspace, int64_t workspace_bytes, void* stream);
 
 /*
@@ -109,7 +126,7 @@ int dspark_verify_attn_staged_fwd(const void* q, const void* k_res, const void* 
                                   const int32_t* cu_q, const int32_t* cu_k, const int32_t* slots,
                                   int n_req, int64_t slot_stride, int64_t tok_stride, int64_t head_stride,
                                   int64_t key_rows_bound, int max_q, float scale, int chunk,
-                                  const int32_t* work, int n_work, void* out,
+                                  const int32_t* work, int n_work, int n_groups, void* out,
                                   void* workspace, int64_t workspace_bytes, void* stream);
 
 /*

@@ -24,6 +24,19 @@ def require_gfx950(device):
     return device
 
 
+_CU_COUNTS = {}
+
+
+def cu_count(device):
+    """Compute units of a GPU (cached per device index)."""
+    device = torch.device(device)
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    n = _CU_COUNTS.get(idx)
+    if n is None:
+        n = _CU_COUNTS[idx] = int(torch.cuda.get_device_properties(idx).multi_processor_count)
+    return n
+
+
 class Workspace:
     """Grow-only device scratch (uint8) reused across calls on one device."""
 

@@ -23,11 +23,11 @@ SIGNATURES = {
     'dspark_last_error': (ctypes.c_char_p, []),
     'dspark_abi_version': (_I, []),
     'dspark_attn_workspace_bytes': (_L, [_I, _L, _I, _I]),
-    'dspark_varlen_attn_fwd': (_I, [_P, _P, _P, _P, _P, _I, _L, _L, _I, _I, _F, _I, _P, _I, _P, _P, _L, _P]),
-    'dspark_verify_attn_fwd': (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _I, _L, _L, _L, _L, _I, _F, _I, _P, _I,
+    'dspark_varlen_attn_fwd': (_I, [_P, _P, _P, _P, _P, _I, _L, _L, _I, _I, _F, _I, _P, _I, _I, _P, _P, _L, _P]),
+    'dspark_verify_attn_fwd': (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _I, _L, _L, _L, _L, _I, _F, _I, _P, _I, _I,
                                     _P, _P, _L, _P]),
     'dspark_verify_attn_staged_fwd': (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _L, _L, _L, _L, _I, _F, _I,
-                                           _P, _I, _P, _P, _L, _P]),
+                                           _P, _I, _I, _P, _P, _L, _P]),
     'dspark_draft_attn_fwd': (_I, [_P, _P, _P, _P, _P, _P, _L, _L, _P, _P, _P, _P, _I, _L, _I, _F, _I, _P, _I,
                                    _P, _P, _L, _P]),
     'dspark_txn_metadata': (_I, [_P, _I, _L, _L, _L, _P, _P, _P, _P, _P, _P, _P, _P]),
@@ -44,7 +44,7 @@ SIGNATURES = {
     'dspark_rows_rebuild': (_I, [_PP, _PP, _PP, _I, _I, _L, _L, _L, _P, _L, _P]),
 }
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 
 class NativeError(RuntimeError):

@@ -30,11 +30,14 @@
 // is irrelevant as long as A and B use the same (lane group, slot) -> k
 // assignment, which both operands here do by construction.
 //
-// Long contexts are split into chunks of keys (flash-decoding, Dao et al.
-// 2023); every (request, chunk, KV head) is one workgroup.  A request with
-// more than one chunk writes FP32 partial (max, sum, unnormalised O) triples
-// that merge_kernel combines; the kernel boundary makes them visible without
-// any per-workgroup cache flush.
+// Long contexts are split into key segments (flash-decoding, Dao et al.
+// 2023).  With a host-built segment list every workgroup (run, KV head)
+// streams the segments of its run: a balanced list gives every run the same
+// number of keys, cutting requests where runs meet (stream-K style), so the
+// grid drains evenly whatever the mix of context lengths.  A request held by
+// more than one segment writes FP32 partial (max, sum, unnormalised O)
+// triples that merge_kernel combines; the kernel boundary makes them visible
+// without any per-workgroup cache flush.
 #include <type_traits>
 
 #include "common.h"
@@ -262,14 +265,15 @@ struct VarlenArgs {
   int64_t slot_stride;    // verify: elements between resident slots
   int64_t a_tok_stride;   // segment A elements between token rows
   int64_t a_head_stride;  // segment A elements between KV heads
-  const int32_t* work;    // optional work records (see the C ABI)
+  const int32_t* work;    // optional segment list (see the C ABI)
   bf16* stage_k;          // verify with staging: scratch written from segment B (k_b/v_b = new rows)
   bf16* stage_v;
   bf16* out;              // [nq, 16, 128]
   float* part_o;          // [n_cl*8*tmax][16][128]
   float* part_ml;         // [n_cl*8*tmax][16][2]
   int n_req;
-  int n_slots;            // (item, KV head) slots: 8 * items
+  int n_work;             // segment records in the work list
+  int n_slots;            // no list: (chunk, KV head) slots, 8 * chunks
   int causal;
   int chunk;
   int tmax;
@@ -279,45 +283,51 @@ struct VarlenArgs {
 constexpr int VARLEN_SMEM = 4 * 16 * OPITCH * 4 + 4 * 16 * 2 * 4;   // 34304 B (>= 4*32*256)
 static_assert(VARLEN_SMEM >= 4 * KT * ROWB, "merge buffer must cover the V tiles");
 
-// One (chunk item, KV head, row tile) of varlen / verify attention.  Every
+// One key segment of one request: keys [k0, k1) of request r, whose
+// queries start at row q0 (ql of them) and whose keys number kl; start is
+// the first key row (varlen) or the resident slot (verify).  A request cut
+// into several segments writes FP32 partials to slot pslot (>= 0) for the
+// merge kernel; a request held by one segment (pslot < 0) writes its output.
+struct Segment {
+  int r, k0, k1, pslot, q0, ql, kl, start;
+};
+
+// Fixed chunking without a work list: linear chunk index cl of the grid
+// (requests in order, ceil(kl / chunk) chunks each, at least one).
+__device__ __forceinline__ bool chunk_segment(const VarlenArgs& a, bool verify, int cl, Segment& s) {
+  int r, first;
+  locate_chunk(a.cu_k, nullptr, a.n_req, a.chunk, cl, r, first);
+  if (r < 0) return false;
+  const int c = cl - first;
+  s.r = r;
+  s.q0 = a.cu_q[r];
+  s.ql = a.cu_q[r + 1] - s.q0;
+  s.kl = a.cu_k[r + 1] - a.cu_k[r];
+  s.start = verify ? a.slots[r] : a.cu_k[r];
+  s.k0 = c * a.chunk;
+  s.k1 = min(s.k0 + a.chunk, s.kl);
+  s.pslot = chunks_for(s.kl, a.chunk) > 1 ? first + c : -1;
+  return true;
+}
+
+// One (segment, KV head, row tile) of varlen / verify attention.  Every
 // early return is uniform across the workgroup.
 template <bool VERIFY>
-__device__ __forceinline__ void varlen_item(const VarlenArgs& a, unsigned char* smem, int idx, int t) {
+__device__ __forceinline__ void varlen_item(const VarlenArgs& a, unsigned char* smem, const Segment& sg, int g, int t) {
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int col = lane & 15;
   const int grp = lane >> 4;
-  const int g = idx & 7;
-  const int cl = idx >> 3;
-
-  // Work record (one scalar load): request, chunk, chunk base, query start
-  // and length, key length, key start (varlen) or resident slot (verify),
-  // chunk count.  Without a list the grid walks the chunks in request order.
-  int r, first, c, q0, ql, kl, start, nch;
-  if (a.work) {
-    const int32_t* w = a.work + WORK_INTS * cl;
-    r = w[0];
-    c = w[1];
-    first = w[2];
-    q0 = w[3];
-    ql = w[4];
-    kl = w[5];
-    start = w[6];
-    nch = w[7];
-  } else {
-    locate_chunk(a.cu_k, nullptr, a.n_req, a.chunk, cl, r, first);
-    if (r < 0) return;
-    c = cl - first;
-    q0 = a.cu_q[r];
-    ql = a.cu_q[r + 1] - q0;
-    kl = a.cu_k[r + 1] - a.cu_k[r];
-    start = VERIFY ? a.slots[r] : a.cu_k[r];
-    nch = chunks_for(kl, a.chunk);
-  }
-  const int item = first + c;   // partial slot (request-major chunk numbering)
+  // The segment is wave-uniform; say so, so that its fields and everything
+  // derived from them stay in scalar registers.
+  const int q0 = __builtin_amdgcn_readfirstlane(sg.q0);
+  const int ql = __builtin_amdgcn_readfirstlane(sg.ql);
+  const int kl = __builtin_amdgcn_readfirstlane(sg.kl);
+  const int start = __builtin_amdgcn_readfirstlane(sg.start);
+  const int k0 = __builtin_amdgcn_readfirstlane(sg.k0);
+  const int k1 = __builtin_amdgcn_readfirstlane(sg.k1);
+  const int pslot = __builtin_amdgcn_readfirstlane(sg.pslot);
   if (8 * t >= ql) return;
-  const int k0 = c * a.chunk;
-  const int k1 = min(k0 + a.chunk, kl);
 
   // Key j of this request lives in segment A for j < a_len, else segment B.
   const bf16* kA;
@@ -333,9 +343,10 @@ __device__ __forceinline__ void varlen_item(const VarlenArgs& a, unsigned char* 
     const size_t bbase = (size_t)q0 * KV_ROW + (size_t)g * HD;
     kB = a.k_b + bbase;
     vB = a.v_b + bbase;
-    if (a.stage_k && c == nch - 1 && t == 0) {
-      // Fused stage: this workgroup is the only reader of the request's new
-      // rows for KV head g, so it also copies them into the scratch layer.
+    if (a.stage_k && k1 == kl && t == 0) {
+      // Fused stage: the workgroup holding the request's last segment is the
+      // only reader of its new rows for KV head g, so it also copies them
+      // into the scratch layer.
       for (int i = threadIdx.x; i < 2 * ql * 16; i += 256) {
         const int which = i / (ql * 16);
         const int rem = i - which * ql * 16;
@@ -435,16 +446,19 @@ __device__ __forceinline__ void varlen_item(const VarlenArgs& a, unsigned char* 
     for (int j = 0; j < 2; ++j) koff[j] = (uint32_t)(((8 * (col >> 2) + 4 * j + (col & 3)) * ts + 8 * grp) * 2);
     #pragma unroll
     for (int i2 = 0; i2 < 8; ++i2) voff[i2] = (uint32_t)(((4 * i2 + grp) * ts + 8 * col) * 2);
-    for (; kt + KT <= kfast; kt += KT * 4) {
-      const char* kb = reinterpret_cast<const char*>(kA + (size_t)kt * ts);
-      const char* vb = reinterpret_cast<const char*>(vA + (size_t)kt * ts);
-      Tile T;
+    auto load_fast = [&](int kk, Tile& T) {
+      const char* kb = reinterpret_cast<const char*>(kA + (size_t)kk * ts);
+      const char* vb = reinterpret_cast<const char*>(vA + (size_t)kk * ts);
       #pragma unroll
       for (int j = 0; j < 2; ++j)
         #pragma unroll
         for (int ks = 0; ks < 4; ++ks) T.k[j][ks] = *reinterpret_cast<const bf16x8*>(kb + koff[j] + 64 * ks);
       #pragma unroll
       for (int i2 = 0; i2 < 8; ++i2) T.v[i2] = *reinterpret_cast<const bf16x8*>(vb + voff[i2]);
+    };
+    for (; kt + KT <= kfast; kt += KT * 4) {
+      Tile T;
+      load_fast(kt, T);
       compute_tile(kt, T, std::false_type{});
     }
   }
@@ -489,8 +503,8 @@ __device__ __forceinline__ void varlen_item(const VarlenArgs& a, unsigned char* 
   const int tok_r = 8 * t + (row >> 1);
   const int head_r = 2 * g + (row & 1);
   bf16* orow = a.out + (size_t)(q0 + tok_r) * Q_ROW + (size_t)head_r * HD + d0;
-  if (nch > 1) {
-    const size_t p = (size_t)(item * 8 + g) * a.tmax + t;
+  if (pslot >= 0) {
+    const size_t p = (size_t)(pslot * 8 + g) * a.tmax + t;
     float* po = a.part_o + (p * 16 + row) * HD + d0;
     *reinterpret_cast<f32x4*>(po) = f32x4{acc[0], acc[1], acc[2], acc[3]};
     *reinterpret_cast<f32x4*>(po + 4) = f32x4{acc[4], acc[5], acc[6], acc[7]};
@@ -508,15 +522,31 @@ __device__ __forceinline__ void varlen_item(const VarlenArgs& a, unsigned char* 
   }
 }
 
-// Persistent grid: each workgroup walks (item, KV head) slots with a stride
-// of the grid size, so per-workgroup start-up is paid once per CU slot
-// rather than once per chunk.
+// With a work list, workgroup (w, g) runs the segments w's range of records
+// names, for KV head g (blockIdx.x = 8w + g).  Without one, a persistent
+// grid walks the fixed chunks (item, KV head) with a stride of the grid
+// size, so per-workgroup start-up is paid once per CU slot.
 template <bool VERIFY>
 __global__ __launch_bounds__(256) void varlen_attn_kernel(VarlenArgs a) {
   __shared__ __attribute__((aligned(16))) unsigned char smem[VARLEN_SMEM];
+  const int g = blockIdx.x & 7;
+  if (a.work) {
+    const int32_t* range = a.work + WORK_INTS * a.n_work + (blockIdx.x >> 3);
+    const int b = min(max(range[0], 0), a.n_work);      // clamped: never past the records
+    const int e = min(max(range[1], b), a.n_work);
+    for (int i = b; i < e; ++i) {
+      const int32_t* w = a.work + WORK_INTS * i;
+      const Segment sg{w[0], w[1], w[2], w[3], w[4], w[5], w[6], w[7]};
+      varlen_item<VERIFY>(a, smem, sg, g, blockIdx.y);
+      __syncthreads();   // the next segment reuses the LDS tiles and merge buffer
+    }
+    return;
+  }
   for (int idx = blockIdx.x; idx < a.n_slots; idx += gridDim.x) {
-    varlen_item<VERIFY>(a, smem, idx, blockIdx.y);
-    __syncthreads();   // the next item reuses the LDS tiles and merge buffer
+    Segment sg;
+    if (!chunk_segment(a, VERIFY, idx >> 3, sg)) break;
+    varlen_item<VERIFY>(a, smem, sg, g, blockIdx.y);
+    __syncthreads();
   }
 }
 
@@ -881,8 +911,7 @@ int launch_merge(const MergeArgs& m, int n_req, int tiles, hipStream_t s) {
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
-int check_common(int n_req, int64_t rows_bound, int tiles, int chunk, float scale,
-                 int64_t ws_bytes, const void* ws) {
+int check_shape(int n_req, int64_t rows_bound, int tiles, int chunk, float scale) {
   DSPARK_REQUIRE(n_req >= 1, "n_req must be >= 1 (got %d)", n_req);
   DSPARK_REQUIRE(rows_bound >= 0, "key row bound must be >= 0");
   DSPARK_REQUIRE(tiles >= 1 && tiles <= 65535, "row tiles out of range (%d)", tiles);
@@ -890,6 +919,13 @@ int check_common(int n_req, int64_t rows_bound, int tiles, int chunk, float scal
   DSPARK_REQUIRE(scale > 0.f && scale < 1e30f, "scale must be positive and finite");
   const int64_t items = n_chunk_items(n_req, rows_bound, chunk) * HKV;
   DSPARK_REQUIRE(items <= 0x7fffffffLL, "too many chunk work items (%lld)", (long long)items);
+  return OK;
+}
+
+int check_common(int n_req, int64_t rows_bound, int tiles, int chunk, float scale,
+                 int64_t ws_bytes, const void* ws) {
+  const int rc = check_shape(n_req, rows_bound, tiles, chunk, scale);
+  if (rc != OK) return rc;
   const int64_t need = workspace_bytes(n_req, rows_bound, tiles, chunk);
   DSPARK_REQUIRE(ws_bytes >= need, "workspace too small: %lld < %lld bytes", (long long)ws_bytes, (long long)need);
   DSPARK_REQUIRE(need == 0 || (ws != nullptr && aligned16(ws)), "workspace must be a 16-byte aligned device pointer");
@@ -903,10 +939,51 @@ extern "C" int64_t dspark_attn_workspace_bytes(int n_req, int64_t key_rows_bound
   return workspace_bytes(n_req, key_rows_bound, row_tiles, chunk);
 }
 
+namespace {
+
+// Shared by the varlen and verification entry points: argument checks that
+// depend on the dispatch form, the split-K workspace layout and both launches.
+// With a work list the partial slots are bounded by its record count, else by
+// the fixed-chunk bound of key_rows_bound.
+template <bool VERIFY>
+int varlen_launch(VarlenArgs& a, int64_t key_rows_bound, int max_q, float scale, int chunk, const int32_t* work,
+                  int n_work, int n_groups, void* workspace, int64_t workspace_bytes_, void* stream, const char* what) {
+  DSPARK_REQUIRE(max_q >= 1, "max_q must be >= 1");
+  DSPARK_REQUIRE(!work || (n_work >= 1 && n_groups >= 1 && n_groups <= (1 << 24)),
+                 "a work list needs n_work >= 1 and n_groups in [1, 2^24]");
+  const int tiles = (max_q + 7) / 8;
+  int rc = check_shape(work ? n_work : a.n_req, work ? 0 : key_rows_bound, tiles, chunk, scale);
+  if (rc != OK) return rc;
+  const int64_t n_cl = work ? (int64_t)n_work : n_chunk_items(a.n_req, key_rows_bound, chunk);
+  const int64_t need = workspace_bytes(work ? n_work : a.n_req, work ? 0 : key_rows_bound, tiles, chunk);
+  DSPARK_REQUIRE(workspace_bytes_ >= need, "workspace too small: %lld < %lld bytes", (long long)workspace_bytes_,
+                 (long long)need);
+  DSPARK_REQUIRE(need == 0 || (workspace != nullptr && aligned16(workspace)),
+                 "workspace must be a 16-byte aligned device pointer");
+  a.work = work;
+  a.n_work = n_work;
+  a.part_o = static_cast<float*>(workspace);
+  a.part_ml = a.part_o + n_cl * HKV * tiles * 16 * HD;
+  a.chunk = chunk;
+  a.tmax = tiles;
+  a.scale_log2 = scale * LOG2E;
+  a.n_slots = (int)(n_cl * HKV);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const unsigned grid = work ? (unsigned)n_groups * HKV : persistent_grid(a.n_slots, tiles);
+  hipLaunchKernelGGL(varlen_attn_kernel<VERIFY>, dim3(grid, tiles), dim3(256), 0, s, a);
+  rc = launch_status(what);
+  if (rc != OK) return rc;
+  MergeArgs m{work ? work + WORK_INTS * n_work + n_groups + 1 : nullptr, a.cu_q, a.cu_k, nullptr, nullptr, a.part_o,
+              a.part_ml, a.out, a.n_req, chunk, tiles, 0};
+  return launch_merge(m, a.n_req, tiles, s);
+}
+
+}  // namespace
+
 extern "C" int dspark_varlen_attn_fwd(const void* q, const void* k, const void* v,
                                       const int32_t* cu_q, const int32_t* cu_k, int n_req,
                                       int64_t q_rows, int64_t k_rows, int max_q, int causal,
-                                      float scale, int chunk, const int32_t* work, int n_work,
+                                      float scale, int chunk, const int32_t* work, int n_work, int n_groups,
                                       void* out, void* workspace,
                                       int64_t workspace_bytes_, void* stream) {
   clear_error();
@@ -914,12 +991,7 @@ extern "C" int dspark_varlen_attn_fwd(const void* q, const void* k, const void* 
   DSPARK_REQUIRE(aligned16(q) && aligned16(k) && aligned16(v) && aligned16(out), "Q/K/V/out must be 16-byte aligned");
   DSPARK_REQUIRE(q_rows >= 1 && k_rows >= 1, "Q and K must be nonempty");
   DSPARK_REQUIRE(max_q >= 1 && max_q <= q_rows, "max_q must be in [1, q_rows]");
-  DSPARK_REQUIRE(!work || n_work >= 1, "n_work must be >= 1 with a work list");
-  const int tiles = (max_q + 7) / 8;
-  int rc = check_common(n_req, k_rows, tiles, chunk, scale, workspace_bytes_, workspace);
-  if (rc != OK) return rc;
-  const int64_t n_cl = n_chunk_items(n_req, k_rows, chunk);
-  DSPARK_REQUIRE(!work || n_work <= n_cl, "work list longer than the chunk bound");
+  DSPARK_REQUIRE(n_req >= 1, "n_req must be >= 1 (got %d)", n_req);
   VarlenArgs a{};
   a.q = static_cast<const bf16*>(q);
   a.k_a = static_cast<const bf16*>(k);
@@ -932,23 +1004,11 @@ extern "C" int dspark_varlen_attn_fwd(const void* q, const void* k, const void* 
   a.slot_stride = 0;
   a.a_tok_stride = KV_ROW;
   a.a_head_stride = HD;
-  a.work = work;
   a.out = static_cast<bf16*>(out);
-  a.part_o = static_cast<float*>(workspace);
-  a.part_ml = a.part_o + n_cl * HKV * tiles * 16 * HD;
   a.n_req = n_req;
   a.causal = causal ? 1 : 0;
-  a.chunk = chunk;
-  a.tmax = tiles;
-  a.scale_log2 = scale * LOG2E;
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  a.n_slots = (int)(work ? (int64_t)n_work * HKV : n_cl * HKV);
-  hipLaunchKernelGGL(varlen_attn_kernel<false>, dim3(persistent_grid(a.n_slots, tiles), tiles), dim3(256), 0, s, a);
-  rc = launch_status("varlen_attn_kernel");
-  if (rc != OK) return rc;
-  MergeArgs m{work ? work + WORK_INTS * n_work : nullptr, cu_q, cu_k, nullptr, nullptr, a.part_o, a.part_ml, a.out,
-              n_req, chunk, tiles, 0};
-  return launch_merge(m, n_req, tiles, s);
+  return varlen_launch<false>(a, k_rows, max_q, scale, chunk, work, n_work, n_groups, workspace, workspace_bytes_,
+                              stream, "varlen_attn_kernel");
 }
 
 namespace {
@@ -956,7 +1016,7 @@ int verify_launch(const void* q, const void* k_res, const void* v_res, const voi
                   void* stage_k, void* stage_v, const int32_t* cu_q, const int32_t* cu_k, const int32_t* slots,
                   int n_req, int64_t slot_stride, int64_t tok_stride, int64_t head_stride,
                   int64_t key_rows_bound, int max_q, float scale, int chunk,
-                  const int32_t* work, int n_work, void* out, void* workspace,
+                  const int32_t* work, int n_work, int n_groups, void* out, void* workspace,
                   int64_t workspace_bytes_, void* stream) {
   DSPARK_REQUIRE(q && k_res && v_res && k_b && v_b && cu_q && cu_k && slots && out, "null pointer argument");
   DSPARK_REQUIRE(aligned16(q) && aligned16(k_res) && aligned16(v_res) && aligned16(k_b) && aligned16(v_b) && aligned16(out) &&
@@ -964,13 +1024,8 @@ int verify_launch(const void* q, const void* k_res, const void* v_res, const voi
                  "Q/K/V/out must be 16-byte aligned");
   DSPARK_REQUIRE(slot_stride >= 0 && tok_stride >= HD && tok_stride % 8 == 0 && head_stride >= HD && head_stride % 8 == 0,
                  "resident strides must be multiples of 8 elements (token/head strides >= 128)");
-  DSPARK_REQUIRE(max_q >= 1, "max_q must be >= 1");
-  DSPARK_REQUIRE(!work || n_work >= 1, "n_work must be >= 1 with a work list");
-  const int tiles = (max_q + 7) / 8;
-  int rc = check_common(n_req, key_rows_bound, tiles, chunk, scale, workspace_bytes_, workspace);
-  if (rc != OK) return rc;
-  const int64_t n_cl = n_chunk_items(n_req, key_rows_bound, chunk);
-  DSPARK_REQUIRE(!work || n_work <= n_cl, "work list longer than the chunk bound");
+  DSPARK_REQUIRE(n_req >= 1, "n_req must be >= 1 (got %d)", n_req);
+  DSPARK_REQUIRE(key_rows_bound >= 0, "key row bound must be >= 0");
   VarlenArgs a{};
   a.q = static_cast<const bf16*>(q);
   a.k_a = static_cast<const bf16*>(k_res);
@@ -985,23 +1040,11 @@ int verify_launch(const void* q, const void* k_res, const void* v_res, const voi
   a.slot_stride = slot_stride;
   a.a_tok_stride = tok_stride;
   a.a_head_stride = head_stride;
-  a.work = work;
   a.out = static_cast<bf16*>(out);
-  a.part_o = static_cast<float*>(workspace);
-  a.part_ml = a.part_o + n_cl * HKV * tiles * 16 * HD;
   a.n_req = n_req;
   a.causal = 1;
-  a.chunk = chunk;
-  a.tmax = tiles;
-  a.scale_log2 = scale * LOG2E;
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  a.n_slots = (int)(work ? (int64_t)n_work * HKV : n_cl * HKV);
-  hipLaunchKernelGGL(varlen_attn_kernel<true>, dim3(persistent_grid(a.n_slots, tiles), tiles), dim3(256), 0, s, a);
-  rc = launch_status("verify_attn_kernel");
-  if (rc != OK) return rc;
-  MergeArgs m{work ? work + WORK_INTS * n_work : nullptr, cu_q, cu_k, nullptr, nullptr, a.part_o, a.part_ml, a.out,
-              n_req, chunk, tiles, 0};
-  return launch_merge(m, n_req, tiles, s);
+  return varlen_launch<true>(a, key_rows_bound, max_q, scale, chunk, work, n_work, n_groups, workspace,
+                             workspace_bytes_, stream, "verify_attn_kernel");
 }
 }  // namespace
 
@@ -1010,12 +1053,12 @@ extern "C" int dspark_verify_attn_fwd(const void* q, const void* k_res, const vo
                                       const int32_t* cu_q, const int32_t* cu_k, const int32_t* slots,
                                       int n_req, int64_t slot_stride, int64_t tok_stride, int64_t head_stride,
                                       int64_t key_rows_bound, int max_q, float scale, int chunk,
-                                      const int32_t* work, int n_work, void* out, void* workspace,
+                                      const int32_t* work, int n_work, int n_groups, void* out, void* workspace,
                                       int64_t workspace_bytes_, void* stream) {
   clear_error();
   return verify_launch(q, k_res, v_res, k_scr, v_scr, nullptr, nullptr, cu_q, cu_k, slots, n_req, slot_stride,
-                       tok_stride, head_stride, key_rows_bound, max_q, scale, chunk, work, n_work, out, workspace,
-                       workspace_bytes_, stream);
+                       tok_stride, head_stride, key_rows_bound, max_q, scale, chunk, work, n_work, n_groups, out,
+                       workspace, workspace_bytes_, stream);
 }
 
 extern "C" int dspark_verify_attn_staged_fwd(const void* q, const void* k_res, const void* v_res,
@@ -1023,14 +1066,14 @@ extern "C" int dspark_verify_attn_staged_fwd(const void* q, const void* k_res, c
                                              const int32_t* cu_q, const int32_t* cu_k, const int32_t* slots,
                                              int n_req, int64_t slot_stride, int64_t tok_stride, int64_t head_stride,
                                              int64_t key_rows_bound, int max_q, float scale, int chunk,
-                                             const int32_t* work, int n_work, void* out, void* workspace,
+                                             const int32_t* work, int n_work, int n_groups, void* out, void* workspace,
                                              int64_t workspace_bytes_, void* stream) {
   clear_error();
   DSPARK_REQUIRE(k_scr && v_scr, "null pointer argument");
   DSPARK_REQUIRE(k_new != k_scr && v_new != v_scr, "new rows and scratch must be distinct buffers");
   return verify_launch(q, k_res, v_res, k_new, v_new, k_scr, v_scr, cu_q, cu_k, slots, n_req, slot_stride,
-                       tok_stride, head_stride, key_rows_bound, max_q, scale, chunk, work, n_work, out, workspace,
-                       workspace_bytes_, stream);
+                       tok_stride, head_stride, key_rows_bound, max_q, scale, chunk, work, n_work, n_groups, out,
+                       workspace, workspace_bytes_, stream);
 }
 
 extern "C" int dspark_draft_attn_fwd(const void* q, const void* k_ctx, const void* v_ctx,

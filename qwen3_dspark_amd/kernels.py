@@ -15,8 +15,8 @@ import math
 import torch
 
 from . import _native
-from ._device import Workspace, require_gfx950
-from .schedule import DEFAULT_CHUNK, upload_work, varlen_work
+from ._device import Workspace, cu_count, require_gfx950
+from .schedule import DEFAULT_CHUNK, SPLITS, run_count, segment_plan, upload_work
 
 Q_HEADS, KV_HEADS, HEAD_DIM = 16, 8, 128
 SCALE = 128 ** -0.5
@@ -33,10 +33,13 @@ class HipVarlenKernel:
     native_varlen_calls_per_layer = 1
     causal = True
 
-    def __init__(self, device, *, chunk=DEFAULT_CHUNK):
+    def __init__(self, device, *, chunk=DEFAULT_CHUNK, split='balanced'):
         self.device = require_gfx950(device)
         _native.load()
+        if split not in SPLITS:
+            raise ValueError(f'split must be one of {SPLITS}')
         self.chunk = int(chunk)
+        self.split = split
         self._workspace = Workspace(self.device)
         self._validated_layout = None
         self._layout_versions = None
@@ -89,17 +92,19 @@ class HipVarlenKernel:
             raise ValueError('Cumulative lengths differ from packed metadata')
         self._validated_layout, self._layout_versions = layout, versions
 
-    def _work_list(self, layout):
-        # One longest-first record list per layout shape (its lengths are
+    def _work_list(self, layout, tiles):
+        # One balanced segment list per layout shape (its lengths are
         # immutable host tuples), uploaded once and reused by every layer.
-        key = (layout.query_lengths, layout.key_lengths, self.chunk)
+        key = (layout.query_lengths, layout.key_lengths, tiles)
         if self._work_for != key:
             starts, acc = [], 0
             for k in layout.key_lengths:
                 starts.append(acc)
                 acc += k
-            records, n_items = varlen_work(layout.query_lengths, layout.key_lengths, starts, self.chunk)
-            self._work = (upload_work(records, self.device), n_items)
+            runs = run_count(acc, cu_count(self.device), tiles)
+            records, n_segments, runs = segment_plan(self.split, layout.query_lengths, layout.key_lengths, starts,
+                                                     runs, self.chunk)
+            self._work = (upload_work(records, self.device), n_segments, runs)
             self._work_for = key
         return self._work
 
@@ -107,13 +112,14 @@ class HipVarlenKernel:
         out = torch.empty_like(query)
         n_req = len(layout.query_lengths)
         tiles = (max_q + 7) // 8
-        need = _native.load().dspark_attn_workspace_bytes(n_req, key_rows, tiles, self.chunk)
+        work, n_work, runs = self._work_list(layout, tiles) or (None, 0, 0)
+        lib = _native.load()
+        need = (lib.dspark_attn_workspace_bytes(n_work, 0, tiles, self.chunk) if work is not None
+                else lib.dspark_attn_workspace_bytes(n_req, key_rows, tiles, self.chunk))
         ws = self._workspace.get(need)
-        work, n_work = self._work_list(layout) or (None, 0)
         _native.call('dspark_varlen_attn_fwd', _native.ptr(query), _native.ptr(key), _native.ptr(value),
                      _native.ptr(layout.cu_query), _native.ptr(layout.cu_key), n_req, query.shape[0], key_rows,
-                     max_q, int(self.causal), float(SCALE), self.chunk, _native.ptr(work),
-                     n_work,
+                     max_q, int(self.causal), float(SCALE), self.chunk, _native.ptr(work), n_work, runs,
                      _native.ptr(out), _native.ptr(ws), ws.numel(), _native.stream_handle(self.device))
         return out
 
@@ -142,9 +148,9 @@ class HipCapacityKernel(HipVarlenKernel):
     """
     backend_name = 'mi355x_hip_capacity_causal_v1'
 
-    def _work_list(self, layout):
-        # Request-order dispatch over a grid sized from the capacity: the
-        # same launch for every transaction of a bucket.
+    def _work_list(self, layout, tiles):
+        # Request-order dispatch of fixed chunks over a grid sized from the
+        # capacity: the same launch for every transaction of a bucket.
         return None
 
     def __call__(self, query, key, value, layout, *, scale):

@@ -28,9 +28,9 @@ from typing import Mapping
 import torch
 
 from . import _native
-from ._device import require_gfx950, upload
+from ._device import cu_count, require_gfx950, upload
 from .kernels import HEAD_DIM, KV_HEADS, Q_HEADS, SCALE, _check_scale
-from .schedule import DEFAULT_CHUNK, REQ_INTS, WORK_INTS, chunk_bound, varlen_work
+from .schedule import DEFAULT_CHUNK, REQ_INTS, SPLITS, WORK_INTS, run_count, segment_plan, varlen_list_bound
 
 
 @dataclass(frozen=True)
@@ -147,7 +147,7 @@ class _Workspace:
     """
     _COUNTS = {'cu_query': 'r1', 'cu_key': 'r1', 'positions': 'q', 'req': 'r3', 'work': 'full', 'attn': 'full'}
 
-    def __init__(self, bucket, heads, dim, dtype, device, chunk, arena=None):
+    def __init__(self, bucket, heads, dim, dtype, device, chunk, split, arena=None):
         self.bucket = bucket
         n, r, q = bucket.key_capacity, bucket.request_count, bucket.query_tokens
         if arena is not None:
@@ -173,10 +173,10 @@ class _Workspace:
         self.cu_key = torch.zeros_like(self.cu_query)
         self.positions = torch.zeros(q, dtype=torch.long, device=device)
         self.req = torch.zeros(3 * r, dtype=torch.int32, device=device)
-        self.work = torch.zeros(WORK_INTS * chunk_bound(r, n, chunk) + REQ_INTS * r, dtype=torch.int32, device=device)
+        self.work = torch.zeros(_work_ints(bucket, device, chunk, split), dtype=torch.int32, device=device)
         self.keys = torch.empty((n, heads, dim), dtype=dtype, device=device)
         self.values = torch.empty_like(self.keys)
-        self.attn = torch.zeros(_attn_workspace_bytes(bucket, chunk), dtype=torch.uint8, device=device)
+        self.attn = torch.zeros(_attn_workspace_bytes(bucket, chunk, device, split), dtype=torch.uint8, device=device)
 
     def pointers(self):
         return {k: v.data_ptr() for k, v in vars(self).items() if isinstance(v, torch.Tensor) and v.is_cuda}
@@ -186,9 +186,29 @@ class _Workspace:
                                 for k, v in vars(self).items() if isinstance(v, torch.Tensor) and v.is_cuda))
 
 
-def _attn_workspace_bytes(bucket, chunk):
+def _max_runs(bucket, device):
+    """Most balanced-list runs any transaction of the bucket uses (its key
+    capacity bounds the keys of every transaction)."""
+    return run_count(bucket.key_capacity, cu_count(device), (bucket.maximum_query_length + 7) // 8)
+
+
+def _max_segments(bucket, device, chunk, split):
+    g, r = _max_runs(bucket, device), bucket.request_count
+    return varlen_list_bound(r, g, bucket.key_capacity, None if split == 'balanced' else chunk)
+
+
+def _work_ints(bucket, device, chunk, split):
+    """int32 length of the largest work list of the bucket."""
+    g, r = _max_runs(bucket, device), bucket.request_count
+    return WORK_INTS * _max_segments(bucket, device, chunk, split) + g + 1 + REQ_INTS * r
+
+
+def _attn_workspace_bytes(bucket, chunk, device, split):
+    """Split-K partials for the largest work list of the bucket (one slot
+    per segment at most)."""
     tiles = (bucket.maximum_query_length + 7) // 8
-    return max(16, int(_native.load().dspark_attn_workspace_bytes(bucket.request_count, bucket.key_capacity, tiles, chunk)))
+    segments = _max_segments(bucket, device, chunk, split)
+    return max(16, int(_native.load().dspark_attn_workspace_bytes(segments, 0, tiles, chunk)))
 
 
 class PersistentTargetKV:
@@ -202,7 +222,7 @@ class PersistentTargetKV:
     """
 
     def __init__(self, *, layers, slots, context_capacity, max_query_tokens,
-                 heads, dim, dtype=torch.bfloat16, device='cuda', chunk=DEFAULT_CHUNK):
+                 heads, dim, dtype=torch.bfloat16, device='cuda', chunk=DEFAULT_CHUNK, split='balanced'):
         dims = (layers, slots, context_capacity, max_query_tokens, heads, dim)
         if any(type(n) is not int or n < 1 for n in dims):
             raise ValueError('All capacities and dimensions must be positive integers')
@@ -216,7 +236,10 @@ class PersistentTargetKV:
         self.layers, self.slot_capacity, self.context_capacity = layers, slots, context_capacity
         self.max_query_tokens, self.heads, self.dim = max_query_tokens, heads, dim
         self.dtype = dtype
+        if split not in SPLITS:
+            raise ValueError(f'split must be one of {SPLITS}')
         self.chunk = int(chunk)
+        self.split = split
         self._elem = elem
         # Head-major storage; the public tensors are reference-shaped views.
         self._keys = torch.zeros((layers, slots, heads, context_capacity, dim), dtype=dtype, device=self.device)
@@ -238,7 +261,7 @@ class PersistentTargetKV:
         self._writers = {}
         self._external = None
         self._submission_generation = 0
-        self._n_work = 0
+        self._n_work = (0, 0)      # (segments, runs) of the open transaction's work list
         # Committed-state generation: bumped by every mutation of slots or
         # lengths; a transaction is valid only while it is unchanged, which
         # replaces a per-call scan over the transaction's handles.
@@ -340,14 +363,15 @@ class PersistentTargetKV:
         if bucket.request_count > 4096:
             raise ValueError('At most 4096 requests per bucket')
         if bucket not in self._workspaces:
-            self._workspaces[bucket] = _Workspace(bucket, self.heads, self.dim, self.dtype, self.device, self.chunk)
+            self._workspaces[bucket] = _Workspace(bucket, self.heads, self.dim, self.dtype, self.device, self.chunk,
+                                                  self.split)
 
     def workspace_bytes(self, bucket):
         """Exact device allocation of a bucket workspace before registering it."""
         n, r, q = bucket.key_capacity, bucket.request_count, bucket.query_tokens
         kv = 2 * n * self.heads * self.dim * self.keys.element_size()
-        return (kv + 18 * n + 8 * (r + 1) + 8 * q + 12 * r + 8 * chunk_bound(r, n, self.chunk)
-                + _attn_workspace_bytes(bucket, self.chunk))
+        return (kv + 18 * n + 8 * (r + 1) + 8 * q + 12 * r + 4 * _work_ints(bucket, self.device, self.chunk, self.split)
+                + _attn_workspace_bytes(bucket, self.chunk, self.device, self.split))
 
     def family_arena_shape(self, families):
         """Validate the complete finite declaration before allocating any storage."""
@@ -371,8 +395,9 @@ class PersistentTargetKV:
         shape = self.family_arena_shape(families)
         if shape.request_count > 4096:
             raise ValueError('At most 4096 requests per bucket')
-        arena = _Workspace(shape, self.heads, self.dim, self.dtype, self.device, self.chunk)
-        views = {f: _Workspace(f, self.heads, self.dim, self.dtype, self.device, self.chunk, arena) for f in families}
+        arena = _Workspace(shape, self.heads, self.dim, self.dtype, self.device, self.chunk, self.split)
+        views = {f: _Workspace(f, self.heads, self.dim, self.dtype, self.device, self.chunk, self.split, arena)
+                 for f in families}
         self._family_arena = arena
         self._families = families
         self._workspaces.update(views)
@@ -463,8 +488,9 @@ class PersistentTargetKV:
             raise ValueError('Varlen cumulative lengths exceed int32')
         ws = self._workspaces[bucket]
         r = len(handles)
-        records, n_items = varlen_work(query_lengths, [c + q for c, q in zip(contexts, query_lengths)], indices,
-                                       self.chunk)
+        key_lengths = [c + q for c, q in zip(contexts, query_lengths)]
+        runs = run_count(sum(key_lengths), cu_count(self.device), (bucket.maximum_query_length + 7) // 8)
+        records, n_items, runs = segment_plan(self.split, query_lengths, key_lengths, indices, runs, self.chunk)
         if len(records) > ws.work.numel():
             raise ValueError('Work list exceeds the bucket workspace')
         upload(self.device, list(indices) + list(contexts) + list(query_lengths), out=ws.req[:3 * r])
@@ -476,7 +502,7 @@ class PersistentTargetKV:
                      _native.ptr(ws.cu_query), _native.ptr(ws.cu_key), _native.stream_handle(self.device))
         self._sequence += 1
         tx = Transaction(self._sequence, handles, contexts, bucket, query_lengths)
-        self._pending, self._staged, self._n_work = tx, set(), n_items
+        self._pending, self._staged, self._n_work = tx, set(), (n_items, runs)
         self._tx_mutations = self._mutations
         # (query tokens, launch maximum query length, bucket key capacity)
         self._tx_shape = (sum(query_lengths), bucket.maximum_query_length, bucket.key_capacity)
@@ -580,7 +606,7 @@ class PersistentTargetKV:
         tail = (ws.cu_query.data_ptr(), ws.cu_key.data_ptr(), ws.req.data_ptr(),
                 len(tx.slots), KV_HEADS * C * HEAD_DIM, HEAD_DIM, C * HEAD_DIM,
                 key_capacity, max_q, SCALE, self.chunk,
-                ws.work.data_ptr(), self._n_work, out.data_ptr(), ws.attn.data_ptr(), ws.attn.numel(),
+                ws.work.data_ptr(), *self._n_work, out.data_ptr(), ws.attn.data_ptr(), ws.attn.numel(),
                 _native.stream_handle(self.device))
         if fused:
             _native.call('dspark_verify_attn_staged_fwd', query.data_ptr(), k, v, keys.data_ptr(), values.data_ptr(),

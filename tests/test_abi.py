@@ -19,8 +19,22 @@ def header_functions():
     return sorted(set(re.findall(r'\b(dspark_[a-z0-9_]+)\s*\(', text)))
 
 
+def header_arity():
+    text = open(os.path.join(ROOT, 'include', 'dspark_amd.h')).read()
+    text = re.sub(r'/\*.*?\*/', '', text, flags=re.S)
+    out = {}
+    for name, params in re.findall(r'\b(dspark_[a-z0-9_]+)\s*\(([^)]*)\)\s*;', text):
+        params = params.strip()
+        out[name] = 0 if params in ('', 'void') else params.count(',') + 1
+    return out
+
+
 def test_header_and_binding_agree():
     assert header_functions() == sorted(_native.SIGNATURES)
+    arity = header_arity()
+    assert sorted(arity) == header_functions()
+    for name, (_, args) in _native.SIGNATURES.items():
+        assert arity[name] == len(args), name
 
 
 def test_library_exports_every_declared_symbol():
@@ -40,6 +54,8 @@ def test_workspace_size_formula():
     assert lib.dspark_attn_workspace_bytes(4, 1000, 1, 512) == (2 + 4) * 8 * 1 * 16 * 130 * 4
     assert lib.dspark_attn_workspace_bytes(64, 524288 + 448, 1, 512) == (1025 + 64) * 8 * 16 * 130 * 4
     assert lib.dspark_attn_workspace_bytes(0, 10, 1, 512) == -1
+    # a call with a work list of n segments needs n partial slots: (n, 0, ...)
+    assert lib.dspark_attn_workspace_bytes(127, 0, 1, 1024) == 127 * 8 * 16 * 130 * 4
 
 
 @pytest.mark.parametrize('name', ['dspark_varlen_attn_fwd', 'dspark_verify_attn_fwd', 'dspark_verify_attn_staged_fwd',
@@ -61,23 +77,23 @@ def test_null_arguments_are_rejected_before_any_launch(name):
 def test_invalid_sizes_are_rejected_before_any_launch():
     lib = _native.load()
     fake = ctypes.c_void_p(1 << 20)  # never dereferenced: validation fails first
-    rc = lib.dspark_varlen_attn_fwd(fake, fake, fake, fake, fake, 0, 8, 8, 1, 1, 0.088, 512, None, 0, fake, fake,
+    rc = lib.dspark_varlen_attn_fwd(fake, fake, fake, fake, fake, 0, 8, 8, 1, 1, 0.088, 512, None, 0, 0, fake, fake,
                                     1 << 20, None)
     assert rc == -1 and 'n_req' in lib.dspark_last_error().decode()
-    rc = lib.dspark_varlen_attn_fwd(fake, fake, fake, fake, fake, 2, 8, 8, 1, 1, 0.088, 500, None, 0, fake, fake,
+    rc = lib.dspark_varlen_attn_fwd(fake, fake, fake, fake, fake, 2, 8, 8, 1, 1, 0.088, 500, None, 0, 0, fake, fake,
                                     1 << 20, None)
     assert rc == -1 and 'chunk' in lib.dspark_last_error().decode()
-    rc = lib.dspark_varlen_attn_fwd(fake, fake, fake, fake, fake, 2, 8, 8, 1, 1, 0.088, 512, None, 0, fake, fake,
+    rc = lib.dspark_varlen_attn_fwd(fake, fake, fake, fake, fake, 2, 8, 8, 1, 1, 0.088, 512, None, 0, 0, fake, fake,
                                     16, None)
     assert rc == -1 and 'workspace too small' in lib.dspark_last_error().decode()
-    rc = lib.dspark_varlen_attn_fwd(fake, fake, fake, fake, fake, 2, 8, 8, 1, 1, 0.088, 512, fake, 0, fake, fake,
+    rc = lib.dspark_varlen_attn_fwd(fake, fake, fake, fake, fake, 2, 8, 8, 1, 1, 0.088, 512, fake, 0, 1, fake, fake,
                                     1 << 20, None)
     assert rc == -1 and 'n_work' in lib.dspark_last_error().decode()
     rc = lib.dspark_draft_attn_fwd(fake, fake, fake, None, fake, fake, 1024, 128, fake, fake, fake, fake,
                                    2, 100, 9, 0.088, 512, None, 0, fake, fake, 1 << 24, None)
     assert rc == -1 and 'max_blocks' in lib.dspark_last_error().decode()
     rc = lib.dspark_verify_attn_fwd(fake, fake, fake, fake, fake, fake, fake, fake, 2, 1 << 20, 100, 128, 1000, 7,
-                                    0.088, 512, None, 0, fake, fake, 1 << 24, None)
+                                    0.088, 512, None, 0, 0, fake, fake, 1 << 24, None)
     assert rc == -1 and 'strides' in lib.dspark_last_error().decode()
     rc = lib.dspark_kv_stage(fake, fake, fake, fake, 4, 24, None)
     assert rc == -1 and 'multiple of 16' in lib.dspark_last_error().decode()

@@ -3,6 +3,7 @@ tests (tests/test_persistent_target_kv.py, tests/test_query_family.py) on the
 HIP store, bit-exact metadata/gather/commit against the oracle, and the fused
 verification attention against the oracle and the materialised path."""
 import copy
+from types import SimpleNamespace
 from unittest.mock import patch
 
 import numpy as np
@@ -297,7 +298,7 @@ def test_fused_verify_attention_parity_commit_and_second_round(dev):
     (plus a second layer), seeded accepted prefix 0..7 committed, rest
     rolled back; the next round attends over the committed rows with the
     staging fused into the attention launch."""
-    from qwen3_dspark_amd.kernels import HipCapacityKernel
+    from qwen3_dspark_amd.kernels import HipCapacityKernel, HipVarlenKernel
     from qwen3_dspark_amd.layout import PersistentAttentionLayout
     from qwen3_dspark_amd.persistent_kv import Bucket, PersistentTargetKV
     rng = np.random.default_rng(SEED)
@@ -317,6 +318,7 @@ def test_fused_verify_attention_parity_commit_and_second_round(dev):
     bucket = Bucket((7,) * B, (C - 7 - 7,) * B, 'config #2 shape')
     pool.register_bucket(bucket)
     cap_kernel = HipCapacityKernel(dev)
+    exact_kernel = HipVarlenKernel(dev)
     for rnd in range(2):
         ctx = [pool.length(h) for h in active]
         say(f'[verify] round {rnd} contexts={ctx}')
@@ -340,11 +342,19 @@ def test_fused_verify_attention_parity_commit_and_second_round(dev):
                                         bits(pool.scratch_keys[layer]), bits(pool.scratch_values[layer]),
                                         [h.index for h in active], ctx, cu_q, scale=SCALE)
             attention_gate(f64(out), ref, segments(cu_q))
-            # The fused path equals the materialised capacity path bit for bit.
+            # The fused path equals exact-K attention over the materialised
+            # gather bit for bit (same key lengths, so the same segment plan);
+            # the capacity kernel's fixed chunks merge in another order.
             k, v, cq, ck, _ = pool.prepare_attention(tx, layer)
-            layout = PersistentAttentionLayout(tx.query_lengths, tuple(c + 7 for c in ctx), cq, ck,
+            keys = tuple(c + 7 for c in ctx)
+            exact = SimpleNamespace(query_lengths=tx.query_lengths, key_lengths=keys, cu_query=cq, cu_key=ck,
+                                    request_markers=tuple(range(B)))
+            assert torch.equal(exact_kernel(q[layer], k[:sum(keys)], v[:sum(keys)], exact, scale=SCALE), out)
+            layout = PersistentAttentionLayout(tx.query_lengths, keys, cq, ck,
                                                bucket.key_capacity, bucket.maximum_key_length, bucket.maximum_query_length)
-            assert torch.equal(cap_kernel(q[layer], k, v, layout, scale=SCALE), out)
+            cap = cap_kernel(q[layer], k, v, layout, scale=SCALE)
+            attention_gate(f64(cap), ref, segments(cu_q))
+            assert float((cap.float() - out.float()).abs().max()) <= 2e-2
         counts = {h: int(rng.integers(0, 8)) for h in active}
         before = [pool.request_kv(h) for h in active]
         pool.commit(tx, counts)

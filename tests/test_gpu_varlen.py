@@ -149,14 +149,17 @@ def test_packed_shapes_against_oracle(dev, kernels, name, q_lens, k_lens, causal
     assert torch.equal(out2, 2 * out)
 
 
-def test_request_order_invariance_is_bit_exact(dev, kernels):
+def test_request_order_invariance(dev, kernels):
+    """A request-local split plan makes every request's output independent of
+    the batch (bit-exact under permutation); the balanced plan moves its cuts
+    with the batch, so its outputs agree to the attention tolerance."""
+    from qwen3_dspark_amd.kernels import HipVarlenKernel
     from qwen3_dspark_amd.layout import PackedLayout
     say('[varlen] request permutation invariance')
     gen = torch.Generator().manual_seed(SEED + 1)
     q_lens, k_lens = [7, 3, 7, 5], [900, 40, 2100, 7]
     meta, q, k, v = make_packed(gen, q_lens, k_lens)
     layout = PackedLayout.from_metadata(*(m.to(dev) for m in meta))
-    out = kernels[0](q.to(dev), k.to(dev), v.to(dev), layout, scale=SCALE)
     perm = [2, 0, 3, 1]
     cq, ck = layout.cu_query.tolist(), layout.cu_key.tolist()
     q2 = torch.cat([q[cq[i]:cq[i + 1]] for i in perm])
@@ -164,10 +167,18 @@ def test_request_order_invariance_is_bit_exact(dev, kernels):
     v2 = torch.cat([v[ck[i]:ck[i + 1]] for i in perm])
     meta2, _, _, _ = make_packed(torch.Generator().manual_seed(0), [q_lens[i] for i in perm], [k_lens[i] for i in perm])
     layout2 = PackedLayout.from_metadata(*(m.to(dev) for m in meta2))
-    out2 = kernels[0](q2.to(dev), k2.to(dev), v2.to(dev), layout2, scale=SCALE)
     cq2 = layout2.cu_query.tolist()
-    for j, i in enumerate(perm):
-        assert torch.equal(out2[cq2[j]:cq2[j + 1]], out[cq[i]:cq[i + 1]])
+    ref = cref.varlen_attention(bits(q), bits(k), bits(v), cq, ck, causal=True, scale=SCALE)
+    for kernel in (HipVarlenKernel(dev, split='request', chunk=512), kernels[0]):
+        out = kernel(q.to(dev), k.to(dev), v.to(dev), layout, scale=SCALE)
+        out2 = kernel(q2.to(dev), k2.to(dev), v2.to(dev), layout2, scale=SCALE)
+        attention_gate(f64(out), ref, segments(cq))
+        for j, i in enumerate(perm):
+            a, b = out2[cq2[j]:cq2[j + 1]], out[cq[i]:cq[i + 1]]
+            if kernel.split == 'request':
+                assert torch.equal(a, b)
+            else:
+                assert float((a.float() - b.float()).abs().max()) <= 2e-2
 
 
 def test_capacity_tail_zero_finite_nan_bit_identical(dev, kernels):

@@ -1,0 +1,109 @@
+"""Host-side work lists (CPU): balanced key segments for varlen/verification
+attention.  The kernels trust these records, so their invariants are checked
+here: every key of every request is covered exactly once, cuts fall on
+32-key tile boundaries, runs carry (nearly) equal key counts, and the merge
+records name exactly the partial slots the segments write."""
+import numpy as np
+import pytest
+
+from qwen3_dspark_amd.schedule import (MIN_SEGMENT, REQ_INTS, TILE, WORK_INTS, request_work, run_count,
+                                       varlen_list_bound, varlen_work)
+
+
+def decode(out, n_seg, groups, n_req):
+    rec = [tuple(out[WORK_INTS * i:WORK_INTS * (i + 1)]) for i in range(n_seg)]
+    base = WORK_INTS * n_seg
+    ranges = out[base:base + groups + 1]
+    reqs = [tuple(out[base + groups + 1 + REQ_INTS * r:base + groups + 1 + REQ_INTS * (r + 1)]) for r in range(n_req)]
+    assert len(out) == base + groups + 1 + REQ_INTS * n_req
+    return rec, ranges, reqs
+
+
+def check(query_lengths, key_lengths, starts, groups, chunk=None):
+    if chunk is None:
+        out, n_seg, runs = varlen_work(query_lengths, key_lengths, starts, groups)
+        assert runs == groups
+    else:
+        out, n_seg, runs = request_work(query_lengths, key_lengths, starts, chunk, groups)
+        assert runs == max(1, min(groups, n_seg))
+        groups = runs
+    n = len(key_lengths)
+    rec, ranges, reqs = decode(out, n_seg, groups, n)
+    assert ranges[0] == 0 and ranges[-1] == n_seg and all(a <= b for a, b in zip(ranges, ranges[1:]))
+    assert n_seg <= varlen_list_bound(n, groups, sum(key_lengths), chunk)
+    q0 = np.concatenate([[0], np.cumsum(query_lengths)[:-1]])
+    by_req = {}
+    for i, (r, k0, k1, slot, qs, ql, kl, st) in enumerate(rec):
+        assert (qs, ql, kl, st) == (q0[r], query_lengths[r], key_lengths[r], starts[r])
+        by_req.setdefault(r, []).append((k0, k1, slot))
+    loads = []
+    for w in range(groups):
+        loads.append(sum(rec[i][2] - rec[i][1] for i in range(ranges[w], ranges[w + 1])))
+    segments_of = {}
+    for r, kl in enumerate(key_lengths):
+        segs = sorted(by_req[r])
+        segments_of[r] = [(a, b) for a, b, _ in segs]
+        first, count, qs, ql = reqs[r]
+        assert count == len(segs) and (qs, ql) == (q0[r], query_lengths[r])
+        # exact cover of [0, kl), cuts on tile boundaries
+        assert segs[0][0] == 0 and segs[-1][1] == kl
+        for (a0, a1, _), (b0, _, _) in zip(segs, segs[1:]):
+            assert a1 == b0 and a1 % (TILE if chunk is None else chunk) == 0 and a1 > a0
+        if count == 1:
+            assert segs[0][2] == -1
+        else:
+            assert [s for _, _, s in segs] == list(range(first, first + count))
+    slots = sorted(s for _, _, s in (x for v in by_req.values() for x in v) if s >= 0)
+    assert slots == list(range(len(slots)))       # dense, request-major partial slots
+    return loads, segments_of
+
+
+def test_balanced_runs_at_the_64_request_stress_shape():
+    rng = np.random.default_rng(20261009)
+    ctx = np.floor(np.exp(rng.uniform(np.log(256), np.log(8192), size=64))).astype(int)
+    kl = [int(c) + 7 for c in ctx]
+    groups = run_count(sum(kl), 256)
+    assert groups == 64
+    loads, _ = check([7] * 64, kl, list(range(64)), groups)
+    # every run within one tile of the mean
+    assert max(loads) - min(loads) <= 2 * TILE
+    assert sum(loads) == sum(kl)
+
+
+@pytest.mark.parametrize('kl,groups', [([5], 1), ([40], 4), ([0, 5], 3), ([1, 1, 1], 8), ([31, 33, 64, 65], 3),
+                                       ([1000, 0, 0, 7, 2048], 5), ([8192] * 3 + [7] * 10, 16)])
+def test_edge_shapes(kl, groups):
+    ql = [max(1, min(k, 7)) for k in kl]
+    check(ql, kl, [3 * i for i in range(len(kl))], groups)
+
+
+def test_run_count_bounds():
+    assert run_count(10, 256) == 1
+    assert run_count(MIN_SEGMENT * 3, 256) == 3
+    assert run_count(10 ** 7, 256) == 64
+    assert run_count(10 ** 7, 256, row_tiles=2) == 32
+    assert run_count(10 ** 7, 304) == 76
+
+
+def test_random_shapes_cover_exactly():
+    rng = np.random.default_rng(7)
+    for _ in range(200):
+        n = int(rng.integers(1, 40))
+        kl = [int(x) for x in rng.integers(0, 3000, size=n)]
+        ql = [max(1, min(k, int(rng.integers(1, 9)))) for k in kl]
+        check(ql, kl, list(range(n)), int(rng.integers(1, 70)))
+
+
+def test_request_plan_cuts_depend_only_on_the_request():
+    rng = np.random.default_rng(11)
+    for _ in range(50):
+        n = int(rng.integers(2, 30))
+        kl = [int(x) for x in rng.integers(1, 5000, size=n)]
+        ql = [min(k, 7) for k in kl]
+        chunk = int(rng.choice([256, 1024]))
+        _, segs = check(ql, kl, list(range(n)), int(rng.integers(1, 70)), chunk=chunk)
+        perm = rng.permutation(n)
+        _, segs2 = check([ql[i] for i in perm], [kl[i] for i in perm], list(range(n)), int(rng.integers(1, 70)),
+                         chunk=chunk)
+        for j, i in enumerate(perm):
+            assert segs2[j] == segs[i] == [(c, min(c + chunk, kl[i])) for c in range(0, kl[i], chunk)]
