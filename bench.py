@@ -19,11 +19,12 @@ contains only the rounds themselves.
 value = verified tokens per second = 448 / round time (wall clock between
 two device synchronisations around the K timed rounds).
 
-Per-launch durations come from HIP events recorded on the launch stream
-inside the timed rounds, around a rotating sample of launches (3 of the 28
-verification-attention calls and 1 of the 5 draft-attention calls per round;
-each call is a split-K chunk kernel followed by its merge kernel).  Events
-around every launch would add ~12 us of marker work each to the round.
+Per-call durations come from HIP events recorded on the launch stream
+inside the timed rounds: one pair around the 28 verification-attention calls
+and one around the 5 draft-attention calls of every round (each call is a
+split-K chunk kernel followed by its merge kernel), divided by the number of
+calls.  The spans contain the gaps between launches but no per-call marker
+work (an event pair around a single call adds ~3-4 us to it).
 
     python bench.py [--gpus 1] [--steps 20] [--warmup 5]
 """
@@ -43,7 +44,6 @@ METRIC = 'attn tokens/s + HBM GB/s (% roofline), 64 ragged reqs, Qwen3-0.6B shap
 SEED = 20261009
 B, Q_LEN, CAPACITY = 64, 7, 8192
 VERIFY_LAYERS, DRAFT_LAYERS, BLOCK = 28, 5, 7
-VERIFY_SAMPLES, DRAFT_SAMPLES = 3, 1  # event-timed launches per round
 ROW_BYTES = 8 * 128 * 2            # one K (or V) token row, all 8 KV heads
 Q_ROW_BYTES = 16 * 128 * 2         # one Q (or O) token row, all 16 query heads
 HBM_PEAK_GBS = 8000.0              # MI355X HBM3E, published
@@ -164,30 +164,27 @@ def main():
 
     def round_(step, timed):
         ctx_now = [pool.length(h) for h in handles]
-        sampled_v = {(step * VERIFY_SAMPLES + j * (VERIFY_LAYERS // VERIFY_SAMPLES)) % VERIFY_LAYERS
-                     for j in range(VERIFY_SAMPLES)} if timed else ()
-        sampled_d = {(step * DRAFT_SAMPLES + j) % DRAFT_LAYERS for j in range(DRAFT_SAMPLES)} if timed else ()
         batch = DraftBatch(dev, draft_offsets, contexts, anchors)
         outs = []
+        if timed:
+            d0, d1 = events()
+            d0.record()
         for layer in range(DRAFT_LAYERS):
-            if layer in sampled_d:
-                e0, e1 = events()
-                e0.record()
             outs.append(draft(qd[layer], bkd[layer], bvd[layer], dctx_k[layer], dctx_v[layer], batch, scale=SCALE))
-            if layer in sampled_d:
-                e1.record()
-                ev_d.append((e0, e1))
+        if timed:
+            d1.record()
+            ev_d.append((d0, d1))
         tx = pool.begin(handles, bucket)
+        if timed:
+            v0, v1 = events()
+            v0.record()
         for layer in range(VERIFY_LAYERS):
-            if layer in sampled_v:
-                e0, e1 = events()
-                e0.record()
             # stage_layer fused into the attention launch (scratch is written
             # by the kernel that reads the new rows)
             outs.append(pool.attend(tx, layer, qv[layer], keys=kn[layer], values=vn[layer]))
-            if layer in sampled_v:
-                e1.record()
-                ev_v.append((e0, e1, verify_bytes(ctx_now)))
+        if timed:
+            v1.record()
+            ev_v.append((v0, v1, verify_bytes(ctx_now)))
         counts = [int(x) for x in accepted[step]]
         pool.commit(tx, dict(zip(handles, counts)))
         step_stats.append((ctx_now, counts))
@@ -213,16 +210,17 @@ def main():
     elapsed = time.perf_counter() - t0
     ms_step = 1e3 * elapsed / args.steps
 
-    v_ms = np.array([a.elapsed_time(b) for a, b, _ in ev_v])
+    v_ms = np.array([a.elapsed_time(b) / VERIFY_LAYERS for a, b, _ in ev_v])
     v_bytes = np.array([n for _, _, n in ev_v], dtype=np.float64)
-    d_ms = np.array([a.elapsed_time(b) for a, b in ev_d])
+    d_ms = np.array([a.elapsed_time(b) / DRAFT_LAYERS for a, b in ev_d])
     v_avg_ms = float(v_ms.mean())
     v_avg_bytes = float(v_bytes.mean())
     d_avg_ms = float(d_ms.mean())
 
-    def pct(x):
+    def pct(x, calls):
+        # percentiles over rounds of the per-call average of each round
         return {'p10': round(float(np.percentile(x, 10)), 5), 'median': round(float(np.median(x)), 5),
-                'p90': round(float(np.percentile(x, 90)), 5), 'samples': int(len(x))}
+                'p90': round(float(np.percentile(x, 90)), 5), 'rounds': int(len(x)), 'calls_per_round': calls}
     d_b = draft_bytes(anchors)
     v_gbs = v_avg_bytes / (v_avg_ms * 1e-3) / 1e9
     d_gbs = d_b / (d_avg_ms * 1e-3) / 1e9
@@ -263,9 +261,9 @@ def main():
             'avg_launch_ms': round(v_avg_ms, 5), 'algorithmic_bytes_per_launch': int(v_avg_bytes),
         },
         'breakdown': {
-            'verify_layer_ms': round(v_avg_ms, 5), 'verify_call_ms': pct(v_ms), 'verify_gbs': round(v_gbs, 1),
+            'verify_layer_ms': round(v_avg_ms, 5), 'verify_call_ms': pct(v_ms, VERIFY_LAYERS), 'verify_gbs': round(v_gbs, 1),
             'verify_attn_tokens_per_s': round(B * Q_LEN / (float(np.median(v_ms)) * 1e-3), 1),
-            'draft_layer_ms': round(d_avg_ms, 5), 'draft_call_ms': pct(d_ms), 'draft_gbs': round(d_gbs, 1),
+            'draft_layer_ms': round(d_avg_ms, 5), 'draft_call_ms': pct(d_ms, DRAFT_LAYERS), 'draft_gbs': round(d_gbs, 1),
             'draft_frac': round(d_gbs / HBM_PEAK_GBS, 4),
             'draft_algorithmic_bytes_per_launch': int(d_b),
             'draft_attn_tokens_per_s': round(nq_d / (float(np.median(d_ms)) * 1e-3), 1),
@@ -274,7 +272,9 @@ def main():
         },
     }
 
-    result['next'] = {'qkv_prologue': prologue_leg(dev, B * Q_LEN)}
+    result['next'] = {'qkv_prologue': prologue_leg(dev, B * Q_LEN),
+                      'draft_context_projection': [draft_projection_leg(dev, B, Q_LEN),
+                                                   draft_projection_leg(dev, 16, None)]}
 
     if not args.no_cpu_baseline:
         result['cpu_baseline'], result['parity'] = cpu_leg(args, pool, bucket, handles, contexts, anchors, qv, qd,
@@ -312,6 +312,65 @@ def prologue_leg(dev, tokens, reps=50):
     flops = 2 * tokens * 1024 * 4096
     return {'tokens': tokens, 'median_ms': round(ms, 5), 'bytes': nbytes, 'gbs': round(nbytes / ms / 1e6, 1),
             'tflops': round(flops / ms / 1e9, 2)}
+
+
+def draft_projection_leg(dev, n_req, per_request, reps=20):
+    """Draft context projection (fc on hipBLASLt + the fused context norm /
+    k_proj / k_norm / RoPE / v_proj launch for 5 draft layers, written into a
+    slotted pool) for one append: n_req requests of `per_request` rows each
+    (a round's committed rows), or, with per_request None, the 16-request
+    prefill of contexts U[128, 1024].  Random-init bf16 weights (hidden
+    1024, features 5 x 1024).  Median of `reps` event-timed appends of each
+    part, run back to back on the pool's stream."""
+    import numpy as np
+    import torch
+
+    from qwen3_dspark_amd.draft_projection import DraftContextProjector
+    from qwen3_dspark_amd._device import upload
+    g = torch.Generator(device=dev).manual_seed(SEED + 11)
+    h, f = 1024, 5 * 1024
+    fc = (torch.randn(h, f, generator=g, device=dev) * f ** -0.5).to(torch.bfloat16)
+    cn = torch.ones(h, device=dev, dtype=torch.bfloat16)
+    layers = [((torch.randn(1024, h, generator=g, device=dev) * h ** -0.5).to(torch.bfloat16),
+               torch.ones(128, device=dev, dtype=torch.bfloat16),
+               (torch.randn(1024, h, generator=g, device=dev) * h ** -0.5).to(torch.bfloat16)) for _ in range(5)]
+    proj = DraftContextProjector(fc, cn, layers)
+    rng = np.random.default_rng(SEED + 11)
+    counts = [per_request] * n_req if per_request else [int(c) for c in rng.integers(128, 1025, size=n_req)]
+    cap = max(counts) + 1
+    keys = torch.empty(5, n_req, 8, cap, 128, dtype=torch.bfloat16, device=dev)
+    values = torch.empty_like(keys)
+    rec, first = [], 0
+    for i, n in enumerate(counts):
+        rec += (i, 0, first, n)
+        first += n
+    records = upload(dev, rec)
+    x = torch.randn(first, f, generator=g, device=dev).to(torch.bfloat16)
+    fc_out = proj.fc_forward(x)
+    for _ in range(3):
+        proj.project_into(proj.fc_forward(x), records, n_req, keys, values)
+    t_fc, t_kv = [], []
+    for _ in range(reps):
+        e = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
+        e[0].record()
+        fc_out = proj.fc_forward(x)
+        e[1].record()
+        proj.project_into(fc_out, records, n_req, keys, values)
+        e[2].record()
+        t_fc.append((e[0], e[1]))
+        t_kv.append((e[1], e[2]))
+    torch.cuda.synchronize()
+    ms_fc = float(np.median([a.elapsed_time(b) for a, b in t_fc]))
+    ms_kv = float(np.median([a.elapsed_time(b) for a, b in t_kv]))
+    fc_bytes = (h * f + first * f + first * h) * 2
+    fc_flops = 2 * first * f * h
+    kv_bytes = (5 * 2 * 1024 * h + first * h + 5 * 2 * first * 1024) * 2
+    kv_flops = 2 * first * h * 5 * 2 * 1024
+    return {'tokens': first, 'requests': n_req,
+            'fc_hipblaslt_ms': round(ms_fc, 5), 'fc_tflops': round(fc_flops / ms_fc / 1e9, 1),
+            'kv_project_ms': round(ms_kv, 5), 'kv_project_tflops': round(kv_flops / ms_kv / 1e9, 1),
+            'kv_project_gbs': round(kv_bytes / ms_kv / 1e6, 1),
+            'append_tokens_per_s': round(first / ((ms_fc + ms_kv) * 1e-3), 1)}
 
 
 def traffic_probe(args):

@@ -171,6 +171,33 @@ int dspark_qkv_prologue(const void* x, const void* wq, const void* wk, const voi
                         void* q_out, void* k_out, void* v_out, int64_t kv_row_stride, void* stream);
 
 /*
+ * Draft context K/V projection: what DSpark's draft does to newly committed
+ * target features after its fc layer, for all `layers` draft layers in one
+ * launch, written into the slotted draft pool.  For token t of x
+ * [tokens, hidden] (the fc output, before the context norm):
+ *   ctx = RMSNorm(x_t, w_c),  k_l = RoPE(RMSNorm(ctx Wk_l^T, k_norm_l)),
+ *   v_l = ctx Wv_l^T                                 (per 128-dim KV head)
+ * w: [layers][2][8*128][hidden] bf16, the k_proj then v_proj weights of each
+ * layer with the context norm weight folded in (W diag(w_c)); k_norm
+ * [layers][128]; eps_ctx / eps_k the two RMSNorm epsilons; RoPE rotate-half
+ * at the token's absolute position with inv_freq (64 float32).  req: int32
+ * [n_req][4] records (pool slot, first position, first token, token count),
+ * ordered by first token, the first at token 0, covering every token once;
+ * token t of record r lands at position first_position + (t - first_token)
+ * of slot `slot` in every layer: element (slot, head, pos, d) of layer l at
+ * k_pool/v_pool + l*layer_stride + slot*slot_stride + head*head_stride +
+ * pos*128 + d.  The caller keeps every position within its pool.  flag
+ * (optional): set to 1 when an output is not finite (never cleared).
+ * Replaces dspark_qwen/model.py:141-146 (DSparkDraft.project_context_kv)
+ * after its fc, and the projection + cat of
+ *   dspark_qwen/packed_draft.py:147-158 (PackedDraft.append_committed).
+ */
+int dspark_draft_kv_project(const void* x, int tokens, int hidden, const void* w, const void* k_norm,
+                            int layers, const float* inv_freq, const int32_t* req, int n_req,
+                            float eps_ctx, float eps_k, void* k_pool, void* v_pool, int64_t layer_stride,
+                            int64_t slot_stride, int64_t head_stride, int32_t* flag, void* stream);
+
+/*
  * Transaction metadata of PersistentTargetKV.begin
  * (dspark_qwen/persistent_target_kv.py:392-411), built on the device from
  * req = int32 [3][n_req] (slot, committed context, query length per request):

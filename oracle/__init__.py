@@ -12,9 +12,14 @@ and bench.py's cpu_baseline leg use it, and only as the checker.
   attn_ref.c    - the same attention in C (OpenMP), used as the CPU baseline
                   and for checks at sizes numpy is slow at; built by
                   oracle/Makefile into oracle/_build/liboracle.so.
+  qkv.py        - the target's verify-layer prologue (q/k/v projection,
+                  q/k RMSNorm, RoPE) in float64.
+  draft_proj.py - the draft's context projection (fc, context norm, per-layer
+                  k_proj / k_norm / RoPE / v_proj) in float64.
 
 Pinning (see tests/test_oracle_golden.py): every function is checked against
 the reference tests' literal vectors (tests/golden/reference_vectors.json),
 closed forms (uniform attention, position ramps), invariants, brute force on
-tiny inputs and torch's scaled_dot_product_attention on explicit masks.
+tiny inputs and torch's scaled_dot_product_attention on explicit masks;
+qkv.py and draft_proj.py against transformers' own Qwen3 modules.
 """

@@ -1,0 +1,151 @@
+// One 128-output-column "head" of a linear layer for 64 tokens, on gfx950:
+//   C^T[dim][token] = W[dim][:] . x[token][:]      (dim < 128, token < 64)
+// shared by the projection kernels (the target's verify-layer prologue and
+// the draft context K/V projection).
+//
+// MFMA mapping (v_mfma_f32_16x16x32_bf16): A = 16 weight rows, B = 16
+// tokens; wave w of the 4-wave workgroup owns tokens t0 + 16w .. +15.  Every
+// lane ends with acc[mt][e] = C^T[16*mt + 4*grp + e][token t0 + 16w + col],
+// i.e. the 128 dims of one token spread over its 4 lane groups, so a
+// per-head reduction (RMSNorm) needs two cross-lane shuffles and the RoPE
+// partner of dim d (d + 64 = tile mt + 4) sits in the same lane.
+//
+// The head's weight slice [128, hidden] and the workgroup's token rows
+// stream through a 6-stage LDS ring fed by direct-to-LDS loads: every thread
+// issues exactly 6 loads per stage (4 weight pieces, 2 of its wave's token
+// pieces), so the weights are read once per workgroup and shared by the 4
+// waves, with 5 stages in flight.
+#pragma once
+#include "common.h"
+
+namespace dspark {
+
+constexpr int HG_TOKENS = 64;                    // tokens per workgroup, 16 per wave
+constexpr int HG_KB = 64;                        // hidden columns per ring stage
+constexpr int HG_STAGES = 6;                     // ring depth (5 stages in flight)
+constexpr int HG_W_BYTES = HD * HG_KB * 2;       // 128 weight rows x 128 B = 16 KiB
+constexpr int HG_X_BYTES = 16 * HG_KB * 2;       // 16 token rows x 128 B per wave
+constexpr int HG_STAGE_BYTES = HG_W_BYTES + 4 * HG_X_BYTES;   // 24 KiB
+constexpr int HG_SMEM = HG_STAGES * HG_STAGE_BYTES;            // 144 KiB
+
+// 16-byte chunk swizzle of a 128-byte LDS row: the 16 rows 16*mt + col that
+// one fragment read touches land on 16 distinct bank groups.
+__device__ __forceinline__ int hg_swz(int row) { return (row >> 1) & 7; }
+
+// w: first of the head's 128 weight rows (row stride `hidden`); x: token
+// rows (row stride `hidden`), `tokens` of them; t0: the workgroup's first
+// token.  Rows past `tokens` re-read the last token (their results are
+// discarded by the caller).  With SUMSQ, ss receives this lane's share of
+// sum(x^2) over its token's row (the 4 lane groups of a column together
+// cover the row once).  Ends with no direct loads in flight; the caller must
+// not reuse smem before a barrier.
+template <bool SUMSQ>
+__device__ __forceinline__ void head_tile_gemm(const bf16* __restrict__ w, const bf16* __restrict__ x, int tokens,
+                                               int hidden, int t0, unsigned char* smem, f32x4 (&acc)[8], float& ss) {
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int col = lane & 15;
+  const int grp = lane >> 4;
+  const int tw = t0 + 16 * wave;
+  const int steps = hidden / HG_KB;
+
+  // Direct loads: lane L of a 1 KiB piece (8 rows x 128 B) fetches row
+  // 8*piece + L/8, global chunk (L%8) ^ swz(row), landing at LDS chunk L%8.
+  const uint32_t smem_lds = lds_address(smem);
+  const int prow = lane >> 3;
+  auto issue = [&](int step) {
+    const int st = min(step, steps - 1);   // past the end: re-read the last stage (never used)
+    const uint32_t base = smem_lds + (uint32_t)((step % HG_STAGES) * HG_STAGE_BYTES);
+    const int k0 = st * HG_KB;
+    #pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int piece = 4 * wave + i;
+      const int row = 8 * piece + prow;
+      const bf16* src = w + (size_t)row * hidden + k0 + 8 * ((lane & 7) ^ hg_swz(row));
+      lds_dma16(src, __builtin_amdgcn_readfirstlane(base + (uint32_t)(piece * 1024)));
+    }
+    #pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int row = 8 * i + prow;
+      const int tok = min(tw + row, tokens - 1);
+      const bf16* src = x + (size_t)tok * hidden + k0 + 8 * ((lane & 7) ^ hg_swz(row));
+      lds_dma16(src, __builtin_amdgcn_readfirstlane(base + (uint32_t)(HG_W_BYTES + wave * HG_X_BYTES + i * 1024)));
+    }
+  };
+
+  #pragma unroll
+  for (int mt = 0; mt < 8; ++mt) acc[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  ss = 0.f;
+  #pragma unroll
+  for (int p = 0; p < HG_STAGES - 1; ++p) issue(p);
+  for (int s = 0; s < steps; ++s) {
+    // this thread's stage-s loads landed: the 6 loads of each of the
+    // HG_STAGES - 2 later stages may still be in flight
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(6 * (HG_STAGES - 2)) : "memory");
+    asm volatile("s_barrier" ::: "memory");            // ... and everyone else's
+    issue(s + HG_STAGES - 1);
+    const unsigned char* wst = smem + (s % HG_STAGES) * HG_STAGE_BYTES;
+    const unsigned char* xst = wst + HG_W_BYTES + wave * HG_X_BYTES;
+    #pragma unroll
+    for (int u = 0; u < HG_KB / 32; ++u) {
+      const int c = 4 * u + grp;
+      const bf16x8 xb = *reinterpret_cast<const bf16x8*>(xst + col * 128 + ((c ^ hg_swz(col)) << 4));
+      if (SUMSQ) {
+        #pragma unroll
+        for (int i = 0; i < 8; ++i) ss += (float)xb[i] * (float)xb[i];
+      }
+      #pragma unroll
+      for (int mt = 0; mt < 8; ++mt) {
+        const int row = 16 * mt + col;
+        const bf16x8 wa = *reinterpret_cast<const bf16x8*>(wst + row * 128 + ((c ^ hg_swz(row)) << 4));
+        acc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wa, xb, acc[mt], 0, 0, 0);
+      }
+    }
+  }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+}
+
+// RMSNorm over the 128 dims of each lane's token (weights nw[128]) in place.
+__device__ __forceinline__ void head_rms_norm(f32x4 (&acc)[8], const bf16* __restrict__ nw, float eps, int grp) {
+  float ss = 0.f;
+  #pragma unroll
+  for (int mt = 0; mt < 8; ++mt)
+    #pragma unroll
+    for (int e = 0; e < 4; ++e) ss += acc[mt][e] * acc[mt][e];
+  ss += __shfl_xor(ss, 16);
+  ss += __shfl_xor(ss, 32);
+  const float r = rsqrtf(ss * (1.0f / HD) + eps);
+  #pragma unroll
+  for (int mt = 0; mt < 8; ++mt)
+    #pragma unroll
+    for (int e = 0; e < 4; ++e) acc[mt][e] = acc[mt][e] * r * (float)nw[16 * mt + 4 * grp + e];
+}
+
+// Rotate-half RoPE at absolute position pos with the model's float32
+// inverse frequencies inv_freq[64]: angle pos * inv_freq[d] formed in FP32.
+__device__ __forceinline__ void head_rope(f32x4 (&acc)[8], const float* __restrict__ inv_freq, float pos, int grp) {
+  #pragma unroll
+  for (int mt = 0; mt < 4; ++mt)
+    #pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      float s, c;
+      sincosf(pos * inv_freq[16 * mt + 4 * grp + e], &s, &c);
+      const float lo = acc[mt][e], hi = acc[mt + 4][e];
+      acc[mt][e] = lo * c - hi * s;
+      acc[mt + 4][e] = hi * c + lo * s;
+    }
+}
+
+// Store the lane's 128 dims as bf16 (4 consecutive dims per tile).
+__device__ __forceinline__ void head_store(const f32x4 (&acc)[8], bf16* out, int grp) {
+  out += 4 * grp;
+  #pragma unroll
+  for (int mt = 0; mt < 8; ++mt) {
+    bf16x4 o;
+    #pragma unroll
+    for (int e = 0; e < 4; ++e) o[e] = (bf16)acc[mt][e];
+    *reinterpret_cast<bf16x4*>(out + 16 * mt) = o;
+  }
+}
+
+}  // namespace dspark

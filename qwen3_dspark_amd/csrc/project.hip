@@ -1,0 +1,139 @@
+// Draft context K/V projection for gfx950: everything DSpark's draft does to
+// newly committed target features after its `fc` layer, for all draft
+// layers in one launch, written straight into the slotted draft pool.
+//
+//   ctx = RMSNorm_ctx(f)                       f = fc(features), [T, hidden]
+//   k_l = RoPE(RMSNorm_k,l(ctx Wk_l^T)),  v_l = ctx Wv_l^T      per 128-dim head
+//
+// (dspark_qwen/model.py:141-146 project_context_kv, :41-45 project_kv and
+// :22-24 rotate, as used by dspark_qwen/packed_draft.py:147-158
+// append_committed).  RMSNorm y = w x / sqrt(mean(x^2) + eps); RoPE in the
+// rotate-half form at each token's absolute position.
+//
+// The context norm is applied without materialising ctx: its weight w_c is
+// folded into the projection weights once by the host (Wk_l diag(w_c),
+// Wv_l diag(w_c)), and its per-token factor 1/sqrt(mean(f^2) + eps) commutes
+// with the projection, so each workgroup accumulates sum(f^2) of its tokens
+// while the rows stream through LDS for the MFMAs and scales the FP32
+// result in the epilogue.  Accumulation and epilogue are FP32; every output
+// is rounded to bf16 once.
+//
+// Work: one workgroup per (layer, K or V, KV head) x 64-token tile (the
+// shared head_tile_gemm), XCD-aware so that the token tiles of one weight
+// slice share an L2.  Token t belongs to the request whose record
+// (slot, first position, first token, count) covers it; its row goes to
+// (slot, position) of every layer's pool.  A non-finite output sets *flag
+// (the caller publishes the rows only when it is clear).
+#include "head_gemm.h"
+
+namespace dspark {
+
+struct DraftProjArgs {
+  const bf16* x;             // [T, hidden] fc output (before the context norm)
+  const bf16* w;             // [layers][2][8*128][hidden]: folded k_proj then v_proj
+  const bf16* k_norm;        // [layers][128]
+  const float* inv_freq;     // [64]
+  const int32_t* req;        // [n_req][4]: slot, first position, first token, token count
+  bf16* k_pool;              // layer 0 of the pool; element (slot, head, pos, d) at
+  bf16* v_pool;              //   slot*slot_stride + head*head_stride + pos*128 + d
+  int64_t layer_stride;      // elements
+  int64_t slot_stride;
+  int64_t head_stride;
+  int32_t* flag;             // optional: set to 1 on a non-finite output
+  int tokens;
+  int hidden;
+  int layers;
+  int n_req;
+  float eps_ctx;
+  float eps_k;
+};
+
+__global__ __launch_bounds__(256) void draft_kv_project_kernel(DraftProjArgs a) {
+  __shared__ __attribute__((aligned(16))) unsigned char smem[HG_SMEM];
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int col = lane & 15;
+  const int grp = lane >> 4;
+  const int tiles = (a.tokens + HG_TOKENS - 1) / HG_TOKENS;
+  const int xcd = blockIdx.x & 7;
+  const int slot_id = blockIdx.x >> 3;
+  const int job = xcd + 8 * (slot_id / tiles);        // layer * 16 + (V ? 8 : 0) + head
+  const int t0 = (slot_id % tiles) * HG_TOKENS;
+  const int layer = job >> 4;
+  const bool is_v = (job & 8) != 0;
+  const int head = job & 7;
+  const bf16* w = a.w + ((size_t)(2 * layer + (is_v ? 1 : 0)) * KV_ROW + (size_t)head * HD) * a.hidden;
+
+  f32x4 acc[8];
+  float ss;
+  head_tile_gemm<true>(w, a.x, a.tokens, a.hidden, t0, smem, acc, ss);
+  const int tw = t0 + 16 * wave;
+  if (tw >= a.tokens) return;   // wave-uniform; no barrier follows
+  const int tok = min(tw + col, a.tokens - 1);
+
+  // Context norm: this token's row sum of squares (its 4 lane groups each
+  // saw a quarter of the row), applied as one scale of the FP32 result.
+  ss += __shfl_xor(ss, 16);
+  ss += __shfl_xor(ss, 32);
+  const float r = rsqrtf(ss / (float)a.hidden + a.eps_ctx);
+  #pragma unroll
+  for (int mt = 0; mt < 8; ++mt) acc[mt] *= r;
+
+  // The request holding this token: the last record whose first token <= tok.
+  int lo = 0, hi = a.n_req - 1;
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (a.req[4 * mid + 2] <= tok) lo = mid;
+    else hi = mid - 1;
+  }
+  const int32_t* rq = a.req + 4 * lo;
+  const int pos = rq[1] + (tok - rq[2]);
+  if (!is_v) {
+    head_rms_norm(acc, a.k_norm + (size_t)layer * HD, a.eps_k, grp);
+    head_rope(acc, a.inv_freq, (float)pos, grp);
+  }
+  const bool valid = tw + col < a.tokens;
+  if (a.flag) {
+    bool bad = false;
+    #pragma unroll
+    for (int mt = 0; mt < 8; ++mt)
+      #pragma unroll
+      for (int e = 0; e < 4; ++e) bad |= !__builtin_isfinite(acc[mt][e]);
+    if (__builtin_amdgcn_ballot_w64(bad && valid) && lane == 0) *a.flag = 1;   // idempotent vector store
+  }
+  if (valid) {
+    bf16* out = (is_v ? a.v_pool : a.k_pool) + (size_t)layer * a.layer_stride + (size_t)rq[0] * a.slot_stride +
+                (size_t)head * a.head_stride + (size_t)pos * HD;
+    head_store(acc, out, grp);
+  }
+}
+
+}  // namespace dspark
+
+using namespace dspark;
+
+extern "C" int dspark_draft_kv_project(const void* x, int tokens, int hidden, const void* w, const void* k_norm,
+                                       int layers, const float* inv_freq, const int32_t* req, int n_req,
+                                       float eps_ctx, float eps_k, void* k_pool, void* v_pool, int64_t layer_stride,
+                                       int64_t slot_stride, int64_t head_stride, int32_t* flag, void* stream) {
+  clear_error();
+  DSPARK_REQUIRE(x && w && k_norm && inv_freq && req && k_pool && v_pool, "null pointer argument");
+  DSPARK_REQUIRE(tokens >= 1 && hidden >= HG_KB && hidden % HG_KB == 0, "need tokens >= 1 and hidden a multiple of %d",
+                 HG_KB);
+  DSPARK_REQUIRE(layers >= 1 && layers <= 64, "layers must be in [1, 64] (got %d)", layers);
+  DSPARK_REQUIRE(n_req >= 1 && n_req <= tokens, "n_req must be in [1, tokens]");
+  DSPARK_REQUIRE(eps_ctx > 0.f && eps_k > 0.f, "eps must be positive");
+  DSPARK_REQUIRE(layer_stride >= 0 && slot_stride >= 0 && head_stride >= HD && head_stride % 8 == 0 &&
+                     slot_stride % 8 == 0 && layer_stride % 8 == 0,
+                 "pool strides must be multiples of 8 elements (head stride >= 128)");
+  const uintptr_t any = (uintptr_t)x | (uintptr_t)w | (uintptr_t)k_pool | (uintptr_t)v_pool;
+  DSPARK_REQUIRE(any % 16 == 0, "tensors must be 16-byte aligned");
+  const int64_t tiles = (tokens + HG_TOKENS - 1) / HG_TOKENS;
+  DSPARK_REQUIRE(tiles * layers * 2 * HKV <= 0x7fffffffLL, "too many tokens");
+  DraftProjArgs a{static_cast<const bf16*>(x), static_cast<const bf16*>(w), static_cast<const bf16*>(k_norm), inv_freq,
+                  req, static_cast<bf16*>(k_pool), static_cast<bf16*>(v_pool), layer_stride, slot_stride, head_stride,
+                  flag, tokens, hidden, layers, n_req, eps_ctx, eps_k};
+  hipLaunchKernelGGL(draft_kv_project_kernel, dim3((unsigned)(tiles * layers * 2 * HKV)), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), a);
+  return launch_status("draft_kv_project_kernel");
+}

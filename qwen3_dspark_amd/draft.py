@@ -200,14 +200,16 @@ class DraftKVPool:
       * crop / remove_request only change lengths; the reference compacts
         every layer with a keep mask;
       * draft attention streams each request's context as one linear run.
-    The projection that produces the rows (fc, context_norm, RoPE, k_proj,
-    k_norm, v_proj: packed_draft.py:147-158) stays with the caller.
+    Rows arrive either already projected (append_projected) or as target
+    features that a DraftContextProjector turns into every layer's K/V in
+    place (append_committed, the reference's method: fc, context_norm, RoPE,
+    k_proj, k_norm, v_proj of packed_draft.py:147-158).
     Appends are transactional: rows land beyond the committed lengths and
     become visible only when every check, including finiteness, passed.
     """
 
     def __init__(self, *, layers, slots, capacity, heads=KV_HEADS, dim=HEAD_DIM, dtype=torch.bfloat16,
-                 device='cuda', chunk=DRAFT_CHUNK):
+                 device='cuda', chunk=DRAFT_CHUNK, projector=None):
         if any(type(n) is not int or n < 1 for n in (layers, slots, capacity, heads, dim)):
             raise ValueError('All pool sizes must be positive integers')
         if dtype not in (torch.bfloat16, torch.float32):
@@ -229,6 +231,10 @@ class DraftKVPool:
         self._attention = HipDraftAttention(self.device, chunk=chunk) if (heads, dim) == (KV_HEADS, HEAD_DIM) else None
         self._flag = torch.zeros(1, dtype=torch.int32, device=self.device)
         self.last_append_work = None
+        if projector is not None and (projector.layers != layers or projector.device != self.device
+                                      or (heads, dim, dtype) != (KV_HEADS, HEAD_DIM, torch.bfloat16)):
+            raise ValueError('The projector needs a bf16 8x128 pool with its layer count on its device')
+        self.projector = projector
 
     @property
     def lengths(self):
@@ -327,6 +333,53 @@ class DraftKVPool:
         self.last_append_work = dict(requests=len(order), new_context_tokens=rows, append_launches=1,
                                      appended_kv_bytes=2 * self.layers * rows * H * D * e,
                                      cache_concatenation_kv_bytes=0)
+        return self.last_append_work
+
+    @torch.no_grad()
+    def append_committed(self, chunks):
+        """Project and append committed target features (packed_draft.py:130-168).
+        chunks: ordered {request: features [1, tokens, 5*hidden]}.  One fc
+        over all chunks and one fused projection launch for every layer
+        write the rows beyond the committed lengths; one device read then
+        decides: non-finite features raise ValueError, a non-finite
+        projection RuntimeError, and either leaves the pool as it was."""
+        proj = self.projector
+        if proj is None:
+            raise ValueError('append_committed needs a DraftContextProjector')
+        if not chunks:
+            raise ValueError('Require at least one committed feature chunk')
+        self.validate_cache()
+        order = list(chunks.items())
+        feats = []
+        for request, value in order:
+            self._request(request)
+            if (not isinstance(value, torch.Tensor) or value.ndim != 3 or value.shape[0] != 1 or value.shape[1] < 1
+                    or value.shape[2] != proj.features or value.device != self.device
+                    or not value.is_floating_point()):
+                raise ValueError('Expected finite nonempty [1, tokens, target_features] on draft device')
+            if self._lengths[request] + value.shape[1] > self.capacity:
+                raise ValueError('Committed draft context exceeds the pool capacity')
+            feats.append(value[0])
+        x = (torch.cat(feats) if len(feats) > 1 else feats[0]).to(torch.bfloat16).contiguous()
+        rec, first = [], 0
+        for (request, _), f in zip(order, feats):
+            rec += (self._slots[request], self._lengths[request], first, f.shape[0])
+            first += f.shape[0]
+        records = upload(self.device, rec)
+        self._flag.zero_()
+        proj.project_into(proj.fc_forward(x), records, len(order), self.keys, self.values, flag=self._flag)
+        bad_in, bad_out = torch.stack((torch.isfinite(x).all().logical_not().to(torch.int32), self._flag[0])).tolist()
+        if bad_in:
+            raise ValueError('Expected finite nonempty [1, tokens, target_features] on draft device')
+        if bad_out:
+            raise RuntimeError('Nonfinite projected draft context')
+        for request, f in zip(order, feats):
+            self._lengths[request[0]] += f.shape[0]
+        e, H, D = self._elem, self.heads, self.dim
+        self.last_append_work = dict(requests=len(order), new_context_tokens=first, context_projection_calls=1,
+                                     kv_projection_calls=self.layers, projection_launches=2,
+                                     appended_kv_bytes=2 * self.layers * first * H * D * e,
+                                     cache_concatenation_kv_elements=0, cache_concatenation_kv_bytes=0)
         return self.last_append_work
 
     def crop(self, request, length):

@@ -299,3 +299,51 @@ def test_qkv_prologue_oracle_matches_transformers_qwen3_modules():
                                 np.ones(128), cfg.rms_norm_eps), pos[0].numpy(), qkv.inv_freq())
     assert not np.allclose(bad, q[0].transpose(0, 1).numpy(), atol=1e-3)
     assert np.allclose(qkv.inv_freq(), rot.inv_freq.numpy(), rtol=0, atol=0)
+
+
+def test_draft_projection_oracle_matches_transformers_qwen3_modules():
+    """The draft context projection oracle against torch's nn.Linear and
+    transformers' Qwen3RMSNorm / Qwen3RotaryEmbedding / apply_rotary_pos_emb
+    (the modules dspark_qwen/model.py builds DSparkDraft from; its rotate is
+    the rotate-half form), float32 on the CPU, 2 draft layers."""
+    from torch import nn
+    from transformers import Qwen3Config
+    from transformers.models.qwen3 import modeling_qwen3 as mq
+
+    from oracle import draft_proj, qkv
+    hidden, feats, t = 256, 5 * 256, 11
+    cfg = Qwen3Config(vocab_size=64, hidden_size=hidden, intermediate_size=256, num_hidden_layers=1,
+                      num_attention_heads=16, num_key_value_heads=8, head_dim=128, rope_theta=1e6)
+    torch.manual_seed(3)
+    fc = nn.Linear(feats, hidden, bias=False)
+    cnorm = mq.Qwen3RMSNorm(hidden, eps=cfg.rms_norm_eps)
+    layers = [(nn.Linear(hidden, 1024, bias=False), mq.Qwen3RMSNorm(128, eps=cfg.rms_norm_eps),
+               nn.Linear(hidden, 1024, bias=False)) for _ in range(2)]
+    with torch.no_grad():
+        cnorm.weight.uniform_(0.5, 1.5)
+        for _, kn, _ in layers:
+            kn.weight.uniform_(0.5, 1.5)
+    rot = mq.Qwen3RotaryEmbedding(cfg)
+    x = torch.randn(1, t, feats)
+    pos = torch.tensor([[5, 6, 7, 0, 1, 2, 3, 4000, 4001, 8190, 8191]])
+    with torch.no_grad():
+        ctx = cnorm(fc(x))
+        cos, sin = rot(ctx, pos)
+        expect = []
+        for kp, kn, vp in layers:
+            k = kn(kp(ctx).view(1, t, 8, 128)).transpose(1, 2)
+            k, _ = mq.apply_rotary_pos_emb(k, k, cos, sin)
+            expect.append((k[0].transpose(0, 1).numpy(), vp(ctx).view(t, 8, 128).numpy()))
+    got = draft_proj.project_context_kv(x[0].numpy(), fc.weight.detach().numpy(), cnorm.weight.detach().numpy(),
+                                        [(kp.weight.detach().numpy(), kn.weight.detach().numpy(),
+                                          vp.weight.detach().numpy()) for kp, kn, vp in layers],
+                                        pos[0].numpy(), eps=cfg.rms_norm_eps)
+    for (ok, ov), (ek, ev) in zip(got, expect):
+        np.testing.assert_allclose(ok, ek, rtol=1e-4, atol=2e-4)
+        np.testing.assert_allclose(ov, ev, rtol=1e-4, atol=2e-4)
+    # Planted mistakes must fail: the context norm left out, and the norm
+    # taken per 128-dim head instead of over the hidden size.
+    f = x[0].numpy().astype(np.float64) @ fc.weight.detach().numpy().T
+    for wrong_ctx in (f, qkv.rms_norm(f.reshape(t, 2, 128), np.ones(128), 1e-6).reshape(t, hidden)):
+        v_bad = (wrong_ctx @ layers[0][2].weight.detach().numpy().T).reshape(t, 8, 128)
+        assert not np.allclose(v_bad, expect[0][1], atol=1e-3)
