@@ -272,7 +272,8 @@ def main():
         },
     }
 
-    result['next'] = {'qkv_prologue': prologue_leg(dev, B * Q_LEN),
+    result['next'] = {'verify_graph': verify_graph_leg(pool, bucket, handles, qv, kn, vn, verify_bytes),
+                      'qkv_prologue': prologue_leg(dev, B * Q_LEN),
                       'draft_context_projection': [draft_projection_leg(dev, B, Q_LEN),
                                                    draft_projection_leg(dev, 16, None)]}
 
@@ -312,6 +313,43 @@ def prologue_leg(dev, tokens, reps=50):
     flops = 2 * tokens * 1024 * 4096
     return {'tokens': tokens, 'median_ms': round(ms, 5), 'bytes': nbytes, 'gbs': round(nbytes / ms / 1e6, 1),
             'tflops': round(flops / ms / 1e9, 2)}
+
+
+def verify_graph_leg(pool, bucket, handles, qv, kn, vn, bytes_of, reps=10):
+    """The 28 verification-attention layers of a round captured in one HIP
+    graph (VerificationGraph) and replayed per transaction, the metadata of
+    begin() outside the graph.  Median replay span (events on the stream
+    around the replay) over `reps` transactions at the current lengths, each
+    aborted after its replay; the replay's outputs are compared bit for bit
+    with eager calls on the same transaction."""
+    import numpy as np
+    import torch
+
+    from qwen3_dspark_amd.graph import VerificationGraph
+    graph = VerificationGraph(pool, bucket).capture()
+    graph.query.copy_(qv)
+    graph.keys.copy_(kn)
+    graph.values.copy_(vn)
+    ctx = [pool.length(h) for h in handles]
+    spans = []
+    for i in range(reps + 2):
+        tx = pool.begin(handles, bucket)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        done = graph.submit(tx)
+        e1.record()
+        graph.wait(done)
+        pool.abort(tx)
+        if i >= 2:
+            spans.append(e0.elapsed_time(e1))
+    tx = pool.begin(handles, bucket)
+    same = all(torch.equal(pool.attend(tx, l, qv[l], keys=kn[l], values=vn[l]), graph.output[l])
+               for l in range(VERIFY_LAYERS))
+    pool.abort(tx)
+    ms = float(np.median(spans))
+    return {'layers': VERIFY_LAYERS, 'replay_ms': round(ms, 4), 'per_layer_ms': round(ms / VERIFY_LAYERS, 5),
+            'gbs': round(bytes_of(ctx) * VERIFY_LAYERS / ms / 1e6, 1), 'replays': reps,
+            'bit_identical_to_eager': bool(same)}
 
 
 def draft_projection_leg(dev, n_req, per_request, reps=20):

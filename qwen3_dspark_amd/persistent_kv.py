@@ -261,7 +261,6 @@ class PersistentTargetKV:
         self._writers = {}
         self._external = None
         self._submission_generation = 0
-        self._n_work = (0, 0)      # (segments, runs) of the open transaction's work list
         # Committed-state generation: bumped by every mutation of slots or
         # lengths; a transaction is valid only while it is unchanged, which
         # replaces a per-call scan over the transaction's handles.
@@ -490,7 +489,10 @@ class PersistentTargetKV:
         r = len(handles)
         key_lengths = [c + q for c, q in zip(contexts, query_lengths)]
         runs = run_count(sum(key_lengths), cu_count(self.device), (bucket.maximum_query_length + 7) // 8)
-        records, n_items, runs = segment_plan(self.split, query_lengths, key_lengths, indices, runs, self.chunk)
+        # fixed-capacity list: the same launch for every transaction of the bucket
+        capacity = (_max_segments(bucket, self.device, self.chunk, self.split), _max_runs(bucket, self.device))
+        records, n_items, runs = segment_plan(self.split, query_lengths, key_lengths, indices, runs, self.chunk,
+                                              capacity)
         if len(records) > ws.work.numel():
             raise ValueError('Work list exceeds the bucket workspace')
         upload(self.device, list(indices) + list(contexts) + list(query_lengths), out=ws.req[:3 * r])
@@ -502,7 +504,7 @@ class PersistentTargetKV:
                      _native.ptr(ws.cu_query), _native.ptr(ws.cu_key), _native.stream_handle(self.device))
         self._sequence += 1
         tx = Transaction(self._sequence, handles, contexts, bucket, query_lengths)
-        self._pending, self._staged, self._n_work = tx, set(), (n_items, runs)
+        self._pending, self._staged = tx, set()
         self._tx_mutations = self._mutations
         # (query tokens, launch maximum query length, bucket key capacity)
         self._tx_shape = (sum(query_lengths), bucket.maximum_query_length, bucket.key_capacity)
@@ -572,7 +574,7 @@ class PersistentTargetKV:
         return ws.keys, ws.values, ws.cu_query, ws.cu_key, ws.positions
 
     @torch.no_grad()
-    def attend(self, tx, layer, query, *, scale=SCALE, keys=None, values=None):
+    def attend(self, tx, layer, query, *, scale=SCALE, keys=None, values=None, out=None):
         """Bottom-right causal attention of one layer: request r's queries see
         its committed rows (resident) then its new rows, read in place.
         query [sum Q, 16, 128] bf16 -> output of the same shape.
@@ -581,8 +583,9 @@ class PersistentTargetKV:
         staged in the same launch: the kernel reads the new rows from them
         and copies them into scratch, exactly what stage_layer followed by
         attend does, minus one launch and one pass over the new rows.
-        Otherwise the layer must have been staged with stage_layer."""
-        ws = self._transaction(tx)
+        Otherwise the layer must have been staged with stage_layer.  out: an
+        optional output buffer (written and returned)."""
+        self._transaction(tx)
         fused = keys is not None or values is not None
         if fused:
             if self._external is not None:
@@ -595,26 +598,44 @@ class PersistentTargetKV:
             raise ValueError('Layer scratch missing')
         if (self.heads, self.dim, self.dtype) != (KV_HEADS, HEAD_DIM, torch.bfloat16):
             raise ValueError('Fused attention requires bf16 Hkv8/D128 storage')
-        q, max_q, key_capacity = self._tx_shape
+        q = self._tx_shape[0]
         if (not isinstance(query, torch.Tensor) or query.dtype != torch.bfloat16 or query.device != self.device
                 or query.shape != (q, Q_HEADS, HEAD_DIM) or not query.is_contiguous() or query.requires_grad):
             raise ValueError('Expected contiguous no-autograd bf16 [Q,16,128] queries on the store device')
         _check_scale(scale, 'Fused verification attention')
-        out = torch.empty_like(query)
+        if out is None:
+            out = torch.empty_like(query)
+        elif (not isinstance(out, torch.Tensor) or out.dtype != torch.bfloat16 or out.device != self.device
+              or out.shape != query.shape or not out.is_contiguous()):
+            raise ValueError('out must be a contiguous bf16 tensor shaped like the queries')
+        self._attention_launch(tx.bucket, layer, query.data_ptr(), out.data_ptr(),
+                               keys.data_ptr() if fused else None, values.data_ptr() if fused else None)
+        if fused:
+            self._staged.add(layer)
+        return out
+
+    def _launch_shape(self, bucket):
+        """(record capacity, runs) of the bucket's fixed-capacity work list."""
+        return _max_segments(bucket, self.device, self.chunk, self.split), _max_runs(bucket, self.device)
+
+    def _attention_launch(self, bucket, layer, query, out, keys=None, values=None):
+        """One layer's fused verification attention (staged when keys/values
+        are given) for the bucket's workspace.  Every argument depends only on
+        the bucket, the layer and the given buffers; the transaction's data is
+        read from the workspace at run time, so a captured launch replays for
+        every later transaction of the bucket."""
+        ws = self._workspaces[bucket]
         C = self.context_capacity
         k, v, sk, sv = self._layer_ptrs[layer]
         tail = (ws.cu_query.data_ptr(), ws.cu_key.data_ptr(), ws.req.data_ptr(),
-                len(tx.slots), KV_HEADS * C * HEAD_DIM, HEAD_DIM, C * HEAD_DIM,
-                key_capacity, max_q, SCALE, self.chunk,
-                ws.work.data_ptr(), *self._n_work, out.data_ptr(), ws.attn.data_ptr(), ws.attn.numel(),
+                bucket.request_count, KV_HEADS * C * HEAD_DIM, HEAD_DIM, C * HEAD_DIM,
+                bucket.key_capacity, bucket.maximum_query_length, SCALE, self.chunk,
+                ws.work.data_ptr(), *self._launch_shape(bucket), out, ws.attn.data_ptr(), ws.attn.numel(),
                 _native.stream_handle(self.device))
-        if fused:
-            _native.call('dspark_verify_attn_staged_fwd', query.data_ptr(), k, v, keys.data_ptr(), values.data_ptr(),
-                         sk, sv, *tail)
-            self._staged.add(layer)
+        if keys is not None:
+            _native.call('dspark_verify_attn_staged_fwd', query, k, v, keys, values, sk, sv, *tail)
         else:
-            _native.call('dspark_verify_attn_fwd', query.data_ptr(), k, v, sk, sv, *tail)
-        return out
+            _native.call('dspark_verify_attn_fwd', query, k, v, sk, sv, *tail)
 
     @torch.no_grad()
     def commit(self, tx, committed_query_lengths: Mapping):

@@ -192,14 +192,29 @@ def varlen_list_bound(n_req, groups, rows_bound=0, chunk=None):
 SPLITS = ('balanced', 'request')
 
 
-def segment_plan(split, query_lengths, key_lengths, starts, groups, chunk):
+def segment_plan(split, query_lengths, key_lengths, starts, groups, chunk, capacity=None):
     """(flat int32 list, segment count, run count) of the named plan; the
-    launch grid must use the returned run count."""
+    launch must pass the returned counts (n_work, n_groups).
+
+    capacity = (segments, runs) lays the list out in regions of fixed size:
+    the records padded to `segments`, the run ranges to `runs` (trailing runs
+    empty).  Every transaction of a bucket then launches with the same
+    arguments and grid, which a captured graph replays."""
     if split == 'balanced':
-        return varlen_work(query_lengths, key_lengths, starts, groups)
-    if split == 'request':
-        return request_work(query_lengths, key_lengths, starts, chunk, groups)
-    raise ValueError(f'split must be one of {SPLITS}')
+        out, n_seg, runs = varlen_work(query_lengths, key_lengths, starts, groups)
+    elif split == 'request':
+        out, n_seg, runs = request_work(query_lengths, key_lengths, starts, chunk, groups)
+    else:
+        raise ValueError(f'split must be one of {SPLITS}')
+    if capacity is None:
+        return out, n_seg, runs
+    seg_cap, run_cap = capacity
+    if n_seg > seg_cap or runs > run_cap:
+        raise ValueError('Segment plan exceeds its fixed capacity')
+    base = WORK_INTS * n_seg
+    ranges = out[base:base + runs + 1]
+    padded = out[:base] + [0] * (WORK_INTS * (seg_cap - n_seg)) + ranges + [ranges[-1]] * (run_cap - runs)
+    return padded + out[base + runs + 1:], seg_cap, run_cap
 
 
 def draft_work(context_lengths, cu_blocks, anchors, chunk):

@@ -107,3 +107,25 @@ def test_request_plan_cuts_depend_only_on_the_request():
                          chunk=chunk)
         for j, i in enumerate(perm):
             assert segs2[j] == segs[i] == [(c, min(c + chunk, kl[i])) for c in range(0, kl[i], chunk)]
+
+
+def test_fixed_capacity_layout_keeps_the_plan():
+    from qwen3_dspark_amd.schedule import segment_plan
+    rng = np.random.default_rng(5)
+    for split in ('balanced', 'request'):
+        for _ in range(30):
+            n = int(rng.integers(1, 20))
+            kl = [int(x) for x in rng.integers(1, 4000, size=n)]
+            ql = [min(k, 7) for k in kl]
+            runs = int(rng.integers(1, 40))
+            out, n_seg, g = segment_plan(split, ql, kl, list(range(n)), runs, 512)
+            cap = (n_seg + int(rng.integers(0, 50)), g + int(rng.integers(0, 9)))
+            pad, n_work, groups = segment_plan(split, ql, kl, list(range(n)), runs, 512, cap)
+            assert (n_work, groups) == cap
+            assert pad[:WORK_INTS * n_seg] == out[:WORK_INTS * n_seg]
+            ranges = pad[WORK_INTS * n_work:WORK_INTS * n_work + groups + 1]
+            assert ranges[:g + 1] == out[WORK_INTS * n_seg:WORK_INTS * n_seg + g + 1]
+            assert all(r == n_seg for r in ranges[g:])
+            assert pad[WORK_INTS * n_work + groups + 1:] == out[WORK_INTS * n_seg + g + 1:]
+            with pytest.raises(ValueError, match='capacity'):
+                segment_plan(split, ql, kl, list(range(n)), runs, 512, (n_seg - 1, g) if n_seg > 1 else (0, g))
