@@ -80,7 +80,7 @@ int64_t dspark_attn_workspace_bytes(int n_req, int64_t key_rows_bound, int row_t
  * causal query i of a request with q queries and k keys sees keys j <= k-q+i.
  * Key rows beyond cu_k[n_req] (a capacity tail) are never read.
  * Replaces aten::_flash_attention_forward as called by
- *   dspark_qwen/rocm_varlen.py:278-281          (PinnedRocmVarlenKernel.__call__, causal)
+ *   dspark_qwen/rocm_varlen.py:111-114          (PinnedRocmVarlenKernel.__call__, causal)
  *   dspark_qwen/packed_draft.py:26-29           (PinnedRocmDraftKernel.__call__, noncausal)
  *   dspark_qwen/persistent_qwen_target.py:231-234 (_native_attention, capacity tail)
  */

@@ -14,7 +14,7 @@
   (the callback finds it through the `fused_verification` forward kwarg, as
   the reference passes `persistent_target`).
 * PersistentQwenTarget - the full-model transaction adapter of
-  dspark_qwen/persistent_qwen_target.py:100-473 (verify / commit / abort /
+  dspark_qwen/persistent_qwen_target.py:100-472 (verify / commit / abort /
   prefill / predict / request_kv, captured layer features) on that path.
 
 The callbacks keep the reference's contract: no attention mask or dropout,
@@ -155,7 +155,7 @@ class FusedVerifier:
 
 
 # ---------------------------------------------------------------------------
-# Full-model transaction adapter (dspark_qwen/persistent_qwen_target.py:100-473)
+# Full-model transaction adapter (dspark_qwen/persistent_qwen_target.py:100-472)
 # ---------------------------------------------------------------------------
 
 @dataclass(frozen=True)
@@ -188,7 +188,7 @@ class PackedFeatures:
 
 class PersistentQwenTarget:
     """HF Qwen3 target over a PersistentTargetKV with the fused MI355X
-    attention (the API of persistent_qwen_target.py:100-473, eager path).
+    attention (the API of persistent_qwen_target.py:100-472, eager path).
 
     verify() runs one packed forward whose layers stage their new K/V rows
     into scratch and attend over resident + scratch rows in place; nothing is

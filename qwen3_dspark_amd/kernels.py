@@ -3,7 +3,7 @@
     kernel(query, key, value, layout, *, scale) -> Tensor
 
 Drop-ins for
-  * dspark_qwen/rocm_varlen.py:209-284  PinnedRocmVarlenKernel (causal, exact K)
+  * dspark_qwen/rocm_varlen.py:42-117   PinnedRocmVarlenKernel (causal, exact K)
   * dspark_qwen/packed_draft.py:19-32   PinnedRocmDraftKernel (noncausal, exact K)
   * dspark_qwen/persistent_qwen_target.py:223-234 _native_attention (causal,
     capacity-tail K with fixed bucket maxima)
@@ -46,7 +46,7 @@ class HipVarlenKernel:
         self._work_for = None
         self._work = None
 
-    # Same contract and error classes as rocm_varlen.py:232-273.
+    # Same contract and error classes as rocm_varlen.py:65-106.
     def _validate_inputs(self, query, key, value, layout, scale):
         tensors = (query, key, value)
         if any(not isinstance(t, torch.Tensor) or not t.is_cuda or t.device != self.device

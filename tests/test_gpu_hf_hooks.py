@@ -122,7 +122,7 @@ def test_varlen_callback_matches_fused_path():
 
 
 def test_persistent_qwen_target_prefill_verify_commit_features():
-    """The full-model adapter (persistent_qwen_target.py:100-473 API):
+    """The full-model adapter (persistent_qwen_target.py:100-472 API):
     prefill ragged prompts, verify 7 tokens per request, commit a prefix,
     verify again; logits via predict() and captured layer features match the
     CPU float32 model over each request's full sequence."""
