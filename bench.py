@@ -275,7 +275,8 @@ def main():
     result['next'] = {'verify_graph': verify_graph_leg(pool, bucket, handles, qv, kn, vn, verify_bytes),
                       'qkv_prologue': prologue_leg(dev, B * Q_LEN),
                       'draft_context_projection': [draft_projection_leg(dev, B, Q_LEN),
-                                                   draft_projection_leg(dev, 16, None)]}
+                                                   draft_projection_leg(dev, 16, None)],
+                      'lm_head_and_verification': sampling_leg(dev, args.no_cpu_baseline)}
 
     if not args.no_cpu_baseline:
         result['cpu_baseline'], result['parity'] = cpu_leg(args, pool, bucket, handles, contexts, anchors, qv, qd,
@@ -350,6 +351,65 @@ def verify_graph_leg(pool, bucket, handles, qv, kn, vn, bytes_of, reps=10):
     return {'layers': VERIFY_LAYERS, 'replay_ms': round(ms, 4), 'per_layer_ms': round(ms / VERIFY_LAYERS, 5),
             'gbs': round(bytes_of(ctx) * VERIFY_LAYERS / ms / 1e6, 1), 'replays': reps,
             'bit_identical_to_eager': bool(same)}
+
+
+def sampling_leg(dev, skip_cpu, reps=10):
+    """The consumer of a verification round: the LM head over each request's
+    7 + 1 verified rows (hidden 1024, vocab 151,936, random-init bf16,
+    hipBLASLt), then float64 speculative verification of 7 proposed tokens
+    per request against draft laws (temperature 0.8): row statistics + one
+    verification launch.  Median of `reps` event-timed rounds; the float64
+    numpy oracle on the host timed on the same logits (one round) unless
+    skipped, and every integer outcome compared with it."""
+    import numpy as np
+    import torch
+
+    from oracle import sampling as oracle
+    from qwen3_dspark_amd.sampling import TargetHead, logits_to_probabilities, sample_categorical, verify_proposals
+    V, H, R, N, T = 151936, 1024, B, Q_LEN, 0.8
+    g = torch.Generator(device=dev).manual_seed(SEED + 21)
+    head = TargetHead((torch.randn(V, H, generator=g, device=dev) * 0.05).to(torch.bfloat16))
+    hidden = torch.randn(R * (N + 1), H, generator=g, device=dev).to(torch.bfloat16)
+    logits = head(hidden)
+    rows = torch.arange(R * (N + 1), device=dev).reshape(R, N + 1)[:, :N].reshape(-1)
+    q = logits_to_probabilities(logits[rows].float() + torch.randn(R * N, V, generator=g, device=dev), T)
+    tokens = sample_categorical(q, torch.rand(R * N, generator=g, device=dev, dtype=torch.float64))
+    uniforms = torch.rand(R * (N + 1), generator=g, device=dev, dtype=torch.float64)
+    budgets = [64] * R
+    for _ in range(2):
+        verify_proposals(head(hidden), tokens, q, uniforms, counts=[N] * R, temperature=T, max_new_tokens=budgets)
+    t_head, t_ver = [], []
+    for _ in range(reps):
+        e = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
+        e[0].record()
+        logits = head(hidden)
+        e[1].record()
+        got = verify_proposals(logits, tokens, q, uniforms, counts=[N] * R, temperature=T, max_new_tokens=budgets)
+        e[2].record()
+        torch.cuda.synchronize()
+        t_head.append(e[0].elapsed_time(e[1]))
+        t_ver.append(e[1].elapsed_time(e[2]))
+    ms_head, ms_ver = float(np.median(t_head)), float(np.median(t_ver))
+    out = {'requests': R, 'rows': R * (N + 1), 'vocab': V,
+           'lm_head_ms': round(ms_head, 4), 'lm_head_tflops': round(2 * R * (N + 1) * H * V / ms_head / 1e9, 1),
+           'verify_ms': round(ms_ver, 4),
+           'verify_logit_gbs': round(logits.numel() * 2 / ms_ver / 1e6, 1),
+           'accepted_draft_tokens': sum(r.accepted_draft_tokens for r in got),
+           'emitted_tokens': sum(int(r.tokens.numel()) for r in got),
+           'rounds_per_s': round(1e3 / (ms_head + ms_ver), 1)}
+    if not skip_cpu:
+        p_in = logits.float().cpu().numpy()
+        q_h, t_h, u_h = q.cpu().numpy(), tokens.cpu().numpy(), uniforms.cpu().numpy()
+        t0 = time.perf_counter()
+        p_h = oracle.logits_to_probabilities(p_in, T)
+        ref = [oracle.verify_proposal(t_h[N * r:N * r + N], q_h[N * r:N * r + N], p_h[(N + 1) * r:(N + 1) * (r + 1)],
+                                      u_h[(N + 1) * r:(N + 1) * (r + 1)], max_new_tokens=64) for r in range(R)]
+        cpu_s = time.perf_counter() - t0
+        same = all((tuple(x.tokens.tolist()), x.accepted_draft_tokens, x.rejected_index, x.extra_token_kind,
+                    x.stop_reason, x.draws) == (y.tokens, y.accepted_draft_tokens, y.rejected_index,
+                                                y.extra_token_kind, y.stop_reason, y.draws) for x, y in zip(got, ref))
+        out.update(cpu_oracle_verify_ms=round(cpu_s * 1e3, 1), identical_to_oracle=bool(same))
+    return out
 
 
 def draft_projection_leg(dev, n_req, per_request, reps=20):

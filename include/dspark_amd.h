@@ -198,6 +198,67 @@ int dspark_draft_kv_project(const void* x, int tokens, int hidden, const void* w
                             int64_t slot_stride, int64_t head_stride, int32_t* flag, void* stream);
 
 /*
+ * Float64 sampling law and speculative verification (the consumer of the
+ * verification round, after the LM head), following
+ * dspark_qwen/tensor_sampling.py.  logits: [rows, >= vocab] bf16 (dtype 0)
+ * or fp32 (dtype 1), row_stride elements apart.
+ *
+ * dspark_logit_row_stats: per row and chunk of 8192 logits, the max of
+ * x / temperature and the sum of exp(x / temperature - max) (float64 pairs,
+ * dspark_row_stats_bytes(rows, vocab) bytes); bad[row] is set to 1 when a
+ * logit or its scaled value is not finite (the caller zeroes `bad` first).
+ * Replaces the softmax of logits_to_probabilities (tensor_sampling.py:37-48)
+ * for callers that never need the law materialised.
+ */
+int64_t dspark_row_stats_bytes(int rows, int vocab);
+int dspark_logit_row_stats(const void* logits, int dtype, int rows, int vocab, int64_t row_stride,
+                           double temperature, double* stats, int32_t* bad, void* stream);
+
+/*
+ * dspark_spec_verify: verify_proposal (tensor_sampling.py:114-162) for every
+ * request at once.  Request r owns logit rows cu_rows[r] .. cu_rows[r+1]
+ * (n_r + 1 rows), draft tokens / draft law rows cu_rows[r] - r .. + n_r of
+ * tokens (int64) and q (float64 [.., vocab]), and draws its uniforms from
+ * uniforms[cu_rows[r] ..] in the reference's order (at most n_r + 1).
+ * budget[r] is the remaining output budget; stops the EOS ids.  Outputs:
+ * the emitted tokens at out_tokens[cu_rows[r] ..] and out_meta[r][8] =
+ * {emitted, accepted draft tokens, rejected index (-1 none), extra (0 none,
+ * 1 residual, 2 bonus), stop (0 round complete, 1 eos, 2 budget), uniforms
+ * used, error (0 ok, 1 token outside the vocabulary, 2 zero q at a proposed
+ * token, 3 non-finite logits, 4 zero residual mass, 5 uniform outside
+ * [0, 1), 6 more than 255 proposed tokens), 0}.  stats/bad from dspark_logit_row_stats with the same
+ * temperature.  The q rows are read at the proposed tokens and, on a
+ * rejection, in full; their sums are not checked.  Three launches: one lane
+ * per request decides, then the final draws (see below).  workspace:
+ * dspark_draw_workspace_bytes(n_req) bytes, 64-byte aligned.
+ *
+ * Categorical draws (the final draw of a verification, and
+ * dspark_sample_rows): the first index whose running sum of the law exceeds
+ * u, else the last index of positive mass (sample_categorical,
+ * tensor_sampling.py:69-76), computed as 256 segment sums per draw, a scan,
+ * and a walk of one segment.
+ */
+int64_t dspark_draw_workspace_bytes(int jobs);
+int dspark_spec_verify(const void* logits, int dtype, int64_t row_stride, int vocab, double temperature,
+                       const double* stats, const int32_t* bad, const int32_t* cu_rows, int n_req,
+                       const int64_t* tokens, const double* q, const double* uniforms,
+                       const int32_t* budget, const int32_t* stops, int n_stops, int64_t* out_tokens,
+                       int32_t* out_meta, void* workspace, int64_t workspace_bytes, void* stream);
+
+/*
+ * dspark_logits_to_probs: the float64 law rows probs [rows, vocab] from the
+ * logits and their row statistics (logits_to_probabilities,
+ * tensor_sampling.py:37-48).  dspark_sample_rows: one categorical draw per
+ * row of float64 laws probs [rows, vocab] with uniforms[row] in [0, 1)
+ * (sample_categorical, tensor_sampling.py:69-76); workspace
+ * dspark_draw_workspace_bytes(rows) bytes, 64-byte aligned.
+ */
+int dspark_logits_to_probs(const void* logits, int dtype, int rows, int vocab, int64_t row_stride,
+                           double temperature, const double* stats, double* probs, void* stream);
+int dspark_sample_rows(const double* probs, int rows, int vocab, const double* uniforms, int64_t* out,
+                       void* workspace, int64_t workspace_bytes, void* stream);
+
+/*
  * Transaction metadata of PersistentTargetKV.begin
  * (dspark_qwen/persistent_target_kv.py:392-411), built on the device from
  * req = int32 [3][n_req] (slot, committed context, query length per request):

@@ -16,6 +16,7 @@ _P = ctypes.c_void_p
 _I = ctypes.c_int
 _L = ctypes.c_int64
 _F = ctypes.c_float
+_D = ctypes.c_double
 _PP = ctypes.POINTER(ctypes.c_void_p)   # host array of device pointers
 
 # name -> (restype, argtypes); mirrors include/dspark_amd.h exactly.
@@ -40,6 +41,12 @@ SIGNATURES = {
     'dspark_pool_append': (_I, [_P, _P, _L, _L, _L, _L, _L, _I, _L, _I, _I, _PP, _PP, _L, _L, _L, _P, _I, _P, _P]),
     'dspark_qkv_prologue': (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _F, _P, _P, _P, _L, _P]),
     'dspark_draft_kv_project': (_I, [_P, _I, _I, _P, _P, _I, _P, _P, _I, _F, _F, _P, _P, _L, _L, _L, _P, _P]),
+    'dspark_row_stats_bytes': (_L, [_I, _I]),
+    'dspark_logit_row_stats': (_I, [_P, _I, _I, _I, _L, _D, _P, _P, _P]),
+    'dspark_draw_workspace_bytes': (_L, [_I]),
+    'dspark_spec_verify': (_I, [_P, _I, _L, _I, _D, _P, _P, _P, _I, _P, _P, _P, _P, _P, _I, _P, _P, _P, _L, _P]),
+    'dspark_logits_to_probs': (_I, [_P, _I, _I, _I, _L, _D, _P, _P, _P]),
+    'dspark_sample_rows': (_I, [_P, _I, _I, _P, _P, _P, _L, _P]),
     'dspark_crop_plan_workspace_bytes': (_L, [_L]),
     'dspark_crop_plan': (_I, [_P, _P, _L, _L, _L, _P, _P, _P, _P, _L, _P]),
     'dspark_rows_rebuild': (_I, [_PP, _PP, _PP, _I, _I, _L, _L, _L, _P, _L, _P]),

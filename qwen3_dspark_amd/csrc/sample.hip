@@ -1,0 +1,573 @@
+// Float64 sampling law and speculative verification on gfx950: the consumer
+// of the target's verification output, after the LM head.
+//
+//   p_j = softmax(logits_j / T) in float64           (tensor_sampling.py:
+//                                                     logits_to_probabilities)
+//   draft token t_j with law q_j is accepted iff u_j < min(1, p_j[t_j] / q_j[t_j]);
+//   the first rejection emits a draw from (p_j - q_j)+ normalised, a fully
+//   accepted block a bonus draw from p_n; EOS and the output budget stop early
+//                                                    (tensor_sampling.py:
+//                                                     verify_proposal)
+//   a draw from a law r is the first index whose running sum of r exceeds u
+//   (searchsorted(cumsum(r), u, right=True)), else the last index of
+//   positive mass                                    (sample_categorical)
+//
+// The p rows are never materialised for verification: one pass over the
+// logits gives each row's max and sum of exp (split over many workgroups),
+// and every p value needed later is formed from them on the fly.  The
+// uniforms are inputs, consumed in the reference's draw order, so a given
+// tape of draws fixes every integer outcome.  All probability arithmetic is
+// float64 (the model's logits are bf16 or fp32).
+#include <cfloat>
+
+#include "common.h"
+
+namespace dspark {
+
+constexpr int ST_CHUNK = 8192;            // logits per row-statistics workgroup
+
+__device__ __forceinline__ double load_logit(const void* logits, int dtype, int64_t idx) {
+  if (dtype == 0) return (double)(float)static_cast<const bf16*>(logits)[idx];
+  return (double)static_cast<const float*>(logits)[idx];
+}
+
+// Block-wide sum for 256 threads (4 waves); `buf` holds 4 doubles.
+__device__ __forceinline__ double block_sum(double x, double* buf) {
+  #pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) x += __shfl_xor(x, off);
+  const int wave = threadIdx.x >> 6;
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) buf[wave] = x;
+  __syncthreads();
+  return buf[0] + buf[1] + buf[2] + buf[3];
+}
+
+// ---------------------------------------------------------------------------
+// Row statistics: per (row, chunk of ST_CHUNK logits) the max of x/T and the
+// sum of exp(x/T - max); a non-finite x or x/T marks the row in `bad`.
+// Division by T > 0 is monotone, so the first pass takes the max of the raw
+// logits and divides once: max(x/T) == max(x)/T exactly.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void row_stats_kernel(const void* logits, int dtype, int64_t row_stride, int vocab,
+                                                        double temperature, int chunks, double* stats,
+                                                        int32_t* bad) {
+  __shared__ double buf[4];
+  const int row = blockIdx.x / chunks;
+  const int c = blockIdx.x - row * chunks;
+  const int v0 = c * ST_CHUNK;
+  const int v1 = min(v0 + ST_CHUNK, vocab);
+  const int64_t base = (int64_t)row * row_stride;
+  double xmax = -INFINITY;
+  bool nonfinite = false;
+  for (int v = v0 + threadIdx.x; v < v1; v += blockDim.x) {
+    const double x = load_logit(logits, dtype, base + v);
+    nonfinite |= !isfinite(x);
+    xmax = fmax(xmax, x);
+  }
+  #pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) xmax = fmax(xmax, __shfl_xor(xmax, off));
+  const int wave = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 0) buf[wave] = xmax;
+  __syncthreads();
+  const double m = fmax(fmax(buf[0], buf[1]), fmax(buf[2], buf[3])) / temperature;
+  double sum = 0.0;
+  for (int v = v0 + threadIdx.x; v < v1; v += blockDim.x) {
+    const double y = load_logit(logits, dtype, base + v) / temperature;
+    nonfinite |= !isfinite(y);
+    sum += exp(y - m);
+  }
+  sum = block_sum(sum, buf);
+  if (threadIdx.x == 0) {
+    stats[2 * ((int64_t)row * chunks + c)] = m;
+    stats[2 * ((int64_t)row * chunks + c) + 1] = sum;
+  }
+  if (__builtin_amdgcn_ballot_w64(nonfinite) && (threadIdx.x & 63) == 0 && bad) bad[row] = 1;   // vector store
+}
+
+// Combined (max, sum) of one row from its chunk statistics.
+__device__ __forceinline__ void row_law(const double* stats, int row, int chunks, double& M, double& S) {
+  const double* st = stats + 2 * (int64_t)row * chunks;
+  M = -INFINITY;
+  for (int c = 0; c < chunks; ++c) M = fmax(M, st[2 * c]);
+  S = 0.0;
+  for (int c = 0; c < chunks; ++c) S += st[2 * c + 1] * exp(st[2 * c] - M);
+}
+
+// ---------------------------------------------------------------------------
+// Categorical draws.  A draw job names one law over the vocabulary:
+//   LAW      p(v) = exp(x_v / T - M) / S of one logit row,
+//   RESIDUAL (p(v) - q(v))+ of one logit row and one draft law row,
+//            normalised by its sum,
+//   PROBS    a materialised float64 law row,
+// and a uniform u.  The draw is the first index whose running sum exceeds u,
+// else the last index of positive mass.  The vocabulary is cut into 256
+// consecutive segments: a wide launch sums every segment of every job with
+// coalesced loads (SEG_SLICES workgroups per job), then one workgroup per
+// job scans its segment sums in order and one wave walks the segment where
+// the running sum passes u with a wave-level inclusive scan.  The sums are
+// float64 in another association than a sequential cumulative sum: only a u
+// within about an ulp of a boundary can land on the neighbouring index.
+// ---------------------------------------------------------------------------
+constexpr int NSEG = 256;                 // segments per job
+constexpr int SEG_SLICES = 32;            // segment-sum workgroups per job
+constexpr int SEG_PER_SLICE = NSEG / SEG_SLICES;
+static_assert(SEG_PER_SLICE % 4 == 0, "each wave sums the same number of segments");
+
+enum DrawKind { DK_NONE = 0, DK_LAW = 1, DK_RESIDUAL = 2, DK_PROBS = 3 };
+
+struct DrawJob {
+  int64_t src;        // element offset of the logit or probability row
+  int64_t qrow;       // element offset of the draft law row (RESIDUAL)
+  int64_t out;        // where the drawn token goes
+  double M, S, u;     // row max / sum of the logit row, the uniform
+  int32_t kind;
+  int32_t req;        // verification request (-1: a plain row draw)
+  int64_t pad;
+};
+static_assert(sizeof(DrawJob) == 64, "draw job layout");
+
+struct DrawSrc {
+  const void* logits;
+  int dtype;
+  double temperature;
+  const double* q;
+  const double* probs;
+  int vocab;
+};
+
+__device__ __forceinline__ double draw_value(const DrawSrc& s, const DrawJob& j, int v) {
+  if (j.kind == DK_PROBS) return s.probs[j.src + v];
+  const double p = exp(load_logit(s.logits, s.dtype, j.src + v) / s.temperature - j.M) / j.S;
+  return j.kind == DK_RESIDUAL ? fmax(p - s.q[j.qrow + v], 0.0) : p;
+}
+
+__device__ __forceinline__ void segment_bounds(int seg, int vocab, int& s0, int& s1) {
+  const int per = (vocab + NSEG - 1) / NSEG;
+  s0 = min(seg * per, vocab);
+  s1 = min(s0 + per, vocab);
+}
+
+// grid: jobs x SEG_SLICES; each wave sums SEG_PER_SLICE / 4 segments.
+__global__ __launch_bounds__(256) void segment_sums_kernel(DrawSrc src, const DrawJob* jobs, double* segsum,
+                                                           int32_t* seglast) {
+  const int job = blockIdx.x / SEG_SLICES;
+  const int slice = blockIdx.x - job * SEG_SLICES;
+  const DrawJob j = jobs[job];
+  if (j.kind == DK_NONE) return;
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  for (int i = 0; i < SEG_PER_SLICE / 4; ++i) {
+    const int seg = slice * SEG_PER_SLICE + wave * (SEG_PER_SLICE / 4) + i;
+    int s0, s1;
+    segment_bounds(seg, src.vocab, s0, s1);
+    double part = 0.0;
+    int last = -1;
+    for (int v = s0 + lane; v < s1; v += WAVE) {
+      const double r = draw_value(src, j, v);
+      part += r;
+      if (r > 0.0) last = v;
+    }
+    #pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+      part += __shfl_xor(part, off);
+      last = max(last, __shfl_xor(last, off));
+    }
+    if (lane == 0) {
+      segsum[(int64_t)job * NSEG + seg] = part;
+      seglast[(int64_t)job * NSEG + seg] = last;
+    }
+  }
+}
+
+__device__ __forceinline__ double wave_inclusive_scan(double x, int lane) {
+  #pragma unroll
+  for (int off = 1; off < WAVE; off <<= 1) {
+    const double y = __shfl_up(x, off);
+    if (lane >= off) x += y;
+  }
+  return x;
+}
+
+struct DrawOut {
+  int64_t* tokens;          // drawn token of job j goes to tokens[jobs[j].out]
+  int32_t* meta;            // verification requests: [n_req][8] (see the C ABI)
+  const int32_t* budget;
+  const int32_t* stops;
+  int n_stops;
+};
+
+enum VerifyError { VE_OK = 0, VE_TOKEN = 1, VE_ZERO_Q = 2, VE_LOGITS = 3, VE_RESIDUAL = 4, VE_UNIFORM = 5, VE_SHAPE = 6 };
+enum Extra { EX_NONE = 0, EX_RESIDUAL = 1, EX_BONUS = 2 };
+enum Stop { ST_ROUND = 0, ST_EOS = 1, ST_BUDGET = 2 };
+
+__device__ __forceinline__ bool is_stop(const int32_t* stops, int n_stops, int64_t tok) {
+  for (int i = 0; i < n_stops; ++i)
+    if (stops[i] == tok) return true;
+  return false;
+}
+
+// grid: jobs; 256 threads (thread t owns segment t).
+__global__ __launch_bounds__(256) void draw_kernel(DrawSrc src, const DrawJob* jobs, const double* segsum,
+                                                   const int32_t* seglast, DrawOut o) {
+  __shared__ double scan[NSEG];
+  __shared__ double buf[4];
+  __shared__ int found[2];
+  const DrawJob j = jobs[blockIdx.x];
+  if (j.kind == DK_NONE) return;                    // uniform across the workgroup
+  const int t = threadIdx.x;
+  const int lane = t & 63;
+  const int wave = t >> 6;
+  const double part = segsum[(int64_t)blockIdx.x * NSEG + t];
+  int last = seglast[(int64_t)blockIdx.x * NSEG + t];
+  #pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) last = max(last, __shfl_xor(last, off));
+  double norm = 1.0;
+  if (j.kind == DK_RESIDUAL) {
+    norm = block_sum(part, buf);
+    if (!(norm > 0.0)) {
+      if (t == 0 && j.req >= 0) o.meta[8 * j.req + 6] = VE_RESIDUAL;
+      return;
+    }
+  }
+  if (t == 0) {
+    found[0] = INT32_MAX;
+    found[1] = -1;
+  }
+  scan[t] = part / norm;
+  __syncthreads();
+  if (lane == 0) atomicMax(&found[1], last);
+  for (int off = 1; off < NSEG; off <<= 1) {         // inclusive scan in segment order
+    const double add = t >= off ? scan[t - off] : 0.0;
+    __syncthreads();
+    scan[t] += add;
+    __syncthreads();
+  }
+  const double before = t ? scan[t - 1] : 0.0;
+  if (before <= j.u && j.u < scan[t]) found[0] = -2 - t;   // at most one segment: the scan never falls
+  __syncthreads();
+  const int mark = found[0];
+  __syncthreads();
+  if (mark <= -2) {
+    if (wave == 0) {
+      const int seg = -2 - mark;
+      int s0, s1;
+      segment_bounds(seg, src.vocab, s0, s1);
+      double run = seg ? scan[seg - 1] : 0.0;
+      int hit = INT32_MAX, pos = -1;
+      for (int v0 = s0; v0 < s1 && hit == INT32_MAX; v0 += WAVE) {
+        const int v = v0 + lane;
+        const double r = v < s1 ? draw_value(src, j, v) / norm : 0.0;
+        if (r > 0.0) pos = v;
+        const double incl = run + wave_inclusive_scan(r, lane);
+        const unsigned long long over = __builtin_amdgcn_ballot_w64(v < s1 && incl > j.u);
+        if (over) hit = v0 + __builtin_ctzll(over);
+        run = __shfl(incl, WAVE - 1);
+      }
+      // no crossing reproduced: the segment's last index of positive mass
+      #pragma unroll
+      for (int off = 32; off >= 1; off >>= 1) pos = max(pos, __shfl_xor(pos, off));
+      if (lane == 0) found[0] = hit != INT32_MAX ? hit : pos;
+    }
+  } else if (t == 0) {
+    found[0] = found[1];                             // u at or beyond the total mass
+  }
+  __syncthreads();
+  if (t == 0) {
+    const int tok = found[0];
+    if (j.req < 0) {
+      o.tokens[j.out] = tok;
+    } else {
+      int32_t* meta = o.meta + 8 * j.req;
+      const int emitted = meta[0];
+      o.tokens[j.out + emitted] = tok;
+      meta[0] = emitted + 1;
+      meta[4] = is_stop(o.stops, o.n_stops, tok) ? ST_EOS : (emitted + 1 == o.budget[j.req] ? ST_BUDGET : ST_ROUND);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Speculative verification decisions: one wave per request (verify_proposal's
+// loop); the final draw, if any, becomes a draw job for the two launches
+// above.
+// ---------------------------------------------------------------------------
+struct VerifyArgs {
+  const void* logits;        // [rows, >= vocab], row_stride apart; request r owns rows cu_rows[r] .. cu_rows[r+1]
+  int dtype;                 // 0 bf16, 1 fp32
+  int64_t row_stride;
+  int vocab;
+  double temperature;
+  const double* stats;       // row statistics, `chunks` (max, sum) pairs per row
+  int chunks;
+  const int32_t* bad;        // [rows] non-finite flags
+  const int32_t* cu_rows;    // [n_req + 1]
+  const int64_t* tokens;     // [rows - n_req] draft tokens; request r's at cu_rows[r] - r
+  const double* q;           // [rows - n_req, vocab] draft laws, same order
+  const double* uniforms;    // [rows]: request r draws from uniforms[cu_rows[r] ..]
+  const int32_t* budget;     // [n_req] remaining output budget
+  const int32_t* stops;      // [n_stops] EOS ids
+  int n_stops;
+  int n_req;
+  int64_t* out_tokens;       // [rows]: request r writes up to n_r + 1 tokens at cu_rows[r]
+  int32_t* out_meta;         // [n_req][8]: emitted, accepted, rejected index, extra, stop, draws, error, 0
+  DrawJob* jobs;             // [n_req]
+};
+
+constexpr int MAX_PROPOSAL = 255;          // draft tokens per request in one verification
+
+// One wave per request: the lanes form every row's (max, sum) and every
+// proposed token's acceptance ratio min(1, p/q) in parallel, then lane 0
+// walks the proposal in order.
+__global__ __launch_bounds__(64) void verify_plan_kernel(VerifyArgs a) {
+  __shared__ double alpha[MAX_PROPOSAL];
+  __shared__ double law[2 * (MAX_PROPOSAL + 1)];
+  const int r = blockIdx.x;
+  const int lane = threadIdx.x;
+  const int row0 = a.cu_rows[r];
+  const int n = a.cu_rows[r + 1] - row0 - 1;
+  const int d0 = row0 - r;
+  const int V = a.vocab;
+  const double T = a.temperature;
+  if (n < 0 || n > MAX_PROPOSAL) {                       // wave-uniform; nothing else is read
+    if (lane == 0) {
+      DrawJob job{};
+      job.kind = DK_NONE;
+      job.req = r;
+      a.jobs[r] = job;
+      int32_t* meta = a.out_meta + 8 * r;
+      for (int i = 0; i < 8; ++i) meta[i] = 0;
+      meta[6] = VE_SHAPE;
+    }
+    return;
+  }
+  int err = VE_OK;
+  for (int j = lane; j <= n; j += WAVE) {
+    if (a.bad[row0 + j]) err = max(err, 3 * 16);            // ordered: logits, then token range, then zero q
+    if (j < n) {
+      const int64_t tok = a.tokens[d0 + j];
+      if (tok < 0 || tok >= V) err = max(err, 2 * 16);
+    }
+  }
+  #pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) err = max(err, __shfl_xor(err, off));
+  if (err == 0) {
+    for (int j = lane; j < n; j += WAVE)
+      if (!(a.q[(int64_t)(d0 + j) * V + a.tokens[d0 + j]] > 0.0)) err = 1 * 16;
+    #pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) err = max(err, __shfl_xor(err, off));
+  }
+  err = err == 3 * 16 ? VE_LOGITS : (err == 2 * 16 ? VE_TOKEN : (err == 1 * 16 ? VE_ZERO_Q : VE_OK));
+  if (err == VE_OK) {
+    for (int j = lane; j <= n; j += WAVE) {
+      double M, S;
+      row_law(a.stats, row0 + j, a.chunks, M, S);
+      law[2 * j] = M;
+      law[2 * j + 1] = S;
+      if (j < n) {
+        const int64_t tok = a.tokens[d0 + j];
+        const double p = exp(load_logit(a.logits, a.dtype, (int64_t)(row0 + j) * a.row_stride + tok) / T - M) / S;
+        alpha[j] = fmin(p / a.q[(int64_t)(d0 + j) * V + tok], 1.0);
+      }
+    }
+  }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+  __syncthreads();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+  if (lane != 0) return;
+  int emitted = 0, accepted = 0, rejected = -1, extra = EX_NONE, stop = ST_ROUND, draws = 0, final_row = -1;
+  if (err == VE_OK && a.budget[r] == 0) {
+    stop = ST_BUDGET;
+  } else if (err == VE_OK) {
+    bool done = false;
+    for (int j = 0; j < n && !done; ++j) {
+      const double u = a.uniforms[row0 + draws++];
+      if (!(u >= 0.0 && u < 1.0)) {
+        err = VE_UNIFORM;
+        break;
+      }
+      if (u >= alpha[j]) {
+        rejected = j;
+        accepted = j;
+        extra = EX_RESIDUAL;
+        final_row = j;
+        done = true;
+        break;
+      }
+      const int64_t tok = a.tokens[d0 + j];
+      a.out_tokens[row0 + emitted++] = tok;
+      accepted = j + 1;
+      if (is_stop(a.stops, a.n_stops, tok)) {
+        stop = ST_EOS;
+        done = true;
+      } else if (emitted == a.budget[r]) {
+        stop = ST_BUDGET;
+        done = true;
+      }
+    }
+    if (!done && err == VE_OK) {
+      extra = EX_BONUS;
+      final_row = n;
+      accepted = n;
+    }
+  }
+  DrawJob job{};
+  job.kind = DK_NONE;
+  job.req = r;
+  job.out = row0;
+  if (err == VE_OK && final_row >= 0) {
+    const double u = a.uniforms[row0 + draws++];
+    if (!(u >= 0.0 && u < 1.0)) {
+      err = VE_UNIFORM;
+    } else {
+      job.M = law[2 * final_row];
+      job.S = law[2 * final_row + 1];
+      job.u = u;
+      job.src = (int64_t)(row0 + final_row) * a.row_stride;
+      job.qrow = (int64_t)(d0 + final_row) * V;
+      job.kind = extra == EX_BONUS ? DK_LAW : DK_RESIDUAL;
+    }
+  }
+  a.jobs[r] = job;
+  int32_t* meta = a.out_meta + 8 * r;
+  meta[0] = emitted;
+  meta[1] = accepted;
+  meta[2] = rejected;
+  meta[3] = extra;
+  meta[4] = stop;
+  meta[5] = draws;
+  meta[6] = err;
+  meta[7] = 0;
+}
+
+// ---------------------------------------------------------------------------
+// Materialised laws and plain categorical draws (the draft's proposal side).
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void probs_kernel(const void* logits, int dtype, int64_t row_stride, int vocab,
+                                                    double temperature, const double* stats, int chunks,
+                                                    double* probs) {
+  const int row = blockIdx.y;
+  double M, S;
+  row_law(stats, row, chunks, M, S);
+  const int64_t base = (int64_t)row * row_stride;
+  for (int v = blockIdx.x * blockDim.x + threadIdx.x; v < vocab; v += gridDim.x * blockDim.x)
+    probs[(int64_t)row * vocab + v] = exp(load_logit(logits, dtype, base + v) / temperature - M) / S;
+}
+
+__global__ __launch_bounds__(256) void row_jobs_kernel(int rows, int vocab, const double* uniforms, DrawJob* jobs) {
+  const int row = blockIdx.x * blockDim.x + threadIdx.x;
+  if (row >= rows) return;
+  DrawJob j{};
+  j.src = (int64_t)row * vocab;
+  j.out = row;
+  j.u = uniforms[row];
+  j.kind = DK_PROBS;
+  j.req = -1;
+  jobs[row] = j;
+}
+
+}  // namespace dspark
+
+using namespace dspark;
+
+namespace {
+int stat_chunks(int vocab) { return (vocab + ST_CHUNK - 1) / ST_CHUNK; }
+}
+
+extern "C" int64_t dspark_row_stats_bytes(int rows, int vocab) {
+  if (rows < 1 || vocab < 1) return -1;
+  return (int64_t)rows * stat_chunks(vocab) * 2 * (int64_t)sizeof(double);
+}
+
+extern "C" int dspark_logit_row_stats(const void* logits, int dtype, int rows, int vocab, int64_t row_stride,
+                                      double temperature, double* stats, int32_t* bad, void* stream) {
+  clear_error();
+  DSPARK_REQUIRE(logits && stats && bad, "null pointer argument");
+  DSPARK_REQUIRE(dtype == 0 || dtype == 1, "dtype must be 0 (bf16) or 1 (fp32)");
+  DSPARK_REQUIRE(rows >= 1 && vocab >= 1 && row_stride >= vocab, "need rows, vocab >= 1 and row_stride >= vocab");
+  DSPARK_REQUIRE(temperature > 0.0 && temperature < DBL_MAX, "temperature must be finite and positive");
+  const int64_t grid = (int64_t)rows * stat_chunks(vocab);
+  DSPARK_REQUIRE(grid <= 0x7fffffffLL, "too many rows");
+  hipLaunchKernelGGL(row_stats_kernel, dim3((unsigned)grid), dim3(256), 0, static_cast<hipStream_t>(stream), logits,
+                     dtype, row_stride, vocab, temperature, stat_chunks(vocab), stats, bad);
+  return launch_status("row_stats_kernel");
+}
+
+namespace {
+// [jobs: DrawJob][segment sums: double x 256][segment last indices: int32 x 256] per job
+int64_t draw_workspace(int jobs) { return (int64_t)jobs * ((int64_t)sizeof(DrawJob) + NSEG * 12); }
+
+int launch_draws(const DrawSrc& src, DrawJob* jobs, int n_jobs, const DrawOut& o, hipStream_t s) {
+  double* segsum = reinterpret_cast<double*>(jobs + n_jobs);
+  int32_t* seglast = reinterpret_cast<int32_t*>(segsum + (int64_t)n_jobs * NSEG);
+  hipLaunchKernelGGL(segment_sums_kernel, dim3((unsigned)((int64_t)n_jobs * SEG_SLICES)), dim3(256), 0, s, src, jobs,
+                     segsum, seglast);
+  int rc = launch_status("segment_sums_kernel");
+  if (rc != OK) return rc;
+  hipLaunchKernelGGL(draw_kernel, dim3(n_jobs), dim3(256), 0, s, src, jobs, segsum, seglast, o);
+  return launch_status("draw_kernel");
+}
+}  // namespace
+
+extern "C" int64_t dspark_draw_workspace_bytes(int jobs) {
+  if (jobs < 1) return -1;
+  return draw_workspace(jobs);
+}
+
+extern "C" int dspark_spec_verify(const void* logits, int dtype, int64_t row_stride, int vocab, double temperature,
+                                  const double* stats, const int32_t* bad, const int32_t* cu_rows, int n_req,
+                                  const int64_t* tokens, const double* q, const double* uniforms,
+                                  const int32_t* budget, const int32_t* stops, int n_stops, int64_t* out_tokens,
+                                  int32_t* out_meta, void* workspace, int64_t workspace_bytes, void* stream) {
+  clear_error();
+  DSPARK_REQUIRE(logits && stats && bad && cu_rows && tokens && q && uniforms && budget && out_tokens && out_meta &&
+                     workspace,
+                 "null pointer argument");
+  DSPARK_REQUIRE(dtype == 0 || dtype == 1, "dtype must be 0 (bf16) or 1 (fp32)");
+  DSPARK_REQUIRE(vocab >= 1 && row_stride >= vocab && n_req >= 1 && n_req <= (1 << 24),
+                 "need vocab >= 1, row_stride >= vocab, n_req in [1, 2^24]");
+  DSPARK_REQUIRE(temperature > 0.0 && temperature < DBL_MAX, "temperature must be finite and positive");
+  DSPARK_REQUIRE(n_stops >= 0 && (n_stops == 0 || stops), "stops must be given when n_stops > 0");
+  DSPARK_REQUIRE(workspace_bytes >= draw_workspace(n_req) && (reinterpret_cast<uintptr_t>(workspace) & 63) == 0,
+                 "workspace must be 64-byte aligned and hold dspark_draw_workspace_bytes(n_req) bytes");
+  DrawJob* jobs = static_cast<DrawJob*>(workspace);
+  VerifyArgs a{logits, dtype, row_stride, vocab, temperature, stats, stat_chunks(vocab), bad, cu_rows, tokens, q,
+               uniforms, budget, stops, n_stops, n_req, out_tokens, out_meta, jobs};
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  hipLaunchKernelGGL(verify_plan_kernel, dim3(n_req), dim3(64), 0, s, a);
+  int rc = launch_status("verify_plan_kernel");
+  if (rc != OK) return rc;
+  const DrawSrc src{logits, dtype, temperature, q, nullptr, vocab};
+  const DrawOut o{out_tokens, out_meta, budget, stops, n_stops};
+  return launch_draws(src, jobs, n_req, o, s);
+}
+
+extern "C" int dspark_logits_to_probs(const void* logits, int dtype, int rows, int vocab, int64_t row_stride,
+                                      double temperature, const double* stats, double* probs, void* stream) {
+  clear_error();
+  DSPARK_REQUIRE(logits && stats && probs, "null pointer argument");
+  DSPARK_REQUIRE(dtype == 0 || dtype == 1, "dtype must be 0 (bf16) or 1 (fp32)");
+  DSPARK_REQUIRE(rows >= 1 && rows <= 65535 && vocab >= 1 && row_stride >= vocab,
+                 "need rows in [1, 65535], vocab >= 1 and row_stride >= vocab");
+  DSPARK_REQUIRE(temperature > 0.0 && temperature < DBL_MAX, "temperature must be finite and positive");
+  const unsigned gx = (unsigned)std::min<int64_t>((vocab + 255) / 256, 64);
+  hipLaunchKernelGGL(probs_kernel, dim3(gx, rows), dim3(256), 0, static_cast<hipStream_t>(stream), logits, dtype,
+                     row_stride, vocab, temperature, stats, stat_chunks(vocab), probs);
+  return launch_status("probs_kernel");
+}
+
+extern "C" int dspark_sample_rows(const double* probs, int rows, int vocab, const double* uniforms, int64_t* out,
+                                  void* workspace, int64_t workspace_bytes, void* stream) {
+  clear_error();
+  DSPARK_REQUIRE(probs && uniforms && out && workspace, "null pointer argument");
+  DSPARK_REQUIRE(rows >= 1 && rows <= (1 << 24) && vocab >= 1, "need rows in [1, 2^24] and vocab >= 1");
+  DSPARK_REQUIRE(workspace_bytes >= draw_workspace(rows) && (reinterpret_cast<uintptr_t>(workspace) & 63) == 0,
+                 "workspace must be 64-byte aligned and hold dspark_draw_workspace_bytes(rows) bytes");
+  DrawJob* jobs = static_cast<DrawJob*>(workspace);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  hipLaunchKernelGGL(row_jobs_kernel, dim3((rows + 255) / 256), dim3(256), 0, s, rows, vocab, uniforms, jobs);
+  int rc = launch_status("row_jobs_kernel");
+  if (rc != OK) return rc;
+  const DrawSrc src{nullptr, 0, 1.0, nullptr, probs, vocab};
+  const DrawOut o{out, nullptr, nullptr, nullptr, 0};
+  return launch_draws(src, jobs, rows, o, s);
+}
