@@ -33,7 +33,7 @@ int dspark_abi_version(void);
  * heads x `row_tiles` 16-row tiles (row_tiles = ceil(max_q/8) for
  * varlen/verify, max blocks per request for draft), where
  *   n = ceil(key_rows_bound / chunk) + n_req    (fixed chunks, no work list)
- * A varlen/verify call with a work list of n_work segments needs
+ * A call with a work list of n_work segments needs
  * dspark_attn_workspace_bytes(n_work, 0, row_tiles, chunk) bytes.  Each
  * attention call is a chunk kernel plus a merge kernel on `stream`; calls
  * that share a workspace must not overlap in time.  Returns -1 on invalid
@@ -64,15 +64,17 @@ int64_t dspark_attn_workspace_bytes(int n_req, int64_t key_rows_bound, int row_t
  * `chunk` keys in request order: the launch depends only on n_req,
  * key_rows_bound and max_q (the capacity-tail kernel relies on this).
  *
- * draft: item lists.  Request r's context is split into ceil(len_r / chunk)
- * chunks (at least one) and one workgroup runs per (chunk, KV head); work
- * holds int32 [n_work][8] item records, every chunk exactly once in dispatch
- * order (longest first balances ragged lengths), then int32 [n_req][4]
- * request records:
- *   item: request, chunk, chunk base (sum of the chunk counts of earlier
- *     requests), context length, first block, block count, largest anchor,
- *     chunk count;
- *   request: chunk base, chunk count, first block, block count.
+ * draft: segment lists of the same shape over the context rows each request
+ * streams (0 .. its largest anchor): workgroup (run w, KV head g) processes
+ * the records of run w:
+ *   [n_work][8] segment records, grouped by run: request, k0, k1, partial
+ *       slot (-1: one segment), first block, block count, largest anchor, 0
+ *   [n_groups + 1] run ranges
+ *   [n_req][4] request records: first partial slot, segment count, first
+ *       block, block count
+ * The segment with k1 equal to the largest anchor (the last) also attends
+ * the blocks' own rows.  Without a list, workgroup (chunk, KV head) runs a
+ * fixed chunk of `chunk` context rows, chunks in request order.
  *
  * Packed varlen attention, bottom-right causal (causal=1) or noncausal.
  * q [q_rows,16,128], k/v [k_rows,8,128], cu_q/cu_k int32 [n_req+1].
@@ -149,7 +151,7 @@ int dspark_draft_attn_fwd(const void* q, const void* k_ctx, const void* v_ctx,
                           const void* k_blk, const void* v_blk,
                           const int32_t* cu_blocks, const int32_t* anchors,
                           int n_req, int64_t ctx_rows_bound, int max_blocks, float scale, int chunk,
-                          const int32_t* work, int n_work,
+                          const int32_t* work, int n_work, int n_groups,
                           void* out, void* workspace, int64_t workspace_bytes, void* stream);
 
 /*

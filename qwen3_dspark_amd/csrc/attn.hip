@@ -569,7 +569,8 @@ struct DraftArgs {
   float* part_ml;
   int64_t tok_stride;
   int64_t head_stride;
-  const int32_t* work;      // optional [n_items][2] (request, chunk) dispatch order
+  const int32_t* work;      // optional segment list (see the C ABI)
+  int n_work;               // segment records in the work list
   int n_req;
   int chunk;
   int tmax;                 // max blocks per request (<= 8)
@@ -589,46 +590,34 @@ static_assert(DRAFT_PIECES == DWAVES * 4, "each thread issues 4 direct loads per
 // (the append-order pool); otherwise they are consecutive rows.  The
 // non-indexed instance has no ordinary global loads inside the stage loop,
 // so nothing forces a full vmcnt drain between ring stages.
+// One context segment of one request: keys [k0, k1) of request r (whose
+// blocks are b0 .. b0+nb, largest anchor amax).  The segment ending the
+// request (`last`) also attends the blocks' own rows.  A request held by
+// more than one segment writes FP32 partials per block to slot pslot (>= 0);
+// a request held by one segment writes its output.
+struct DraftSeg {
+  int r, k0, k1, pslot, b0, nb, amax;
+  bool last;
+};
+
+// No early return: every wave reaches the end, so a caller may place
+// workgroup barriers between items.
 template <bool INDEXED>
-__global__ __launch_bounds__(512) void draft_attn_kernel(DraftArgs a) {
-  __shared__ __attribute__((aligned(16))) unsigned char smem[DRAFT_SMEM];
+__device__ __forceinline__ void draft_item(const DraftArgs& a, unsigned char* smem, const DraftSeg& sg, int g) {
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
   const int col = lane & 15;
   const int grp = lane >> 4;
-  const int g = blockIdx.x & 7;
-  const int cl = blockIdx.x >> 3;
-
-  // Work record (one scalar load): request, chunk, chunk base, context
-  // length, first block, block count, largest anchor, chunk count.
-  int r, first, c, ctx, b0, nb, amax, nch;
-  if (a.work) {
-    const int32_t* w = a.work + WORK_INTS * cl;
-    r = w[0];
-    c = w[1];
-    first = w[2];
-    ctx = w[3];
-    b0 = w[4];
-    nb = w[5];
-    amax = w[6];
-    nch = w[7];
-  } else {
-    locate_chunk(nullptr, a.ctx_len, a.n_req, a.chunk, cl, r, first);
-    if (r < 0) return;
-    c = cl - first;
-    ctx = a.ctx_len[r];
-    nch = chunks_for(ctx, a.chunk);
-    b0 = a.cu_b[r];
-    nb = a.cu_b[r + 1] - b0;
-    amax = 0;
-    for (int b = 0; b < nb; ++b) amax = max(amax, a.anchors[b0 + b]);
-  }
-  const int item = first + c;
-  const int k0 = c * a.chunk;
-  const int k1 = min(k0 + a.chunk, ctx);
+  const int r = __builtin_amdgcn_readfirstlane(sg.r);
+  const int k0 = __builtin_amdgcn_readfirstlane(sg.k0);
+  const int k1 = __builtin_amdgcn_readfirstlane(sg.k1);
+  const int pslot = __builtin_amdgcn_readfirstlane(sg.pslot);
+  const int b0 = __builtin_amdgcn_readfirstlane(sg.b0);
+  const int nb = __builtin_amdgcn_readfirstlane(sg.nb);
+  const int amax = __builtin_amdgcn_readfirstlane(sg.amax);
+  const bool last = sg.last;
   const int kend = min(k1, amax);
-
   // This wave's block (if any): rows = 7 tokens x the 2 query heads of KV head g.
   const int b = wave;
   const bool active = b < nb;
@@ -721,7 +710,7 @@ __global__ __launch_bounds__(512) void draft_attn_kernel(DraftArgs a) {
     #pragma unroll
     for (int p = 0; p < DSTAGES - 1; ++p) issue(p);
     for (int s = 0; s < n_steps; ++s) {
-      asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+      asm volatile("s_waitcnt vmcnt(%0)" ::"n"(4 * (DSTAGES - 2)) : "memory");
       asm volatile("s_barrier" ::: "memory");
       issue(s + DSTAGES - 1);
       if (active) compute(s);
@@ -731,7 +720,7 @@ __global__ __launch_bounds__(512) void draft_attn_kernel(DraftArgs a) {
   }
 
   // Own-block keys (bidirectional within the block), once per request.
-  if (c == nch - 1 && active) {
+  if (last && active) {
     unsigned char* wv = smem + wave * 8 * ROWB;   // 8 rows per wave
     const size_t rb = (size_t)BLOCK_ROWS * (b0 + b);
     bf16x8 kf[2][4];
@@ -763,30 +752,65 @@ __global__ __launch_bounds__(512) void draft_attn_kernel(DraftArgs a) {
     wave_lds_sync();
   }
 
-  if (!active) return;
-  const float l = wave_sum_across_groups(st.l);
-  const size_t orow0 = (size_t)BLOCK_ROWS * (b0 + b);
-  if (nch == 1) {
-    if (row_ok) {
-      bf16* op = a.out + (orow0 + tok) * Q_ROW + (size_t)(2 * g + (col & 1)) * HD + 4 * grp;
-      #pragma unroll
-      for (int nbk = 0; nbk < 8; ++nbk) {
-        bf16x4 ov;
+  if (active) {
+    const float l = wave_sum_across_groups(st.l);
+    const size_t orow0 = (size_t)BLOCK_ROWS * (b0 + b);
+    if (pslot < 0) {
+      if (row_ok) {
+        bf16* op = a.out + (orow0 + tok) * Q_ROW + (size_t)(2 * g + (col & 1)) * HD + 4 * grp;
         #pragma unroll
-        for (int e = 0; e < 4; ++e) ov[e] = (bf16)(st.o[nbk][e] / l);
-        *reinterpret_cast<bf16x4*>(op + 16 * nbk) = ov;
+        for (int nbk = 0; nbk < 8; ++nbk) {
+          bf16x4 ov;
+          #pragma unroll
+          for (int e = 0; e < 4; ++e) ov[e] = (bf16)(st.o[nbk][e] / l);
+          *reinterpret_cast<bf16x4*>(op + 16 * nbk) = ov;
+        }
       }
+    } else {
+      const size_t p = (size_t)(pslot * 8 + g) * a.tmax + b;
+      float* po = a.part_o + (p * 16 + col) * HD + 4 * grp;
+      #pragma unroll
+      for (int nbk = 0; nbk < 8; ++nbk) *reinterpret_cast<f32x4*>(po + 16 * nbk) = st.o[nbk];
+      if (grp == 0) {
+        a.part_ml[(p * 16 + col) * 2 + 0] = st.m;
+        a.part_ml[(p * 16 + col) * 2 + 1] = l;
+      }
+    }
+  }
+}
+
+// With a work list, workgroup (run w, KV head g) runs the segments of run w
+// (blockIdx.x = 8w + g).  Without one, workgroup (chunk, KV head) runs one
+// fixed chunk of `chunk` context rows, chunks in request order.
+template <bool INDEXED>
+__global__ __launch_bounds__(512) void draft_attn_kernel(DraftArgs a) {
+  __shared__ __attribute__((aligned(16))) unsigned char smem[DRAFT_SMEM];
+  const int g = blockIdx.x & 7;
+  if (a.work) {
+    const int32_t* range = a.work + WORK_INTS * a.n_work + (blockIdx.x >> 3);
+    const int lo = min(max(range[0], 0), a.n_work);     // clamped: never past the records
+    const int hi = min(max(range[1], lo), a.n_work);
+    for (int i = lo; i < hi; ++i) {
+      const int32_t* w = a.work + WORK_INTS * i;
+      const DraftSeg sg{w[0], w[1], w[2], w[3], w[4], w[5], w[6], w[2] >= w[6]};
+      draft_item<INDEXED>(a, smem, sg, g);
+      __syncthreads();   // the next segment refills the ring the last one read
     }
     return;
   }
-  const size_t p = (size_t)(item * 8 + g) * a.tmax + b;
-  float* po = a.part_o + (p * 16 + col) * HD + 4 * grp;
-  #pragma unroll
-  for (int nbk = 0; nbk < 8; ++nbk) *reinterpret_cast<f32x4*>(po + 16 * nbk) = st.o[nbk];
-  if (grp == 0) {
-    a.part_ml[(p * 16 + col) * 2 + 0] = st.m;
-    a.part_ml[(p * 16 + col) * 2 + 1] = l;
-  }
+  int r, first;
+  locate_chunk(nullptr, a.ctx_len, a.n_req, a.chunk, blockIdx.x >> 3, r, first);
+  if (r < 0) return;
+  const int c = (blockIdx.x >> 3) - first;
+  const int ctx = a.ctx_len[r];
+  const int nch = chunks_for(ctx, a.chunk);
+  const int b0 = a.cu_b[r];
+  const int nb = a.cu_b[r + 1] - b0;
+  int amax = 0;
+  for (int b = 0; b < nb; ++b) amax = max(amax, a.anchors[b0 + b]);
+  const DraftSeg sg{r, c * a.chunk, min(c * a.chunk + a.chunk, ctx), nch > 1 ? first + c : -1, b0, nb, amax,
+                    c == nch - 1};
+  draft_item<INDEXED>(a, smem, sg, g);
 }
 
 // ---------------------------------------------------------------------------
@@ -1082,7 +1106,7 @@ extern "C" int dspark_draft_attn_fwd(const void* q, const void* k_ctx, const voi
                                      const void* k_blk, const void* v_blk,
                                      const int32_t* cu_blocks, const int32_t* anchors,
                                      int n_req, int64_t ctx_rows_bound, int max_blocks, float scale, int chunk,
-                                     const int32_t* work, int n_work,
+                                     const int32_t* work, int n_work, int n_groups,
                                      void* out, void* workspace, int64_t workspace_bytes_, void* stream) {
   clear_error();
   DSPARK_REQUIRE(q && k_ctx && v_ctx && ctx_off && ctx_len && k_blk && v_blk && cu_blocks && anchors && out,
@@ -1094,9 +1118,17 @@ extern "C" int dspark_draft_attn_fwd(const void* q, const void* k_ctx, const voi
   DSPARK_REQUIRE(max_blocks >= 1 && max_blocks <= DWAVES,
                  "max_blocks must be in [1, %d] (got %d)", DWAVES, max_blocks);
   DSPARK_REQUIRE(chunk % DSTEP == 0, "draft chunk must be a multiple of %d", DSTEP);
-  int rc = check_common(n_req, ctx_rows_bound, max_blocks, chunk, scale, workspace_bytes_, workspace);
+  DSPARK_REQUIRE(n_req >= 1, "n_req must be >= 1 (got %d)", n_req);
+  DSPARK_REQUIRE(!work || (n_work >= 1 && n_groups >= 1 && n_groups <= (1 << 24)),
+                 "a work list needs n_work >= 1 and n_groups in [1, 2^24]");
+  int rc = check_shape(work ? n_work : n_req, work ? 0 : ctx_rows_bound, max_blocks, chunk, scale);
   if (rc != OK) return rc;
-  const int64_t n_cl = n_chunk_items(n_req, ctx_rows_bound, chunk);
+  const int64_t n_cl = work ? (int64_t)n_work : n_chunk_items(n_req, ctx_rows_bound, chunk);
+  const int64_t need = workspace_bytes(work ? n_work : n_req, work ? 0 : ctx_rows_bound, max_blocks, chunk);
+  DSPARK_REQUIRE(workspace_bytes_ >= need, "workspace too small: %lld < %lld bytes", (long long)workspace_bytes_,
+                 (long long)need);
+  DSPARK_REQUIRE(need == 0 || (workspace != nullptr && aligned16(workspace)),
+                 "workspace must be a 16-byte aligned device pointer");
   DraftArgs a{};
   a.q = static_cast<const bf16*>(q);
   a.k_ctx = static_cast<const bf16*>(k_ctx);
@@ -1114,20 +1146,21 @@ extern "C" int dspark_draft_attn_fwd(const void* q, const void* k_ctx, const voi
   a.tok_stride = tok_stride;
   a.head_stride = head_stride;
   a.work = work;
+  a.n_work = n_work;
   a.n_req = n_req;
   a.chunk = chunk;
   a.tmax = max_blocks;
   a.scale_log2 = scale * LOG2E;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  DSPARK_REQUIRE(!work || (n_work >= 1 && n_work <= n_cl), "work list length out of range");
-  const int64_t grid = work ? (int64_t)n_work * HKV : n_cl * HKV;
+  const int64_t grid = work ? (int64_t)n_groups * HKV : n_cl * HKV;
+  DSPARK_REQUIRE(grid <= 0x7fffffffLL, "grid too large");
   if (ctx_idx)
     hipLaunchKernelGGL(draft_attn_kernel<true>, dim3((unsigned)grid), dim3(DWAVES * WAVE), 0, s, a);
   else
     hipLaunchKernelGGL(draft_attn_kernel<false>, dim3((unsigned)grid), dim3(DWAVES * WAVE), 0, s, a);
   rc = launch_status("draft_attn_kernel");
   if (rc != OK) return rc;
-  MergeArgs m{work ? work + WORK_INTS * n_work : nullptr, nullptr, nullptr, ctx_len, cu_blocks, a.part_o, a.part_ml,
-              a.out, n_req, chunk, max_blocks, 1};
+  MergeArgs m{work ? work + WORK_INTS * n_work + n_groups + 1 : nullptr, nullptr, nullptr, ctx_len, cu_blocks,
+              a.part_o, a.part_ml, a.out, n_req, chunk, max_blocks, 1};
   return launch_merge(m, n_req, max_blocks, s);
 }

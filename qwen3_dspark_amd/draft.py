@@ -22,9 +22,9 @@ The context K/V of one draft layer may live in
 import torch
 
 from . import _native
-from ._device import Workspace, require_gfx950, upload
+from ._device import Workspace, cu_count, require_gfx950, upload
 from .kernels import HEAD_DIM, KV_HEADS, Q_HEADS, SCALE, _check_scale
-from .schedule import DRAFT_CHUNK, draft_work, upload_work
+from .schedule import DRAFT_CHUNK, draft_run_count, draft_work, upload_work
 
 BLOCK_SIZE = 7
 MAX_BLOCKS = 8
@@ -93,12 +93,21 @@ class DraftBatch:
             self._offsets[capacity] = upload(self.device, offs, torch.int64)
         return self._offsets[capacity]
 
-    def work(self, chunk):
-        if chunk not in self._work:
-            records, n_items = draft_work(self.context_lengths, self.cu_blocks_host,
-                                          [a for b in self.anchors for a in b], chunk)
-            self._work[chunk] = (upload_work(records, self.device), n_items)
-        return self._work[chunk]
+    def work(self, chunk, runs=None):
+        """(device list, segment count, run count) of the draft plan: fixed
+        chunks longest first (runs None), or `runs` balanced runs per KV head
+        (0: one per CU).  Uploaded once per plan."""
+        key = (chunk, runs)
+        if key not in self._work:
+            flat = [a for b in self.anchors for a in b]
+            if runs is None:
+                plan = draft_work(self.context_lengths, self.cu_blocks_host, flat, chunk=chunk)
+            else:
+                runs = runs or draft_run_count(sum(max(b) for b in self.anchors), cu_count(self.device))
+                plan = draft_work(self.context_lengths, self.cu_blocks_host, flat, runs)
+            records, n_seg, n_runs = plan
+            self._work[key] = (upload_work(records, self.device), n_seg, n_runs)
+        return self._work[key]
 
     def index_max(self):
         """Largest physical index addressed through context_indices (one
@@ -121,12 +130,15 @@ class HipDraftAttention:
     backend_name = 'mi355x_hip_draft_blocks_v1'
     native_varlen_calls_per_layer = 1
 
-    def __init__(self, device, *, chunk=DRAFT_CHUNK):
+    def __init__(self, device, *, chunk=DRAFT_CHUNK, runs=None):
         self.device = require_gfx950(device)
         _native.load()
         if chunk % 64:
             raise ValueError('Draft chunk must be a multiple of 64')
+        if runs is not None and (type(runs) is not int or runs < 0):
+            raise ValueError('runs must be None (fixed chunks) or a nonnegative integer (balanced runs)')
         self.chunk = int(chunk)
+        self.runs = runs            # None: fixed chunks; else balanced runs per KV head (0: one per CU)
         self._workspace = Workspace(self.device)
         self._geometry_for = None
         self._geometry = None
@@ -176,14 +188,14 @@ class HipDraftAttention:
         offsets, tok_stride, head_stride = self._geometry
         out = torch.empty_like(query)
         bound = max(batch.context_rows, 1)
-        need = _native.load().dspark_attn_workspace_bytes(batch.request_count, bound, batch.max_blocks, self.chunk)
+        work, n_work, n_runs = batch.work(self.chunk, self.runs)
+        need = _native.load().dspark_attn_workspace_bytes(n_work, 0, batch.max_blocks, self.chunk)
         ws = self._workspace.get(need)
-        work, n_work = batch.work(self.chunk)
         _native.call('dspark_draft_attn_fwd', _native.ptr(query), _native.ptr(context_keys), _native.ptr(context_values),
                      _native.ptr(batch.context_indices), _native.ptr(offsets), _native.ptr(batch.ctx_len),
                      tok_stride, head_stride, _native.ptr(block_keys), _native.ptr(block_values),
                      _native.ptr(batch.cu_blocks), _native.ptr(batch.anchor_rows), batch.request_count, bound,
-                     batch.max_blocks, float(SCALE), self.chunk, _native.ptr(work), n_work,
+                     batch.max_blocks, float(SCALE), self.chunk, _native.ptr(work), n_work, n_runs,
                      _native.ptr(out), _native.ptr(ws), ws.numel(), _native.stream_handle(self.device))
         return out
 

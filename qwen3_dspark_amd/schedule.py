@@ -20,16 +20,12 @@ the merge.
            length, key length, first key row (varlen) or resident slot (verify)
   request: first partial slot, segment count, first query row, query length
 
-Draft attention: fixed chunks.  Every request's context is cut into chunks
-of `chunk` rows (at least one chunk per request) and each (request, chunk)
-pair is one work item per KV head, dispatched longest first so that the
-short tail chunks of ragged requests fill the end of the grid (greedy
-longest-processing-time order); the partial slot of an item stays its
-request-major index, so the dispatch order does not affect results.
+Draft attention: the same balanced segments over the context rows each
+request streams (up to its largest anchor), one run per (workgroup, KV
+head), cuts on 64-row ring-stage boundaries (draft_work).
 
-  draft item: request, chunk, chunk base, context length, first block,
-              block count, largest anchor, chunk count
-  request:    chunk base, chunk count, first block, block count
+Without a list, both kernels walk fixed chunks of `chunk` rows in request
+order over a grid sized from the row bound.
 """
 from ._device import upload
 
@@ -37,8 +33,10 @@ DEFAULT_CHUNK = 1024          # verification / varlen: fixed chunks when no list
 TILE = 32                     # segment cuts fall on multiples of this many keys
 MIN_SEGMENT = 256             # fewest keys a run is given (tiny calls use fewer runs)
 RESIDENT_PER_CU = 2           # varlen/verify workgroups resident per CU (register budget)
-# Draft items carry up to 8 blocks of FP32 partials each, so they are cut
-# more coarsely: only contexts longer than this are split.
+DRAFT_TILE = 64               # draft cuts fall on multiples of the ring stage
+MIN_DRAFT_SEGMENT = 1024      # fewest context rows a draft run is given
+# Fixed draft chunks when no list is given (a chunk carries up to 8 blocks
+# of FP32 partials, so draft chunks are coarser).
 DRAFT_CHUNK = 4096
 WORK_INTS = 8
 REQ_INTS = 4
@@ -80,11 +78,12 @@ def run_count(total_keys, n_cu, row_tiles=1):
     return max(1, min(slots, -(-int(total_keys) // MIN_SEGMENT)))
 
 
-def _segment_list(query_lengths, key_lengths, starts, per_run):
+def _flatten(n, per_run, record, request):
     """Flatten per-run [(request, k0, k1)] segment lists into the int32 list
     format, giving split requests consecutive request-major partial slots in
-    key order.  Returns (list, segment count, run count)."""
-    n = len(key_lengths)
+    key order.  record(r, k0, k1, slot) and request(r, first, count) give the
+    8 and 4 ints of a segment and a request.  Returns (list, segment count,
+    run count)."""
     count = [0] * n
     for run in per_run:
         for r, _, _ in run:
@@ -93,10 +92,6 @@ def _segment_list(query_lengths, key_lengths, starts, per_run):
     for c in count:
         first.append(slot if c > 1 else -1)
         slot += c if c > 1 else 0
-    q0, acc = [], 0
-    for q in query_lengths:
-        q0.append(acc)
-        acc += int(q)
     keyed = {}
     # partial slot of a segment = first slot of its request + its key-order rank
     for run in per_run:
@@ -106,35 +101,44 @@ def _segment_list(query_lengths, key_lengths, starts, per_run):
     out, ranges = [], [0]
     for run in per_run:
         for r, k0, k1 in run:
-            slot = first[r] + rank[r][k0] if first[r] >= 0 else -1
-            out += (r, k0, k1, slot, q0[r], int(query_lengths[r]), int(key_lengths[r]), int(starts[r]))
+            out += record(r, k0, k1, first[r] + rank[r][k0] if first[r] >= 0 else -1)
         ranges.append(ranges[-1] + len(run))
     out += ranges
     for r in range(n):
-        out += (max(first[r], 0), count[r], q0[r], int(query_lengths[r]))
+        out += request(r, max(first[r], 0), count[r])
     return out, ranges[-1], len(per_run)
 
 
-def varlen_work(query_lengths, key_lengths, starts, groups):
-    """Balanced plan: (flat int32 list, segment count, run count) for varlen (starts =
-    first key row of each request) or verify (starts = resident slot of each
-    request); groups = number of runs (workgroups per KV head).  The cut
-    points depend on every request's length, so a request's output can
-    differ in the last bits between batches; request_work keeps them apart."""
+def _segment_list(query_lengths, key_lengths, starts, per_run):
+    """Varlen/verify records: request, k0, k1, slot, first query row, query
+    length, key length, start; request records: first slot, count, first
+    query row, query length."""
+    q0, acc = [], 0
+    for q in query_lengths:
+        q0.append(acc)
+        acc += int(q)
+    return _flatten(len(key_lengths), per_run,
+                    lambda r, k0, k1, slot: (r, k0, k1, slot, q0[r], int(query_lengths[r]), int(key_lengths[r]),
+                                             int(starts[r])),
+                    lambda r, first, count: (first, count, q0[r], int(query_lengths[r])))
+
+
+def _balanced_runs(key_lengths, groups, tile):
+    """Per-run [(request, k0, k1)] lists: the keys of all requests end to end,
+    cut into `groups` runs of (nearly) equal length, each cut moved down to a
+    `tile` boundary of the request holding it."""
     n = len(key_lengths)
     groups = max(1, int(groups))
     begin, total = [], 0
     for k in key_lengths:
         begin.append(total)
         total += int(k)
-    # Run boundaries in the concatenated key stream, each moved down to a
-    # tile boundary of the request holding it; monotone by construction.
     cuts, r = [0], 0
     for w in range(1, groups):
         x = (w * total) // groups
         while r + 1 < n and begin[r + 1] <= x:
             r += 1
-        cuts.append(max(cuts[-1], begin[r] + ((x - begin[r]) // TILE) * TILE))
+        cuts.append(max(cuts[-1], begin[r] + ((x - begin[r]) // tile) * tile))
     cuts.append(total)
     per_run = [[] for _ in range(groups)]
     w = 0
@@ -153,7 +157,16 @@ def varlen_work(query_lengths, key_lengths, starts, groups):
             if cuts[v + 1] >= a + kl or v + 1 == groups:
                 break
             v += 1
-    return _segment_list(query_lengths, key_lengths, starts, per_run)
+    return per_run
+
+
+def varlen_work(query_lengths, key_lengths, starts, groups):
+    """Balanced plan: (flat int32 list, segment count, run count) for varlen (starts =
+    first key row of each request) or verify (starts = resident slot of each
+    request); groups = number of runs (workgroups per KV head).  The cut
+    points depend on every request's length, so a request's output can
+    differ in the last bits between batches; request_work keeps them apart."""
+    return _segment_list(query_lengths, key_lengths, starts, _balanced_runs(key_lengths, groups, TILE))
 
 
 def request_work(query_lengths, key_lengths, starts, chunk, groups):
@@ -217,19 +230,42 @@ def segment_plan(split, query_lengths, key_lengths, starts, groups, chunk, capac
     return padded + out[base + runs + 1:], seg_cap, run_cap
 
 
-def draft_work(context_lengths, cu_blocks, anchors, chunk):
-    """(flat int32 list, item count) for draft attention; anchors is the
-    flat per-block list, cu_blocks the block offsets per request."""
-    first = _bases(context_lengths, chunk)
-    rec = []
-    items = chunk_items(context_lengths, chunk)
-    for r, c in items:
-        b0, b1 = cu_blocks[r], cu_blocks[r + 1]
-        rec += (r, c, first[r], context_lengths[r], b0, b1 - b0, max(anchors[b0:b1]),
-                n_chunks(context_lengths[r], chunk))
-    for r, n in enumerate(context_lengths):
-        rec += (first[r], n_chunks(n, chunk), cu_blocks[r], cu_blocks[r + 1] - cu_blocks[r])
-    return rec, len(items)
+def draft_work(context_lengths, cu_blocks, anchors, groups=None, *, chunk=None):
+    """Draft plan: (flat int32 list, segment count, run count).  Request r
+    streams its context up to its largest anchor (the rows any of its blocks
+    sees), and the segment ending a request also attends its blocks' own rows.
+      * chunk given (the default plan): every request is cut at multiples of
+        `chunk` of its own rows, one segment per run (workgroup), longest
+        first, so the hardware dispatcher balances the ragged tail (each
+        workgroup's 128 KiB ring fills a CU's LDS, one resident per CU);
+      * else: the rows of all requests, end to end, are cut into `groups` runs
+        of equal length at DRAFT_TILE boundaries.
+
+      segment: request, k0, k1, partial slot (-1: one segment), first block,
+               block count, largest anchor, 0
+      request: first partial slot, segment count, first block, block count
+    """
+    amax = [max(anchors[cu_blocks[r]:cu_blocks[r + 1]]) for r in range(len(context_lengths))]
+    if any(not 0 <= a <= int(c) for a, c in zip(amax, context_lengths)):
+        raise ValueError('Anchors must lie in [0, context length]')
+    if chunk is not None:
+        segs = []
+        for r, n in enumerate(amax):
+            for c in range(n_chunks(n, chunk)):
+                segs.append((min(chunk, n - c * chunk) if n > 0 else 0, r, c * chunk, min(n, c * chunk + chunk)))
+        segs.sort(key=lambda x: (-x[0], x[1], x[2]))
+        per_run = [[(r, k0, k1)] for _, r, k0, k1 in segs]
+    else:
+        per_run = _balanced_runs(amax, groups, DRAFT_TILE)
+    return _flatten(len(amax), per_run,
+                    lambda r, k0, k1, slot: (r, k0, k1, slot, cu_blocks[r], cu_blocks[r + 1] - cu_blocks[r], amax[r], 0),
+                    lambda r, first, count: (first, count, cu_blocks[r], cu_blocks[r + 1] - cu_blocks[r]))
+
+
+def draft_run_count(total_rows, n_cu):
+    """Draft runs per KV head: one workgroup per CU (its 128 KiB ring fills
+    the CU's LDS), never fewer than MIN_DRAFT_SEGMENT rows per run."""
+    return max(1, min(max(1, int(n_cu) // 8), -(-int(total_rows) // MIN_DRAFT_SEGMENT)))
 
 
 def upload_work(records, device):

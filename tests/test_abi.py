@@ -92,7 +92,7 @@ def test_invalid_sizes_are_rejected_before_any_launch():
                                     1 << 20, None)
     assert rc == -1 and 'n_work' in lib.dspark_last_error().decode()
     rc = lib.dspark_draft_attn_fwd(fake, fake, fake, None, fake, fake, 1024, 128, fake, fake, fake, fake,
-                                   2, 100, 9, 0.088, 512, None, 0, fake, fake, 1 << 24, None)
+                                   2, 100, 9, 0.088, 512, None, 0, 0, fake, fake, 1 << 24, None)
     assert rc == -1 and 'max_blocks' in lib.dspark_last_error().decode()
     rc = lib.dspark_verify_attn_fwd(fake, fake, fake, fake, fake, fake, fake, fake, 2, 1 << 20, 100, 128, 1000, 7,
                                     0.088, 512, None, 0, 0, fake, fake, 1 << 24, None)

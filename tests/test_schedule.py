@@ -129,3 +129,54 @@ def test_fixed_capacity_layout_keeps_the_plan():
             assert pad[WORK_INTS * n_work + groups + 1:] == out[WORK_INTS * n_seg + g + 1:]
             with pytest.raises(ValueError, match='capacity'):
                 segment_plan(split, ql, kl, list(range(n)), runs, 512, (n_seg - 1, g) if n_seg > 1 else (0, g))
+
+
+def test_draft_plan_covers_each_streamed_context_once():
+    """Draft segments cover [0, largest anchor) of every request exactly once,
+    cut on 64-row boundaries, runs balanced; requests whose anchors are all 0
+    still get the one (empty) segment that attends their own blocks."""
+    from qwen3_dspark_amd.schedule import DRAFT_TILE, draft_work
+    rng = np.random.default_rng(9)
+    for _ in range(60):
+        n = int(rng.integers(1, 40))
+        ctx = [int(x) for x in rng.integers(0, 9000, size=n)]
+        anchors, cu = [], [0]
+        for c in ctx:
+            k = int(rng.integers(1, 9))
+            row = [int(x) for x in rng.integers(0, c + 1, size=k)]
+            if rng.random() < 0.5:
+                row[0] = c
+            anchors += row
+            cu.append(cu[-1] + k)
+        groups = int(rng.integers(1, 40))
+        if rng.random() < 0.3:
+            out, n_seg, runs = draft_work(ctx, cu, anchors, chunk=1024)
+            groups = runs
+            assert runs == n_seg                                        # one segment per run
+        else:
+            out, n_seg, runs = draft_work(ctx, cu, anchors, groups)
+            assert runs == groups
+        rec = [tuple(out[WORK_INTS * i:WORK_INTS * (i + 1)]) for i in range(n_seg)]
+        ranges = out[WORK_INTS * n_seg:WORK_INTS * n_seg + groups + 1]
+        reqs = [tuple(out[WORK_INTS * n_seg + groups + 1 + REQ_INTS * r:][:REQ_INTS]) for r in range(n)]
+        by_req = {}
+        for r, k0, k1, slot, b0, nb, amax, zero in rec:
+            assert (b0, nb, amax, zero) == (cu[r], cu[r + 1] - cu[r], max(anchors[cu[r]:cu[r + 1]]), 0)
+            by_req.setdefault(r, []).append((k0, k1, slot))
+        for r in range(n):
+            amax = max(anchors[cu[r]:cu[r + 1]])
+            segs = sorted(by_req[r])
+            assert segs[0][0] == 0 and segs[-1][1] == amax
+            assert sum(1 for s in segs if s[1] >= amax) == 1       # exactly one segment attends the blocks
+            for (a0, a1, _), (b0_, _, _) in zip(segs, segs[1:]):
+                assert a1 == b0_ and a1 % DRAFT_TILE == 0
+            first, count, b0, nb = reqs[r]
+            assert count == len(segs) and (b0, nb) == (cu[r], cu[r + 1] - cu[r])
+            assert [s for _, _, s in segs] == ([-1] if count == 1 else list(range(first, first + count)))
+        loads = [sum(rec[i][2] - rec[i][1] for i in range(ranges[w], ranges[w + 1])) for w in range(groups)]
+        total = sum(max(anchors[cu[r]:cu[r + 1]]) for r in range(n))
+        assert sum(loads) == total
+        if runs != n_seg or groups == 1:
+            assert max(loads) - min(loads) <= 2 * DRAFT_TILE + (total % groups > 0)
+        else:
+            assert loads == sorted(loads, reverse=True) and max(loads) <= 1024   # longest first
