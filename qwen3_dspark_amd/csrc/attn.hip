@@ -310,215 +310,272 @@ __device__ __forceinline__ bool chunk_segment(const VarlenArgs& a, bool verify, 
   return true;
 }
 
-// One (segment, KV head, row tile) of varlen / verify attention.  Every
-// early return is uniform across the workgroup.
-template <bool VERIFY>
-__device__ __forceinline__ void varlen_item(const VarlenArgs& a, unsigned char* smem, const Segment& sg, int g, int t) {
-  const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
-  const int col = lane & 15;
-  const int grp = lane >> 4;
-  // The segment is wave-uniform; say so, so that its fields and everything
-  // derived from them stay in scalar registers.
-  const int q0 = __builtin_amdgcn_readfirstlane(sg.q0);
-  const int ql = __builtin_amdgcn_readfirstlane(sg.ql);
-  const int kl = __builtin_amdgcn_readfirstlane(sg.kl);
-  const int start = __builtin_amdgcn_readfirstlane(sg.start);
-  const int k0 = __builtin_amdgcn_readfirstlane(sg.k0);
-  const int k1 = __builtin_amdgcn_readfirstlane(sg.k1);
-  const int pslot = __builtin_amdgcn_readfirstlane(sg.pslot);
-  if (8 * t >= ql) return;
-
-  // Key j of this request lives in segment A for j < a_len, else segment B.
+// The addressing of one segment for one (KV head, row tile); every field is
+// wave-uniform.  Key j of the request lives in part A (committed rows) for
+// j < a_len, else in part B (rows new to this call).
+struct SegView {
   const bf16* kA;
   const bf16* vA;
   const bf16* kB;
   const bf16* vB;
+  size_t bbase;   // part B offset of the request's first new row, KV head g
   int a_len;
+  int k0;
+  int kend;       // keys [k0, kend) are visible to some row of the tile
+  int kfast;      // tiles below kfast need no clamping, source choice or mask
+  int q0, ql, kl, pslot;
+  bool live;      // the tile has query rows (8t < ql)
+  bool ends;      // the segment holds the request's last key
+};
+
+template <bool VERIFY>
+__device__ __forceinline__ SegView seg_view(const VarlenArgs& a, const Segment& sg, int g, int t) {
+  SegView v;
+  // The segment is wave-uniform; say so, so that its fields and everything
+  // derived from them stay in scalar registers.
+  v.q0 = __builtin_amdgcn_readfirstlane(sg.q0);
+  v.ql = __builtin_amdgcn_readfirstlane(sg.ql);
+  v.kl = __builtin_amdgcn_readfirstlane(sg.kl);
+  const int start = __builtin_amdgcn_readfirstlane(sg.start);
+  v.k0 = __builtin_amdgcn_readfirstlane(sg.k0);
+  const int k1 = __builtin_amdgcn_readfirstlane(sg.k1);
+  v.pslot = __builtin_amdgcn_readfirstlane(sg.pslot);
+  v.live = 8 * t < v.ql;
+  v.ends = k1 == v.kl;
   if (VERIFY) {
-    a_len = kl - ql;
+    v.a_len = v.kl - v.ql;
     const size_t abase = (size_t)start * (size_t)a.slot_stride + (size_t)g * a.a_head_stride;
-    kA = a.k_a + abase;
-    vA = a.v_a + abase;
-    const size_t bbase = (size_t)q0 * KV_ROW + (size_t)g * HD;
-    kB = a.k_b + bbase;
-    vB = a.v_b + bbase;
-    if (a.stage_k && k1 == kl && t == 0) {
-      // Fused stage: the workgroup holding the request's last segment is the
-      // only reader of its new rows for KV head g, so it also copies them
-      // into the scratch layer.
-      for (int i = threadIdx.x; i < 2 * ql * 16; i += 256) {
-        const int which = i / (ql * 16);
-        const int rem = i - which * ql * 16;
-        const size_t off = bbase + (size_t)(rem >> 4) * KV_ROW + (size_t)(rem & 15) * 8;
-        *reinterpret_cast<bf16x8*>((which ? a.stage_v : a.stage_k) + off) =
-            *reinterpret_cast<const bf16x8*>((which ? a.v_b : a.k_b) + off);
-      }
-    }
+    v.kA = a.k_a + abase;
+    v.vA = a.v_a + abase;
+    v.bbase = (size_t)v.q0 * KV_ROW + (size_t)g * HD;
+    v.kB = a.k_b + v.bbase;
+    v.vB = a.v_b + v.bbase;
   } else {
-    a_len = kl;
+    v.a_len = v.kl;
     const size_t abase = (size_t)start * KV_ROW + (size_t)g * HD;
-    kA = a.k_a + abase;
-    vA = a.v_a + abase;
-    kB = kA;
-    vB = vA;
+    v.kA = a.k_a + abase;
+    v.vA = a.v_a + abase;
+    v.kB = v.kA;
+    v.vB = v.vA;
+    v.bbase = 0;
   }
+  const int last_tok = min(8 * t + 7, v.ql - 1);
+  const int tile_lim = a.causal ? v.kl - v.ql + last_tok + 1 : v.kl;
+  v.kend = v.live ? min(k1, tile_lim) : v.k0;
+  // Keys below kfast come from part A and are visible to every row of this
+  // tile (bottom-right causal: row tok sees keys <= kl - ql + tok).
+  v.kfast = min(min(v.kend, v.a_len), a.causal ? v.kl - v.ql + 8 * t + 1 : v.kl);
+  return v;
+}
 
-  // This lane's query row.
-  const int tok = 8 * t + (col >> 1);
-  const int head = 2 * g + (col & 1);
-  const bool row_ok = tok < ql;
-  const int lim = row_ok ? (a.causal ? kl - ql + tok + 1 : kl) : 0;
-  const int last_tok = min(8 * t + 7, ql - 1);
-  const int tile_lim = a.causal ? kl - ql + last_tok + 1 : kl;
-  const int kend = min(k1, tile_lim);
-  const int vis = min(lim, kend);
+// One 32-key tile in registers: K as the S^T A-operand (lane (m, grp) holds
+// key 8*(m/4)+4j+m%4, dims 32ks+8grp..+8), V as 4 full rows per load (lane
+// (col, grp) holds key 4*i2+grp, dims 8col..+8).
+struct Tile {
+  bf16x8 k[2][4];
+  bf16x8 v[8];
+};
 
-  bf16x8 qf[4];
-  {
-    const bf16* qp = a.q + (size_t)(q0 + (row_ok ? tok : 0)) * Q_ROW + (size_t)head * HD + 8 * grp;
+// Per-lane byte offsets of the fast (unclamped, part A) tile loads; they
+// depend only on the token stride, so they hold for every segment.
+struct FastOffsets {
+  uint32_t k[2];
+  uint32_t v[8];
+};
+
+// A tile below kfast: part A rows at wave-uniform base + per-lane offsets.
+__device__ __forceinline__ void load_fast(const VarlenArgs& a, const SegView& s, const FastOffsets& fo, int kt,
+                                          Tile& T) {
+  const char* kb = reinterpret_cast<const char*>(s.kA + (size_t)kt * a.a_tok_stride);
+  const char* vb = reinterpret_cast<const char*>(s.vA + (size_t)kt * a.a_tok_stride);
+  #pragma unroll
+  for (int j = 0; j < 2; ++j)
     #pragma unroll
-    for (int ks = 0; ks < 4; ++ks) qf[ks] = row_ok ? ld8(qp + 32 * ks) : zero8();
-  }
+    for (int ks = 0; ks < 4; ++ks) T.k[j][ks] = *reinterpret_cast<const bf16x8*>(kb + fo.k[j] + 64 * ks);
+  #pragma unroll
+  for (int i2 = 0; i2 < 8; ++i2) T.v[i2] = *reinterpret_cast<const bf16x8*>(vb + fo.v[i2]);
+}
 
-  RowState st;
-  row_init(st);
-  unsigned char* vs = smem + wave * KT * ROWB;
-
+// Any tile: rows clamped, each from part A or B.
+__device__ __forceinline__ void load_slow(const VarlenArgs& a, const SegView& s, int kt, Tile& T) {
+  const int lane = threadIdx.x & 63;
+  const int col = lane & 15;
+  const int grp = lane >> 4;
   // Row kk of this request, clamped to kend-1 so that every load is in
   // range; rows past kend are masked out of the softmax and zeroed in V.
-  auto krow = [&](int kk) -> const bf16* {
-    kk = min(kk, kend - 1);
-    return kk < a_len ? kA + (size_t)kk * a.a_tok_stride : kB + (size_t)(kk - a_len) * KV_ROW;
+  auto row = [&](const bf16* pa, const bf16* pb, int kk) -> const bf16* {
+    kk = min(kk, s.kend - 1);
+    return kk < s.a_len ? pa + (size_t)kk * a.a_tok_stride : pb + (size_t)(kk - s.a_len) * KV_ROW;
   };
-  auto vrow = [&](int kk) -> const bf16* {
-    kk = min(kk, kend - 1);
-    return kk < a_len ? vA + (size_t)kk * a.a_tok_stride : vB + (size_t)(kk - a_len) * KV_ROW;
-  };
-  // One 32-key tile: K as the S^T A-operand (lane (m, grp) holds key
-  // 8*(m/4)+4j+m%4, dims 32ks+8grp..+8), V as 4 full rows per load.
-  struct Tile {
-    bf16x8 k[2][4];
-    bf16x8 v[8];
-  };
-  auto load_tile = [&](int kt, Tile& T) {
+  #pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const bf16* p = row(s.kA, s.kB, kt + 8 * (col >> 2) + 4 * j + (col & 3)) + 8 * grp;
     #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const bf16* p = krow(kt + 8 * (col >> 2) + 4 * j + (col & 3)) + 8 * grp;
-      #pragma unroll
-      for (int ks = 0; ks < 4; ++ks) T.k[j][ks] = ld8(p + 32 * ks);
-    }
-    #pragma unroll
-    for (int i2 = 0; i2 < 8; ++i2) T.v[i2] = ld8(vrow(kt + 4 * i2 + grp) + 8 * col);
-  };
-  auto compute_tile = [&](int kt, Tile& T, auto masked) {
-    constexpr bool MASKED = decltype(masked)::value;
-    if (MASKED && kt + KT > kend) {
-      #pragma unroll
-      for (int i2 = 0; i2 < 8; ++i2)
-        if (kt + 4 * i2 + grp >= kend) T.v[i2] = zero8();
-    }
-    f32x4 s0, s1;
-    qk_tile(T.k, qf, s0, s1);
-    #pragma unroll
-    for (int i2 = 0; i2 < 8; ++i2)
-      *reinterpret_cast<bf16x8*>(vs + lds_chunk_off(4 * i2 + grp, col)) = T.v[i2];
-    const bf16x8 pb = softmax_update<MASKED>(st, s0, s1, kt + 8 * grp, vis, a.scale_log2);
-    wave_lds_sync();
-    bf16x8 vt[8];
-    #pragma unroll
-    for (int nb = 0; nb < 8; ++nb) vt[nb] = lds_vt(vs, nb, lane);
-    pv_update(st, pb, vt);
-    wave_lds_sync();
-  };
+    for (int ks = 0; ks < 4; ++ks) T.k[j][ks] = ld8(p + 32 * ks);
+  }
+  #pragma unroll
+  for (int i2 = 0; i2 < 8; ++i2) T.v[i2] = ld8(row(s.vA, s.vB, kt + 4 * i2 + grp) + 8 * col);
+}
 
-  // Keys below kfast come from segment A and are visible to every row of
-  // this tile (bottom-right causal: row tok sees keys <= kl - ql + tok), so
-  // their tiles need no clamping, source selection or masking.  The tile
-  // base is wave-uniform; each lane adds loop-invariant 32-bit offsets.
-  const int kfast = min(min(kend, a_len), a.causal ? kl - ql + 8 * t + 1 : kl);
+// Q of this lane's row of segment s.
+__device__ __forceinline__ void load_q(const VarlenArgs& a, const SegView& s, int g, int t, bf16x8 (&qf)[4]) {
+  const int lane = threadIdx.x & 63;
+  const int col = lane & 15;
+  const int grp = lane >> 4;
+  const int tok = 8 * t + (col >> 1);
+  const bool row_ok = tok < s.ql;
+  const bf16* qp = a.q + (size_t)(s.q0 + (row_ok ? tok : 0)) * Q_ROW + (size_t)(2 * g + (col & 1)) * HD + 8 * grp;
+  #pragma unroll
+  for (int ks = 0; ks < 4; ++ks) qf[ks] = row_ok ? ld8(qp + 32 * ks) : zero8();
+}
+
+// One run of segments for one (KV head, row tile): wave w computes tiles
+// k0 + 32w, k0 + 32(w+4), ... of each segment.
+// fetch(n, sg) yields the run's n-th segment (false past the end); every
+// branch on it is uniform across the workgroup.
+template <bool VERIFY, typename Fetch>
+__device__ __forceinline__ void varlen_run(const VarlenArgs& a, unsigned char* smem, int g, int t, Fetch fetch) {
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int col = lane & 15;
+  const int grp = lane >> 4;
   const int wave_u = __builtin_amdgcn_readfirstlane(wave);
-  int kt = k0 + KT * wave_u;
+  FastOffsets fo;
   {
     const int64_t ts = a.a_tok_stride;
-    uint32_t koff[2], voff[8];
     #pragma unroll
-    for (int j = 0; j < 2; ++j) koff[j] = (uint32_t)(((8 * (col >> 2) + 4 * j + (col & 3)) * ts + 8 * grp) * 2);
+    for (int j = 0; j < 2; ++j) fo.k[j] = (uint32_t)(((8 * (col >> 2) + 4 * j + (col & 3)) * ts + 8 * grp) * 2);
     #pragma unroll
-    for (int i2 = 0; i2 < 8; ++i2) voff[i2] = (uint32_t)(((4 * i2 + grp) * ts + 8 * col) * 2);
-    auto load_fast = [&](int kk, Tile& T) {
-      const char* kb = reinterpret_cast<const char*>(kA + (size_t)kk * ts);
-      const char* vb = reinterpret_cast<const char*>(vA + (size_t)kk * ts);
-      #pragma unroll
-      for (int j = 0; j < 2; ++j)
+    for (int i2 = 0; i2 < 8; ++i2) fo.v[i2] = (uint32_t)(((4 * i2 + grp) * ts + 8 * col) * 2);
+  }
+  unsigned char* vs = smem + wave * KT * ROWB;
+  const int tok = 8 * t + (col >> 1);
+
+  Segment sg;
+  if (!fetch(0, sg)) return;
+  SegView cur = seg_view<VERIFY>(a, sg, g, t);
+  bf16x8 qf[4];
+  for (int n = 0;; ++n) {
+    load_q(a, cur, g, t, qf);
+    Segment nsg;
+    const bool more = fetch(n + 1, nsg);
+
+    const bool row_ok = tok < cur.ql;
+    const int lim = row_ok ? (a.causal ? cur.kl - cur.ql + tok + 1 : cur.kl) : 0;
+    const int vis = min(lim, cur.kend);
+    RowState st;
+    row_init(st);
+    auto compute = [&](Tile& T, int kt, auto masked) {
+      constexpr bool MASKED = decltype(masked)::value;
+      if (MASKED && kt + KT > cur.kend) {
         #pragma unroll
-        for (int ks = 0; ks < 4; ++ks) T.k[j][ks] = *reinterpret_cast<const bf16x8*>(kb + koff[j] + 64 * ks);
+        for (int i2 = 0; i2 < 8; ++i2)
+          if (kt + 4 * i2 + grp >= cur.kend) T.v[i2] = zero8();
+      }
+      f32x4 s0, s1;
+      qk_tile(T.k, qf, s0, s1);
       #pragma unroll
-      for (int i2 = 0; i2 < 8; ++i2) T.v[i2] = *reinterpret_cast<const bf16x8*>(vb + voff[i2]);
+      for (int i2 = 0; i2 < 8; ++i2)
+        *reinterpret_cast<bf16x8*>(vs + lds_chunk_off(4 * i2 + grp, col)) = T.v[i2];
+      const bf16x8 pb = softmax_update<MASKED>(st, s0, s1, kt + 8 * grp, vis, a.scale_log2);
+      wave_lds_sync();
+      bf16x8 vt[8];
+      #pragma unroll
+      for (int nb = 0; nb < 8; ++nb) vt[nb] = lds_vt(vs, nb, lane);
+      pv_update(st, pb, vt);
+      wave_lds_sync();
     };
-    for (; kt + KT <= kfast; kt += KT * 4) {
+    int kt = cur.k0 + KT * wave_u;
+    for (; kt + KT <= cur.kfast; kt += KT * 4) {
       Tile T;
-      load_fast(kt, T);
-      compute_tile(kt, T, std::false_type{});
+      load_fast(a, cur, fo, kt, T);
+      compute(T, kt, std::false_type{});
     }
-  }
-  for (; kt < kend; kt += KT * 4) {
-    Tile T;
-    load_tile(kt, T);
-    compute_tile(kt, T, std::true_type{});
-  }
-
-  st.l = wave_sum_across_groups(st.l);
-  __syncthreads();
-  float* ob = reinterpret_cast<float*>(smem);
-  float* mlb = reinterpret_cast<float*>(smem + 4 * 16 * OPITCH * 4);
-  #pragma unroll
-  for (int nb = 0; nb < 8; ++nb)
-    *reinterpret_cast<f32x4*>(ob + (wave * 16 + col) * OPITCH + 16 * nb + 4 * grp) = st.o[nb];
-  if (grp == 0) {
-    mlb[(wave * 16 + col) * 2 + 0] = st.m;
-    mlb[(wave * 16 + col) * 2 + 1] = st.l;
-  }
-  __syncthreads();
-
-  const int tid = threadIdx.x;
-  const int row = tid >> 4;
-  const int d0 = (tid & 15) * 8;
-  float M = -INFINITY;
-  #pragma unroll
-  for (int w = 0; w < 4; ++w) M = fmaxf(M, mlb[(w * 16 + row) * 2]);
-  float L = 0.f;
-  float acc[8];
-  #pragma unroll
-  for (int i = 0; i < 8; ++i) acc[i] = 0.f;
-  #pragma unroll
-  for (int w = 0; w < 4; ++w) {
-    const float mw = mlb[(w * 16 + row) * 2];
-    const float sc = (mw == -INFINITY) ? 0.f : fast_exp2(mw - M);
-    L += sc * mlb[(w * 16 + row) * 2 + 1];
-    const float* src = ob + (w * 16 + row) * OPITCH + d0;
-    #pragma unroll
-    for (int i = 0; i < 8; ++i) acc[i] += sc * src[i];
-  }
-  const int tok_r = 8 * t + (row >> 1);
-  const int head_r = 2 * g + (row & 1);
-  bf16* orow = a.out + (size_t)(q0 + tok_r) * Q_ROW + (size_t)head_r * HD + d0;
-  if (pslot >= 0) {
-    const size_t p = (size_t)(pslot * 8 + g) * a.tmax + t;
-    float* po = a.part_o + (p * 16 + row) * HD + d0;
-    *reinterpret_cast<f32x4*>(po) = f32x4{acc[0], acc[1], acc[2], acc[3]};
-    *reinterpret_cast<f32x4*>(po + 4) = f32x4{acc[4], acc[5], acc[6], acc[7]};
-    if ((tid & 15) == 0) {
-      a.part_ml[(p * 16 + row) * 2 + 0] = M;
-      a.part_ml[(p * 16 + row) * 2 + 1] = L;
+    for (; kt < cur.kend; kt += KT * 4) {
+      Tile T;
+      load_slow(a, cur, kt, T);
+      compute(T, kt, std::true_type{});
     }
-    return;
-  }
-  if (tok_r < ql) {
-    bf16x8 ov;
-    #pragma unroll
-    for (int i = 0; i < 8; ++i) ov[i] = (bf16)(acc[i] / L);
-    *reinterpret_cast<bf16x8*>(orow) = ov;
+    // Fused stage: the workgroup holding the request's last segment (row
+    // tile 0) is the only reader of its new rows for KV head g, so it also
+    // copies them into the scratch layer.  The first 256 16-byte pieces are
+    // loaded here and stored after the merge, which hides their latency.
+    const bool stage = VERIFY && a.stage_k && cur.ends && t == 0;
+    const int n_stage = 2 * cur.ql * 16;
+    auto stage_off = [&](int i, bool& v_half) -> size_t {
+      v_half = i >= cur.ql * 16;
+      const int rem = v_half ? i - cur.ql * 16 : i;
+      return cur.bbase + (size_t)(rem >> 4) * KV_ROW + (size_t)(rem & 15) * 8;
+    };
+    bf16x8 staged = zero8();
+    if (stage && (int)threadIdx.x < n_stage) {
+      bool vh;
+      const size_t off = stage_off(threadIdx.x, vh);
+      staged = *reinterpret_cast<const bf16x8*>((vh ? a.v_b : a.k_b) + off);
+    }
+
+    if (cur.live) {
+      st.l = wave_sum_across_groups(st.l);
+      __syncthreads();
+      float* ob = reinterpret_cast<float*>(smem);
+      float* mlb = reinterpret_cast<float*>(smem + 4 * 16 * OPITCH * 4);
+      #pragma unroll
+      for (int nb = 0; nb < 8; ++nb)
+        *reinterpret_cast<f32x4*>(ob + (wave * 16 + col) * OPITCH + 16 * nb + 4 * grp) = st.o[nb];
+      if (grp == 0) {
+        mlb[(wave * 16 + col) * 2 + 0] = st.m;
+        mlb[(wave * 16 + col) * 2 + 1] = st.l;
+      }
+      __syncthreads();
+
+      const int tid = threadIdx.x;
+      const int row = tid >> 4;
+      const int d0 = (tid & 15) * 8;
+      float M = -INFINITY;
+      #pragma unroll
+      for (int w = 0; w < 4; ++w) M = fmaxf(M, mlb[(w * 16 + row) * 2]);
+      float L = 0.f;
+      float acc[8];
+      #pragma unroll
+      for (int i = 0; i < 8; ++i) acc[i] = 0.f;
+      #pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        const float mw = mlb[(w * 16 + row) * 2];
+        const float sc = (mw == -INFINITY) ? 0.f : fast_exp2(mw - M);
+        L += sc * mlb[(w * 16 + row) * 2 + 1];
+        const float* src = ob + (w * 16 + row) * OPITCH + d0;
+        #pragma unroll
+        for (int i = 0; i < 8; ++i) acc[i] += sc * src[i];
+      }
+      const int tok_r = 8 * t + (row >> 1);
+      const int head_r = 2 * g + (row & 1);
+      if (cur.pslot >= 0) {
+        const size_t p = (size_t)(cur.pslot * 8 + g) * a.tmax + t;
+        float* po = a.part_o + (p * 16 + row) * HD + d0;
+        *reinterpret_cast<f32x4*>(po) = f32x4{acc[0], acc[1], acc[2], acc[3]};
+        *reinterpret_cast<f32x4*>(po + 4) = f32x4{acc[4], acc[5], acc[6], acc[7]};
+        if ((tid & 15) == 0) {
+          a.part_ml[(p * 16 + row) * 2 + 0] = M;
+          a.part_ml[(p * 16 + row) * 2 + 1] = L;
+        }
+      } else if (tok_r < cur.ql) {
+        bf16x8 ov;
+        #pragma unroll
+        for (int i = 0; i < 8; ++i) ov[i] = (bf16)(acc[i] / L);
+        *reinterpret_cast<bf16x8*>(a.out + (size_t)(cur.q0 + tok_r) * Q_ROW + (size_t)head_r * HD + d0) = ov;
+      }
+    }
+    if (stage) {
+      for (int i = threadIdx.x; i < n_stage; i += 256) {
+        bool vh;
+        const size_t off = stage_off(i, vh);
+        const bf16x8 x = i < 256 ? staged : *reinterpret_cast<const bf16x8*>((vh ? a.v_b : a.k_b) + off);
+        *reinterpret_cast<bf16x8*>((vh ? a.stage_v : a.stage_k) + off) = x;
+      }
+    }
+    __syncthreads();   // the next segment reuses the V tiles and the merge buffer
+    if (!more) break;
+    cur = seg_view<VERIFY>(a, nsg, g, t);
   }
 }
 
@@ -527,27 +584,25 @@ __device__ __forceinline__ void varlen_item(const VarlenArgs& a, unsigned char* 
 // grid walks the fixed chunks (item, KV head) with a stride of the grid
 // size, so per-workgroup start-up is paid once per CU slot.
 template <bool VERIFY>
-__global__ __launch_bounds__(256) void varlen_attn_kernel(VarlenArgs a) {
+__global__ __launch_bounds__(256, 2) void varlen_attn_kernel(VarlenArgs a) {
   __shared__ __attribute__((aligned(16))) unsigned char smem[VARLEN_SMEM];
   const int g = blockIdx.x & 7;
   if (a.work) {
     const int32_t* range = a.work + WORK_INTS * a.n_work + (blockIdx.x >> 3);
     const int b = min(max(range[0], 0), a.n_work);      // clamped: never past the records
     const int e = min(max(range[1], b), a.n_work);
-    for (int i = b; i < e; ++i) {
-      const int32_t* w = a.work + WORK_INTS * i;
-      const Segment sg{w[0], w[1], w[2], w[3], w[4], w[5], w[6], w[7]};
-      varlen_item<VERIFY>(a, smem, sg, g, blockIdx.y);
-      __syncthreads();   // the next segment reuses the LDS tiles and merge buffer
-    }
+    varlen_run<VERIFY>(a, smem, g, blockIdx.y, [&](int n, Segment& sg) {
+      if (b + n >= e) return false;
+      const int32_t* w = a.work + WORK_INTS * (b + n);
+      sg = Segment{w[0], w[1], w[2], w[3], w[4], w[5], w[6], w[7]};
+      return true;
+    });
     return;
   }
-  for (int idx = blockIdx.x; idx < a.n_slots; idx += gridDim.x) {
-    Segment sg;
-    if (!chunk_segment(a, VERIFY, idx >> 3, sg)) break;
-    varlen_item<VERIFY>(a, smem, sg, g, blockIdx.y);
-    __syncthreads();
-  }
+  varlen_run<VERIFY>(a, smem, g, blockIdx.y, [&](int n, Segment& sg) {
+    const int idx = blockIdx.x + n * gridDim.x;
+    return idx < a.n_slots && chunk_segment(a, VERIFY, idx >> 3, sg);
+  });
 }
 
 // ---------------------------------------------------------------------------
