@@ -413,9 +413,11 @@ def sampling_leg(dev, skip_cpu, reps=10):
 
 
 def draft_projection_leg(dev, n_req, per_request, reps=20):
-    """Draft context projection (fc on hipBLASLt + the fused context norm /
-    k_proj / k_norm / RoPE / v_proj launch for 5 draft layers, written into a
-    slotted pool) for one append: n_req requests of `per_request` rows each
+    """Draft context projection (fc on hipBLASLt, then for 5 draft layers the
+    context norm / k_proj / k_norm / RoPE / v_proj written into a slotted
+    pool: one fused launch for short appends, a hipBLASLt GEMM plus the
+    epilogue launch from GEMM_MIN_TOKENS rows on) for one append: n_req
+    requests of `per_request` rows each
     (a round's committed rows), or, with per_request None, the 16-request
     prefill of contexts U[128, 1024].  Random-init bf16 weights (hidden
     1024, features 5 x 1024).  Median of `reps` event-timed appends of each
@@ -423,7 +425,7 @@ def draft_projection_leg(dev, n_req, per_request, reps=20):
     import numpy as np
     import torch
 
-    from qwen3_dspark_amd.draft_projection import DraftContextProjector
+    from qwen3_dspark_amd.draft_projection import GEMM_MIN_TOKENS, DraftContextProjector
     from qwen3_dspark_amd._device import upload
     g = torch.Generator(device=dev).manual_seed(SEED + 11)
     h, f = 1024, 5 * 1024
@@ -465,6 +467,7 @@ def draft_projection_leg(dev, n_req, per_request, reps=20):
     kv_bytes = (5 * 2 * 1024 * h + first * h + 5 * 2 * first * 1024) * 2
     kv_flops = 2 * first * h * 5 * 2 * 1024
     return {'tokens': first, 'requests': n_req,
+            'kv_path': 'hipblaslt_gemm+epilogue' if first >= GEMM_MIN_TOKENS else 'fused',
             'fc_hipblaslt_ms': round(ms_fc, 5), 'fc_tflops': round(fc_flops / ms_fc / 1e9, 1),
             'kv_project_ms': round(ms_kv, 5), 'kv_project_tflops': round(kv_flops / ms_kv / 1e9, 1),
             'kv_project_gbs': round(kv_bytes / ms_kv / 1e6, 1),

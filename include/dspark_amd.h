@@ -200,6 +200,22 @@ int dspark_draft_kv_project(const void* x, int tokens, int hidden, const void* w
                             int64_t slot_stride, int64_t head_stride, int32_t* flag, void* stream);
 
 /*
+ * The same projection after a library GEMM, for large appends: y [tokens,
+ * y_stride] bf16 holds x Wfold^T (columns [layer][K, V][head][128], the
+ * folded weights of dspark_draft_kv_project as one [layers*2*1024, hidden]
+ * matrix); this applies the context-norm factor of x's rows, k_norm and
+ * RoPE on K, and stores K/V into the pool exactly as dspark_draft_kv_project
+ * does.  Row i of y and x is token token0 + i of the records, so a long
+ * append can be projected in chunks.  Same flag convention.
+ * Replaces the same reference code as dspark_draft_kv_project.
+ */
+int dspark_draft_kv_epilogue(const void* y, int64_t y_stride, const void* x, int tokens, int token0,
+                             int hidden, const void* k_norm, int layers, const float* inv_freq,
+                             const int32_t* req, int n_req, float eps_ctx, float eps_k, void* k_pool,
+                             void* v_pool, int64_t layer_stride, int64_t slot_stride, int64_t head_stride,
+                             int32_t* flag, void* stream);
+
+/*
  * Float64 sampling law and speculative verification (the consumer of the
  * verification round, after the LM head), following
  * dspark_qwen/tensor_sampling.py.  logits: [rows, >= vocab] bf16 (dtype 0)

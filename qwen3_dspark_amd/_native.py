@@ -41,6 +41,8 @@ SIGNATURES = {
     'dspark_pool_append': (_I, [_P, _P, _L, _L, _L, _L, _L, _I, _L, _I, _I, _PP, _PP, _L, _L, _L, _P, _I, _P, _P]),
     'dspark_qkv_prologue': (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _F, _P, _P, _P, _L, _P]),
     'dspark_draft_kv_project': (_I, [_P, _I, _I, _P, _P, _I, _P, _P, _I, _F, _F, _P, _P, _L, _L, _L, _P, _P]),
+    'dspark_draft_kv_epilogue': (_I, [_P, _L, _P, _I, _I, _I, _P, _I, _P, _P, _I, _F, _F, _P, _P, _L, _L, _L, _P,
+                                      _P]),
     'dspark_row_stats_bytes': (_L, [_I, _I]),
     'dspark_logit_row_stats': (_I, [_P, _I, _I, _I, _L, _D, _P, _P, _P]),
     'dspark_draw_workspace_bytes': (_L, [_I]),

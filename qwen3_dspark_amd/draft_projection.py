@@ -14,12 +14,22 @@ Two launches for all draft layers and requests:
     result), every layer's k_proj / k_norm / RoPE and v_proj, and the store
     into each request's pool slot at its absolute positions, with a device
     finiteness flag.
+From GEMM_MIN_TOKENS appended tokens on, the k/v projection itself is a
+plain GEMM that hipBLASLt runs faster than the fused tiles: it then runs as
+one library GEMM per GEMM_CHUNK tokens (all layers' folded weights as one
+matrix) followed by dspark_draft_kv_epilogue (norm factor, k_norm, RoPE,
+pool store, flag).
 """
 import torch
 
 from . import _native
 from .kernels import HEAD_DIM, KV_HEADS
 from .prologue import rope_inv_freq
+
+
+GEMM_MIN_TOKENS = 2048   # appends at least this long take the GEMM + epilogue path
+GEMM_CHUNK = 16384       # tokens per library GEMM (bounds its bf16 output)
+PATHS = ('fused', 'gemm')
 
 
 class DraftContextProjector:
@@ -79,13 +89,27 @@ class DraftContextProjector:
         """fc over the concatenated features [T, F] -> [T, hidden] bf16."""
         return torch.nn.functional.linear(features, self.fc)
 
-    def project_into(self, fc_out, records, n_req, keys, values, *, flag=None):
-        """The fused projection of fc_out [T, hidden] into pool tensors keys /
+    def project_into(self, fc_out, records, n_req, keys, values, *, flag=None, path=None):
+        """The projection of fc_out [T, hidden] into pool tensors keys /
         values [layers, slots, 8, capacity, 128] (bf16); records: int32 device
-        tensor of n_req (slot, first position, first token, count) rows."""
+        tensor of n_req (slot, first position, first token, count) rows.
+        path: 'fused', 'gemm' or None (by length: GEMM_MIN_TOKENS)."""
+        if path is not None and path not in PATHS:
+            raise ValueError(f'path must be one of {PATHS} or None')
         t = fc_out.shape[0]
         s = keys.stride()
-        _native.call('dspark_draft_kv_project', fc_out.data_ptr(), t, self.hidden, self.w.data_ptr(),
-                     self.k_norm.data_ptr(), self.layers, self.inv_freq.data_ptr(), records.data_ptr(), n_req,
-                     self.eps, self.eps, keys.data_ptr(), values.data_ptr(), s[0], s[1], s[2],
-                     None if flag is None else flag.data_ptr(), _native.stream_handle(self.device))
+        stream = _native.stream_handle(self.device)
+        flag_ptr = None if flag is None else flag.data_ptr()
+        if (path or ('gemm' if t >= GEMM_MIN_TOKENS else 'fused')) == 'fused':
+            _native.call('dspark_draft_kv_project', fc_out.data_ptr(), t, self.hidden, self.w.data_ptr(),
+                         self.k_norm.data_ptr(), self.layers, self.inv_freq.data_ptr(), records.data_ptr(), n_req,
+                         self.eps, self.eps, keys.data_ptr(), values.data_ptr(), s[0], s[1], s[2], flag_ptr, stream)
+            return
+        w = self.w.view(-1, self.hidden)
+        for c0 in range(0, t, GEMM_CHUNK):
+            x = fc_out[c0:c0 + GEMM_CHUNK]
+            y = torch.nn.functional.linear(x, w)              # hipBLASLt, [rows, layers*2*1024] bf16
+            _native.call('dspark_draft_kv_epilogue', y.data_ptr(), y.stride(0), x.data_ptr(), x.shape[0], c0,
+                         self.hidden, self.k_norm.data_ptr(), self.layers, self.inv_freq.data_ptr(),
+                         records.data_ptr(), n_req, self.eps, self.eps, keys.data_ptr(), values.data_ptr(), s[0],
+                         s[1], s[2], flag_ptr, stream)

@@ -1,5 +1,6 @@
 """Draft context projection on the GPU: DraftContextProjector and
-DraftKVPool.append_committed (hipBLASLt fc + dspark_draft_kv_project) against
+DraftKVPool.append_committed (hipBLASLt fc + dspark_draft_kv_project, or for
+long appends hipBLASLt k/v GEMM + dspark_draft_kv_epilogue) against
 the float64 oracle (oracle/draft_proj.py, itself pinned to transformers'
 Qwen3 modules), its transactional contract (packed_draft.py:130-168), and
 the full 5-layer draft context path of the 16-request workload feeding draft
@@ -59,13 +60,21 @@ def pool_rows(pool, layer, request, start, n):
     return f64(k), f64(v)
 
 
+@pytest.mark.parametrize('path', ['auto', 'gemm', 'gemm_chunked'])
 @pytest.mark.parametrize('counts', [[7] * 64, [1], [60, 3, 37], [2, 3]])
-def test_append_committed_against_oracle(counts):
+def test_append_committed_against_oracle(counts, path, monkeypatch):
     """Rows of one append (request token counts `counts`, after a first
     append that gives the requests different starting positions) against
     the oracle, with the fc output taken from the device (the kernel's input)
-    and, for the whole chain, from the float64 fc."""
+    and, for the whole chain, from the float64 fc.  `gemm` forces the
+    library-GEMM + dspark_draft_kv_epilogue path at these sizes, and
+    `gemm_chunked` also cuts it into GEMMs of 64 tokens (token0 offsets)."""
+    from qwen3_dspark_amd import draft_projection
     from qwen3_dspark_amd.draft import DraftKVPool
+    if path != 'auto':
+        monkeypatch.setattr(draft_projection, 'GEMM_MIN_TOKENS', 1)
+    if path == 'gemm_chunked':
+        monkeypatch.setattr(draft_projection, 'GEMM_CHUNK', 64)
     gen = torch.Generator().manual_seed(SEED + len(counts) + sum(counts))
     fc, cn, per = make_weights(gen)
     proj = projector(fc, cn, per)
@@ -80,6 +89,11 @@ def test_append_committed_against_oracle(counts):
     torch.cuda.synchronize()
     assert work['new_context_tokens'] == sum(counts) and work['kv_projection_calls'] == LAYERS
     assert pool.lengths == {r: first[r] + n for r, n in zip(names, counts)}
+    # The GEMM path rounds k_proj / v_proj outputs to bf16 before the norms,
+    # as the reference's autocast linear does; the fused path keeps FP32 to
+    # the end.  One more bf16 rounding of O(1) values adds ~2^-9 relative
+    # error, hence the whole-chain bar of 4e-3 on the mean for it.
+    bar = 2e-3 if path == 'auto' else 4e-3
     x = torch.cat([v[0] for v in chunks.values()])
     pos = np.concatenate([np.arange(first[r], first[r] + n) for r, n in zip(names, counts)])
     fc_dev = proj.fc_forward(x.to(DEV))
@@ -94,10 +108,10 @@ def test_append_committed_against_oracle(counts):
             got_k.append(k)
             got_v.append(v)
         got_k, got_v = np.concatenate(got_k), np.concatenate(got_v)
-        errs.append((gate(got_k, ref_dev[layer][0]), gate(got_v, ref_dev[layer][1])))
+        errs.append((gate(got_k, ref_dev[layer][0], bar), gate(got_v, ref_dev[layer][1], bar)))
         gate(got_k, ref_full[layer][0], mean_abs=4e-3)
         gate(got_v, ref_full[layer][1], mean_abs=4e-3)
-    say(f'[draft proj] counts={counts[:4]}.. max-abs per layer (k, v) {errs}')
+    say(f'[draft proj] {path} counts={counts[:4]}.. max-abs per layer (k, v) {errs}')
 
 
 def test_refused_appends_leave_the_pool_unchanged():
@@ -168,10 +182,12 @@ def test_full_draft_context_path_feeds_draft_attention():
     pos = np.concatenate([np.arange(c) for c in ctx])
     weights = [(f64(kp), f64(kn), f64(vp)) for kp, kn, vp in per]
     ref = draft_proj.project_context_kv(None, None, f64(cn), weights, pos, fc_out=fc_dev)
+    # both appends hold thousands of tokens, so they take the GEMM path and
+    # its bar (see test_append_committed_against_oracle)
     for layer in range(LAYERS):
         got = [pool_rows(pool, layer, r, 0, c) for r, c in zip(names, ctx)]
-        gate(np.concatenate([k for k, _ in got]), ref[layer][0])
-        gate(np.concatenate([v for _, v in got]), ref[layer][1])
+        gate(np.concatenate([k for k, _ in got]), ref[layer][0], 4e-3)
+        gate(np.concatenate([v for _, v in got]), ref[layer][1], 4e-3)
     anchors = {r: sorted(int(a) for a in rng.choice(c + 1, size=4, replace=False)) for r, c in zip(names, ctx)}
     batch = pool.batch(anchors)
     nb = 4 * 16
