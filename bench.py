@@ -234,12 +234,15 @@ def main():
     # HBM bytes per call from the two counter passes of --traffic-probe
     # (FETCH_SIZE, WRITE_SIZE, calibrated against a plain 1 GiB copy), for
     # the first round of this workload; summarised in profiles/.
-    traffic, traffic_ratio = None, None
-    tpath = os.path.join(ROOT, 'profiles', 'verify_attn_traffic.json')
-    if os.path.exists(tpath):
+    def counted(name):
+        tpath = os.path.join(ROOT, 'profiles', name)
+        if not os.path.exists(tpath):
+            return None, None
         with open(tpath) as f:
             tj = json.load(f)
-        traffic, traffic_ratio = tj.get('hbm_bytes_per_launch'), tj.get('ratio')
+        return tj.get('hbm_bytes_per_launch'), tj.get('ratio')
+    traffic, traffic_ratio = counted('verify_attn_traffic.json')
+    d_traffic, d_traffic_ratio = counted('draft_attn_traffic.json')
 
     result = {
         'metric': METRIC, 'value': round(value, 1), 'unit': 'tokens/s', 'n_gpus': 1,
@@ -265,7 +268,8 @@ def main():
             'verify_attn_tokens_per_s': round(B * Q_LEN / (float(np.median(v_ms)) * 1e-3), 1),
             'draft_layer_ms': round(d_avg_ms, 5), 'draft_call_ms': pct(d_ms, DRAFT_LAYERS), 'draft_gbs': round(d_gbs, 1),
             'draft_frac': round(d_gbs / HBM_PEAK_GBS, 4),
-            'draft_algorithmic_bytes_per_launch': int(d_b),
+            'draft_algorithmic_bytes_per_launch': int(d_b), 'draft_traffic': d_traffic,
+            'draft_traffic_per_algorithmic_byte': d_traffic_ratio,
             'draft_attn_tokens_per_s': round(nq_d / (float(np.median(d_ms)) * 1e-3), 1),
             'round_algorithmic_bytes': int(round_bytes), 'round_gbs': round(round_gbs, 1),
             'round_frac': round(round_gbs / HBM_PEAK_GBS, 4),
@@ -476,18 +480,19 @@ def draft_projection_leg(dev, n_req, per_request, reps=20):
 
 def traffic_probe(args):
     """Kernels for `rocprofv3 --pmc FETCH_SIZE` / `--pmc WRITE_SIZE` passes:
-    the verification-attention launches of the workload, staging fused in as
-    in the timed rounds (store contents are
-    irrelevant to the bytes moved, so it stays zero-filled), then a plain
-    copy of exactly 2**30 bytes whose counter reading calibrates the
-    counters to bytes."""
+    3 verification-attention launches of the workload, staging fused in as
+    in the timed rounds, then 3 draft-attention launches (store and pool
+    contents are irrelevant to the bytes moved, so they stay zero-filled),
+    then a plain copy of exactly 2**30 bytes whose counter reading
+    calibrates the counters to bytes."""
     import torch
 
-    from qwen3_dspark_amd.kernels import DEFAULT_CHUNK
+    from qwen3_dspark_amd.draft import DraftBatch, HipDraftAttention
+    from qwen3_dspark_amd.kernels import DEFAULT_CHUNK, SCALE
     from qwen3_dspark_amd.persistent_kv import Bucket, PersistentTargetKV
 
     dev = torch.device('cuda:0')
-    contexts, _, _ = workload(args.warmup + args.steps)
+    contexts, anchors, _ = workload(args.warmup + args.steps)
     pool = PersistentTargetKV(layers=3, slots=B, context_capacity=CAPACITY, max_query_tokens=B * Q_LEN,
                               heads=8, dim=128, device=dev, chunk=args.chunk or DEFAULT_CHUNK)
     handles = [pool.add_request(f'req{i}') for i in range(B)]
@@ -501,11 +506,23 @@ def traffic_probe(args):
     for layer in range(3):
         pool.attend(tx, layer, q, keys=kn, values=kn)
     pool.abort(tx)
+    torch.cuda.synchronize()
+    del pool
+    ctx_k = torch.zeros(B, 8, CAPACITY, 128, dtype=torch.bfloat16, device=dev)
+    ctx_v = torch.zeros_like(ctx_k)
+    n_rows = BLOCK * sum(len(a) for a in anchors)
+    qd = torch.zeros(n_rows, 16, 128, dtype=torch.bfloat16, device=dev)
+    kd = torch.zeros(n_rows, 8, 128, dtype=torch.bfloat16, device=dev)
+    batch = DraftBatch(dev, [i * CAPACITY for i in range(B)], contexts, anchors)
+    draft = HipDraftAttention(dev)
+    for _ in range(3):
+        draft(qd, kd, kd, ctx_k, ctx_v, batch, scale=SCALE)
     src = torch.ones(1 << 30, dtype=torch.uint8, device=dev)
     dst = torch.empty_like(src)
     dst.copy_(src)
     torch.cuda.synchronize()
     print(json.dumps({'traffic_probe': 'done', 'verify_algorithmic_bytes_per_launch': verify_bytes(contexts),
+                      'draft_algorithmic_bytes_per_launch': draft_bytes(anchors),
                       'context_rows': sum(contexts),
                       'calibration_copy_bytes': 1 << 30}), flush=True)
 
