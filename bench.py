@@ -63,8 +63,10 @@ def parse():
     ap.add_argument('--draft-chunk', type=int, default=None, help='keys per split-K draft work item')
     ap.add_argument('--no-cpu-baseline', action='store_true', help='skip the CPU oracle leg (profiling runs)')
     ap.add_argument('--traffic-probe', action='store_true',
-                    help='untimed run for hardware-counter passes: 3 verification-attention layers of the '
-                         'workload, then a 1 GiB device-to-device copy as the counter calibration')
+                    help='untimed run for hardware-counter passes: 3 verification-attention and 3 draft-attention '
+                         'layers of the workload, then a 1 GiB device-to-device copy as the counter calibration')
+    ap.add_argument('--mfma-probe', action='store_true',
+                    help='only run the draft kernels for a rocprofv3 --pmc MfmaUtil MfmaFlopsBF16 pass')
     ap.add_argument('--cpu-verify-layers', type=int, default=VERIFY_LAYERS, help='verify layers in the CPU sample')
     ap.add_argument('--cpu-draft-layers', type=int, default=DRAFT_LAYERS, help='draft layers in the CPU sample')
     return ap.parse_args()
@@ -109,6 +111,8 @@ def main():
         sys.exit(2)
     if args.traffic_probe:
         return traffic_probe(args)
+    if args.mfma_probe:
+        return mfma_probe(args)
     import numpy as np
     import torch
 
@@ -525,6 +529,70 @@ def traffic_probe(args):
                       'draft_algorithmic_bytes_per_launch': draft_bytes(anchors),
                       'context_rows': sum(contexts),
                       'calibration_copy_bytes': 1 << 30}), flush=True)
+
+
+def draft_pairs(anchors):
+    """Visible (query row, key) pairs of draft attention: each block's 7
+    rows see the context up to its anchor and the block's 7 rows."""
+    return sum(BLOCK * (a + BLOCK) for row in anchors for a in row)
+
+
+def mfma_probe(args):
+    """Kernels for a `rocprofv3 --pmc MfmaUtil MfmaFlopsBF16` pass (MFMA busy
+    cycles over active SIMD cycles, and bf16 MFMA flops, per dispatch):
+    three launches each of
+      1. draft attention in the long-context 8-block case: 64 requests with
+         8192-row contexts, 8 blocks each, anchors evenly spread up to 8192;
+      2. draft attention of the bench workload (1..8 blocks per request);
+      3. the 9,840-row draft context projection of 5 layers: the fused
+         kernel, then the hipBLASLt GEMM + epilogue path.
+    Pool and input contents are zero: MFMA work does not depend on them."""
+    import numpy as np
+    import torch
+
+    from qwen3_dspark_amd.draft import DraftBatch, HipDraftAttention
+    from qwen3_dspark_amd.draft_projection import DraftContextProjector
+    from qwen3_dspark_amd.kernels import SCALE
+    from qwen3_dspark_amd._device import upload
+
+    dev = torch.device('cuda:0')
+    contexts, anchors, _ = workload(args.warmup + args.steps)
+    long_ctx = [CAPACITY] * B
+    long_anchors = [[CAPACITY * (j + 1) // 8 for j in range(8)] for _ in range(B)]
+    ctx_k = torch.zeros(B, 8, CAPACITY, 128, dtype=torch.bfloat16, device=dev)
+    ctx_v = torch.zeros_like(ctx_k)
+    draft = HipDraftAttention(dev)
+    cases = {}
+    for name, ctx, anc in (('draft_8_blocks_8192', long_ctx, long_anchors), ('draft_workload', contexts, anchors)):
+        rows = BLOCK * sum(len(a) for a in anc)
+        qd = torch.zeros(rows, 16, 128, dtype=torch.bfloat16, device=dev)
+        kd = torch.zeros(rows, 8, 128, dtype=torch.bfloat16, device=dev)
+        batch = DraftBatch(dev, [i * CAPACITY for i in range(B)], ctx, anc)
+        for _ in range(3):
+            draft(qd, kd, kd, ctx_k, ctx_v, batch, scale=SCALE)
+        torch.cuda.synchronize()
+        cases[name] = {'flops_per_launch': 8192 * draft_pairs(anc), 'algorithmic_bytes_per_launch': draft_bytes(anc)}
+    del ctx_k, ctx_v
+    h, f, n_req = 1024, 5 * 1024, 16
+    z = torch.zeros(1024, h, dtype=torch.bfloat16, device=dev)
+    proj = DraftContextProjector(torch.zeros(h, f, dtype=torch.bfloat16, device=dev),
+                                 torch.ones(h, dtype=torch.bfloat16, device=dev),
+                                 [(z, torch.ones(128, dtype=torch.bfloat16, device=dev), z)] * 5)
+    counts = [int(c) for c in np.random.default_rng(SEED + 11).integers(128, 1025, size=n_req)]
+    keys = torch.zeros(5, n_req, 8, max(counts) + 1, 128, dtype=torch.bfloat16, device=dev)
+    values = torch.zeros_like(keys)
+    rec, first = [], 0
+    for i, n in enumerate(counts):
+        rec += (i, 0, first, n)
+        first += n
+    records = upload(dev, rec)
+    fc_out = torch.zeros(first, h, dtype=torch.bfloat16, device=dev)
+    for path in ('fused', 'gemm'):
+        for _ in range(3):
+            proj.project_into(fc_out, records, n_req, keys, values, path=path)
+        torch.cuda.synchronize()
+    cases['context_projection'] = {'tokens': first, 'flops_per_launch': 2 * first * h * 5 * 2 * 1024}
+    print(json.dumps({'mfma_probe': 'done', 'cases': cases}), flush=True)
 
 
 def cpu_leg(args, pool, bucket, handles, contexts, anchors, qv, qd, bkd, bvd, dctx_k, dctx_v, draft, draft_offsets):
