@@ -531,6 +531,18 @@ def traffic_probe(args):
                       'calibration_copy_bytes': 1 << 30}), flush=True)
 
 
+def cpu_model():
+    """The host CPU's model name (/proc/cpuinfo), for the CPU baseline."""
+    try:
+        with open('/proc/cpuinfo') as f:
+            for line in f:
+                if line.startswith('model name'):
+                    return line.split(':', 1)[1].strip()
+    except OSError:
+        pass
+    return 'unknown'
+
+
 def draft_pairs(anchors):
     """Visible (query row, key) pairs of draft attention: each block's 7
     rows see the context up to its anchor and the block's 7 rows."""
@@ -675,7 +687,7 @@ def cpu_leg(args, pool, bucket, handles, contexts, anchors, qv, qd, bkd, bvd, dc
         'value': round(B * Q_LEN / round_s, 3), 'unit': 'tokens/s', 'cores': threads, 'kind': 'port',
         'sample': f'C oracle (oracle/attn_ref.c, FP32, OpenMP, {threads} threads) over one round of the same '
                   f'64-request workload: {n_verify} verification layers ({t_verify:.2f} s) and {n_draft} draft '
-                  f'layers ({t_draft:.2f} s){scaled}; round time {round_s:.2f} s',
+                  f'layers ({t_draft:.2f} s){scaled}; round time {round_s:.2f} s; host CPU {cpu_model()}',
     }
     return cpu, stats
 
