@@ -33,6 +33,7 @@ DEFAULT_CHUNK = 1024          # verification / varlen: fixed chunks when no list
 TILE = 32                     # segment cuts fall on multiples of this many keys
 MIN_SEGMENT = 256             # fewest keys a run is given (tiny calls use fewer runs)
 RESIDENT_PER_CU = 2           # varlen/verify workgroups resident per CU (register budget)
+SEGMENT_COST = 64             # keys' worth of fixed work per segment in balanced varlen plans (measured)
 DRAFT_TILE = 64               # draft cuts fall on multiples of the ring stage
 MIN_DRAFT_SEGMENT = 1024      # fewest context rows a draft run is given
 # Fixed draft chunks when no list is given (a chunk carries up to 8 blocks
@@ -123,22 +124,28 @@ def _segment_list(query_lengths, key_lengths, starts, per_run):
                     lambda r, first, count: (first, count, q0[r], int(query_lengths[r])))
 
 
-def _balanced_runs(key_lengths, groups, tile):
+def _balanced_runs(key_lengths, groups, tile, seg_cost=0):
     """Per-run [(request, k0, k1)] lists: the keys of all requests end to end,
-    cut into `groups` runs of (nearly) equal length, each cut moved down to a
-    `tile` boundary of the request holding it."""
+    cut into `groups` runs of (nearly) equal cost, each cut moved down to a
+    `tile` boundary of the request holding it.  A request costs its keys
+    plus seg_cost (the fixed work of starting a segment, in keys), so runs
+    that hold more request starts get fewer keys."""
     n = len(key_lengths)
     groups = max(1, int(groups))
-    begin, total = [], 0
+    seg_cost = max(0, int(seg_cost))
+    begin, vbegin, total, vtotal = [], [], 0, 0
     for k in key_lengths:
         begin.append(total)
+        vbegin.append(vtotal)
         total += int(k)
+        vtotal += int(k) + seg_cost
     cuts, r = [0], 0
     for w in range(1, groups):
-        x = (w * total) // groups
-        while r + 1 < n and begin[r + 1] <= x:
+        x = (w * vtotal) // groups                    # cut in cost space
+        while r + 1 < n and vbegin[r + 1] <= x:
             r += 1
-        cuts.append(max(cuts[-1], begin[r] + ((x - begin[r]) // tile) * tile))
+        into = max(0, x - vbegin[r] - seg_cost)       # keys of request r before the cut
+        cuts.append(max(cuts[-1], begin[r] + (min(into, int(key_lengths[r])) // tile) * tile))
     cuts.append(total)
     per_run = [[] for _ in range(groups)]
     w = 0
@@ -160,13 +167,15 @@ def _balanced_runs(key_lengths, groups, tile):
     return per_run
 
 
-def varlen_work(query_lengths, key_lengths, starts, groups):
+def varlen_work(query_lengths, key_lengths, starts, groups, seg_cost=None):
     """Balanced plan: (flat int32 list, segment count, run count) for varlen (starts =
     first key row of each request) or verify (starts = resident slot of each
-    request); groups = number of runs (workgroups per KV head).  The cut
+    request); groups = number of runs (workgroups per KV head); seg_cost
+    (default SEGMENT_COST) the fixed cost of a segment in keys.  The cut
     points depend on every request's length, so a request's output can
     differ in the last bits between batches; request_work keeps them apart."""
-    return _segment_list(query_lengths, key_lengths, starts, _balanced_runs(key_lengths, groups, TILE))
+    cost = SEGMENT_COST if seg_cost is None else seg_cost
+    return _segment_list(query_lengths, key_lengths, starts, _balanced_runs(key_lengths, groups, TILE, cost))
 
 
 def request_work(query_lengths, key_lengths, starts, chunk, groups):

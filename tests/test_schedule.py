@@ -1,13 +1,14 @@
 """Host-side work lists (CPU): balanced key segments for varlen/verification
 attention.  The kernels trust these records, so their invariants are checked
 here: every key of every request is covered exactly once, cuts fall on
-32-key tile boundaries, runs carry (nearly) equal key counts, and the merge
-records name exactly the partial slots the segments write."""
+32-key tile boundaries, runs carry (nearly) equal cost (keys, plus a fixed
+cost per request starting in the run), and the merge records name exactly
+the partial slots the segments write."""
 import numpy as np
 import pytest
 
-from qwen3_dspark_amd.schedule import (MIN_SEGMENT, REQ_INTS, TILE, WORK_INTS, request_work, run_count,
-                                       varlen_list_bound, varlen_work)
+from qwen3_dspark_amd.schedule import (MIN_SEGMENT, REQ_INTS, SEGMENT_COST, TILE, WORK_INTS, request_work,
+                                       run_count, varlen_list_bound, varlen_work)
 
 
 def decode(out, n_seg, groups, n_req):
@@ -19,9 +20,9 @@ def decode(out, n_seg, groups, n_req):
     return rec, ranges, reqs
 
 
-def check(query_lengths, key_lengths, starts, groups, chunk=None):
+def check(query_lengths, key_lengths, starts, groups, chunk=None, seg_cost=None):
     if chunk is None:
-        out, n_seg, runs = varlen_work(query_lengths, key_lengths, starts, groups)
+        out, n_seg, runs = varlen_work(query_lengths, key_lengths, starts, groups, seg_cost)
         assert runs == groups
     else:
         out, n_seg, runs = request_work(query_lengths, key_lengths, starts, chunk, groups)
@@ -39,6 +40,7 @@ def check(query_lengths, key_lengths, starts, groups, chunk=None):
     loads = []
     for w in range(groups):
         loads.append(sum(rec[i][2] - rec[i][1] for i in range(ranges[w], ranges[w + 1])))
+    check.starts = [sum(1 for i in range(ranges[w], ranges[w + 1]) if rec[i][1] == 0) for w in range(groups)]
     segments_of = {}
     for r, kl in enumerate(key_lengths):
         segs = sorted(by_req[r])
@@ -64,10 +66,20 @@ def test_balanced_runs_at_the_64_request_stress_shape():
     kl = [int(c) + 7 for c in ctx]
     groups = run_count(sum(kl), 256)
     assert groups == 64
-    loads, _ = check([7] * 64, kl, list(range(64)), groups)
-    # every run within one tile of the mean
+    # keys only: every run within a tile or two of the mean
+    loads, _ = check([7] * 64, kl, list(range(64)), groups, seg_cost=0)
     assert max(loads) - min(loads) <= 2 * TILE
     assert sum(loads) == sum(kl)
+    # with the fixed cost of a segment: keys + cost x (requests starting in
+    # the run) balanced instead; runs holding more starts get fewer keys
+    loads, _ = check([7] * 64, kl, list(range(64)), groups)
+    # each of a run's two cuts moves its cost by at most a tile plus one
+    # segment cost (a cut inside a request's start cost lands at its start)
+    cost = [k + SEGMENT_COST * n for k, n in zip(loads, check.starts)]
+    assert max(cost) - min(cost) <= 2 * (TILE + SEGMENT_COST)
+    assert sum(loads) == sum(kl)
+    starts = np.array(check.starts)
+    assert np.mean([k for k, n in zip(loads, starts) if n == starts.max()]) < np.mean(loads)
 
 
 @pytest.mark.parametrize('kl,groups', [([5], 1), ([40], 4), ([0, 5], 3), ([1, 1, 1], 8), ([31, 33, 64, 65], 3),
