@@ -35,6 +35,8 @@ MIN_SEGMENT = 256             # fewest keys a run is given (tiny calls use fewer
 RESIDENT_PER_CU = 2           # varlen/verify workgroups resident per CU (register budget)
 SEGMENT_COST = 64             # keys' worth of fixed work per segment in balanced varlen plans (measured)
 DRAFT_TILE = 64               # draft cuts fall on multiples of the ring stage
+DRAFT_SEGMENT_COST = 512      # balanced draft plans: fixed cost of a segment, in context rows (measured)
+DRAFT_BLOCK_WEIGHT = 0.055    # balanced draft plans: extra cost of a row per block beyond the first (measured)
 MIN_DRAFT_SEGMENT = 1024      # fewest context rows a draft run is given
 # Fixed draft chunks when no list is given (a chunk carries up to 8 blocks
 # of FP32 partials, so draft chunks are coarser).
@@ -124,27 +126,29 @@ def _segment_list(query_lengths, key_lengths, starts, per_run):
                     lambda r, first, count: (first, count, q0[r], int(query_lengths[r])))
 
 
-def _balanced_runs(key_lengths, groups, tile, seg_cost=0):
+def _balanced_runs(key_lengths, groups, tile, seg_cost=0, weights=None):
     """Per-run [(request, k0, k1)] lists: the keys of all requests end to end,
     cut into `groups` runs of (nearly) equal cost, each cut moved down to a
-    `tile` boundary of the request holding it.  A request costs its keys
-    plus seg_cost (the fixed work of starting a segment, in keys), so runs
-    that hold more request starts get fewer keys."""
+    `tile` boundary of the request holding it.  A request costs seg_cost
+    (the fixed work of starting a segment, in keys) plus its keys, each
+    weighted by weights[r] (default 1), so runs that hold more request
+    starts or heavier keys get fewer keys."""
     n = len(key_lengths)
     groups = max(1, int(groups))
-    seg_cost = max(0, int(seg_cost))
-    begin, vbegin, total, vtotal = [], [], 0, 0
-    for k in key_lengths:
+    seg_cost = max(0.0, float(seg_cost))
+    wt = [1.0] * n if weights is None else [max(1e-3, float(x)) for x in weights]
+    begin, vbegin, total, vtotal = [], [], 0, 0.0
+    for k, w in zip(key_lengths, wt):
         begin.append(total)
         vbegin.append(vtotal)
         total += int(k)
-        vtotal += int(k) + seg_cost
+        vtotal += seg_cost + w * int(k)
     cuts, r = [0], 0
     for w in range(1, groups):
-        x = (w * vtotal) // groups                    # cut in cost space
+        x = w * vtotal / groups                       # cut in cost space
         while r + 1 < n and vbegin[r + 1] <= x:
             r += 1
-        into = max(0, x - vbegin[r] - seg_cost)       # keys of request r before the cut
+        into = int(max(0.0, (x - vbegin[r] - seg_cost) / wt[r]))   # keys of request r before the cut
         cuts.append(max(cuts[-1], begin[r] + (min(into, int(key_lengths[r])) // tile) * tile))
     cuts.append(total)
     per_run = [[] for _ in range(groups)]
@@ -248,7 +252,10 @@ def draft_work(context_lengths, cu_blocks, anchors, groups=None, *, chunk=None):
         first, so the hardware dispatcher balances the ragged tail (each
         workgroup's 128 KiB ring fills a CU's LDS, one resident per CU);
       * else: the rows of all requests, end to end, are cut into `groups` runs
-        of equal length at DRAFT_TILE boundaries.
+        of equal cost at DRAFT_TILE boundaries: a request costs
+        DRAFT_SEGMENT_COST plus its rows weighted by 1 + DRAFT_BLOCK_WEIGHT
+        per block beyond the first (more blocks, more MFMA and LDS work per
+        row).
 
       segment: request, k0, k1, partial slot (-1: one segment), first block,
                block count, largest anchor, 0
@@ -265,7 +272,9 @@ def draft_work(context_lengths, cu_blocks, anchors, groups=None, *, chunk=None):
         segs.sort(key=lambda x: (-x[0], x[1], x[2]))
         per_run = [[(r, k0, k1)] for _, r, k0, k1 in segs]
     else:
-        per_run = _balanced_runs(amax, groups, DRAFT_TILE)
+        nb = [cu_blocks[r + 1] - cu_blocks[r] for r in range(len(amax))]
+        per_run = _balanced_runs(amax, groups, DRAFT_TILE, DRAFT_SEGMENT_COST,
+                                 [1.0 + DRAFT_BLOCK_WEIGHT * (b - 1) for b in nb])
     return _flatten(len(amax), per_run,
                     lambda r, k0, k1, slot: (r, k0, k1, slot, cu_blocks[r], cu_blocks[r + 1] - cu_blocks[r], amax[r], 0),
                     lambda r, first, count: (first, count, cu_blocks[r], cu_blocks[r + 1] - cu_blocks[r]))
