@@ -161,7 +161,8 @@ def test_draft_plan_covers_each_streamed_context_once():
             anchors += row
             cu.append(cu[-1] + k)
         groups = int(rng.integers(1, 40))
-        if rng.random() < 0.3:
+        chunked = rng.random() < 0.3
+        if chunked:
             out, n_seg, runs = draft_work(ctx, cu, anchors, chunk=1024)
             groups = runs
             assert runs == n_seg                                        # one segment per run
@@ -188,7 +189,15 @@ def test_draft_plan_covers_each_streamed_context_once():
         loads = [sum(rec[i][2] - rec[i][1] for i in range(ranges[w], ranges[w + 1])) for w in range(groups)]
         total = sum(max(anchors[cu[r]:cu[r + 1]]) for r in range(n))
         assert sum(loads) == total
-        if runs != n_seg or groups == 1:
-            assert max(loads) - min(loads) <= 2 * DRAFT_TILE + (total % groups > 0)
+        if not chunked:
+            # balanced in cost: a segment start costs DRAFT_SEGMENT_COST, a row
+            # 1 + DRAFT_BLOCK_WEIGHT per block beyond the first; each of a
+            # run's two cuts moves its cost by at most a tile of the heaviest
+            # rows plus one segment cost
+            from qwen3_dspark_amd.schedule import DRAFT_BLOCK_WEIGHT, DRAFT_SEGMENT_COST
+            weight = lambda r: 1 + DRAFT_BLOCK_WEIGHT * (cu[r + 1] - cu[r] - 1)
+            cost = [sum(weight(rec[i][0]) * (rec[i][2] - rec[i][1]) + DRAFT_SEGMENT_COST * (rec[i][1] == 0)
+                        for i in range(ranges[w], ranges[w + 1])) for w in range(groups)]
+            assert max(cost) - min(cost) <= 2 * (DRAFT_TILE * (1 + 7 * DRAFT_BLOCK_WEIGHT) + DRAFT_SEGMENT_COST) + 1
         else:
             assert loads == sorted(loads, reverse=True) and max(loads) <= 1024   # longest first
