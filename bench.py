@@ -328,9 +328,10 @@ def verify_graph_leg(pool, bucket, handles, qv, kn, vn, bytes_of, reps=10):
     """The 28 verification-attention layers of a round captured in one HIP
     graph (VerificationGraph) and replayed per transaction, the metadata of
     begin() outside the graph.  Median replay span (events on the stream
-    around the replay) over `reps` transactions at the current lengths, each
-    aborted after its replay; the replay's outputs are compared bit for bit
-    with eager calls on the same transaction."""
+    around the replay, with GPU work queued ahead so that the host's graph
+    submission does not show) over `reps` transactions at the current
+    lengths, each aborted after its replay; the replay's outputs are
+    compared bit for bit with eager calls on the same transaction."""
     import numpy as np
     import torch
 
@@ -340,10 +341,16 @@ def verify_graph_leg(pool, bucket, handles, qv, kn, vn, bytes_of, reps=10):
     graph.keys.copy_(kn)
     graph.values.copy_(vn)
     ctx = [pool.length(h) for h in handles]
+    # A ~1 ms copy queued ahead keeps the GPU busy while the host submits
+    # the graph, so the span is the replay's execution, not host latency.
+    pad = torch.empty(1 << 30, dtype=torch.uint8, device=pool.device)
+    pad_src = torch.empty_like(pad)
     spans = []
     for i in range(reps + 2):
         tx = pool.begin(handles, bucket)
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        for _ in range(4):
+            pad.copy_(pad_src)
         e0.record()
         done = graph.submit(tx)
         e1.record()
