@@ -689,6 +689,26 @@ __device__ __forceinline__ void draft_item(const DraftArgs& a, unsigned char* sm
   }
   RowState st;
   row_init(st);
+  // The segment ending the request also attends the wave's own 7 rows: their
+  // K fragments and V rows are fetched now, so that their latency hides
+  // under the context stream instead of following its drain.
+  const bool own = last && active;
+  const size_t rb = (size_t)BLOCK_ROWS * (b0 + (active ? b : 0));
+  bf16x8 own_k[2][4], own_v[2];
+  if (own) {
+    #pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int kk = 8 * (col >> 2) + 4 * j + (col & 3);
+      const bf16* p = a.k_blk + (rb + min(kk, BLOCK_ROWS - 1)) * KV_ROW + (size_t)g * HD + 8 * grp;
+      #pragma unroll
+      for (int ks = 0; ks < 4; ++ks) own_k[j][ks] = ld8(p + 32 * ks);
+    }
+    #pragma unroll
+    for (int i2 = 0; i2 < 2; ++i2) {
+      const int kk = 4 * i2 + grp;
+      own_v[i2] = (kk < BLOCK_ROWS) ? ld8(a.v_blk + (rb + kk) * KV_ROW + (size_t)g * HD + 8 * col) : zero8();
+    }
+  }
 
   // Context row kk of this request for KV head g (clamped into range).
   const int64_t coff = a.ctx_off[r];
@@ -775,25 +795,13 @@ __device__ __forceinline__ void draft_item(const DraftArgs& a, unsigned char* sm
   }
 
   // Own-block keys (bidirectional within the block), once per request.
-  if (last && active) {
+  if (own) {
     unsigned char* wv = smem + wave * 8 * ROWB;   // 8 rows per wave
-    const size_t rb = (size_t)BLOCK_ROWS * (b0 + b);
-    bf16x8 kf[2][4];
     #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int kk = 8 * (col >> 2) + 4 * j + (col & 3);
-      const bf16* p = a.k_blk + (rb + min(kk, BLOCK_ROWS - 1)) * KV_ROW + (size_t)g * HD + 8 * grp;
-      #pragma unroll
-      for (int ks = 0; ks < 4; ++ks) kf[j][ks] = ld8(p + 32 * ks);
-    }
-    #pragma unroll
-    for (int i2 = 0; i2 < 2; ++i2) {
-      const int kk = 4 * i2 + grp;
-      const bf16x8 v = (kk < BLOCK_ROWS) ? ld8(a.v_blk + (rb + kk) * KV_ROW + (size_t)g * HD + 8 * col) : zero8();
-      *reinterpret_cast<bf16x8*>(wv + lds_chunk_off(kk, col)) = v;
-    }
+    for (int i2 = 0; i2 < 2; ++i2)
+      *reinterpret_cast<bf16x8*>(wv + lds_chunk_off(4 * i2 + grp, col)) = own_v[i2];
     f32x4 s0, s1;
-    qk_tile(kf, qf, s0, s1);
+    qk_tile(own_k, qf, s0, s1);
     const bf16x8 pb = softmax_update<true>(st, s0, s1, 8 * grp, row_ok ? BLOCK_ROWS : 0, a.scale_log2);
     wave_lds_sync();
     bf16x8 vt[8];
