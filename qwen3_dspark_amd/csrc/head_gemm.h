@@ -4,27 +4,32 @@
 // the draft context K/V projection).
 //
 // MFMA mapping (v_mfma_f32_16x16x32_bf16): A = 16 weight rows, B = 16
-// tokens; wave w of the 4-wave workgroup owns tokens t0 + 16w .. +15.  Every
-// lane ends with acc[mt][e] = C^T[16*mt + 4*grp + e][token t0 + 16w + col],
-// i.e. the 128 dims of one token spread over its 4 lane groups, so a
-// per-head reduction (RMSNorm) needs two cross-lane shuffles and the RoPE
-// partner of dim d (d + 64 = tile mt + 4) sits in the same lane.
+// tokens.  The workgroup has 8 waves, two per SIMD so that one wave's LDS
+// reads and MFMA chain overlap the other's: wave w owns token group
+// tg = w mod 4 (tokens t0 + 16 tg .. +15) and column half kh = w / 4 of
+// every ring stage (split K); the two halves are summed through LDS at the
+// end.  Every lane of waves 0-3 then holds
+// acc[mt][e] = C^T[16*mt + 4*grp + e][token t0 + 16w + col], i.e. the 128
+// dims of one token spread over its 4 lane groups, so a per-head reduction
+// (RMSNorm) needs two cross-lane shuffles and the RoPE partner of dim d
+// (d + 64 = tile mt + 4) sits in the same lane.
 //
 // The head's weight slice [128, hidden] and the workgroup's token rows
 // stream through a 6-stage LDS ring fed by direct-to-LDS loads: every thread
-// issues exactly 6 loads per stage (4 weight pieces, 2 of its wave's token
-// pieces), so the weights are read once per workgroup and shared by the 4
-// waves, with 5 stages in flight.
+// issues exactly 3 loads per stage (2 weight pieces, 1 token piece), so the
+// weights are read once per workgroup and shared by the 8 waves, with 5
+// stages in flight.
 #pragma once
 #include "common.h"
 
 namespace dspark {
 
-constexpr int HG_TOKENS = 64;                    // tokens per workgroup, 16 per wave
+constexpr int HG_TOKENS = 64;                    // tokens per workgroup, 16 per token group
+constexpr int HG_WAVES = 8;                      // 4 token groups x 2 column halves
 constexpr int HG_KB = 64;                        // hidden columns per ring stage
 constexpr int HG_STAGES = 6;                     // ring depth (5 stages in flight)
 constexpr int HG_W_BYTES = HD * HG_KB * 2;       // 128 weight rows x 128 B = 16 KiB
-constexpr int HG_X_BYTES = 16 * HG_KB * 2;       // 16 token rows x 128 B per wave
+constexpr int HG_X_BYTES = 16 * HG_KB * 2;       // 16 token rows x 128 B per token group
 constexpr int HG_STAGE_BYTES = HG_W_BYTES + 4 * HG_X_BYTES;   // 24 KiB
 constexpr int HG_SMEM = HG_STAGES * HG_STAGE_BYTES;            // 144 KiB
 
@@ -37,8 +42,9 @@ __device__ __forceinline__ int hg_swz(int row) { return (row >> 1) & 7; }
 // token.  Rows past `tokens` re-read the last token (their results are
 // discarded by the caller).  With SUMSQ, ss receives this lane's share of
 // sum(x^2) over its token's row (the 4 lane groups of a column together
-// cover the row once).  Ends with no direct loads in flight; the caller must
-// not reuse smem before a barrier.
+// cover the row once).  acc and ss are complete in waves 0-3 only; the
+// caller returns waves 4-7 before using them.  Ends with a workgroup
+// barrier and no direct loads in flight.
 template <bool SUMSQ>
 __device__ __forceinline__ void head_tile_gemm(const bf16* __restrict__ w, const bf16* __restrict__ x, int tokens,
                                                int hidden, int t0, unsigned char* smem, f32x4 (&acc)[8], float& ss) {
@@ -46,11 +52,13 @@ __device__ __forceinline__ void head_tile_gemm(const bf16* __restrict__ w, const
   const int wave = threadIdx.x >> 6;
   const int col = lane & 15;
   const int grp = lane >> 4;
-  const int tw = t0 + 16 * wave;
+  const int tg = wave & 3;
+  const int kh = wave >> 2;
   const int steps = hidden / HG_KB;
 
   // Direct loads: lane L of a 1 KiB piece (8 rows x 128 B) fetches row
   // 8*piece + L/8, global chunk (L%8) ^ swz(row), landing at LDS chunk L%8.
+  // Wave w loads weight pieces 2w, 2w+1 and token rows 8w .. 8w+7.
   const uint32_t smem_lds = lds_address(smem);
   const int prow = lane >> 3;
   auto issue = [&](int step) {
@@ -58,19 +66,16 @@ __device__ __forceinline__ void head_tile_gemm(const bf16* __restrict__ w, const
     const uint32_t base = smem_lds + (uint32_t)((step % HG_STAGES) * HG_STAGE_BYTES);
     const int k0 = st * HG_KB;
     #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int piece = 4 * wave + i;
+    for (int i = 0; i < 2; ++i) {
+      const int piece = 2 * wave + i;
       const int row = 8 * piece + prow;
       const bf16* src = w + (size_t)row * hidden + k0 + 8 * ((lane & 7) ^ hg_swz(row));
       lds_dma16(src, __builtin_amdgcn_readfirstlane(base + (uint32_t)(piece * 1024)));
     }
-    #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const int row = 8 * i + prow;
-      const int tok = min(tw + row, tokens - 1);
-      const bf16* src = x + (size_t)tok * hidden + k0 + 8 * ((lane & 7) ^ hg_swz(row));
-      lds_dma16(src, __builtin_amdgcn_readfirstlane(base + (uint32_t)(HG_W_BYTES + wave * HG_X_BYTES + i * 1024)));
-    }
+    const int row = 8 * wave + prow;      // token row of the tile; row % 16 within its group
+    const int tok = min(t0 + row, tokens - 1);
+    const bf16* src = x + (size_t)tok * hidden + k0 + 8 * ((lane & 7) ^ hg_swz(row & 15));
+    lds_dma16(src, __builtin_amdgcn_readfirstlane(base + (uint32_t)(HG_W_BYTES + wave * 1024)));
   };
 
   #pragma unroll
@@ -79,30 +84,40 @@ __device__ __forceinline__ void head_tile_gemm(const bf16* __restrict__ w, const
   #pragma unroll
   for (int p = 0; p < HG_STAGES - 1; ++p) issue(p);
   for (int s = 0; s < steps; ++s) {
-    // this thread's stage-s loads landed: the 6 loads of each of the
+    // this thread's stage-s loads landed: the 3 loads of each of the
     // HG_STAGES - 2 later stages may still be in flight
-    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(6 * (HG_STAGES - 2)) : "memory");
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(3 * (HG_STAGES - 2)) : "memory");
     asm volatile("s_barrier" ::: "memory");            // ... and everyone else's
     issue(s + HG_STAGES - 1);
     const unsigned char* wst = smem + (s % HG_STAGES) * HG_STAGE_BYTES;
-    const unsigned char* xst = wst + HG_W_BYTES + wave * HG_X_BYTES;
-    #pragma unroll
-    for (int u = 0; u < HG_KB / 32; ++u) {
-      const int c = 4 * u + grp;
-      const bf16x8 xb = *reinterpret_cast<const bf16x8*>(xst + col * 128 + ((c ^ hg_swz(col)) << 4));
-      if (SUMSQ) {
-        #pragma unroll
-        for (int i = 0; i < 8; ++i) ss += (float)xb[i] * (float)xb[i];
-      }
+    const unsigned char* xst = wst + HG_W_BYTES + tg * HG_X_BYTES;
+    const int c = 4 * kh + grp;
+    const bf16x8 xb = *reinterpret_cast<const bf16x8*>(xst + col * 128 + ((c ^ hg_swz(col)) << 4));
+    if (SUMSQ) {
       #pragma unroll
-      for (int mt = 0; mt < 8; ++mt) {
-        const int row = 16 * mt + col;
-        const bf16x8 wa = *reinterpret_cast<const bf16x8*>(wst + row * 128 + ((c ^ hg_swz(row)) << 4));
-        acc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wa, xb, acc[mt], 0, 0, 0);
-      }
+      for (int i = 0; i < 8; ++i) ss += (float)xb[i] * (float)xb[i];
+    }
+    #pragma unroll
+    for (int mt = 0; mt < 8; ++mt) {
+      const int row = 16 * mt + col;
+      const bf16x8 wa = *reinterpret_cast<const bf16x8*>(wst + row * 128 + ((c ^ hg_swz(row)) << 4));
+      acc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wa, xb, acc[mt], 0, 0, 0);
     }
   }
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();   // every wave is done with the ring: reuse it for the sum
+  float* part = reinterpret_cast<float*>(smem) + ((size_t)tg * 64 + lane) * 36;
+  if (kh == 1) {
+    #pragma unroll
+    for (int mt = 0; mt < 8; ++mt) *reinterpret_cast<f32x4*>(part + 4 * mt) = acc[mt];
+    part[32] = ss;
+  }
+  __syncthreads();
+  if (kh == 0) {
+    #pragma unroll
+    for (int mt = 0; mt < 8; ++mt) acc[mt] += *reinterpret_cast<const f32x4*>(part + 4 * mt);
+    ss += part[32];
+  }
 }
 
 // RMSNorm over the 128 dims of each lane's token (weights nw[128]) in place.

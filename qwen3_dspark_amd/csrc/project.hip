@@ -48,7 +48,7 @@ struct DraftProjArgs {
   float eps_k;
 };
 
-__global__ __launch_bounds__(256) void draft_kv_project_kernel(DraftProjArgs a) {
+__global__ __launch_bounds__(HG_WAVES * WAVE) void draft_kv_project_kernel(DraftProjArgs a) {
   __shared__ __attribute__((aligned(16))) unsigned char smem[HG_SMEM];
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
@@ -67,6 +67,7 @@ __global__ __launch_bounds__(256) void draft_kv_project_kernel(DraftProjArgs a) 
   f32x4 acc[8];
   float ss;
   head_tile_gemm<true>(w, a.x, a.tokens, a.hidden, t0, smem, acc, ss);
+  if (wave >= 4) return;        // the second column half; no barrier follows
   const int tw = t0 + 16 * wave;
   if (tw >= a.tokens) return;   // wave-uniform; no barrier follows
   const int tok = min(tw + col, a.tokens - 1);
@@ -133,7 +134,7 @@ extern "C" int dspark_draft_kv_project(const void* x, int tokens, int hidden, co
   DraftProjArgs a{static_cast<const bf16*>(x), static_cast<const bf16*>(w), static_cast<const bf16*>(k_norm), inv_freq,
                   req, static_cast<bf16*>(k_pool), static_cast<bf16*>(v_pool), layer_stride, slot_stride, head_stride,
                   flag, tokens, hidden, layers, n_req, eps_ctx, eps_k};
-  hipLaunchKernelGGL(draft_kv_project_kernel, dim3((unsigned)(tiles * layers * 2 * HKV)), dim3(256), 0,
+  hipLaunchKernelGGL(draft_kv_project_kernel, dim3((unsigned)(tiles * layers * 2 * HKV)), dim3(HG_WAVES * WAVE), 0,
                      static_cast<hipStream_t>(stream), a);
   return launch_status("draft_kv_project_kernel");
 }

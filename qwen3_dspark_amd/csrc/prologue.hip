@@ -40,8 +40,9 @@ struct PrologueArgs {
 };
 
 // grid: 32 heads (0-15 q, 16-23 k, 24-31 v) x ceil(T / 64) token tiles, one
-// dimension (see the XCD mapping below); 4 waves of 16 tokens.
-__global__ __launch_bounds__(256) void qkv_prologue_kernel(PrologueArgs a) {
+// dimension (see the XCD mapping below); 8 waves, of which waves 0-3 (16
+// tokens each) run the epilogue.
+__global__ __launch_bounds__(HG_WAVES * WAVE) void qkv_prologue_kernel(PrologueArgs a) {
   __shared__ __attribute__((aligned(16))) unsigned char smem[HG_SMEM];
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
@@ -63,6 +64,7 @@ __global__ __launch_bounds__(256) void qkv_prologue_kernel(PrologueArgs a) {
   f32x4 acc[8];
   float ss;
   head_tile_gemm<false>(w, a.x, a.tokens, a.hidden, t0, smem, acc, ss);
+  if (wave >= 4) return;        // the second column half; no barrier follows
   const int tw = t0 + 16 * wave;
   if (tw >= a.tokens) return;   // wave-uniform; no barrier follows
   const int tok = min(tw + col, a.tokens - 1);
@@ -99,7 +101,7 @@ extern "C" int dspark_qkv_prologue(const void* x, const void* wq, const void* wk
                  static_cast<const bf16*>(wv), static_cast<const bf16*>(q_norm), static_cast<const bf16*>(k_norm),
                  inv_freq, positions, static_cast<bf16*>(q_out), static_cast<bf16*>(k_out),
                  static_cast<bf16*>(v_out), kv_row_stride, tokens, hidden, eps};
-  hipLaunchKernelGGL(qkv_prologue_kernel, dim3((HQ + 2 * HKV) * ((tokens + HG_TOKENS - 1) / HG_TOKENS)), dim3(256), 0,
+  hipLaunchKernelGGL(qkv_prologue_kernel, dim3((HQ + 2 * HKV) * ((tokens + HG_TOKENS - 1) / HG_TOKENS)), dim3(HG_WAVES * WAVE), 0,
                      static_cast<hipStream_t>(stream), a);
   return launch_status("qkv_prologue_kernel");
 }
