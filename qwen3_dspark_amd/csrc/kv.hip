@@ -26,29 +26,31 @@ constexpr int MAX_SCAN = 4096;   // requests per transaction handled by the bloc
 // Exclusive block scan of a[0..n) (n <= MAX_SCAN) into out[0..n] (out[n] = total),
 // executed by all 256 threads of the workgroup.
 __device__ void block_exclusive_scan(const int32_t* vals, int n, int32_t* out, int32_t* tmp) {
+  // 256 threads: each sums a run of `per` values, the runs are scanned with
+  // wave shuffles plus the 4 wave totals, then each thread writes its run.
   const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
   const int per = (n + 255) / 256;
   const int beg = min(n, tid * per);
   const int end = min(n, beg + per);
   int s = 0;
   for (int i = beg; i < end; ++i) s += vals[i];
-  tmp[tid] = s;
-  __syncthreads();
-  if (tid == 0) {
-    int run = 0;
-    for (int i = 0; i < 256; ++i) {
-      const int v = tmp[i];
-      tmp[i] = run;
-      run += v;
-    }
-    out[n] = run;
+  int incl = s;
+  #pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const int t = __shfl_up(incl, off);
+    if (lane >= off) incl += t;
   }
+  if (lane == 63) tmp[wave] = incl;
   __syncthreads();
-  int run = tmp[tid];
+  int run = incl - s;
+  for (int w = 0; w < wave; ++w) run += tmp[w];
   for (int i = beg; i < end; ++i) {
     out[i] = run;
     run += vals[i];
   }
+  if (tid == 0) out[n] = tmp[0] + tmp[1] + tmp[2] + tmp[3];
   __syncthreads();
 }
 
