@@ -894,10 +894,13 @@ struct MergeArgs {
   int draft;
 };
 
+// Workgroup (8r + g, t) merges request r, KV head g, row tile t: its id is
+// g mod 8, so it runs on the XCD whose L2 holds the partials that the chunk
+// kernel's head-g workgroups (ids = g mod 8 as well) just wrote.
 __global__ __launch_bounds__(256) void merge_kernel(MergeArgs a) {
-  const int r = blockIdx.x;
-  const int g = blockIdx.y;
-  const int t = blockIdx.z;
+  const int r = blockIdx.x >> 3;
+  const int g = blockIdx.x & 7;
+  const int t = blockIdx.y;
   int len, out_row0, rows_valid;
   if (a.req) {
     const int32_t* m = a.req + REQ_INTS * r;
@@ -992,7 +995,8 @@ int64_t workspace_bytes(int n_req, int64_t rows_bound, int tiles, int chunk) {
 }
 
 int launch_merge(const MergeArgs& m, int n_req, int tiles, hipStream_t s) {
-  hipLaunchKernelGGL(merge_kernel, dim3(n_req, HKV, tiles), dim3(256), 0, s, m);
+  DSPARK_REQUIRE((int64_t)n_req * HKV <= 0x7fffffffLL, "too many requests for the merge grid (%d)", n_req);
+  hipLaunchKernelGGL(merge_kernel, dim3((unsigned)n_req * HKV, tiles), dim3(256), 0, s, m);
   return launch_status("merge_kernel");
 }
 
