@@ -107,7 +107,7 @@ def main():
     world = int(os.environ.get('WORLD_SIZE', '1'))
     if args.gpus != 1 or world != 1:
         print(json.dumps({'error': 'this build measures one GPU only; the attention path has no cross-GPU '
-                                   'exchange (requests shard across GPUs, see DESIGN.md); run with --gpus 1'}))
+                                   'exchange (requests would shard across GPUs); run with --gpus 1'}))
         sys.exit(2)
     if args.traffic_probe:
         return traffic_probe(args)

@@ -4,7 +4,7 @@ import torch
 
 SEED = 20261009
 SCALE = 128 ** -0.5
-# BASELINE tolerance (bf16 vs FP32/FP64 oracle) plus the reference gate
+# Target tolerance (bf16 vs FP32/FP64 oracle) plus the reference gate
 # (scripts/probe_qwen_varlen.py:84-96): |d| <= .02 + .02|ref|, RMS <= .005.
 MAX_ABS = 2e-2
 MEAN_ABS = 2e-3
