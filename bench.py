@@ -106,7 +106,7 @@ def main():
     args = parse()
     world = int(os.environ.get('WORLD_SIZE', '1'))
     if args.gpus != 1 or world != 1:
-        print(json.dumps({'error': 'this build measures one GPU only; the attention path has no cross-GPU '
+        print(json.dumps({'error': 'bench.py measures one GPU only; the attention path has no cross-GPU '
                                    'exchange (requests would shard across GPUs); run with --gpus 1'}))
         sys.exit(2)
     if args.traffic_probe:

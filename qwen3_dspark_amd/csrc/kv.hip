@@ -15,7 +15,7 @@
 //
 // The copy kernels move 16-byte vectors.  The resident store is addressed
 // through byte strides, so both its head-major layout [slots, H, cap, D]
-// (what this build uses: one contiguous stream per (slot, KV head)) and a
+// (PersistentTargetKV's: one contiguous stream per (slot, KV head)) and a
 // token-major layout work; scratch and outputs are token-major rows.
 #include "common.h"
 

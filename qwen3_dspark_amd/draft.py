@@ -13,7 +13,7 @@ its blocks.
 The context K/V of one draft layer may live in
   * a row store [rows, 8, 128]: request r uses rows off_r .. off_r + c_r;
   * a head-major slotted pool [slots, 8, capacity, 128] (one contiguous run
-    per (slot, KV head), the layout this build streams fastest): off_r =
+    per (slot, KV head), the layout the draft kernel streams fastest): off_r =
     slot * capacity + first position;
   * the reference's append-order pool layer [1, 8, N, 128] with per-request
     physical indices (PackedLayout.gather_indices order): off_r indexes the
