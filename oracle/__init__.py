@@ -2,7 +2,7 @@
 
 TEST INFRASTRUCTURE ONLY.  Nothing in the product package (qwen3_dspark_amd)
 imports, links or calls this package; only tests/, __graft_entry__.smoke()
-and bench.py's cpu_baseline leg use it, and only as the checker.
+and bench.py's cpu_baseline leg use it, and only to check results.
 
   semantics.py  - integer/index semantics (layouts, transaction metadata,
                   materialised gather, commit/rollback, masks, work counters)
