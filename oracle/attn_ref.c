@@ -1,6 +1,6 @@
 /*
  * CPU restatement of the DSpark attention hot path (TEST INFRASTRUCTURE ONLY:
- * used by tests/ as a checker and by bench.py as the CPU baseline).
+ * used by tests/ to check results and by bench.py as the CPU baseline).
  *
  * Semantics restated from
  *   dspark_qwen/varlen_target.py:98-112        (bottom-right causal oracle)
