@@ -187,22 +187,26 @@ struct CommitArgs {
   int max_q;
 };
 
-// grid: (ceil(total / 256), layers); one 16-byte vector per thread.
+// grid: (ceil(total / 256), layers); one 16-byte vector per thread.  The
+// host keeps total below 2^31, so the index splits in 32-bit arithmetic, and
+// the request's four values are loaded together before the accepted test.
 __global__ __launch_bounds__(256) void kv_commit_kernel(CommitArgs a) {
-  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int i = blockIdx.x * 256 + threadIdx.x;
   if (i >= a.total) return;
-  const int64_t row_vecs = (int64_t)a.geo.heads * a.geo.piece_vecs;
-  const int64_t rowi = i / row_vecs;
-  const int64_t within = i - rowi * row_vecs;
-  const int64_t h = within / a.geo.piece_vecs;
-  const int64_t v = within - h * a.geo.piece_vecs;
-  const int r = (int)(rowi / a.max_q);
-  const int t = (int)(rowi - (int64_t)r * a.max_q);
+  const int row_vecs = a.geo.heads * a.geo.piece_vecs;
+  const int rowi = i / row_vecs;
+  const int within = i - rowi * row_vecs;
+  const int h = within / a.geo.piece_vecs;
+  const int v = within - h * a.geo.piece_vecs;
+  const int r = rowi / a.max_q;
+  const int t = rowi - r * a.max_q;
   const int layer = blockIdx.y;
-  if (t >= a.n_acc[r]) return;
+  const int n_acc = a.n_acc[r];
   const int32_t slot = a.req[r];
   const int32_t c = a.req[a.n_req + r];
-  const int64_t src = layer * a.layer_scr + ((int64_t)a.cu_q[r] + t) * row_vecs + within;
+  const int32_t q0 = a.cu_q[r];
+  if (t >= n_acc) return;
+  const int64_t src = layer * a.layer_scr + ((int64_t)q0 + t) * row_vecs + within;
   *resident_vec(a.k_res, a.geo, layer, slot, h, c + t, v) = a.k_scr[src];
   *resident_vec(a.v_res, a.geo, layer, slot, h, c + t, v) = a.v_scr[src];
 }
@@ -389,7 +393,7 @@ extern "C" int dspark_kv_commit(void* k_res, void* v_res, const void* k_scr, con
   const int64_t row_vecs = (int64_t)heads * geo.piece_vecs;
   const int64_t total = (int64_t)n_req * max_q * row_vecs;
   const int64_t blocks = (total + 255) / 256;
-  DSPARK_REQUIRE(blocks <= 0x7fffffffLL, "commit grid too large");
+  DSPARK_REQUIRE(total <= 0x7fffffffLL, "commit grid too large");
   CommitArgs a{static_cast<char*>(k_res), static_cast<char*>(v_res),
                static_cast<const u32x4*>(k_scr), static_cast<const u32x4*>(v_scr),
                req, cu_q, n_accepted, geo, scratch_rows * row_vecs, total, n_req, max_q};
