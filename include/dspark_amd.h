@@ -24,7 +24,7 @@ extern "C" {
 /* Thread-local message for the last failing call on this thread. */
 const char* dspark_last_error(void);
 
-/* ABI revision of this header (currently 3). */
+/* ABI revision of this header (currently 4). */
 int dspark_abi_version(void);
 
 /*
@@ -141,13 +141,19 @@ int dspark_verify_attn_staged_fwd(const void* q, const void* k_res, const void* 
  * so both a slotted pool ([slots*cap, 8, 128]) and the append-order pool of
  * dspark_qwen/packed_draft.py ([1, 8, N, 128] with gather indices) are read
  * in place.  q/out [7*n_blocks,16,128]; k_blk/v_blk [7*n_blocks,8,128].
+ * V (context and block) and out are bf16.  q_dtype / k_dtype select bf16 (0)
+ * or fp32 (1) for Q and for K (context and block K share one type, with the
+ * same element strides as V): fp32 values are rounded to bf16 (nearest even)
+ * as they are loaded, which is the autocast boundary cast of the reference's
+ * AMP pool (FP32 K, BF16 V; packed_draft.py:222-235), so an fp32-K pool gives
+ * the same output bits as a bf16 pool holding the rounded values.
  * Replaces the cat + index_select + cast + noncausal kernel sequence of
  *   dspark_qwen/packed_draft.py:219-236 (PackedDraft.backbone)
  * with the block_mask semantics of dspark_qwen/model.py:12-19.
  */
-int dspark_draft_attn_fwd(const void* q, const void* k_ctx, const void* v_ctx,
-                          const int64_t* ctx_idx, const int64_t* ctx_off, const int32_t* ctx_len,
-                          int64_t tok_stride, int64_t head_stride,
+int dspark_draft_attn_fwd(const void* q, int q_dtype, const void* k_ctx, const void* v_ctx,
+                          int k_dtype, const int64_t* ctx_idx, const int64_t* ctx_off,
+                          const int32_t* ctx_len, int64_t tok_stride, int64_t head_stride,
                           const void* k_blk, const void* v_blk,
                           const int32_t* cu_blocks, const int32_t* anchors,
                           int n_req, int64_t ctx_rows_bound, int max_blocks, float scale, int chunk,
@@ -372,7 +378,8 @@ int dspark_pool_gather(const void* k_src, const void* v_src, int64_t src_rows, i
  * written beyond the caller's committed lengths, so the append becomes
  * visible only when the caller advances them.  nonfinite (optional, int32)
  * is set to 1 if any appended element is Inf/NaN (elem_bytes 2 = bf16,
- * 4 = fp32).
+ * 4 = fp32).  Either pool may be NULL (with its source array) to append K
+ * or V alone, e.g. the two halves of a pool whose K and V types differ.
  */
 int dspark_pool_append(void* k_pool, void* v_pool, int64_t layer_stride, int64_t slot_stride,
                        int64_t head_stride, int64_t tok_stride, int64_t capacity, int heads,

@@ -609,14 +609,14 @@ __global__ __launch_bounds__(256, 2) void varlen_attn_kernel(VarlenArgs a) {
 // draft (multi-block, context streamed once per request)
 // ---------------------------------------------------------------------------
 struct DraftArgs {
-  const bf16* q;            // [7*n_blocks, 16, 128], request-major, block-major
-  const bf16* k_ctx;        // context pool, element (row, head, d) at
+  const void* q;            // [7*n_blocks, 16, 128] bf16 or fp32 (q_f32), request-major, block-major
+  const void* k_ctx;        // context pool (bf16, or fp32 in the KF32 instance), element (row, head, d) at
   const bf16* v_ctx;        //   row*tok_stride + head*head_stride + d
   const int64_t* ctx_idx;   // optional physical row per (request, position)
   const int64_t* ctx_off;   // [B] first row (or first ctx_idx entry) of request r
   const int32_t* ctx_len;   // [B] committed context rows of request r
-  const bf16* k_blk;        // [7*n_blocks, 8, 128] projected block K/V
-  const bf16* v_blk;
+  const void* k_blk;        // [7*n_blocks, 8, 128] projected block K (same type as k_ctx)
+  const bf16* v_blk;        //   and V (bf16)
   const int32_t* cu_b;      // [B+1] block offsets
   const int32_t* anchors;   // [n_blocks] context rows visible to each block
   bf16* out;                // [7*n_blocks, 16, 128]
@@ -629,22 +629,34 @@ struct DraftArgs {
   int n_req;
   int chunk;
   int tmax;                 // max blocks per request (<= 8)
+  int q_f32;                // Q is fp32 (rounded to bf16 at load)
   float scale_log2;
 };
 
 constexpr int BLOCK_ROWS = 7;
 constexpr int DWAVES = 8;                            // one draft block per wave
 constexpr int DSTEP = 64;                            // context keys per ring stage
-constexpr int DSTAGES = 4;                           // ring depth (3 stages in flight)
-constexpr int DSTAGE_BYTES = 2 * DSTEP * ROWB;       // K + V tiles (32 KiB)
-constexpr int DRAFT_SMEM = DSTAGES * DSTAGE_BYTES;   // 128 KiB
-constexpr int DRAFT_PIECES = 2 * DSTEP * ROWB / 1024;  // 1 KiB pieces per stage (32)
-static_assert(DRAFT_PIECES == DWAVES * 4, "each thread issues 4 direct loads per stage");
 
-// INDEXED: context rows come through a per-request physical index vector
-// (the append-order pool); otherwise they are consecutive rows.  The
-// non-indexed instance has no ordinary global loads inside the stage loop,
-// so nothing forces a full vmcnt drain between ring stages.
+// The context ring: each stage holds DSTEP K rows then DSTEP V rows, both
+// XOR-swizzled by 16-byte chunk.  A bf16 K row is 256 B (chunk c at
+// c ^ swz(k)); an fp32 K row (the reference's AMP pool, packed_draft.py:222-235)
+// is 512 B, the low four floats of bf16 chunk c at position c ^ swz(k) and the
+// high four at 16 + (c ^ swz(k)), so that the 16 lanes reading one chunk of
+// 16 rows touch 16 distinct bank groups.  Stages are filled by direct
+// global->LDS loads of 1 KiB pieces, PER_WAVE pieces per wave.
+template <bool KF32>
+struct DraftRing {
+  static constexpr int KROW = KF32 ? 2 * ROWB : ROWB;   // bytes per staged K row
+  static constexpr int STAGES = KF32 ? 3 : 4;            // 144 KiB or 128 KiB of LDS
+  static constexpr int K_BYTES = DSTEP * KROW;
+  static constexpr int STAGE_BYTES = K_BYTES + DSTEP * ROWB;
+  static constexpr int K_PIECES = K_BYTES / 1024;
+  static constexpr int PER_WAVE = STAGE_BYTES / 1024 / DWAVES;
+  static constexpr int SMEM = STAGES * STAGE_BYTES;
+  static_assert(PER_WAVE * DWAVES * 1024 == STAGE_BYTES, "stage pieces must divide evenly over the waves");
+  static_assert(SMEM <= 160 * 1024, "ring exceeds the LDS of a CU");
+};
+
 // One context segment of one request: keys [k0, k1) of request r (whose
 // blocks are b0 .. b0+nb, largest anchor amax).  The segment ending the
 // request (`last`) also attends the blocks' own rows.  A request held by
@@ -655,10 +667,24 @@ struct DraftSeg {
   bool last;
 };
 
+// 8 K values (dims 8c .. 8c+7 of one row) from global memory as bf16.
+template <bool KF32>
+__device__ __forceinline__ bf16x8 ld8_k(const void* base, size_t elem) {
+  if constexpr (KF32) return ld8(static_cast<const float*>(base) + elem);
+  else return ld8(static_cast<const bf16*>(base) + elem);
+}
+
+// INDEXED: context rows come through a per-request physical index vector
+// (the append-order pool); otherwise they are consecutive rows.  The
+// non-indexed instance has no ordinary global loads inside the stage loop,
+// so nothing forces a full vmcnt drain between ring stages.
+// KF32: context and block K are fp32 and rounded to bf16 when their MFMA
+// fragments are formed, which gives the same bits as attending a bf16 copy.
 // No early return: every wave reaches the end, so a caller may place
 // workgroup barriers between items.
-template <bool INDEXED>
+template <bool INDEXED, bool KF32>
 __device__ __forceinline__ void draft_item(const DraftArgs& a, unsigned char* smem, const DraftSeg& sg, int g) {
+  using R = DraftRing<KF32>;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
@@ -682,27 +708,38 @@ __device__ __forceinline__ void draft_item(const DraftArgs& a, unsigned char* sm
   const int vis = row_ok ? tile_anchor : 0;
   bf16x8 qf[4];
   {
-    const bf16* qp = a.q + (size_t)(BLOCK_ROWS * (b0 + (active ? b : 0)) + (row_ok ? tok : 0)) * Q_ROW +
-                     (size_t)(2 * g + (col & 1)) * HD + 8 * grp;
-    #pragma unroll
-    for (int ks = 0; ks < 4; ++ks) qf[ks] = (active && row_ok) ? ld8(qp + 32 * ks) : zero8();
+    const size_t qe = (size_t)(BLOCK_ROWS * (b0 + (active ? b : 0)) + (row_ok ? tok : 0)) * Q_ROW +
+                      (size_t)(2 * g + (col & 1)) * HD + 8 * grp;
+    const bool q_ok = active && row_ok;
+    if (a.q_f32) {
+      #pragma unroll
+      for (int ks = 0; ks < 4; ++ks) qf[ks] = q_ok ? ld8(static_cast<const float*>(a.q) + qe + 32 * ks) : zero8();
+    } else {
+      #pragma unroll
+      for (int ks = 0; ks < 4; ++ks) qf[ks] = q_ok ? ld8(static_cast<const bf16*>(a.q) + qe + 32 * ks) : zero8();
+    }
   }
   RowState st;
   row_init(st);
   // The segment ending the request also attends the wave's own 7 rows: their
   // K fragments and V rows are fetched now, so that their latency hides
-  // under the context stream instead of following its drain.
+  // under the context stream instead of following its drain.  (fp32 K rows
+  // are fetched after the drain: held unconverted through the stream they
+  // would need twice the registers.)
   const bool own = last && active;
   const size_t rb = (size_t)BLOCK_ROWS * (b0 + (active ? b : 0));
   bf16x8 own_k[2][4], own_v[2];
-  if (own) {
+  auto load_own_k = [&]() {
     #pragma unroll
     for (int j = 0; j < 2; ++j) {
       const int kk = 8 * (col >> 2) + 4 * j + (col & 3);
-      const bf16* p = a.k_blk + (rb + min(kk, BLOCK_ROWS - 1)) * KV_ROW + (size_t)g * HD + 8 * grp;
+      const size_t e = (rb + min(kk, BLOCK_ROWS - 1)) * KV_ROW + (size_t)g * HD + 8 * grp;
       #pragma unroll
-      for (int ks = 0; ks < 4; ++ks) own_k[j][ks] = ld8(p + 32 * ks);
+      for (int ks = 0; ks < 4; ++ks) own_k[j][ks] = ld8_k<KF32>(a.k_blk, e + 32 * ks);
     }
+  };
+  if (own) {
+    if constexpr (!KF32) load_own_k();
     #pragma unroll
     for (int i2 = 0; i2 < 2; ++i2) {
       const int kk = 4 * i2 + grp;
@@ -710,30 +747,48 @@ __device__ __forceinline__ void draft_item(const DraftArgs& a, unsigned char* sm
     }
   }
 
-  // Context row kk of this request for KV head g (clamped into range).
+  // Context row kk of this request for KV head g (clamped into range), as a
+  // byte address.
+  constexpr int KEL = KF32 ? 4 : 2;
   const int64_t coff = a.ctx_off[r];
-  const bf16* kbase = a.k_ctx + (size_t)g * a.head_stride;
-  const bf16* vbase = a.v_ctx + (size_t)g * a.head_stride;
-  auto ctx_row = [&](const bf16* base, int kk) -> const bf16* {
+  const char* kbase = static_cast<const char*>(a.k_ctx) + (size_t)g * a.head_stride * KEL;
+  const char* vbase = reinterpret_cast<const char*>(a.v_ctx) + (size_t)g * a.head_stride * 2;
+  auto ctx_row = [&](const char* base, int el, int kk) -> const char* {
     kk = min(kk, kend - 1);
     const int64_t phys = INDEXED ? a.ctx_idx[coff + kk] : coff + kk;
-    return base + (size_t)phys * (size_t)a.tok_stride;
+    return base + (size_t)phys * (size_t)a.tok_stride * el;
   };
   const uint32_t smem_lds = lds_address(smem);
-  // Stage `step` of the ring: 32 pieces of 1 KiB (pieces 0-15: K rows,
-  // 16-31: V rows, 4 rows each); wave w issues pieces 4w..4w+3.  Lane L of a
-  // piece fetches row 4*piece + L/16, 16-byte chunk (L%16) ^ swz(row).
+  // Stage `step` of the ring, pieces of 1 KiB; wave w issues pieces
+  // PER_WAVE*w .. +PER_WAVE-1 (the K/V choice is uniform per piece).
+  //  * bf16 K / V piece: rows 4*pr .. +3; lane L fetches row 4*pr + L/16,
+  //    16-byte chunk (L%16) ^ swz(row).
+  //  * fp32 K piece: rows 2*pr, 2*pr+1; lane L fetches row 2*pr + L/32 at
+  //    position p = L%32: floats 4*(2*((p%16) ^ swz(row)) + p/16) .. +3.
   auto issue = [&](int step) {
     const int ks = k0 + step * DSTEP;
-    const uint32_t stage = smem_lds + (uint32_t)((step % DSTAGES) * DSTAGE_BYTES);
+    const uint32_t stage = smem_lds + (uint32_t)((step % R::STAGES) * R::STAGE_BYTES);
     #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int piece = wave * 4 + i;
-      const bool is_v = piece >= 16;
-      const int pr = piece & 15;
-      const int k = 4 * pr + grp;
-      const bf16* src = ctx_row(is_v ? vbase : kbase, ks + k) + 8 * (col ^ swz(k));
-      const uint32_t dst = stage + (uint32_t)((is_v ? DSTEP * ROWB : 0) + pr * 1024);
+    for (int i = 0; i < R::PER_WAVE; ++i) {
+      const int piece = wave * R::PER_WAVE + i;
+      const char* src;
+      uint32_t dst;
+      if (piece < R::K_PIECES) {
+        if constexpr (KF32) {
+          const int k = 2 * piece + (lane >> 5);
+          const int p = lane & 31;
+          src = ctx_row(kbase, 4, ks + k) + 16 * (2 * ((p & 15) ^ swz(k)) + (p >> 4));
+        } else {
+          const int k = 4 * piece + grp;
+          src = ctx_row(kbase, 2, ks + k) + 16 * (col ^ swz(k));
+        }
+        dst = stage + (uint32_t)(piece * 1024);
+      } else {
+        const int pr = piece - R::K_PIECES;
+        const int k = 4 * pr + grp;
+        src = ctx_row(vbase, 2, ks + k) + 16 * (col ^ swz(k));
+        dst = stage + (uint32_t)(R::K_BYTES + pr * 1024);
+      }
       lds_dma16(src, __builtin_amdgcn_readfirstlane(dst));
     }
   };
@@ -742,16 +797,37 @@ __device__ __forceinline__ void draft_item(const DraftArgs& a, unsigned char* sm
   const int full_lim = min(tile_anchor, kend);
   auto compute_sub = [&](const unsigned char* kt_lds, const unsigned char* vt_lds, int h, int kt, auto masked) {
     constexpr bool MASKED = decltype(masked)::value;
-    bf16x8 kf[2][4];
-    #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int k = KT * h + 8 * (col >> 2) + 4 * j + (col & 3);
-      #pragma unroll
-      for (int ks = 0; ks < 4; ++ks)
-        kf[j][ks] = *reinterpret_cast<const bf16x8*>(kt_lds + lds_chunk_off(k, 4 * ks + grp));
-    }
     f32x4 s0, s1;
-    qk_tile(kf, qf, s0, s1);
+    if constexpr (KF32) {
+      // Each fp32 fragment is rounded and consumed at once (8 fragments of
+      // 8 floats held together would exceed the register budget).
+      s0 = f32x4{0.f, 0.f, 0.f, 0.f};
+      s1 = s0;
+      #pragma unroll
+      for (int ks = 0; ks < 4; ++ks) {
+        #pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          const int k = KT * h + 8 * (col >> 2) + 4 * j + (col & 3);
+          const unsigned char* row = kt_lds + k * R::KROW;
+          const int p = (4 * ks + grp) ^ swz(k);
+          const bf16x8 kf = to_bf16x8(*reinterpret_cast<const f32x4*>(row + 16 * p),
+                                      *reinterpret_cast<const f32x4*>(row + 16 * (16 + p)));
+          if (j == 0) s0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf, qf[ks], s0, 0, 0, 0);
+          else s1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf, qf[ks], s1, 0, 0, 0);
+        }
+        __builtin_amdgcn_sched_barrier(0);   // at most two fp32 fragments in flight
+      }
+    } else {
+      bf16x8 kf[2][4];
+      #pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int k = KT * h + 8 * (col >> 2) + 4 * j + (col & 3);
+        #pragma unroll
+        for (int ks = 0; ks < 4; ++ks)
+          kf[j][ks] = *reinterpret_cast<const bf16x8*>(kt_lds + lds_chunk_off(k, 4 * ks + grp));
+      }
+      qk_tile(kf, qf, s0, s1);
+    }
     const bf16x8 pb = softmax_update<MASKED>(st, s0, s1, kt + 8 * grp, vis, a.scale_log2);
     bf16x8 vt[8];
     #pragma unroll
@@ -767,8 +843,8 @@ __device__ __forceinline__ void draft_item(const DraftArgs& a, unsigned char* sm
     pv_update(st, pb, vt);
   };
   auto compute = [&](int step) {
-    const unsigned char* kt_lds = smem + (step % DSTAGES) * DSTAGE_BYTES;
-    const unsigned char* vt_lds = kt_lds + DSTEP * ROWB;
+    const unsigned char* kt_lds = smem + (step % R::STAGES) * R::STAGE_BYTES;
+    const unsigned char* vt_lds = kt_lds + R::K_BYTES;
     #pragma unroll
     for (int h = 0; h < 2; ++h) {
       const int kt = k0 + step * DSTEP + KT * h;
@@ -779,15 +855,15 @@ __device__ __forceinline__ void draft_item(const DraftArgs& a, unsigned char* sm
   };
   const int n_steps = kend > k0 ? (kend - k0 + DSTEP - 1) / DSTEP : 0;
   if (n_steps > 0) {
-    // Every thread issues exactly 4 loads per stage (stages past the end
-    // re-read the clamped last row), so "stage s has landed" is always
-    // vmcnt(4 * (DSTAGES - 2)) at the top of step s.
+    // Every thread issues exactly PER_WAVE loads per stage (stages past the
+    // end re-read the clamped last row), so "stage s has landed" is always
+    // vmcnt(PER_WAVE * (STAGES - 2)) at the top of step s.
     #pragma unroll
-    for (int p = 0; p < DSTAGES - 1; ++p) issue(p);
+    for (int p = 0; p < R::STAGES - 1; ++p) issue(p);
     for (int s = 0; s < n_steps; ++s) {
-      asm volatile("s_waitcnt vmcnt(%0)" ::"n"(4 * (DSTAGES - 2)) : "memory");
+      asm volatile("s_waitcnt vmcnt(%0)" ::"n"(R::PER_WAVE * (R::STAGES - 2)) : "memory");
       asm volatile("s_barrier" ::: "memory");
-      issue(s + DSTAGES - 1);
+      issue(s + R::STAGES - 1);
       if (active) compute(s);
     }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
@@ -796,6 +872,7 @@ __device__ __forceinline__ void draft_item(const DraftArgs& a, unsigned char* sm
 
   // Own-block keys (bidirectional within the block), once per request.
   if (own) {
+    if constexpr (KF32) load_own_k();
     unsigned char* wv = smem + wave * 8 * ROWB;   // 8 rows per wave
     #pragma unroll
     for (int i2 = 0; i2 < 2; ++i2)
@@ -845,9 +922,9 @@ __device__ __forceinline__ void draft_item(const DraftArgs& a, unsigned char* sm
 // With a work list, workgroup (run w, KV head g) runs the segments of run w
 // (blockIdx.x = 8w + g).  Without one, workgroup (chunk, KV head) runs one
 // fixed chunk of `chunk` context rows, chunks in request order.
-template <bool INDEXED>
+template <bool INDEXED, bool KF32>
 __global__ __launch_bounds__(512) void draft_attn_kernel(DraftArgs a) {
-  __shared__ __attribute__((aligned(16))) unsigned char smem[DRAFT_SMEM];
+  __shared__ __attribute__((aligned(16))) unsigned char smem[DraftRing<KF32>::SMEM];
   const int g = blockIdx.x & 7;
   if (a.work) {
     const int32_t* range = a.work + WORK_INTS * a.n_work + (blockIdx.x >> 3);
@@ -856,7 +933,7 @@ __global__ __launch_bounds__(512) void draft_attn_kernel(DraftArgs a) {
     for (int i = lo; i < hi; ++i) {
       const int32_t* w = a.work + WORK_INTS * i;
       const DraftSeg sg{w[0], w[1], w[2], w[3], w[4], w[5], w[6], w[2] >= w[6]};
-      draft_item<INDEXED>(a, smem, sg, g);
+      draft_item<INDEXED, KF32>(a, smem, sg, g);
       __syncthreads();   // the next segment refills the ring the last one read
     }
     return;
@@ -873,7 +950,7 @@ __global__ __launch_bounds__(512) void draft_attn_kernel(DraftArgs a) {
   for (int b = 0; b < nb; ++b) amax = max(amax, a.anchors[b0 + b]);
   const DraftSeg sg{r, c * a.chunk, min(c * a.chunk + a.chunk, ctx), nch > 1 ? first + c : -1, b0, nb, amax,
                     c == nch - 1};
-  draft_item<INDEXED>(a, smem, sg, g);
+  draft_item<INDEXED, KF32>(a, smem, sg, g);
 }
 
 // ---------------------------------------------------------------------------
@@ -1167,9 +1244,9 @@ extern "C" int dspark_verify_attn_staged_fwd(const void* q, const void* k_res, c
                        workspace, workspace_bytes_, stream);
 }
 
-extern "C" int dspark_draft_attn_fwd(const void* q, const void* k_ctx, const void* v_ctx,
-                                     const int64_t* ctx_idx, const int64_t* ctx_off, const int32_t* ctx_len,
-                                     int64_t tok_stride, int64_t head_stride,
+extern "C" int dspark_draft_attn_fwd(const void* q, int q_dtype, const void* k_ctx, const void* v_ctx,
+                                     int k_dtype, const int64_t* ctx_idx, const int64_t* ctx_off,
+                                     const int32_t* ctx_len, int64_t tok_stride, int64_t head_stride,
                                      const void* k_blk, const void* v_blk,
                                      const int32_t* cu_blocks, const int32_t* anchors,
                                      int n_req, int64_t ctx_rows_bound, int max_blocks, float scale, int chunk,
@@ -1182,6 +1259,8 @@ extern "C" int dspark_draft_attn_fwd(const void* q, const void* k_ctx, const voi
                  "Q/K/V/out must be 16-byte aligned");
   DSPARK_REQUIRE(tok_stride >= HD && tok_stride % 8 == 0 && head_stride >= HD && head_stride % 8 == 0,
                  "context strides must be multiples of 8 elements and >= 128");
+  DSPARK_REQUIRE((q_dtype == 0 || q_dtype == 1) && (k_dtype == 0 || k_dtype == 1),
+                 "q_dtype and k_dtype must be 0 (bf16) or 1 (fp32)");
   DSPARK_REQUIRE(max_blocks >= 1 && max_blocks <= DWAVES,
                  "max_blocks must be in [1, %d] (got %d)", DWAVES, max_blocks);
   DSPARK_REQUIRE(chunk % DSTEP == 0, "draft chunk must be a multiple of %d", DSTEP);
@@ -1197,13 +1276,14 @@ extern "C" int dspark_draft_attn_fwd(const void* q, const void* k_ctx, const voi
   DSPARK_REQUIRE(need == 0 || (workspace != nullptr && aligned16(workspace)),
                  "workspace must be a 16-byte aligned device pointer");
   DraftArgs a{};
-  a.q = static_cast<const bf16*>(q);
-  a.k_ctx = static_cast<const bf16*>(k_ctx);
+  a.q = q;
+  a.q_f32 = q_dtype;
+  a.k_ctx = k_ctx;
   a.v_ctx = static_cast<const bf16*>(v_ctx);
   a.ctx_idx = ctx_idx;
   a.ctx_off = ctx_off;
   a.ctx_len = ctx_len;
-  a.k_blk = static_cast<const bf16*>(k_blk);
+  a.k_blk = k_blk;
   a.v_blk = static_cast<const bf16*>(v_blk);
   a.cu_b = cu_blocks;
   a.anchors = anchors;
@@ -1221,10 +1301,15 @@ extern "C" int dspark_draft_attn_fwd(const void* q, const void* k_ctx, const voi
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int64_t grid = work ? (int64_t)n_groups * HKV : n_cl * HKV;
   DSPARK_REQUIRE(grid <= 0x7fffffffLL, "grid too large");
-  if (ctx_idx)
-    hipLaunchKernelGGL(draft_attn_kernel<true>, dim3((unsigned)grid), dim3(DWAVES * WAVE), 0, s, a);
+  const dim3 blocks((unsigned)grid), threads(DWAVES * WAVE);
+  if (ctx_idx && k_dtype)
+    hipLaunchKernelGGL((draft_attn_kernel<true, true>), blocks, threads, 0, s, a);
+  else if (ctx_idx)
+    hipLaunchKernelGGL((draft_attn_kernel<true, false>), blocks, threads, 0, s, a);
+  else if (k_dtype)
+    hipLaunchKernelGGL((draft_attn_kernel<false, true>), blocks, threads, 0, s, a);
   else
-    hipLaunchKernelGGL(draft_attn_kernel<false>, dim3((unsigned)grid), dim3(DWAVES * WAVE), 0, s, a);
+    hipLaunchKernelGGL((draft_attn_kernel<false, false>), blocks, threads, 0, s, a);
   rc = launch_status("draft_attn_kernel");
   if (rc != OK) return rc;
   MergeArgs m{work ? work + WORK_INTS * n_work + n_groups + 1 : nullptr, nullptr, nullptr, ctx_len, cu_blocks,

@@ -35,6 +35,22 @@ __device__ __forceinline__ bf16x8 ld8(const bf16* p) {
   return *reinterpret_cast<const bf16x8*>(p);
 }
 
+// Eight FP32 values rounded to bf16 (round to nearest even, as torch's
+// Tensor.to(torch.bfloat16)).
+__device__ __forceinline__ bf16x8 to_bf16x8(const f32x4& lo, const f32x4& hi) {
+  bf16x8 r;
+  #pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    r[i] = (bf16)lo[i];
+    r[4 + i] = (bf16)hi[i];
+  }
+  return r;
+}
+
+__device__ __forceinline__ bf16x8 ld8(const float* p) {
+  return to_bf16x8(*reinterpret_cast<const f32x4*>(p), *reinterpret_cast<const f32x4*>(p + 4));
+}
+
 __device__ __forceinline__ float wave_max_across_groups(float x) {
   // The 4 lanes {n, n+16, n+32, n+48} hold the same MFMA column (query row).
   x = fmaxf(x, __shfl_xor(x, 16));
@@ -97,9 +113,11 @@ __device__ __forceinline__ void locate_chunk(const int32_t* __restrict__ cu,
 // assembly so that the compiler neither waits on it nor reorders LDS reads
 // around it; kernels order it with explicit vmcnt waits and barriers, and
 // must then issue no compiler-visible global loads while such loads are in
-// flight (the compiler's own vmcnt waits would drain them).
+// flight (the compiler's own vmcnt waits would drain them).  The LDS address
+// is an M0 input operand ("{m0}"): the compiler writes M0 itself and knows
+// its value, so no M0 use of its own can be corrupted by this statement.
 __device__ __forceinline__ void lds_dma16(const void* gptr, uint32_t lds) {
-  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(lds), "v"(gptr) : "memory");
+  asm volatile("global_load_lds_dwordx4 %0, off" ::"v"(gptr), "{m0}"(lds) : "memory");
 }
 
 __device__ __forceinline__ uint32_t lds_address(const void* p) {

@@ -314,11 +314,18 @@ __global__ __launch_bounds__(256) void pool_append_kernel(AppendArgs a) {
   if (t < 0 || t >= a.req[3 * a.n_req + lo]) return;
   const int64_t slot = a.req[lo], pos = a.req[a.n_req + lo] + t;
   const int64_t src = h * a.src_head_stride + row * a.src_row_stride + v * 16;
-  const u32x4 kx = *reinterpret_cast<const u32x4*>(a.k_src[layer] + src);
-  const u32x4 vx = *reinterpret_cast<const u32x4*>(a.v_src[layer] + src);
-  *resident_vec(a.k_pool, a.geo, layer, slot, h, pos, v) = kx;
-  *resident_vec(a.v_pool, a.geo, layer, slot, h, pos, v) = vx;
-  if (a.nonfinite && (vec_nonfinite(kx, a.elem_bytes) || vec_nonfinite(vx, a.elem_bytes))) atomicOr(a.nonfinite, 1);
+  bool bad = false;
+  if (a.k_pool) {
+    const u32x4 kx = *reinterpret_cast<const u32x4*>(a.k_src[layer] + src);
+    *resident_vec(a.k_pool, a.geo, layer, slot, h, pos, v) = kx;
+    bad = vec_nonfinite(kx, a.elem_bytes);
+  }
+  if (a.v_pool) {
+    const u32x4 vx = *reinterpret_cast<const u32x4*>(a.v_src[layer] + src);
+    *resident_vec(a.v_pool, a.geo, layer, slot, h, pos, v) = vx;
+    bad = bad || vec_nonfinite(vx, a.elem_bytes);
+  }
+  if (a.nonfinite && bad) atomicOr(a.nonfinite, 1);
 }
 
 }  // namespace dspark
@@ -438,7 +445,7 @@ extern "C" int dspark_pool_append(void* k_pool, void* v_pool, int64_t layer_stri
                                   int64_t src_head_stride, int64_t src_row_stride, int64_t src_rows,
                                   const int32_t* req, int n_req, int32_t* nonfinite, void* stream) {
   clear_error();
-  DSPARK_REQUIRE(k_pool && v_pool && k_src && v_src && req, "null pointer argument");
+  DSPARK_REQUIRE((k_pool || v_pool) && !k_pool == !k_src && !v_pool == !v_src && req, "null pointer argument");
   DSPARK_REQUIRE(layers >= 1 && layers <= APPEND_MAX_LAYERS, "layers must be in [1, %d]", APPEND_MAX_LAYERS);
   DSPARK_REQUIRE(n_req >= 1 && src_rows >= 1, "sizes must be positive");
   DSPARK_REQUIRE(elem_bytes == 2 || elem_bytes == 4, "element size must be 2 or 4 bytes");
@@ -447,10 +454,10 @@ extern "C" int dspark_pool_append(void* k_pool, void* v_pool, int64_t layer_stri
   DSPARK_REQUIRE(aligned16(k_pool) && aligned16(v_pool), "buffers must be 16-byte aligned");
   AppendArgs a{};
   for (int l = 0; l < layers; ++l) {
-    DSPARK_REQUIRE(k_src[l] && v_src[l], "null pointer argument");
-    DSPARK_REQUIRE(aligned16(k_src[l]) && aligned16(v_src[l]), "buffers must be 16-byte aligned");
-    a.k_src[l] = static_cast<const char*>(k_src[l]);
-    a.v_src[l] = static_cast<const char*>(v_src[l]);
+    DSPARK_REQUIRE((!k_pool || k_src[l]) && (!v_pool || v_src[l]), "null pointer argument");
+    a.k_src[l] = k_pool ? static_cast<const char*>(k_src[l]) : nullptr;
+    a.v_src[l] = v_pool ? static_cast<const char*>(v_src[l]) : nullptr;
+    DSPARK_REQUIRE(aligned16(a.k_src[l]) && aligned16(a.v_src[l]), "buffers must be 16-byte aligned");
   }
   ResidentGeometry geo{layer_stride, slot_stride, head_stride, tok_stride, capacity, heads, (int)(piece_bytes / 16)};
   int rc = check_geometry(geo);

@@ -21,13 +21,14 @@ The context K/V of one draft layer may live in
 """
 import torch
 
-from . import _native
+from . import _native, backends
 from ._device import Workspace, cu_count, require_gfx950, upload
 from .kernels import HEAD_DIM, KV_HEADS, Q_HEADS, SCALE, _check_scale
 from .schedule import DRAFT_CHUNK, draft_run_count, draft_work, upload_work
 
 BLOCK_SIZE = 7
 MAX_BLOCKS = 8
+_QK_DTYPES = (torch.bfloat16, torch.float32)
 
 
 class DraftBatch:
@@ -127,7 +128,7 @@ class DraftBatch:
 class HipDraftAttention:
     """Multi-block draft attention kernel object (one chunk launch per layer
     plus a split-K merge launch)."""
-    backend_name = 'mi355x_hip_draft_blocks_v1'
+    backend_name = backends.DRAFT_BLOCKS_BACKEND
     native_varlen_calls_per_layer = 1
 
     def __init__(self, device, *, chunk=DRAFT_CHUNK, runs=None):
@@ -165,33 +166,45 @@ class HipDraftAttention:
         raise ValueError('Context K/V must be [rows,8,128], [slots,8,capacity,128] or [1,8,N,128]')
 
     def __call__(self, query, block_keys, block_values, context_keys, context_values, batch, *, scale):
+        """Q [7*blocks, 16, 128], block K/V [7*blocks, 8, 128], context K/V in
+        one of the pool forms of the module docstring.  V is bf16.  Q and K
+        (context and block K alike) may be bf16 or fp32: fp32 values are
+        rounded to bf16 as the kernel loads them, the cast the reference
+        applies at its kernel boundary under autocast (packed_draft.py:222-235),
+        so an fp32-K pool (the reference's AMP form: FP32 K, BF16 V) needs no
+        cast copy.  Returns bf16 [7*blocks, 16, 128]."""
         if not isinstance(batch, DraftBatch) or batch.device != self.device:
             raise ValueError('DraftBatch on the kernel device required')
         _check_scale(scale, 'HIP draft attention')
         nq = batch.query_rows
-        for t, shape in ((query, (nq, Q_HEADS, HEAD_DIM)), (block_keys, (nq, KV_HEADS, HEAD_DIM)),
-                         (block_values, (nq, KV_HEADS, HEAD_DIM))):
-            if (not isinstance(t, torch.Tensor) or t.dtype != torch.bfloat16 or t.device != self.device
+        for t, shape, dtypes in ((query, (nq, Q_HEADS, HEAD_DIM), _QK_DTYPES),
+                                 (block_keys, (nq, KV_HEADS, HEAD_DIM), _QK_DTYPES),
+                                 (block_values, (nq, KV_HEADS, HEAD_DIM), (torch.bfloat16,))):
+            if (not isinstance(t, torch.Tensor) or t.dtype not in dtypes or t.device != self.device
                     or tuple(t.shape) != shape or not t.is_contiguous() or t.requires_grad):
-                raise ValueError('Draft Q/block K/V must be contiguous no-autograd bf16 [7*blocks,H,128] on the GPU')
+                raise ValueError('Draft Q/block K (bf16 or fp32) and block V (bf16) must be contiguous '
+                                 'no-autograd [7*blocks,H,128] tensors on the GPU')
         if (not isinstance(context_keys, torch.Tensor) or not isinstance(context_values, torch.Tensor)
-                or context_keys.shape != context_values.shape or context_keys.dtype != torch.bfloat16
+                or context_keys.shape != context_values.shape or context_keys.dtype not in _QK_DTYPES
                 or context_values.dtype != torch.bfloat16 or context_keys.device != self.device
                 or context_values.device != self.device
                 or not context_keys.is_contiguous() or not context_values.is_contiguous()):
-            raise ValueError('Context K/V must be matching contiguous bf16 tensors on the GPU')
+            raise ValueError('Context K (bf16 or fp32) and V (bf16) must be matching contiguous tensors on the GPU')
+        if block_keys.dtype != context_keys.dtype:
+            raise ValueError('Backbone/cache precision mismatch')
         # The batch is immutable: its pool bounds are checked once per pool shape.
         key = (batch, context_keys.shape)
         if self._geometry_for is None or self._geometry_for[0] is not batch or self._geometry_for[1] != key[1]:
             self._geometry = self._context_geometry(context_keys, batch)
             self._geometry_for = key
         offsets, tok_stride, head_stride = self._geometry
-        out = torch.empty_like(query)
+        out = torch.empty(query.shape, dtype=torch.bfloat16, device=self.device)
         bound = max(batch.context_rows, 1)
         work, n_work, n_runs = batch.work(self.chunk, self.runs)
         need = _native.load().dspark_attn_workspace_bytes(n_work, 0, batch.max_blocks, self.chunk)
         ws = self._workspace.get(need)
-        _native.call('dspark_draft_attn_fwd', _native.ptr(query), _native.ptr(context_keys), _native.ptr(context_values),
+        _native.call('dspark_draft_attn_fwd', _native.ptr(query), int(query.dtype == torch.float32),
+                     _native.ptr(context_keys), _native.ptr(context_values), int(context_keys.dtype == torch.float32),
                      _native.ptr(batch.context_indices), _native.ptr(offsets), _native.ptr(batch.ctx_len),
                      tok_stride, head_stride, _native.ptr(block_keys), _native.ptr(block_values),
                      _native.ptr(batch.cu_blocks), _native.ptr(batch.anchor_rows), batch.request_count, bound,
@@ -218,25 +231,34 @@ class DraftKVPool:
     k_proj, k_norm, v_proj of packed_draft.py:147-158).
     Appends are transactional: rows land beyond the committed lengths and
     become visible only when every check, including finiteness, passed.
+
+    K and V may differ in precision: key_dtype / value_dtype (default dtype).
+    The reference's pool under bf16 autocast holds FP32 K (its k_norm runs in
+    FP32) and BF16 V (packed_draft.py:222-235); attention reads such a pool in
+    place and rounds K to bf16 in registers.
     """
 
     def __init__(self, *, layers, slots, capacity, heads=KV_HEADS, dim=HEAD_DIM, dtype=torch.bfloat16,
-                 device='cuda', chunk=DRAFT_CHUNK, projector=None):
+                 key_dtype=None, value_dtype=None, device='cuda', chunk=DRAFT_CHUNK, projector=None):
         if any(type(n) is not int or n < 1 for n in (layers, slots, capacity, heads, dim)):
             raise ValueError('All pool sizes must be positive integers')
-        if dtype not in (torch.bfloat16, torch.float32):
+        key_dtype = dtype if key_dtype is None else key_dtype
+        value_dtype = dtype if value_dtype is None else value_dtype
+        if any(d not in (torch.bfloat16, torch.float32) for d in (dtype, key_dtype, value_dtype)):
             raise ValueError('Draft pool dtype must be bfloat16 or float32')
         if layers > 16:
             raise ValueError('At most 16 draft layers per pool')
         self.device = require_gfx950(device)
         _native.load()
         self.layers, self.slot_capacity, self.capacity, self.heads, self.dim = layers, slots, capacity, heads, dim
-        self.dtype = dtype
-        self._elem = torch.empty((), dtype=dtype).element_size()
-        if (dim * self._elem) % 16:
+        self.key_dtype, self.value_dtype = key_dtype, value_dtype
+        self.dtype = key_dtype if key_dtype == value_dtype else None
+        self._elems = (torch.empty((), dtype=key_dtype).element_size(),
+                       torch.empty((), dtype=value_dtype).element_size())
+        if any((dim * e) % 16 for e in self._elems):
             raise ValueError('A KV head row must be a multiple of 16 bytes')
-        self.keys = torch.zeros((layers, slots, heads, capacity, dim), dtype=dtype, device=self.device)
-        self.values = torch.zeros_like(self.keys)
+        self.keys = torch.zeros((layers, slots, heads, capacity, dim), dtype=key_dtype, device=self.device)
+        self.values = torch.zeros((layers, slots, heads, capacity, dim), dtype=value_dtype, device=self.device)
         self._lengths = {}
         self._slots = {}
         self._free = list(range(slots))
@@ -244,7 +266,7 @@ class DraftKVPool:
         self._flag = torch.zeros(1, dtype=torch.int32, device=self.device)
         self.last_append_work = None
         if projector is not None and (projector.layers != layers or projector.device != self.device
-                                      or (heads, dim, dtype) != (KV_HEADS, HEAD_DIM, torch.bfloat16)):
+                                      or (heads, dim, self.dtype) != (KV_HEADS, HEAD_DIM, torch.bfloat16)):
             raise ValueError('The projector needs a bf16 8x128 pool with its layer count on its device')
         self.projector = projector
 
@@ -276,14 +298,14 @@ class DraftKVPool:
         if any(not 0 <= n <= self.capacity for n in self._lengths.values()):
             raise RuntimeError('Draft cache must be the complete request-local committed prefix')
 
-    def _source(self, t, rows):
+    def _source(self, t, rows, dtype):
         """(head stride, row stride) in bytes of a [1, H, rows, D] or
-        [rows, H, D] tensor of new K or V rows."""
+        [rows, H, D] tensor of new K or V rows of the pool's `dtype`."""
         if not isinstance(t, torch.Tensor) or t.device != self.device:
             raise ValueError('Projected K/V must be tensors on the pool device')
-        if t.dtype != self.dtype:
+        if t.dtype != dtype:
             raise ValueError('Draft cache precision cannot change across appends')
-        e = self._elem
+        e = t.element_size()
         if t.ndim == 4 and tuple(t.shape) == (1, self.heads, rows, self.dim) and t.stride(3) == 1:
             strides = (t.stride(1) * e, t.stride(2) * e)
         elif t.ndim == 3 and tuple(t.shape) == (rows, self.heads, self.dim) and t.stride(2) == 1:
@@ -315,12 +337,13 @@ class DraftKVPool:
         rows = sum(n for _, n in order)
         if len(projected) != self.layers:
             raise ValueError('Draft cache layer count mismatch')
-        strides = None
+        strides = [None, None]
         for k, v in projected:
-            sk, sv = self._source(k, rows), self._source(v, rows)
-            if sk != sv or (strides is not None and sk != strides):
-                raise ValueError('Projected K/V must share one layout across layers')
-            strides = sk
+            for i, (t, dt) in enumerate(((k, self.key_dtype), (v, self.value_dtype))):
+                st = self._source(t, rows, dt)
+                if strides[i] is not None and st != strides[i]:
+                    raise ValueError('Projected K/V must share one layout across layers')
+                strides[i] = st
         req, offset = [[], [], [], []], 0
         for request, n in order:
             req[0].append(self._slots[request])
@@ -331,19 +354,27 @@ class DraftKVPool:
         dev_req = upload(self.device, [x for row in req for x in row])
         if check_finite:
             self._flag.zero_()
-        e, H, C, D = self._elem, self.heads, self.capacity, self.dim
-        _native.call('dspark_pool_append', self.keys.data_ptr(), self.values.data_ptr(),
-                     self.slot_capacity * H * C * D * e, H * C * D * e, C * D * e, D * e, C, H, D * e, e,
-                     self.layers, _native.pointer_array([k for k, _ in projected]),
-                     _native.pointer_array([v for _, v in projected]), strides[0], strides[1], rows,
-                     dev_req.data_ptr(), len(order), self._flag.data_ptr() if check_finite else None,
-                     _native.stream_handle(self.device))
+        H, C, D = self.heads, self.capacity, self.dim
+        ks, vs = [k for k, _ in projected], [v for _, v in projected]
+        # One launch for K and V together when they share a row size, else one each.
+        if self._elems[0] == self._elems[1] and strides[0] == strides[1]:
+            parts = [(self.keys, self.values, ks, vs, self._elems[0], strides[0])]
+        else:
+            parts = [(self.keys, None, ks, None, self._elems[0], strides[0]),
+                     (None, self.values, None, vs, self._elems[1], strides[1])]
+        for kp, vp, ksrc, vsrc, e, st in parts:
+            _native.call('dspark_pool_append', _native.ptr(kp), _native.ptr(vp),
+                         self.slot_capacity * H * C * D * e, H * C * D * e, C * D * e, D * e, C, H, D * e, e,
+                         self.layers, None if ksrc is None else _native.pointer_array(ksrc),
+                         None if vsrc is None else _native.pointer_array(vsrc), st[0], st[1], rows,
+                         dev_req.data_ptr(), len(order), self._flag.data_ptr() if check_finite else None,
+                         _native.stream_handle(self.device))
         if check_finite and int(self._flag.item()):
             raise RuntimeError('Nonfinite projected draft context')
         for request, n in order:
             self._lengths[request] += n
-        self.last_append_work = dict(requests=len(order), new_context_tokens=rows, append_launches=1,
-                                     appended_kv_bytes=2 * self.layers * rows * H * D * e,
+        self.last_append_work = dict(requests=len(order), new_context_tokens=rows, append_launches=len(parts),
+                                     appended_kv_bytes=self.layers * rows * H * D * sum(self._elems),
                                      cache_concatenation_kv_bytes=0)
         return self.last_append_work
 
@@ -387,7 +418,7 @@ class DraftKVPool:
             raise RuntimeError('Nonfinite projected draft context')
         for request, f in zip(order, feats):
             self._lengths[request[0]] += f.shape[0]
-        e, H, D = self._elem, self.heads, self.dim
+        e, H, D = self._elems[0], self.heads, self.dim
         self.last_append_work = dict(requests=len(order), new_context_tokens=first, context_projection_calls=1,
                                      kv_projection_calls=self.layers, projection_launches=2,
                                      appended_kv_bytes=2 * self.layers * first * H * D * e,

@@ -28,6 +28,7 @@ import torch
 from transformers import Cache
 from transformers.modeling_utils import ALL_ATTENTION_FUNCTIONS
 
+from .kernels import HipCapacityKernel
 from .layout import PackedLayout
 from .persistent_kv import Bucket, PersistentTargetKV, QueryFamily
 from .schedule import DEFAULT_CHUNK
@@ -219,6 +220,10 @@ class PersistentQwenTarget:
                                         dim=cfg.head_dim, dtype=dtype, device=device, chunk=chunk)
         self.verifier = FusedVerifier(model, self.store)
         self.model = self.verifier.model
+        # The kernel identity the reference's session guard reads
+        # (packed_sampling.py:110-115): the capacity-tail drop-in of
+        # _native_attention.  verify() itself runs the fused store attention.
+        self._varlen_kernel = HipCapacityKernel(device)
         self._handles = {}
         self._pending = None
         self._captured = {}

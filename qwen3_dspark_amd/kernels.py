@@ -14,7 +14,7 @@ import math
 
 import torch
 
-from . import _native
+from . import _native, backends
 from ._device import Workspace, cu_count, require_gfx950
 from .schedule import DEFAULT_CHUNK, SPLITS, run_count, segment_plan, upload_work
 
@@ -29,7 +29,7 @@ def _check_scale(scale, what):
 
 class HipVarlenKernel:
     """Bottom-right causal packed attention over an exact-K PackedLayout."""
-    backend_name = 'mi355x_hip_varlen_causal_v1'
+    backend_name = backends.TARGET_BACKEND
     native_varlen_calls_per_layer = 1
     causal = True
 
@@ -134,7 +134,7 @@ class HipVarlenKernel:
 class HipDraftVarlenKernel(HipVarlenKernel):
     """Noncausal packed attention: every query sees all keys of its request
     (the single-block packed draft path, packed_draft.py:19-47)."""
-    backend_name = 'mi355x_hip_varlen_noncausal_v1'
+    backend_name = backends.DRAFT_BACKEND
     causal = False
 
 
@@ -146,7 +146,7 @@ class HipCapacityKernel(HipVarlenKernel):
     depends only on the bucket (capacity and maximum query length), never on
     the current lengths.
     """
-    backend_name = 'mi355x_hip_capacity_causal_v1'
+    backend_name = backends.CAPACITY_BACKEND
 
     def _work_list(self, layout, tiles):
         # Request-order dispatch of fixed chunks over a grid sized from the

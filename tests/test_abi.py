@@ -92,9 +92,12 @@ def test_invalid_sizes_are_rejected_before_any_launch():
     rc = lib.dspark_varlen_attn_fwd(fake, fake, fake, fake, fake, 2, 8, 8, 1, 1, 0.088, 512, fake, 0, 1, fake, fake,
                                     1 << 20, None)
     assert rc == -1 and 'n_work' in lib.dspark_last_error().decode()
-    rc = lib.dspark_draft_attn_fwd(fake, fake, fake, None, fake, fake, 1024, 128, fake, fake, fake, fake,
+    rc = lib.dspark_draft_attn_fwd(fake, 0, fake, fake, 0, None, fake, fake, 1024, 128, fake, fake, fake, fake,
                                    2, 100, 9, 0.088, 512, None, 0, 0, fake, fake, 1 << 24, None)
     assert rc == -1 and 'max_blocks' in lib.dspark_last_error().decode()
+    rc = lib.dspark_draft_attn_fwd(fake, 0, fake, fake, 2, None, fake, fake, 1024, 128, fake, fake, fake, fake,
+                                   2, 100, 8, 0.088, 512, None, 0, 0, fake, fake, 1 << 24, None)
+    assert rc == -1 and 'k_dtype' in lib.dspark_last_error().decode()
     rc = lib.dspark_verify_attn_fwd(fake, fake, fake, fake, fake, fake, fake, fake, 2, 1 << 20, 100, 128, 1000, 7,
                                     0.088, 512, None, 0, 0, fake, fake, 1 << 24, None)
     assert rc == -1 and 'strides' in lib.dspark_last_error().decode()
