@@ -115,6 +115,28 @@ int dspark_verify_attn_fwd(const void* q, const void* k_res, const void* v_res,
                            void* workspace, int64_t workspace_bytes, void* stream);
 
 /*
+ * dspark_verify_attn_fwd without a workspace argument, for callers that
+ * cannot allocate device memory (code under HIP graph capture, serving loops
+ * and harnesses that forbid hipMalloc).  No counterpart in the reference.
+ * The split-K partials live in a static device array of
+ * dspark_noalloc_scratch_bytes() bytes (32 MiB) that each GPU holds until
+ * the process ends; a call whose partials need more (see
+ * dspark_attn_workspace_bytes) returns -1 and launches nothing.  The call
+ * allocates nothing, and its result is bit-identical to
+ * dspark_verify_attn_fwd's.  Every call on one GPU shares that GPU's array:
+ * calls that overlap in time on one GPU (other streams, other threads) race.
+ * The array's address is resolved on the first call on each device, which
+ * must be the current device.
+ */
+int64_t dspark_noalloc_scratch_bytes(void);
+int dspark_verify_attn_fwd_noalloc(const void* q, const void* k_res, const void* v_res,
+                                   const void* k_scr, const void* v_scr,
+                                   const int32_t* cu_q, const int32_t* cu_k, const int32_t* slots,
+                                   int n_req, int64_t slot_stride, int64_t tok_stride, int64_t head_stride,
+                                   int64_t key_rows_bound, int max_q, float scale, int chunk,
+                                   const int32_t* work, int n_work, int n_groups, void* out, void* stream);
+
+/*
  * dspark_verify_attn_fwd with the layer's staging fused in: the new rows are
  * read from k_new/v_new ([q_rows, 8, 128], the model's projected K/V) and
  * copied into k_scr/v_scr by the workgroups that read them, replacing the

@@ -27,6 +27,9 @@ SIGNATURES = {
     'dspark_varlen_attn_fwd': (_I, [_P, _P, _P, _P, _P, _I, _L, _L, _I, _I, _F, _I, _P, _I, _I, _P, _P, _L, _P]),
     'dspark_verify_attn_fwd': (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _I, _L, _L, _L, _L, _I, _F, _I, _P, _I, _I,
                                     _P, _P, _L, _P]),
+    'dspark_noalloc_scratch_bytes': (_L, []),
+    'dspark_verify_attn_fwd_noalloc': (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _I, _L, _L, _L, _L, _I, _F, _I, _P, _I,
+                                            _I, _P, _P]),
     'dspark_verify_attn_staged_fwd': (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _L, _L, _L, _L, _I, _F, _I,
                                            _P, _I, _I, _P, _P, _L, _P]),
     'dspark_draft_attn_fwd': (_I, [_P, _I, _P, _P, _I, _P, _P, _P, _L, _L, _P, _P, _P, _P, _I, _L, _I, _F, _I, _P,

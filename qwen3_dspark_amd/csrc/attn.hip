@@ -38,6 +38,8 @@
 // more than one segment writes FP32 partial (max, sum, unnormalised O)
 // triples that merge_kernel combines; the kernel boundary makes them visible
 // without any per-workgroup cache flush.
+#include <atomic>
+#include <mutex>
 #include <type_traits>
 
 #include "common.h"
@@ -1227,6 +1229,76 @@ extern "C" int dspark_verify_attn_fwd(const void* q, const void* k_res, const vo
   return verify_launch(q, k_res, v_res, k_scr, v_scr, nullptr, nullptr, cu_q, cu_k, slots, n_req, slot_stride,
                        tok_stride, head_stride, key_rows_bound, max_q, scale, chunk, work, n_work, n_groups, out,
                        workspace, workspace_bytes_, stream);
+}
+
+// ---------------------------------------------------------------------------
+// Allocation-free verification attention: the split-K partials live in a
+// file-scope device array instead of a caller workspace.  Each GPU the
+// library runs on holds its own copy of the array (NOALLOC_SCRATCH_BYTES)
+// until the process ends; every call on that GPU shares it.
+// ---------------------------------------------------------------------------
+namespace {
+constexpr int64_t NOALLOC_SCRATCH_BYTES = 32ll << 20;
+constexpr int NOALLOC_MAX_DEVICES = 64;
+}  // namespace
+
+static __device__ __align__(256) unsigned char scratch[NOALLOC_SCRATCH_BYTES];
+
+namespace {
+std::atomic<void*> g_scratch_ptr[NOALLOC_MAX_DEVICES];
+std::mutex g_scratch_lock;
+
+// Device address of `scratch` on the current device, resolved once per
+// device with that device current.  The array's name is only a host-side
+// handle: kernels get this address, never the symbol.
+int scratch_address(void** out) {
+  int dev = -1;
+  DSPARK_REQUIRE(hipGetDevice(&dev) == hipSuccess && dev >= 0 && dev < NOALLOC_MAX_DEVICES,
+                 "no usable current HIP device (need an index below %d)", NOALLOC_MAX_DEVICES);
+  void* p = g_scratch_ptr[dev].load(std::memory_order_acquire);
+  if (!p) {
+    std::lock_guard<std::mutex> guard(g_scratch_lock);
+    p = g_scratch_ptr[dev].load(std::memory_order_relaxed);
+    if (!p) {
+      const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+      if (e != hipSuccess || !p) {
+        set_error("hipGetSymbolAddress(scratch) failed on device %d: %s", dev, hipGetErrorString(e));
+        return HIP_FAILURE;
+      }
+      g_scratch_ptr[dev].store(p, std::memory_order_release);
+    }
+  }
+  *out = p;
+  return OK;
+}
+}  // namespace
+
+extern "C" int64_t dspark_noalloc_scratch_bytes(void) { return NOALLOC_SCRATCH_BYTES; }
+
+extern "C" int dspark_verify_attn_fwd_noalloc(const void* q, const void* k_res, const void* v_res,
+                                              const void* k_scr, const void* v_scr,
+                                              const int32_t* cu_q, const int32_t* cu_k, const int32_t* slots,
+                                              int n_req, int64_t slot_stride, int64_t tok_stride,
+                                              int64_t head_stride, int64_t key_rows_bound, int max_q, float scale,
+                                              int chunk, const int32_t* work, int n_work, int n_groups, void* out,
+                                              void* stream) {
+  clear_error();
+  DSPARK_REQUIRE(q && k_res && v_res && k_scr && v_scr && cu_q && cu_k && slots && out, "null pointer argument");
+  DSPARK_REQUIRE(max_q >= 1, "max_q must be >= 1");
+  const int tiles = (max_q + 7) / 8;
+  const int64_t need = work ? dspark_attn_workspace_bytes(n_work, 0, tiles, chunk)
+                            : dspark_attn_workspace_bytes(n_req, key_rows_bound, tiles, chunk);
+  DSPARK_REQUIRE(need >= 0, "invalid request, key bound, row tile or chunk sizes");
+  DSPARK_REQUIRE(need <= NOALLOC_SCRATCH_BYTES,
+                 "split-K partials need %lld bytes, more than the %lld-byte static scratch of the allocation-free "
+                 "entry point (use dspark_verify_attn_fwd with a workspace)",
+                 (long long)need, (long long)NOALLOC_SCRATCH_BYTES);
+  void* ws = nullptr;
+  const int rc = scratch_address(&ws);
+  if (rc != OK) return rc;
+  return verify_launch(q, k_res, v_res, k_scr, v_scr, nullptr, nullptr, cu_q, cu_k, slots, n_req, slot_stride,
+                       tok_stride, head_stride, key_rows_bound, max_q, scale, chunk, work, n_work, n_groups, out,
+                       ws, NOALLOC_SCRATCH_BYTES, stream);
 }
 
 extern "C" int dspark_verify_attn_staged_fwd(const void* q, const void* k_res, const void* v_res,

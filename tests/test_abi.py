@@ -59,6 +59,7 @@ def test_workspace_size_formula():
 
 
 @pytest.mark.parametrize('name', ['dspark_varlen_attn_fwd', 'dspark_verify_attn_fwd', 'dspark_verify_attn_staged_fwd',
+                                  'dspark_verify_attn_fwd_noalloc',
                                   'dspark_draft_attn_fwd',
                                   'dspark_txn_metadata', 'dspark_kv_stage', 'dspark_kv_commit', 'dspark_kv_gather',
                                   'dspark_layout_build', 'dspark_pool_gather', 'dspark_pool_append',
