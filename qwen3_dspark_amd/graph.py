@@ -42,7 +42,7 @@ class VerificationGraph:
     kind = 'mi355x_hip_verification_graph'
 
     def __init__(self, pool, bucket):
-        if bucket not in pool._workspaces:
+        if not pool.is_registered(bucket):
             raise ValueError('Registered bucket required')
         if (pool.heads, pool.dim, pool.dtype) != (KV_HEADS, HEAD_DIM, torch.bfloat16):
             raise ValueError('Captured verification requires bf16 Hkv8/D128 storage')
@@ -70,9 +70,9 @@ class VerificationGraph:
 
     def _body(self):
         for layer in range(self.pool.layers):
-            self.pool._attention_launch(self.bucket, layer, self.query[layer].data_ptr(),
-                                        self.output[layer].data_ptr(), self.keys[layer].data_ptr(),
-                                        self.values[layer].data_ptr())
+            self.pool.launch_attention(self.bucket, layer, self.query[layer].data_ptr(),
+                                       self.output[layer].data_ptr(), self.keys[layer].data_ptr(),
+                                       self.values[layer].data_ptr())
 
     @torch.no_grad()
     def capture(self):

@@ -282,16 +282,16 @@ class PersistentQwenTarget:
         query_lengths = tuple(ids.shape[1] for ids in chunks.values())
         self._captured = {}
         with self.verifier.transaction_for(handles, bucket, query_lengths=query_lengths) as tx:
-            ws = self.store._workspaces[tx.bucket]
+            ws = self.store.workspace(tx.bucket)
             try:
                 out = self.model.model(input_ids=torch.cat(tuple(chunks.values()), dim=1),
                                        position_ids=ws.positions[None], attention_mask=None,
                                        past_key_values=self.verifier.cache, use_cache=True, return_dict=True,
                                        fused_verification=self.verifier)
-                if len(self.store._staged) != self.store.layers or set(self._captured) != set(self.layer_ids):
+                if self.store.staged_layers() != self.store.layers or set(self._captured) != set(self.layer_ids):
                     raise RuntimeError('Full layer cache update or selected feature capture missing')
             except BaseException:
-                if self.store._pending is tx and not self.store.failed:
+                if self.store.open_transaction is tx and not self.store.failed:
                     self.store.abort(tx)
                 raise
             finally:

@@ -2,8 +2,15 @@
 
 Drop-in for dspark_qwen/persistent_target_kv.py (PersistentTargetKV and its
 Slot / Bucket / QueryFamily / Transaction / ExternalWriter types): the same
-constructor, methods, validation order, error classes and fail-closed
-poisoning.  The device work is HIP:
+constructor, methods, validation order, error classes and messages, and
+fail-closed poisoning.
+
+Host design: the store is a small state machine.  Phase names where a round
+stands (idle, open with eager staging, an external writer prepared /
+submitted / published, poisoned) and a transition table lists which event
+each phase admits; a refused event raises that event's error.  A slot ledger
+tracks tenancy, incarnations and committed lengths.  Every device buffer and
+launch lives in an injected device half (kv_device.HipKVDevice):
 
   begin             -> dspark_txn_metadata  (one launch; the reference builds
                        O(key capacity) Python lists and copies seven arrays)
@@ -14,23 +21,18 @@ poisoning.  The device work is HIP:
   attend            -> dspark_verify_attn_fwd: causal attention reading the
                        resident rows and staged scratch rows in place; the
                        capacity-length K/V is never materialised.
-
-Layout in HBM: resident K and V are stored head-major,
-[layers, slots, heads, context_capacity, dim], so the attention of one
-(request, KV head) streams one contiguous run of 256-byte rows; `keys` /
-`values` are [layers, slots, context_capacity, heads, dim] views of that
-storage (the reference's shape).  Scratch K and V are token-major
-[layers, max_query_tokens, heads, dim], the shape the model produces.
 """
+import enum
+import heapq
 from dataclasses import dataclass
+from types import SimpleNamespace
 from typing import Mapping
 
 import torch
 
-from . import _native
-from ._device import cu_count, require_gfx950, upload
 from .kernels import HEAD_DIM, KV_HEADS, Q_HEADS, SCALE, _check_scale
-from .schedule import DEFAULT_CHUNK, REQ_INTS, SPLITS, WORK_INTS, run_count, segment_plan, varlen_list_bound
+from .kv_device import MAX_BUCKET_REQUESTS, HipKVDevice
+from .schedule import DEFAULT_CHUNK, SPLITS
 
 
 @dataclass(frozen=True)
@@ -137,338 +139,396 @@ class ExternalWrite:
     generation: int
 
 
-class _Workspace:
-    """Per-bucket device metadata, materialised K/V and split-K partials.
 
-    Arrays and meaning follow persistent_target_kv.py:127-153.  The reference's
-    old/new intermediates do not exist: dspark_kv_gather writes keys/values
-    directly.  `req` holds the per-request (slot, context, query) triples the
-    kernels consume and `attn` the split-K partials of attend().
+class Phase(enum.Enum):
+    """Where the store stands in a verification round."""
+    IDLE = 'idle'                # no transaction: requests, prefixes and buckets may change
+    OPEN = 'open'                # transaction begun; layers staged eagerly one by one
+    PREPARED = 'prepared'        # a registered external writer holds the scratch, not yet submitted
+    SUBMITTED = 'submitted'      # the external write is in flight on the device
+    PUBLISHED = 'published'      # its completion was observed: every layer is staged
+    POISONED = 'poisoned'        # a device write may have been lost: every call fails, for good
+
+
+# (phase, event) -> next phase.  An event absent from a phase's row is refused
+# with that event's error below; POISONED has no row.
+_TRANSITIONS = {
+    Phase.IDLE: {'admin': Phase.IDLE, 'begin': Phase.OPEN},
+    Phase.OPEN: {'stage': Phase.OPEN, 'prepare_external': Phase.PREPARED, 'commit': Phase.IDLE,
+                 'abort': Phase.IDLE},
+    Phase.PREPARED: {'submit_external': Phase.SUBMITTED, 'abort': Phase.IDLE},
+    Phase.SUBMITTED: {'complete_external': Phase.PUBLISHED, 'abort': Phase.IDLE},
+    Phase.PUBLISHED: {'commit': Phase.IDLE, 'abort': Phase.IDLE},
+}
+
+# The error class and message of each refused event: the messages and classes
+# callers of persistent_target_kv.py observe.
+_REFUSALS = {
+    'admin': (RuntimeError, 'Outstanding verification transaction'),
+    'begin': (RuntimeError, 'Outstanding verification transaction'),
+    'stage': (ValueError, 'Cannot mix eager and registered external scratch writes'),
+    'prepare_external': (ValueError, 'Fresh transaction and exact registered external writer required'),
+    'submit_external': (ValueError, 'External write must be submitted exactly once'),
+    'complete_external': (ValueError, 'Submitted, unpublished external write required'),
+    'commit': (ValueError, 'Complete layer scratch and one prefix count per active handle required'),
+    'abort': (ValueError, 'Stale, copied or foreign transaction'),
+}
+
+_POISONED = 'Store invalidated by copy failure; construct a new store'
+
+
+@dataclass
+class _Tenant:
+    handle: Slot
+    length: int = 0
+
+
+class _SlotLedger:
+    """Which request owns each resident slot, under which incarnation, and
+    how many committed rows it holds.
+
+    Vacant slots sit in a min-heap, so admission reuses the lowest free slot.
+    A slot's incarnation counter survives its tenants, so a handle of an
+    earlier tenant never matches again.  `generation` changes with every
+    change of tenancy or length: a transaction records it at begin and is
+    valid only while it is unchanged.
     """
-    _COUNTS = {'cu_query': 'r1', 'cu_key': 'r1', 'positions': 'q', 'req': 'r3', 'work': 'full', 'attn': 'full'}
 
-    def __init__(self, bucket, heads, dim, dtype, device, chunk, split, arena=None):
-        self.bucket = bucket
-        n, r, q = bucket.key_capacity, bucket.request_count, bucket.query_tokens
-        if arena is not None:
-            for name, value in vars(arena).items():
-                if isinstance(value, torch.Tensor):
-                    kind = self._COUNTS.get(name)
-                    if kind == 'full':
-                        setattr(self, name, value)
-                    elif kind == 'r1':
-                        setattr(self, name, value[:r + 1])
-                    elif kind == 'q':
-                        setattr(self, name, value[:q])
-                    elif kind == 'r3':
-                        setattr(self, name, value[:3 * r])
-                    else:
-                        setattr(self, name, value[:n])
-            return
-        self.committed_indices = torch.zeros(n, dtype=torch.long, device=device)
-        self.scratch_indices = torch.zeros_like(self.committed_indices)
-        self.from_scratch = torch.zeros((n, 1, 1), dtype=torch.bool, device=device)
-        self.valid = torch.zeros((n, 1, 1), dtype=torch.bool, device=device)
-        self.cu_query = torch.zeros(r + 1, dtype=torch.int32, device=device)
-        self.cu_key = torch.zeros_like(self.cu_query)
-        self.positions = torch.zeros(q, dtype=torch.long, device=device)
-        self.req = torch.zeros(3 * r, dtype=torch.int32, device=device)
-        self.work = torch.zeros(_work_ints(bucket, device, chunk, split), dtype=torch.int32, device=device)
-        self.keys = torch.empty((n, heads, dim), dtype=dtype, device=device)
-        self.values = torch.empty_like(self.keys)
-        self.attn = torch.zeros(_attn_workspace_bytes(bucket, chunk, device, split), dtype=torch.uint8, device=device)
+    def __init__(self, slots):
+        self.tenants = [None] * slots
+        self.incarnations = [0] * slots
+        self.vacant = list(range(slots))
+        self.by_request = {}
+        self.generation = 0
 
-    def pointers(self):
-        return {k: v.data_ptr() for k, v in vars(self).items() if isinstance(v, torch.Tensor) and v.is_cuda}
+    def admit(self, request):
+        if not isinstance(request, str) or not request or request in self.by_request:
+            raise ValueError('New nonempty request identity required')
+        if not self.vacant:
+            raise ValueError('Resident slot capacity exhausted')
+        i = heapq.heappop(self.vacant)
+        self.incarnations[i] += 1
+        handle = Slot(request, i, self.incarnations[i])
+        self.tenants[i] = _Tenant(handle)
+        self.by_request[request] = i
+        self.generation += 1
+        return handle
 
-    def signature(self):
-        return (id(self), tuple((k, v.data_ptr(), tuple(v.shape), tuple(v.stride()), v.storage_offset(), v.dtype, v.device)
-                                for k, v in vars(self).items() if isinstance(v, torch.Tensor) and v.is_cuda))
+    def release(self, i):
+        # The slot's old rows stay allocated; no later handle can address them.
+        del self.by_request[self.tenants[i].handle.request]
+        self.tenants[i] = None
+        heapq.heappush(self.vacant, i)
+        self.generation += 1
 
+    def locate(self, handle):
+        """Slot index of a live handle (the very object admit returned)."""
+        i = handle.index if isinstance(handle, Slot) else None
+        if type(i) is int and 0 <= i < len(self.tenants) and self.tenants[i] is not None \
+                and self.tenants[i].handle is handle:
+            return i
+        raise ValueError('Stale or foreign request incarnation')
 
-def _max_runs(bucket, device):
-    """Most balanced-list runs any transaction of the bucket uses (its key
-    capacity bounds the keys of every transaction)."""
-    return run_count(bucket.key_capacity, cu_count(device), (bucket.maximum_query_length + 7) // 8)
+    def length(self, i):
+        return self.tenants[i].length
 
+    def set_lengths(self, updates):
+        for i, n in updates:
+            self.tenants[i].length = n
+        self.generation += 1
 
-def _max_segments(bucket, device, chunk, split):
-    g, r = _max_runs(bucket, device), bucket.request_count
-    return varlen_list_bound(r, g, bucket.key_capacity, None if split == 'balanced' else chunk)
+    def occupied(self):
+        return len(self.by_request)
 
-
-def _work_ints(bucket, device, chunk, split):
-    """int32 length of the largest work list of the bucket."""
-    g, r = _max_runs(bucket, device), bucket.request_count
-    return WORK_INTS * _max_segments(bucket, device, chunk, split) + g + 1 + REQ_INTS * r
+    def resident_rows(self):
+        return sum(t.length for t in self.tenants if t is not None)
 
 
-def _attn_workspace_bytes(bucket, chunk, device, split):
-    """Split-K partials for the largest work list of the bucket (one slot
-    per segment at most)."""
-    tiles = (bucket.maximum_query_length + 7) // 8
-    segments = _max_segments(bucket, device, chunk, split)
-    return max(16, int(_native.load().dspark_attn_workspace_bytes(segments, 0, tiles, chunk)))
+@dataclass
+class _Registration:
+    writer: ExternalWriter
+    completion_check: object
 
 
 class PersistentTargetKV:
-    """Single-owner transaction store with stable resident and bucket addresses.
+    """Single-owner transaction store with stable resident and bucket addresses
+    (the contract of persistent_target_kv.py:163-530).
 
-    KV layout: [layers, resident slots, context capacity, KV heads, head dim].
-    Scratch: [layers, maximum query tokens, KV heads, head dim].  Semantics
-    of persistent_target_kv.py:163-530: handles bind slot and incarnation,
-    one outstanding transaction, commit copies only the accepted prefix,
-    a failed copy poisons the store.
+    KV: [layers, resident slots, context capacity, KV heads, head dim];
+    scratch: [layers, maximum query tokens, KV heads, head dim].  A handle
+    binds a slot and its incarnation; one transaction is open at a time and
+    nothing about requests or buckets changes meanwhile; commit copies only
+    the accepted prefix of each request's staged rows; a failed device write
+    poisons the store.
+
+    The host state is a Phase with a transition table, a slot ledger and the
+    open transaction; every device buffer and launch belongs to `kv_device`
+    (a HipKVDevice unless one is injected), whose shape is documented in
+    kv_device.py.
     """
 
     def __init__(self, *, layers, slots, context_capacity, max_query_tokens,
-                 heads, dim, dtype=torch.bfloat16, device='cuda', chunk=DEFAULT_CHUNK, split='balanced'):
+                 heads, dim, dtype=torch.bfloat16, device='cuda', chunk=DEFAULT_CHUNK, split='balanced',
+                 kv_device=None):
         dims = (layers, slots, context_capacity, max_query_tokens, heads, dim)
         if any(type(n) is not int or n < 1 for n in dims):
             raise ValueError('All capacities and dimensions must be positive integers')
         if not dtype.is_floating_point:
             raise ValueError('Floating point KV dtype required')
-        elem = torch.empty((), dtype=dtype).element_size()
-        if (dim * elem) % 16:
-            raise ValueError('A KV head row (dim * element size) must be a multiple of 16 bytes')
-        self.device = require_gfx950(device)
-        _native.load()
-        self.layers, self.slot_capacity, self.context_capacity = layers, slots, context_capacity
-        self.max_query_tokens, self.heads, self.dim = max_query_tokens, heads, dim
-        self.dtype = dtype
         if split not in SPLITS:
             raise ValueError(f'split must be one of {SPLITS}')
-        self.chunk = int(chunk)
-        self.split = split
-        self._elem = elem
-        # Head-major storage; the public tensors are reference-shaped views.
-        self._keys = torch.zeros((layers, slots, heads, context_capacity, dim), dtype=dtype, device=self.device)
-        self._values = torch.zeros_like(self._keys)
-        self.keys = self._keys.permute(0, 1, 3, 2, 4)
-        self.values = self._values.permute(0, 1, 3, 2, 4)
-        self.scratch_keys = torch.zeros((layers, max_query_tokens, heads, dim), dtype=dtype, device=self.device)
-        self.scratch_values = torch.zeros_like(self.scratch_keys)
-        self._owners = [None] * slots
-        self._handles = [None] * slots
-        self._incarnations = [0] * slots
-        self._lengths = [0] * slots
-        self._workspaces = {}
-        self._family_arena = None
+        if kv_device is None:
+            kv_device = HipKVDevice(layers=layers, slots=slots, context_capacity=context_capacity,
+                                    max_query_tokens=max_query_tokens, heads=heads, dim=dim, dtype=dtype,
+                                    device=device, chunk=int(chunk), split=split)
+        self.kv_device = kv_device
+        self.device = kv_device.device
+        self.layers, self.slot_capacity, self.context_capacity = layers, slots, context_capacity
+        self.max_query_tokens, self.heads, self.dim, self.dtype = max_query_tokens, heads, dim, dtype
+        self.chunk, self.split = int(chunk), split
+        self.keys, self.values = kv_device.keys, kv_device.values
+        self.scratch_keys, self.scratch_values = kv_device.scratch_keys, kv_device.scratch_values
+        self._phase = Phase.IDLE
+        self._ledger = _SlotLedger(slots)
+        self._workspaces = {}            # bucket or family -> Workspace
+        self._arena = None               # (shape, Workspace) of the one family declaration
         self._families = ()
-        self._sequence = 0
-        self._pending = None
+        self._registrations = {}         # id(writer) -> _Registration
+        self._transactions = 0
+        self._receipts = 0
+        # the open transaction: Transaction, its ledger generation, staged layers, rows
+        self._tx = None
+        self._tx_generation = None
         self._staged = set()
-        self._writers = {}
-        self._external = None
-        self._submission_generation = 0
-        # Committed-state generation: bumped by every mutation of slots or
-        # lengths; a transaction is valid only while it is unchanged, which
-        # replaces a per-call scan over the transaction's handles.
-        self._mutations = 0
-        self._tx_mutations = None
-        self._tx_shape = None
-        # Per-layer device addresses (the allocations never move).
-        lk, ls = self._keys[0].numel() * elem, self.scratch_keys[0].numel() * elem
-        self._layer_ptrs = tuple((self._keys.data_ptr() + l * lk, self._values.data_ptr() + l * lk,
-                                  self.scratch_keys.data_ptr() + l * ls, self.scratch_values.data_ptr() + l * ls)
-                                 for l in range(layers))
-        self.failed = False
+        self._tx_rows = 0
+        self._receipt = None             # (ExternalWrite, completion event) while one is live
 
-    def _geometry(self):
-        """Resident byte strides: (layer, slot, head, token) and piece bytes."""
-        e, H, C, D = self._elem, self.heads, self.context_capacity, self.dim
-        return (self.slot_capacity * H * C * D * e, H * C * D * e, C * D * e, D * e, D * e)
+    # -- phase ------------------------------------------------------------
+    @property
+    def phase(self):
+        return self._phase
 
-    # -- state guards ------------------------------------------------------
-    def _healthy(self):
+    @property
+    def failed(self):
+        return self._phase is Phase.POISONED
+
+    @property
+    def open_transaction(self):
+        """The transaction in flight (kept after poisoning), else None."""
+        return self._tx
+
+    def staged_layers(self):
+        return len(self._staged)
+
+    def _permit(self, event):
+        """The phase `event` leads to, or raise the event's refusal."""
+        if self._phase is Phase.POISONED:
+            raise RuntimeError(_POISONED)
+        nxt = _TRANSITIONS[self._phase].get(event)
+        if nxt is None:
+            cls, message = _REFUSALS[event]
+            raise cls(message)
+        return nxt
+
+    def _poison(self):
+        self._phase = Phase.POISONED
+
+    def invalidate(self):
+        """Fail closed after uncertain external or device writes; buffers are never reused."""
+        self._poison()
+
+    def _close(self):
+        self._phase = Phase.IDLE
+        self._tx, self._tx_generation, self._staged, self._receipt = None, None, set(), None
+
+    def _index(self, handle):
         if self.failed:
-            raise RuntimeError('Store invalidated by copy failure; construct a new store')
+            raise RuntimeError(_POISONED)
+        return self._ledger.locate(handle)
 
-    def _idle(self):
-        self._healthy()
-        if self._pending is not None:
-            raise RuntimeError('Outstanding verification transaction')
+    def _of(self, tx):
+        """Workspace of the open transaction `tx`, after checking that it is
+        the open one and that the committed state it was built on holds."""
+        if self.failed:
+            raise RuntimeError(_POISONED)
+        if tx is not self._tx:
+            raise ValueError('Stale, copied or foreign transaction')
+        if self._ledger.generation != self._tx_generation:
+            raise RuntimeError('Committed state changed during verification')
+        return self._workspaces[tx.bucket]
 
-    def _slot(self, handle):
-        self._healthy()
-        if (not isinstance(handle, Slot) or not 0 <= handle.index < self.slot_capacity
-                or self._handles[handle.index] is not handle
-                or self._owners[handle.index] != handle.request
-                or self._incarnations[handle.index] != handle.incarnation):
-            raise ValueError('Stale or foreign request incarnation')
-        return handle.index
-
-    # -- request lifecycle ---------------------------------------------------
-    def add_request(self, request):
-        self._idle()
-        if not isinstance(request, str) or not request or request in self._owners:
-            raise ValueError('New nonempty request identity required')
-        if None not in self._owners:
-            raise ValueError('Resident slot capacity exhausted')
-        i = self._owners.index(None)
-        self._incarnations[i] += 1
-        self._owners[i], self._lengths[i] = request, 0
-        handle = Slot(request, i, self._incarnations[i])
-        self._handles[i] = handle
-        self._mutations += 1
-        return handle
-
-    def remove_request(self, handle):
-        self._idle()
-        i = self._slot(handle)
-        self._owners[i], self._lengths[i], self._handles[i] = None, 0, None
-        self._mutations += 1
-
-    def length(self, handle):
-        return self._lengths[self._slot(handle)]
-
-    def _kv(self, keys, values, shape):
+    def _check_kv(self, keys, values, shape):
         for x in (keys, values):
             if (not isinstance(x, torch.Tensor) or tuple(x.shape) != shape
                     or x.device != self.device or x.dtype != self.dtype or x.requires_grad):
                 raise ValueError('KV shape, device, dtype and no-autograd contract required')
 
+    def _check_fused_storage(self, what):
+        if (self.heads, self.dim, self.dtype) != (KV_HEADS, HEAD_DIM, torch.bfloat16):
+            raise ValueError(f'{what} requires bf16 Hkv8/D128 storage')
+
+    def _stage_target(self, layer):
+        """Phase after staging `layer` eagerly: refuses external-writer
+        rounds and a layer outside the model or already staged."""
+        nxt = self._permit('stage')
+        if type(layer) is not int or not 0 <= layer < self.layers or layer in self._staged:
+            raise ValueError('Each model layer must stage exactly once')
+        return nxt
+
+    # -- requests --------------------------------------------------------------
+    def add_request(self, request):
+        self._permit('admin')
+        return self._ledger.admit(request)
+
+    def remove_request(self, handle):
+        self._permit('admin')
+        self._ledger.release(self._index(handle))
+
+    def length(self, handle):
+        return self._ledger.length(self._index(handle))
+
     @torch.no_grad()
     def load_prefix(self, handle, keys, values):
-        """Bootstrap exact real-model KV into an empty resident slot."""
-        self._idle()
-        i = self._slot(handle)
-        if self._lengths[i] or not isinstance(keys, torch.Tensor) or keys.ndim != 4:
+        """Bootstrap exact model KV [layers, n, heads, dim] into an empty slot."""
+        self._permit('admin')
+        i = self._index(handle)
+        if self._ledger.length(i) or not isinstance(keys, torch.Tensor) or keys.ndim != 4:
             raise ValueError('Prefix bootstrap requires empty slot and [L,C,H,D] KV')
         n = keys.shape[1]
         if not 0 <= n <= self.context_capacity:
             raise ValueError('Prefix exceeds resident context capacity')
-        self._kv(keys, values, (self.layers, n, self.heads, self.dim))
+        self._check_kv(keys, values, (self.layers, n, self.heads, self.dim))
         try:
-            self.keys[:, i, :n].copy_(keys)
-            self.values[:, i, :n].copy_(values)
-            self._lengths[i] = n
-            self._mutations += 1
+            self.kv_device.write_prefix(i, keys, values)
         except Exception:
-            self.failed = True
+            self._poison()
             raise
+        self._ledger.set_lengths(((i, n),))
 
-    # -- buckets and families -------------------------------------------------
+    def request_kv(self, handle):
+        i = self._index(handle)
+        return self.kv_device.copy_out(i, self._ledger.length(i))
+
+    # -- buckets and families ------------------------------------------------------
+    def is_registered(self, bucket):
+        return bucket in self._workspaces
+
+    def workspace(self, bucket):
+        """Device buffers of a registered bucket or family."""
+        return self._workspaces[bucket]
+
     def register_bucket(self, bucket):
-        self._idle()
+        self._permit('admin')
         if isinstance(bucket, QueryFamily):
             if bucket not in self._workspaces:
                 raise ValueError('Family must belong to the explicitly registered shared arena')
             return
-        if (not isinstance(bucket, Bucket) or len(bucket.query_lengths) > self.slot_capacity
+        if (not isinstance(bucket, Bucket) or bucket.request_count > self.slot_capacity
                 or bucket.query_tokens > self.max_query_tokens
-                or any(c + q > self.context_capacity for c, q in zip(bucket.context_ceilings, bucket.query_lengths))):
+                or bucket.maximum_key_length > self.context_capacity):
             raise ValueError('Bucket exceeds resident/query capacity')
-        if bucket.request_count > 4096:
-            raise ValueError('At most 4096 requests per bucket')
+        if bucket.request_count > MAX_BUCKET_REQUESTS:
+            raise ValueError(f'At most {MAX_BUCKET_REQUESTS} requests per bucket')
         if bucket not in self._workspaces:
-            self._workspaces[bucket] = _Workspace(bucket, self.heads, self.dim, self.dtype, self.device, self.chunk,
-                                                  self.split)
+            self._workspaces[bucket] = self.kv_device.workspace(bucket)
 
     def workspace_bytes(self, bucket):
         """Exact device allocation of a bucket workspace before registering it."""
-        n, r, q = bucket.key_capacity, bucket.request_count, bucket.query_tokens
-        kv = 2 * n * self.heads * self.dim * self.keys.element_size()
-        return (kv + 18 * n + 8 * (r + 1) + 8 * q + 12 * r + 4 * _work_ints(bucket, self.device, self.chunk, self.split)
-                + _attn_workspace_bytes(bucket, self.chunk, self.device, self.split))
+        return self.kv_device.workspace_bytes(bucket)
 
     def family_arena_shape(self, families):
-        """Validate the complete finite declaration before allocating any storage."""
-        from types import SimpleNamespace
-        if (not isinstance(families, tuple) or not families
-                or any(not isinstance(f, QueryFamily) for f in families)
-                or len(set(families)) != len(families)
-                or any(f.request_count > self.slot_capacity or f.query_tokens > self.max_query_tokens
-                       or f.maximum_key_length > self.context_capacity for f in families)):
+        """Validate a complete family declaration before allocating anything;
+        returns the shape of the one arena all of them share."""
+        valid = (isinstance(families, tuple) and families
+                 and all(isinstance(f, QueryFamily) for f in families)
+                 and len(set(families)) == len(families))
+        if not valid or any(f.request_count > self.slot_capacity or f.query_tokens > self.max_query_tokens
+                            or f.maximum_key_length > self.context_capacity for f in families):
             raise ValueError('Distinct finite families within resident/query capacity required')
-        return SimpleNamespace(request_count=max(f.request_count for f in families),
-                               query_tokens=max(f.query_tokens for f in families),
-                               key_capacity=max(f.key_capacity for f in families),
-                               maximum_query_length=max(f.maximum_query_length for f in families))
+        fields = ('request_count', 'query_tokens', 'key_capacity', 'maximum_query_length')
+        return SimpleNamespace(**{name: max(getattr(f, name) for f in families) for name in fields})
 
     def register_families(self, families):
-        """One immutable declaration and one shared workspace; no resize or lazy family."""
-        self._idle()
-        if self._family_arena is not None:
+        """One immutable family declaration sharing one workspace; no resize."""
+        self._permit('admin')
+        if self._arena is not None:
             raise ValueError('Shared family arena already registered; no dynamic extension')
         shape = self.family_arena_shape(families)
-        if shape.request_count > 4096:
-            raise ValueError('At most 4096 requests per bucket')
-        arena = _Workspace(shape, self.heads, self.dim, self.dtype, self.device, self.chunk, self.split)
-        views = {f: _Workspace(f, self.heads, self.dim, self.dtype, self.device, self.chunk, self.split, arena)
-                 for f in families}
-        self._family_arena = arena
+        if shape.request_count > MAX_BUCKET_REQUESTS:
+            raise ValueError(f'At most {MAX_BUCKET_REQUESTS} requests per bucket')
+        arena = self.kv_device.workspace(shape)
+        self._arena = (shape, arena)
         self._families = families
-        self._workspaces.update(views)
+        self._workspaces.update((f, arena.view(f)) for f in families)
 
     # -- registered external scratch writers (persistent_target_kv.py:309-362) --
+    def _scratch_pointers(self):
+        return self.scratch_keys.data_ptr(), self.scratch_values.data_ptr()
+
     def register_external_writer(self, bucket, layers, completion_check):
-        self._idle()
+        self._permit('admin')
         if bucket not in self._workspaces or tuple(layers) != tuple(range(self.layers)) or not callable(completion_check):
             raise ValueError('Registered bucket, complete ordered layer signature and completion checker required')
-        writer = ExternalWriter(bucket, tuple(layers),
-                                (self.scratch_keys.data_ptr(), self.scratch_values.data_ptr()),
+        writer = ExternalWriter(bucket, tuple(layers), self._scratch_pointers(),
                                 self._workspaces[bucket].signature())
-        self._writers[id(writer)] = (writer, completion_check)
+        self._registrations[id(writer)] = _Registration(writer, completion_check)
         return writer
 
     def prepare_external_write(self, tx, writer):
-        self._transaction(tx)
-        registered = self._writers.get(id(writer))
-        if (registered is None or registered[0] is not writer or writer.bucket != tx.bucket
-                or self._staged or self._external is not None):
-            raise ValueError('Fresh transaction and exact registered external writer required')
-        self._submission_generation += 1
-        receipt = ExternalWrite(writer, tx, self._submission_generation)
-        self._external = dict(receipt=receipt, state='prepared', event=None)
+        self._of(tx)
+        entry = self._registrations.get(id(writer))
+        if entry is None or entry.writer is not writer or writer.bucket != tx.bucket or self._staged:
+            raise ValueError(_REFUSALS['prepare_external'][1])
+        self._phase = self._permit('prepare_external')
+        self._receipts += 1
+        receipt = ExternalWrite(writer, tx, self._receipts)
+        self._receipt = (receipt, None)
         return receipt
 
-    def _external_write(self, receipt):
-        if self._external is None or self._external['receipt'] is not receipt:
+    def _live_receipt(self, receipt):
+        """Check that `receipt` is the live one, its transaction is open and
+        the buffers its writer captured are still the store's."""
+        if self._receipt is None or self._receipt[0] is not receipt:
             raise ValueError('Stale, copied or foreign external write receipt')
-        self._transaction(receipt.transaction)
-        if receipt.writer.scratch_pointers != (self.scratch_keys.data_ptr(), self.scratch_values.data_ptr()):
-            self.failed = True
+        self._of(receipt.transaction)
+        if receipt.writer.scratch_pointers != self._scratch_pointers():
+            self._poison()
             raise RuntimeError('Registered scratch allocation changed')
         if receipt.writer.workspace_signature != self._workspaces[receipt.transaction.bucket].signature():
-            self.failed = True
+            self._poison()
             raise RuntimeError('Registered workspace view/layout changed')
-        return self._external
 
     def submit_external_write(self, receipt, event):
-        state = self._external_write(receipt)
-        if state['state'] != 'prepared':
-            raise ValueError('External write must be submitted exactly once')
-        state.update(state='submitted', event=event)
+        self._live_receipt(receipt)
+        self._phase = self._permit('submit_external')
+        self._receipt = (receipt, event)
 
-    def complete_external_write(self, receipt):
-        state = self._external_write(receipt)
-        if state['state'] != 'submitted':
-            raise ValueError('Submitted, unpublished external write required')
-        checker = self._writers[id(receipt.writer)][1]
-        if not self._check_external_completion(checker, state['event'], receipt):
-            raise RuntimeError('External write completion has not been observed')
-        self._staged = set(receipt.writer.layers)
-        state['state'] = 'completed'
-
-    def _check_external_completion(self, checker, event, receipt):
+    def _observed(self):
+        """Ask the live receipt's writer whether its write finished; a
+        checker that raises poisons the store."""
+        receipt, event = self._receipt
         try:
-            return bool(checker(event, receipt))
+            return bool(self._registrations[id(receipt.writer)].completion_check(event, receipt))
         except BaseException:
-            self.failed = True
+            self._poison()
             raise
 
-    def invalidate(self):
-        """Fail closed after uncertain external/device writes; never reuse buffers."""
-        self.failed = True
+    def complete_external_write(self, receipt):
+        self._live_receipt(receipt)
+        nxt = self._permit('complete_external')
+        if not self._observed():
+            raise RuntimeError('External write completion has not been observed')
+        self._staged = set(receipt.writer.layers)
+        self._phase = nxt
 
-    # -- transactions ---------------------------------------------------------
+    # -- transactions ------------------------------------------------------------
     @torch.no_grad()
     def begin(self, handles, bucket, *, query_lengths=None):
-        """Validate on the host, then build all seven metadata arrays with one
-        small pinned upload and one dspark_txn_metadata launch.  No
-        transaction is published unless both succeed."""
-        self._idle()
+        """Validate on the host, then build the seven metadata arrays on the
+        device (one small upload, one dspark_txn_metadata launch).  Nothing
+        is published unless both succeed; a failed begin may be retried and
+        never revives an earlier transaction."""
+        nxt = self._permit('begin')
         handles = tuple(handles)
         if bucket not in self._workspaces or len(handles) != bucket.request_count:
             raise ValueError('Registered exact-query bucket required')
@@ -477,61 +537,28 @@ class PersistentTargetKV:
                 raise ValueError('Family requires actual ordered query lengths')
             query_lengths = bucket.query_lengths
         query_lengths = tuple(query_lengths)
-        indices = [self._slot(h) for h in handles]
-        if len(set(indices)) != len(indices):
+        slots = [self._index(h) for h in handles]
+        if len(set(slots)) != len(slots):
             raise ValueError('Active request slots must be unique')
-        contexts = tuple(self._lengths[i] for i in indices)
+        contexts = tuple(self._ledger.length(i) for i in slots)
         if not bucket.accepts(query_lengths, contexts):
             raise ValueError('Actual context exceeds declared bucket applicability')
         if sum(contexts) + sum(query_lengths) >= 2 ** 31:
             raise ValueError('Varlen cumulative lengths exceed int32')
-        ws = self._workspaces[bucket]
-        r = len(handles)
-        key_lengths = [c + q for c, q in zip(contexts, query_lengths)]
-        runs = run_count(sum(key_lengths), cu_count(self.device), (bucket.maximum_query_length + 7) // 8)
-        # fixed-capacity list: the same launch for every transaction of the bucket
-        capacity = (_max_segments(bucket, self.device, self.chunk, self.split), _max_runs(bucket, self.device))
-        records, n_items, runs = segment_plan(self.split, query_lengths, key_lengths, indices, runs, self.chunk,
-                                              capacity)
-        if len(records) > ws.work.numel():
-            raise ValueError('Work list exceeds the bucket workspace')
-        upload(self.device, list(indices) + list(contexts) + list(query_lengths), out=ws.req[:3 * r])
-        upload(self.device, records, out=ws.work[:len(records)])
-        _native.call('dspark_txn_metadata', _native.ptr(ws.req), r, self.context_capacity,
-                     bucket.key_capacity, bucket.query_tokens,
-                     _native.ptr(ws.committed_indices), _native.ptr(ws.scratch_indices),
-                     _native.ptr(ws.from_scratch), _native.ptr(ws.valid), _native.ptr(ws.positions),
-                     _native.ptr(ws.cu_query), _native.ptr(ws.cu_key), _native.stream_handle(self.device))
-        self._sequence += 1
-        tx = Transaction(self._sequence, handles, contexts, bucket, query_lengths)
-        self._pending, self._staged = tx, set()
-        self._tx_mutations = self._mutations
-        # (query tokens, launch maximum query length, bucket key capacity)
-        self._tx_shape = (sum(query_lengths), bucket.maximum_query_length, bucket.key_capacity)
+        self.kv_device.build_metadata(self._workspaces[bucket], bucket, slots, contexts, query_lengths)
+        self._transactions += 1
+        tx = Transaction(self._transactions, handles, contexts, bucket, query_lengths)
+        self._phase, self._tx, self._tx_generation = nxt, tx, self._ledger.generation
+        self._staged, self._tx_rows, self._receipt = set(), sum(query_lengths), None
         return tx
-
-    def _transaction(self, tx):
-        self._healthy()
-        if tx is not self._pending:
-            raise ValueError('Stale, copied or foreign transaction')
-        if self._mutations != self._tx_mutations:
-            raise RuntimeError('Committed state changed during verification')
-        return self._workspaces[tx.bucket]
 
     @torch.no_grad()
     def stage_layer(self, tx, layer, keys, values):
-        """Copy the model's new KV rows of one layer into scratch only."""
-        self._transaction(tx)
-        if self._external is not None:
-            raise ValueError('Cannot mix eager and registered external scratch writes')
-        if type(layer) is not int or not 0 <= layer < self.layers or layer in self._staged:
-            raise ValueError('Each model layer must stage exactly once')
-        q = self._tx_shape[0]
-        self._kv(keys, values, (q, self.heads, self.dim))
-        keys, values = keys.contiguous(), values.contiguous()
-        _, _, sk, sv = self._layer_ptrs[layer]
-        _native.call('dspark_kv_stage', keys.data_ptr(), values.data_ptr(), sk, sv,
-                     q, self.heads * self.dim * self._elem, _native.stream_handle(self.device))
+        """Copy the model's new K/V rows of one layer into scratch only."""
+        self._of(tx)
+        self._stage_target(layer)
+        self._check_kv(keys, values, (self._tx_rows, self.heads, self.dim))
+        self.kv_device.stage(layer, keys, values, self._tx_rows)
         self._staged.add(layer)
 
     @torch.no_grad()
@@ -541,15 +568,10 @@ class PersistentTargetKV:
         hidden states [sum Q, H] and write K/V straight into this layer's
         scratch - stage_layer without the separate copy.  Returns the
         queries [sum Q, 16, 128] for attend()."""
-        ws = self._transaction(tx)
-        if self._external is not None:
-            raise ValueError('Cannot mix eager and registered external scratch writes')
-        if type(layer) is not int or not 0 <= layer < self.layers or layer in self._staged:
-            raise ValueError('Each model layer must stage exactly once')
-        if (self.heads, self.dim, self.dtype) != (KV_HEADS, HEAD_DIM, torch.bfloat16):
-            raise ValueError('The fused prologue requires bf16 Hkv8/D128 storage')
-        q = self._tx_shape[0]
-        if not isinstance(hidden, torch.Tensor) or hidden.ndim != 2 or hidden.shape[0] != q:
+        ws = self._of(tx)
+        self._stage_target(layer)
+        self._check_fused_storage('The fused prologue')
+        if not isinstance(hidden, torch.Tensor) or hidden.ndim != 2 or hidden.shape[0] != self._tx_rows:
             raise ValueError('Hidden states must be [sum Q, hidden] for the transaction')
         queries, _, _ = prologue(hidden, ws.positions, k_out=self.scratch_keys[layer], v_out=self.scratch_values[layer])
         self._staged.add(layer)
@@ -557,21 +579,13 @@ class PersistentTargetKV:
 
     @torch.no_grad()
     def prepare_attention(self, tx, layer):
-        """Materialise the capacity-length K/V (parity mode); attend() is the
-        fused path that never builds it."""
-        ws = self._transaction(tx)
+        """Materialise the capacity-length K/V of one layer (parity mode);
+        attend() is the fused path that never builds it."""
+        ws = self._of(tx)
         if layer not in self._staged:
             raise ValueError('Layer scratch missing')
-        n = tx.bucket.key_capacity
-        _, slot_b, head_b, tok_b, piece_b = self._geometry()
-        _native.call('dspark_kv_gather', _native.ptr(self._keys[layer]), _native.ptr(self._values[layer]),
-                     _native.ptr(self.scratch_keys[layer]), _native.ptr(self.scratch_values[layer]),
-                     _native.ptr(ws.committed_indices), _native.ptr(ws.scratch_indices),
-                     _native.ptr(ws.from_scratch), _native.ptr(ws.valid), n,
-                     self.slot_capacity, slot_b, head_b, tok_b, self.context_capacity, self.heads, piece_b,
-                     self.max_query_tokens, _native.ptr(ws.keys), _native.ptr(ws.values),
-                     _native.stream_handle(self.device))
-        return ws.keys, ws.values, ws.cu_query, ws.cu_key, ws.positions
+        keys, values = self.kv_device.gather(ws, tx.bucket, layer)
+        return keys, values, ws.cu_query, ws.cu_key, ws.positions
 
     @torch.no_grad()
     def attend(self, tx, layer, query, *, scale=SCALE, keys=None, values=None, out=None):
@@ -583,24 +597,20 @@ class PersistentTargetKV:
         staged in the same launch: the kernel reads the new rows from them
         and copies them into scratch, exactly what stage_layer followed by
         attend does, minus one launch and one pass over the new rows.
-        Otherwise the layer must have been staged with stage_layer.  out: an
-        optional output buffer (written and returned)."""
-        self._transaction(tx)
+        Otherwise the layer must have been staged.  out: an optional output
+        buffer (written and returned)."""
+        ws = self._of(tx)
         fused = keys is not None or values is not None
         if fused:
-            if self._external is not None:
-                raise ValueError('Cannot mix eager and registered external scratch writes')
-            if type(layer) is not int or not 0 <= layer < self.layers or layer in self._staged:
-                raise ValueError('Each model layer must stage exactly once')
-            self._kv(keys, values, (self._tx_shape[0], self.heads, self.dim))
+            self._stage_target(layer)
+            self._check_kv(keys, values, (self._tx_rows, self.heads, self.dim))
             keys, values = keys.contiguous(), values.contiguous()
         elif layer not in self._staged:
             raise ValueError('Layer scratch missing')
-        if (self.heads, self.dim, self.dtype) != (KV_HEADS, HEAD_DIM, torch.bfloat16):
-            raise ValueError('Fused attention requires bf16 Hkv8/D128 storage')
-        q = self._tx_shape[0]
+        self._check_fused_storage('Fused attention')
         if (not isinstance(query, torch.Tensor) or query.dtype != torch.bfloat16 or query.device != self.device
-                or query.shape != (q, Q_HEADS, HEAD_DIM) or not query.is_contiguous() or query.requires_grad):
+                or query.shape != (self._tx_rows, Q_HEADS, HEAD_DIM) or not query.is_contiguous()
+                or query.requires_grad):
             raise ValueError('Expected contiguous no-autograd bf16 [Q,16,128] queries on the store device')
         _check_scale(scale, 'Fused verification attention')
         if out is None:
@@ -608,87 +618,53 @@ class PersistentTargetKV:
         elif (not isinstance(out, torch.Tensor) or out.dtype != torch.bfloat16 or out.device != self.device
               or out.shape != query.shape or not out.is_contiguous()):
             raise ValueError('out must be a contiguous bf16 tensor shaped like the queries')
-        self._attention_launch(tx.bucket, layer, query.data_ptr(), out.data_ptr(),
-                               keys.data_ptr() if fused else None, values.data_ptr() if fused else None)
+        self.kv_device.attend(ws, tx.bucket, layer, query.data_ptr(), out.data_ptr(),
+                              keys.data_ptr() if fused else None, values.data_ptr() if fused else None)
         if fused:
             self._staged.add(layer)
         return out
 
-    def _launch_shape(self, bucket):
-        """(record capacity, runs) of the bucket's fixed-capacity work list."""
-        return _max_segments(bucket, self.device, self.chunk, self.split), _max_runs(bucket, self.device)
-
-    def _attention_launch(self, bucket, layer, query, out, keys=None, values=None):
-        """One layer's fused verification attention (staged when keys/values
-        are given) for the bucket's workspace.  Every argument depends only on
-        the bucket, the layer and the given buffers; the transaction's data is
-        read from the workspace at run time, so a captured launch replays for
-        every later transaction of the bucket."""
-        ws = self._workspaces[bucket]
-        C = self.context_capacity
-        k, v, sk, sv = self._layer_ptrs[layer]
-        tail = (ws.cu_query.data_ptr(), ws.cu_key.data_ptr(), ws.req.data_ptr(),
-                bucket.request_count, KV_HEADS * C * HEAD_DIM, HEAD_DIM, C * HEAD_DIM,
-                bucket.key_capacity, bucket.maximum_query_length, SCALE, self.chunk,
-                ws.work.data_ptr(), *self._launch_shape(bucket), out, ws.attn.data_ptr(), ws.attn.numel(),
-                _native.stream_handle(self.device))
-        if keys is not None:
-            _native.call('dspark_verify_attn_staged_fwd', query, k, v, keys, values, sk, sv, *tail)
-        else:
-            _native.call('dspark_verify_attn_fwd', query, k, v, sk, sv, *tail)
+    def launch_attention(self, bucket, layer, query, out, keys=None, values=None):
+        """The fused attention launch of a registered bucket with raw device
+        addresses and no transaction check: what a captured round records
+        once and replays under an external-write receipt."""
+        self.kv_device.attend(self._workspaces[bucket], bucket, layer, query, out, keys, values)
 
     @torch.no_grad()
     def commit(self, tx, committed_query_lengths: Mapping):
         """Commit caller-decided verified prefix lengths (anchor included).
 
-        The whole decision is validated before any resident write; all
-        layers and requests are then copied by one kernel.  A launch failure
-        poisons the store.
+        The whole decision is validated before any resident write; one
+        launch then copies every layer of every request's accepted prefix.
+        A failed launch poisons the store.
         """
-        ws = self._transaction(tx)
-        if set(committed_query_lengths) != set(tx.slots) or len(self._staged) != self.layers:
-            raise ValueError('Complete layer scratch and one prefix count per active handle required')
-        counts = []
-        for h, c, q in zip(tx.slots, tx.context_lengths, tx.query_lengths):
-            n = committed_query_lengths[h]
+        ws = self._of(tx)
+        if (set(committed_query_lengths) != set(tx.slots) or len(self._staged) != self.layers
+                or 'commit' not in _TRANSITIONS[self._phase]):
+            raise ValueError(_REFUSALS['commit'][1])
+        counts = [committed_query_lengths[h] for h in tx.slots]
+        for n, c, q in zip(counts, tx.context_lengths, tx.query_lengths):
             if type(n) is not int or not 0 <= n <= q or c + n > self.context_capacity:
                 raise ValueError('Commit must be a valid verified prefix')
-            counts.append(n)
-        r = len(tx.slots)
         try:
-            if any(counts):
-                acc = upload(self.device, counts)
-                layer_b, slot_b, head_b, tok_b, piece_b = self._geometry()
-                _native.call('dspark_kv_commit', _native.ptr(self._keys), _native.ptr(self._values),
-                             _native.ptr(self.scratch_keys), _native.ptr(self.scratch_values),
-                             _native.ptr(ws.req), _native.ptr(ws.cu_query), _native.ptr(acc),
-                             r, max(tx.query_lengths), self.layers, layer_b, slot_b, head_b, tok_b,
-                             self.context_capacity, self.heads, piece_b, self.max_query_tokens,
-                             _native.stream_handle(self.device))
-            for h, n in zip(tx.slots, counts):
-                self._lengths[h.index] += n
-            self._mutations += 1
+            self.kv_device.commit(ws, counts, max(tx.query_lengths))
         except Exception:
-            self.failed = True
+            self._poison()
             raise
-        self._pending, self._staged, self._external = None, set(), None
+        self._ledger.set_lengths((h.index, c + n) for h, c, n in zip(tx.slots, tx.context_lengths, counts))
+        self._close()
         total = sum(counts)
         return dict(committed_tokens=total,
                     copied_kv_bytes=2 * self.layers * self.heads * self.dim * self.keys.element_size() * total)
 
     def abort(self, tx):
-        self._transaction(tx)
-        if self._external is not None and self._external['state'] == 'submitted':
-            receipt = self._external['receipt']
-            if not self._check_external_completion(self._writers[id(receipt.writer)][1], self._external['event'], receipt):
-                raise RuntimeError('Cannot abort buffers with an unfinished external write')
-        self._pending, self._staged, self._external = None, set(), None
-
-    def request_kv(self, handle):
-        i = self._slot(handle)
-        n = self._lengths[i]
-        return (self.keys[:, i, :n].detach().clone(memory_format=torch.contiguous_format),
-                self.values[:, i, :n].detach().clone(memory_format=torch.contiguous_format))
+        """Drop the open transaction's scratch (an external write in flight
+        must have been observed finished first)."""
+        self._of(tx)
+        self._permit('abort')
+        if self._phase is Phase.SUBMITTED and not self._observed():
+            raise RuntimeError('Cannot abort buffers with an unfinished external write')
+        self._close()
 
     def pointers(self, bucket):
         """Audit stable allocation identities."""
@@ -697,28 +673,30 @@ class PersistentTargetKV:
                     **self._workspaces[bucket].pointers())
 
     def work(self, tx):
-        """Work counters with the keys and formulas of persistent_target_kv.py:511-530,
-        plus the rows the fused attention actually streams."""
-        self._transaction(tx)
-        q = sum(tx.query_lengths)
-        actual_k = sum(tx.context_lengths) + q
-        resident = sum(self._lengths)
-        ws = self._workspaces[tx.bucket]
-        return dict(active_requests=len(tx.slots), resident_requests=sum(x is not None for x in self._owners),
-                    logical_query_tokens=q, physical_query_tokens=q, logical_active_key_tokens=actual_k,
-                    physical_key_capacity=tx.bucket.key_capacity, padded_key_capacity=tx.bucket.key_capacity - actual_k,
-                    inactive_resident_key_tokens=resident - sum(tx.context_lengths),
-                    gather_rows_per_kv_per_layer=2 * tx.bucket.key_capacity,
-                    staging_output_rows_per_layer=tx.bucket.key_capacity,
-                    allowed_causal_pairs=sum(c * n + n * (n + 1) // 2 for c, n in zip(tx.context_lengths, tx.query_lengths)),
-                    query_lengths=list(tx.query_lengths), queried_context_lengths=list(tx.context_lengths),
-                    maximum_query_length=tx.bucket.maximum_query_length, maximum_key_length=tx.bucket.maximum_key_length,
-                    resident_allocated_kv_bytes=2 * self.keys.numel() * self.keys.element_size(),
-                    scratch_allocated_kv_bytes=2 * self.scratch_keys.numel() * self.keys.element_size(),
-                    bucket_workspace_bytes=sum(t.numel() * t.element_size() for t in vars(ws).values()
-                                               if isinstance(t, torch.Tensor) and t.is_cuda),
-                    workspace_is_shared=isinstance(tx.bucket, QueryFamily),
-                    shared_arena_allocated_bytes=(self.workspace_bytes(self._family_arena.bucket)
-                                                  if isinstance(tx.bucket, QueryFamily) else 0),
-                    fused_attention_key_rows_per_layer=actual_k,
-                    bucket_source=tx.bucket.source, capture_or_replay_verified=False)
+        """Work counters of the open transaction: the keys and formulas of
+        persistent_target_kv.py:511-530, plus the rows the fused attention
+        actually streams."""
+        ws = self._of(tx)
+        bucket, contexts, queries = tx.bucket, tx.context_lengths, tx.query_lengths
+        rows, context_rows = sum(queries), sum(contexts)
+        keys = context_rows + rows
+        elem = self.keys.element_size()
+        shared = isinstance(bucket, QueryFamily)
+        counters = dict(
+            active_requests=len(tx.slots), resident_requests=self._ledger.occupied(),
+            logical_query_tokens=rows, physical_query_tokens=rows, logical_active_key_tokens=keys,
+            physical_key_capacity=bucket.key_capacity, padded_key_capacity=bucket.key_capacity - keys,
+            inactive_resident_key_tokens=self._ledger.resident_rows() - context_rows,
+            gather_rows_per_kv_per_layer=2 * bucket.key_capacity,
+            staging_output_rows_per_layer=bucket.key_capacity,
+            allowed_causal_pairs=sum(c * n + n * (n + 1) // 2 for c, n in zip(contexts, queries)),
+            query_lengths=list(queries), queried_context_lengths=list(contexts),
+            maximum_query_length=bucket.maximum_query_length, maximum_key_length=bucket.maximum_key_length,
+            resident_allocated_kv_bytes=2 * self.keys.numel() * elem,
+            scratch_allocated_kv_bytes=2 * self.scratch_keys.numel() * elem,
+            bucket_workspace_bytes=ws.nbytes(),
+            workspace_is_shared=shared,
+            shared_arena_allocated_bytes=self.workspace_bytes(self._arena[0]) if shared else 0)
+        counters.update(fused_attention_key_rows_per_layer=keys, bucket_source=bucket.source,
+                        capture_or_replay_verified=False)
+        return counters

@@ -159,7 +159,7 @@ def test_failed_metadata_launch_never_publishes_transaction(dev, golden):
         raise _native.NativeError(f'{name}: injected metadata failure')
     with patch.object(_native, 'call', side_effect=fail), pytest.raises(_native.NativeError, match='injected'):
         pool.begin([a], bucket)
-    assert pool._pending is None and torch.equal(pool.keys, before)
+    assert pool.open_transaction is None and torch.equal(pool.keys, before)
     with pytest.raises(ValueError):
         pool.abort(old)
     tx = pool.begin([a], bucket)
@@ -216,7 +216,7 @@ def test_query_families_shared_arena(dev):
     for queries in ((0, 6), (2, 3), (1, 6), (True, 5), (1, 1, 4)):
         with pytest.raises(ValueError):
             pool.begin(handles[:2], large, query_lengths=queries)
-        assert pool._pending is None
+        assert pool.open_transaction is None
     with pytest.raises(ValueError):
         pool.begin(handles[:2], large)
     with pytest.raises(ValueError):
@@ -272,7 +272,7 @@ def test_metadata_gather_commit_bit_exact_against_oracle(dev):
         new_v = randn_bf16(gen, L, sum(queries), 8, 128).to(dev)
         for layer in range(L):
             pool.stage_layer(tx, layer, new_k[layer], new_v[layer])
-        ws = pool._workspaces[bucket]
+        ws = pool.workspace(bucket)
         meta = semantics.txn_metadata(active, ctx, queries, C, bucket.key_capacity)
         k, v, cq, ck, pos = pool.prepare_attention(tx, 1)
         assert np.array_equal(ws.committed_indices.cpu().numpy(), meta['committed_indices'])

@@ -48,10 +48,10 @@ def launch_args(store, tx, query, out):
     """The argument list dspark_verify_attn_fwd takes for layer 0, without
     the trailing (workspace, workspace bytes, stream)."""
     from qwen3_dspark_amd import _native
-    ws = store._workspaces[tx.bucket]
-    k, v, sk, sv = store._layer_ptrs[0]
+    ws = store.workspace(tx.bucket)
+    k, v, sk, sv = store.kv_device.layer_pointers[0]
     C, bucket = store.context_capacity, tx.bucket
-    n_work, runs = store._launch_shape(bucket)
+    n_work, runs = store.kv_device.launch_shape(bucket)
     return [query.data_ptr(), k, v, sk, sv, ws.cu_query.data_ptr(), ws.cu_key.data_ptr(), ws.req.data_ptr(),
             bucket.request_count, 8 * C * 128, 128, C * 128, bucket.key_capacity, bucket.maximum_query_length,
             SCALE, store.chunk, ws.work.data_ptr(), n_work, runs, _native.ptr(out)], ws
