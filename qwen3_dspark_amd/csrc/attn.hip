@@ -385,6 +385,12 @@ struct FastOffsets {
   uint32_t v[8];
 };
 
+// K/V rows are read once per call: non-temporal loads.
+__device__ __forceinline__ bf16x8 ld8_nt(const void* p) {
+  typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+  return __builtin_bit_cast(bf16x8, __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(p)));
+}
+
 // A tile below kfast: part A rows at wave-uniform base + per-lane offsets.
 __device__ __forceinline__ void load_fast(const VarlenArgs& a, const SegView& s, const FastOffsets& fo, int kt,
                                           Tile& T) {
@@ -393,9 +399,9 @@ __device__ __forceinline__ void load_fast(const VarlenArgs& a, const SegView& s,
   #pragma unroll
   for (int j = 0; j < 2; ++j)
     #pragma unroll
-    for (int ks = 0; ks < 4; ++ks) T.k[j][ks] = *reinterpret_cast<const bf16x8*>(kb + fo.k[j] + 64 * ks);
+    for (int ks = 0; ks < 4; ++ks) T.k[j][ks] = ld8_nt(kb + fo.k[j] + 64 * ks);
   #pragma unroll
-  for (int i2 = 0; i2 < 8; ++i2) T.v[i2] = *reinterpret_cast<const bf16x8*>(vb + fo.v[i2]);
+  for (int i2 = 0; i2 < 8; ++i2) T.v[i2] = ld8_nt(vb + fo.v[i2]);
 }
 
 // Any tile: rows clamped, each from part A or B.
@@ -413,10 +419,10 @@ __device__ __forceinline__ void load_slow(const VarlenArgs& a, const SegView& s,
   for (int j = 0; j < 2; ++j) {
     const bf16* p = row(s.kA, s.kB, kt + 8 * (col >> 2) + 4 * j + (col & 3)) + 8 * grp;
     #pragma unroll
-    for (int ks = 0; ks < 4; ++ks) T.k[j][ks] = ld8(p + 32 * ks);
+    for (int ks = 0; ks < 4; ++ks) T.k[j][ks] = ld8_nt(p + 32 * ks);
   }
   #pragma unroll
-  for (int i2 = 0; i2 < 8; ++i2) T.v[i2] = ld8(row(s.vA, s.vB, kt + 4 * i2 + grp) + 8 * col);
+  for (int i2 = 0; i2 < 8; ++i2) T.v[i2] = ld8_nt(row(s.vA, s.vB, kt + 4 * i2 + grp) + 8 * col);
 }
 
 // Q of this lane's row of segment s.
