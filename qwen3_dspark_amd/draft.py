@@ -31,6 +31,33 @@ MAX_BLOCKS = 8
 _QK_DTYPES = (torch.bfloat16, torch.float32)
 
 
+def draft_work_counters(context_lengths, anchors, *, layers=1, physical_context_rows=None, block_size=BLOCK_SIZE,
+                        key_element_bytes=2, value_element_bytes=2):
+    """Work counters of a packed draft backbone's attention, with the keys
+    of packed_draft.py:245-249, for the fused multi-block path.
+
+    Rows and pair domain follow the reference's layout (a request's keys are
+    its context up to its largest anchor plus its blocks' rows; each block
+    pairs its rows with anchor + block_size keys).  The reference's
+    concatenation, gather and cast copies do not exist on this path (the
+    kernel reads the pool in place and rounds K to bf16 in registers), so
+    their counters are 0; kv_bytes_read_per_layer is what the kernel reads.
+    """
+    blocks = sum(len(b) for b in anchors)
+    streamed = sum(max(b) for b in anchors)
+    gathered = streamed + block_size * blocks
+    row_bytes = KV_HEADS * HEAD_DIM * (key_element_bytes + value_element_bytes)
+    return dict(
+        requests=len(anchors), query_rows=block_size * blocks, gathered_key_rows=gathered,
+        physical_context_rows=sum(context_lengths) if physical_context_rows is None else physical_context_rows,
+        attention_pair_domain=sum(block_size * (a + block_size) for b in anchors for a in b),
+        attention_calls=layers,
+        context_block_concatenation_kv_elements=0, context_block_concatenation_kv_bytes=0,
+        gathered_kv_elements=0, gathered_kv_bytes=0, attention_cast_elements=0, attention_cast_output_bytes=0,
+        draft_blocks=blocks, context_rows_read_per_layer=streamed, kv_bytes_read_per_layer=gathered * row_bytes,
+        scope='Work counts only; context rows read in place once per request for all of its blocks')
+
+
 class DraftBatch:
     """Host-validated per-round draft metadata, uploaded once and reused by
     every draft layer.
@@ -82,6 +109,13 @@ class DraftBatch:
         self._offsets = {}
         self._work = {}
         self._index_max = None
+        self.physical_context_rows = self.context_rows
+
+    def counters(self, layers=1, *, key_element_bytes=2, value_element_bytes=2):
+        """draft_work_counters of this batch over `layers` attention calls."""
+        return draft_work_counters(self.context_lengths, self.anchors, layers=layers,
+                                   physical_context_rows=self.physical_context_rows,
+                                   key_element_bytes=key_element_bytes, value_element_bytes=value_element_bytes)
 
     def device_offsets(self, capacity):
         """int64 per-request first kernel row: offsets as given, or - for a
@@ -452,8 +486,16 @@ class DraftKVPool:
         names = list(anchors)
         for r in names:
             self._request(r)
-        return DraftBatch(self.device, [self._slots[r] * self.capacity for r in names],
-                          [self._lengths[r] for r in names], [list(anchors[r]) for r in names])
+        batch = DraftBatch(self.device, [self._slots[r] * self.capacity for r in names],
+                           [self._lengths[r] for r in names], [list(anchors[r]) for r in names])
+        batch.physical_context_rows = sum(self._lengths.values())
+        return batch
+
+    def counters(self, batch):
+        """draft_work_counters of a batch over every pool layer, with this
+        pool's element sizes."""
+        return batch.counters(self.layers, key_element_bytes=self.keys.element_size(),
+                              value_element_bytes=self.values.element_size())
 
     def attention(self, layer, query, block_keys, block_values, batch, *, scale=SCALE):
         """Multi-block draft attention of one layer over the pool."""

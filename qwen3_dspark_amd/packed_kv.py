@@ -91,14 +91,16 @@ class AppendOrderKV:
                 except ValueError as e:
                     raise RuntimeError('Request positions are not exactly a cached prefix') from e
 
-    def _rebuild(self, n_out, *, plan=None, added=None):
-        """New per-layer tensors with n_out rows: from `plan` (crop) or the old
-        rows followed by `added` (append).  One launch for all layers."""
+    def _rebuild(self, n_out, *, plan=None, added=None, layers=None):
+        """New K/V tensors with n_out rows for `layers` (default: all): from
+        `plan` (crop) or the old rows followed by `added` (append).  One
+        launch for all of them."""
+        layers = tuple(range(self.layers)) if layers is None else tuple(layers)
         new = [(torch.empty((1, self.heads, n_out, self.dim), dtype=self.dtype, device=self.device),
                 torch.empty((1, self.heads, n_out, self.dim), dtype=self.dtype, device=self.device))
-               for _ in range(self.layers)]
+               for _ in layers]
         if n_out:
-            src = [t for kv in self.kv for t in kv]
+            src = [t for l in layers for t in self.kv[l]]
             dst = [t for kv in new for t in kv]
             add = None if added is None else _native.pointer_array([t for kv in added for t in kv])
             _native.call('dspark_rows_rebuild', _native.pointer_array(src), add, _native.pointer_array(dst),
@@ -107,36 +109,70 @@ class AppendOrderKV:
                          n_out, _native.stream_handle(self.device))
         return new
 
-    @torch.no_grad()
-    def append(self, chunks, projected):
-        """chunks: ordered {request: new rows}; projected: per layer (keys,
-        values) [1, H, sum rows, D] holding the chunks' rows in that order."""
+    def _check_chunks(self, chunks):
         if not isinstance(chunks, dict) or not chunks:
             raise ValueError('Need a nonempty request-to-rows mapping')
-        self.validate_cache()
         for r, n in chunks.items():
             self._known(r)
             if type(n) is not int or n < 1:
                 raise ValueError('Each chunk needs a positive row count')
-        n_new = sum(chunks.values())
-        if len(projected) != self.layers:
-            raise ValueError('Unexpected number of packed cache layers')
-        for k, v in projected:
-            for t in (k, v):
-                if (not isinstance(t, torch.Tensor) or t.shape != (1, self.heads, n_new, self.dim)
-                        or t.dtype != self.dtype or t.device != self.device or not t.is_contiguous()):
-                    raise ValueError('Appended KV must be contiguous [1, H, rows, D] of the cache dtype and device')
+        return sum(chunks.values())
+
+    def _check_rows(self, t, n):
+        if (not isinstance(t, torch.Tensor) or t.shape != (1, self.heads, n, self.dim)
+                or t.dtype != self.dtype or t.device != self.device or not t.is_contiguous()):
+            raise ValueError('Appended KV must be contiguous [1, H, rows, D] of the cache dtype and device')
+
+    def _record(self, chunks, n_new):
+        """Markers and request-local positions of n_new rows appended in
+        chunk order; the requests' lengths grow by their chunks."""
         markers, positions = [], []
         for r, n in chunks.items():
             markers += [self._markers[r]] * n
             positions += range(self._lengths[r], self._lengths[r] + n)
-        new = self._rebuild(self.rows + n_new, added=projected)
         meta = upload(self.device, markers + positions, torch.long)
         self.key_requests = torch.cat((self.key_requests, meta[:n_new]))
         self.key_positions = torch.cat((self.key_positions, meta[n_new:]))
-        self.kv = new
         for r, n in chunks.items():
             self._lengths[r] += n
+
+    @torch.no_grad()
+    def append(self, chunks, projected):
+        """chunks: ordered {request: new rows}; projected: per layer (keys,
+        values) [1, H, sum rows, D] holding the chunks' rows in that order."""
+        n_new = self._check_chunks(chunks)
+        self.validate_cache()
+        if len(projected) != self.layers:
+            raise ValueError('Unexpected number of packed cache layers')
+        for k, v in projected:
+            self._check_rows(k, n_new)
+            self._check_rows(v, n_new)
+        self.kv = self._rebuild(self.rows + n_new, added=projected)
+        self._record(chunks, n_new)
+
+    @torch.no_grad()
+    def append_layer(self, layer, keys, values):
+        """Grow one layer's K and V by keys / values [1, H, n, D] (one
+        launch) and return the layer's new [1, H, rows + n, D] tensors: what
+        a model forward's per-layer cache update does.  commit_rows records
+        the new rows once every layer has grown by them."""
+        if type(layer) is not int or not 0 <= layer < self.layers:
+            raise ValueError('Invalid cache layer')
+        if self.kv[layer][0].shape[2] != self.rows:
+            raise RuntimeError('Cache layer already grew in this forward')
+        n = keys.shape[2] if isinstance(keys, torch.Tensor) and keys.ndim == 4 else -1
+        self._check_rows(keys, n)
+        self._check_rows(values, n)
+        self.kv[layer] = self._rebuild(self.rows + n, added=[(keys, values)], layers=(layer,))[0]
+        return self.kv[layer]
+
+    def commit_rows(self, chunks):
+        """Record the rows (ordered {request: rows}) by which append_layer
+        grew every layer."""
+        n_new = self._check_chunks(chunks)
+        if any(k.shape[2] != self.rows + n_new for k, _ in self.kv):
+            raise RuntimeError('Full layer cache update missing')
+        self._record(chunks, n_new)
 
     def crop(self, request_id, length):
         """Keep one request's local prefix of `length` rows; all other rows
