@@ -413,6 +413,10 @@ class PersistentTargetKV:
     def is_registered(self, bucket):
         return bucket in self._workspaces
 
+    def registered(self):
+        """Every registered bucket and family."""
+        return tuple(self._workspaces)
+
     def workspace(self, bucket):
         """Device buffers of a registered bucket or family."""
         return self._workspaces[bucket]

@@ -93,7 +93,8 @@ def test_config4_verification_round_full_size():
     seqs = [rng.integers(0, 151936, size=n).tolist() for n in lengths]
     names = [f'r{i}' for i in range(REQUESTS)]
     capacity = HI + 2 * NEW
-    target = PersistentQwenTarget(model, slots=REQUESTS, context_capacity=capacity, max_query_tokens=sum(lengths))
+    target = PersistentQwenTarget(model, slots=REQUESTS, context_capacity=capacity, max_query_tokens=sum(lengths),
+                                  workspace_byte_budget=1 << 31)
     for n in names:
         target.add_request(n)
     t = lambda ids: torch.tensor([ids], device=DEV)
