@@ -62,6 +62,8 @@ def parse():
     ap.add_argument('--chunk', type=int, default=None, help='keys per split-K verification work item')
     ap.add_argument('--draft-chunk', type=int, default=None, help='keys per split-K draft work item')
     ap.add_argument('--no-cpu-baseline', action='store_true', help='skip the CPU oracle leg (profiling runs)')
+    ap.add_argument('--traffic-summary', nargs=2, metavar=('FETCH_DIR', 'WRITE_DIR'),
+                    help='turn the FETCH_SIZE and WRITE_SIZE passes of --traffic-probe into profiles/*_traffic.json')
     ap.add_argument('--traffic-probe', action='store_true',
                     help='untimed run for hardware-counter passes: 3 verification-attention and 3 draft-attention '
                          'layers of the workload, then a 1 GiB device-to-device copy as the counter calibration')
@@ -109,6 +111,8 @@ def main():
         print(json.dumps({'error': 'bench.py measures one GPU only; the attention path has no cross-GPU '
                                    'exchange (requests would shard across GPUs); run with --gpus 1'}))
         sys.exit(2)
+    if args.traffic_summary:
+        return traffic_summary(*args.traffic_summary)
     if args.traffic_probe:
         return traffic_probe(args)
     if args.mfma_probe:
@@ -238,15 +242,18 @@ def main():
     # HBM bytes per call from the two counter passes of --traffic-probe
     # (FETCH_SIZE, WRITE_SIZE, calibrated against a plain 1 GiB copy), for
     # the first round of this workload; summarised in profiles/.
+    # Figures measured on older kernel sources are withheld (None) and flagged.
     def counted(name):
         tpath = os.path.join(ROOT, 'profiles', name)
         if not os.path.exists(tpath):
-            return None, None
+            return None, None, None
         with open(tpath) as f:
             tj = json.load(f)
-        return tj.get('hbm_bytes_per_launch'), tj.get('ratio')
-    traffic, traffic_ratio = counted('verify_attn_traffic.json')
-    d_traffic, d_traffic_ratio = counted('draft_attn_traffic.json')
+        if tj.get('kernel_source_sha256') != kernel_source_hash():
+            return None, None, 'stale: measured on other kernel sources'
+        return tj.get('hbm_bytes_per_launch'), tj.get('ratio'), tj.get('algorithmic_bytes_per_launch')
+    traffic, traffic_ratio, traffic_round = counted('verify_attn_traffic.json')
+    d_traffic, d_traffic_ratio, d_traffic_round = counted('draft_attn_traffic.json')
 
     result = {
         'metric': METRIC, 'value': round(value, 1), 'unit': 'tokens/s', 'n_gpus': 1,
@@ -264,6 +271,7 @@ def main():
         'roofline': {
             'bound': 'hbm', 'achieved': round(v_gbs, 1), 'peak': HBM_PEAK_GBS, 'unit': 'GB/s',
             'frac': round(v_gbs / HBM_PEAK_GBS, 4), 'traffic': traffic, 'traffic_per_algorithmic_byte': traffic_ratio,
+            'traffic_round_algorithmic_bytes': traffic_round,
             'kernel': 'fused verification attention: varlen_attn_kernel<true> + merge_kernel',
             'avg_launch_ms': round(v_avg_ms, 5), 'algorithmic_bytes_per_launch': int(v_avg_bytes),
         },
@@ -273,7 +281,7 @@ def main():
             'draft_layer_ms': round(d_avg_ms, 5), 'draft_call_ms': pct(d_ms, DRAFT_LAYERS), 'draft_gbs': round(d_gbs, 1),
             'draft_frac': round(d_gbs / HBM_PEAK_GBS, 4),
             'draft_algorithmic_bytes_per_launch': int(d_b), 'draft_traffic': d_traffic,
-            'draft_traffic_per_algorithmic_byte': d_traffic_ratio,
+            'draft_traffic_per_algorithmic_byte': d_traffic_ratio, 'draft_traffic_round_algorithmic_bytes': d_traffic_round,
             'draft_attn_tokens_per_s': round(nq_d / (float(np.median(d_ms)) * 1e-3), 1),
             'round_algorithmic_bytes': int(round_bytes), 'round_gbs': round(round_gbs, 1),
             'round_frac': round(round_gbs / HBM_PEAK_GBS, 4),
@@ -289,6 +297,7 @@ def main():
     if not args.no_cpu_baseline:
         result['cpu_baseline'], result['parity'] = cpu_leg(args, pool, bucket, handles, contexts, anchors, qv, qd,
                                                            bkd, bvd, dctx_k, dctx_v, draft, draft_offsets)
+        result['cpu_configs'] = cpu_configs(result['cpu_baseline']['cores'])
     print(json.dumps(result), flush=True)
 
 
@@ -553,10 +562,99 @@ def traffic_probe(args):
     dst = torch.empty_like(src)
     dst.copy_(src)
     torch.cuda.synchronize()
+    del ctx_k, ctx_v
     print(json.dumps({'traffic_probe': 'done', 'verify_algorithmic_bytes_per_launch': verify_bytes(contexts),
                       'draft_algorithmic_bytes_per_launch': draft_bytes(anchors),
                       'context_rows': sum(contexts),
-                      'calibration_copy_bytes': 1 << 30}), flush=True)
+                      'calibration_copy_bytes': 1 << 30,
+                      'streaming_reference': streaming_reference(dev, src, dst)}), flush=True)
+
+
+def streaming_reference(dev, src, dst, reps=10):
+    """What the runtime's own 1 GiB device copy streams on this box (read +
+    write bytes over its time; median of `reps` event-timed launches after
+    one warm-up), as a reference for the attention kernels' GB/s."""
+    import torch
+
+    def median_ms(fn):
+        fn()
+        times = []
+        for _ in range(reps):
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record()
+            fn()
+            b.record()
+            b.synchronize()
+            times.append(a.elapsed_time(b))
+        return sorted(times)[len(times) // 2]
+    copy_ms = median_ms(lambda: dst.copy_(src))
+    return {'copy_1gib_gbs': round(2 * (1 << 30) / copy_ms / 1e6, 1)}
+
+
+def kernel_source_hash():
+    """sha256 of the attention kernels' sources: stamps the traffic figures
+    measured with them."""
+    import hashlib
+    h = hashlib.sha256()
+    for name in ('attn.hip', 'common.h'):
+        with open(os.path.join(ROOT, 'qwen3_dspark_amd', 'csrc', name), 'rb') as f:
+            h.update(f.read())
+    return h.hexdigest()
+
+
+def traffic_summary(fetch_dir, write_dir):
+    """profiles/{verify,draft}_attn_traffic.json from the counter CSVs of
+    `rocprofv3 --pmc FETCH_SIZE` and `--pmc WRITE_SIZE` runs of
+    --traffic-probe.  Dispatches in order: 3 x (verification chunk kernel,
+    merge), 3 x (draft chunk kernel, merge), then the 2**30-byte copy, whose
+    counts calibrate KiB to bytes.  Per call = chunk + merge, mean of 3."""
+    import csv
+    import glob
+
+    def read(directory, counter):
+        path = glob.glob(os.path.join(directory, '**', '*counter_collection.csv'), recursive=True)[0]
+        rows = [r for r in csv.DictReader(open(path)) if r['Counter_Name'] == counter]
+        rows.sort(key=lambda r: int(r['Dispatch_Id']))
+        phase, out = None, {'verify_chunk': [], 'verify_merge': [], 'draft_chunk': [], 'draft_merge': [], 'copy': []}
+        for r in rows:
+            name, value = r['Kernel_Name'], float(r['Counter_Value'])
+            if 'varlen_attn_kernel' in name:
+                phase = 'verify'
+                out['verify_chunk'].append(value)
+            elif 'draft_attn_kernel' in name:
+                phase = 'draft'
+                out['draft_chunk'].append(value)
+            elif 'merge_kernel' in name and phase:
+                out[phase + '_merge'].append(value)
+            elif 'copyBuffer' in name and phase == 'draft' and int(r['Grid_Size']) >= 65536:   # the 1 GiB copy
+                out['copy'].append(value)
+        if not all(len(out[k]) == 3 for k in ('verify_chunk', 'verify_merge', 'draft_chunk', 'draft_merge')):
+            raise SystemExit(f'unexpected dispatches in {path}: { {k: len(v) for k, v in out.items()} }')
+        return {k: (v[0] if k == 'copy' else sum(v) / len(v)) for k, v in out.items()}
+
+    fetch, write = read(fetch_dir, 'FETCH_SIZE'), read(write_dir, 'WRITE_SIZE')
+    copy_bytes = 1 << 30
+    f_factor, w_factor = fetch['copy'] * 1024 / copy_bytes, write['copy'] * 1024 / copy_bytes
+    contexts, anchors, _ = workload(1)
+    source = kernel_source_hash()
+    for kind, algorithmic in (('verify', verify_bytes(contexts)), ('draft', draft_bytes(anchors))):
+        read_b = (fetch[kind + '_chunk'] + fetch[kind + '_merge']) * 1024 / f_factor
+        write_b = (write[kind + '_chunk'] + write[kind + '_merge']) * 1024 / w_factor
+        total = read_b + write_b
+        doc = dict(hbm_bytes_per_launch=round(total), read_bytes=round(read_b), write_bytes=round(write_b),
+                   algorithmic_bytes_per_launch=int(algorithmic), ratio=round(total / algorithmic, 4),
+                   fetch_factor=round(f_factor, 4), write_factor=round(w_factor, 4),
+                   fetch_kib={'chunk': fetch[kind + '_chunk'], 'merge': fetch[kind + '_merge'],
+                              'calibration_copy': fetch['copy']},
+                   write_kib={'chunk': write[kind + '_chunk'], 'merge': write[kind + '_merge'],
+                              'calibration_copy': write['copy']},
+                   context_rows=sum(contexts), workload_round='first round of the bench workload',
+                   kernel_source_sha256=source)
+        with open(os.path.join(ROOT, 'profiles', f'{kind}_attn_traffic.json'), 'w') as f:
+            json.dump(doc, f, indent=1)
+        print(json.dumps({kind: {k: doc[k] for k in ('hbm_bytes_per_launch', 'read_bytes', 'write_bytes',
+                                                     'algorithmic_bytes_per_launch', 'ratio', 'fetch_kib',
+                                                     'write_kib')}}))
 
 
 def cpu_model():
@@ -569,6 +667,76 @@ def cpu_model():
     except OSError:
         pass
     return 'unknown'
+
+
+def cpu_configs(threads):
+    """The C oracle's attention time at the four smaller workloads, on the
+    host, at `threads` threads and at 2 threads (the reference CI's count):
+      1. draft, 2 requests, contexts 128 / 96, one 7-row block each;
+      2. verification, 1 layer, 4 requests, contexts U[64, 512], 7 new rows;
+      3. draft attention of 5 layers, 16 requests, contexts U[128, 1024],
+         4 blocks each at anchors U[0, c];
+      4. verification of 28 layers, 32 requests, contexts U[256, 2048].
+    Inputs are seeded N(0,1) draws rounded to bf16 (the oracle computes in
+    FP32).  Per call: median of 5 reps (3 at 28 layers' scale, 1 for the
+    2-thread 28-layer case); layers of one config are identical in cost, so
+    a round is `layers` calls."""
+    import numpy as np
+    import torch
+
+    from oracle import cref
+
+    scale = 128 ** -0.5
+    rng = np.random.default_rng(SEED + 21)
+    gen = torch.Generator().manual_seed(SEED + 21)
+
+    def bits(*shape):
+        return torch.randn(*shape, generator=gen).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+
+    def median_s(fn, reps):
+        times = []
+        for _ in range(reps):
+            t0 = time.perf_counter()
+            fn()
+            times.append(time.perf_counter() - t0)
+        return float(np.median(times))
+
+    def report(call, rows, layers, reps):
+        row = {'query_rows': rows, 'layers': layers}
+        for th, n in ((threads, reps), (2, max(1, reps if reps >= 5 else 1))):
+            t = median_s(lambda: call(th), n)
+            row[f'{th}_threads'] = {'call_ms': round(1e3 * t, 3), 'round_ms': round(1e3 * t * layers, 2),
+                                    'tokens_per_s': round(rows / (t * layers), 1), 'reps': n}
+        return row
+
+    def draft_case(contexts, anchors, layers, reps):
+        rows = BLOCK * sum(len(a) for a in anchors)
+        ck, cv = bits(sum(contexts), 8, 128), bits(sum(contexts), 8, 128)
+        q, bk, bv = bits(rows, 16, 128), bits(rows, 8, 128), bits(rows, 8, 128)
+        offs = np.concatenate([[0], np.cumsum(contexts)[:-1]]).tolist()
+        cu_b = np.cumsum([0] + [len(a) for a in anchors])
+        flat = [x for a in anchors for x in a]
+        return report(lambda th: cref.draft_attention(q, ck, cv, offs, contexts, bk, bv, cu_b, flat, scale=scale,
+                                                      threads=th), rows, layers, reps)
+
+    def verify_case(contexts, layers, reps):
+        n = len(contexts)
+        k_res, v_res = bits(n, max(contexts), 8, 128), bits(n, max(contexts), 8, 128)
+        ks, vs, q = bits(n * Q_LEN, 8, 128), bits(n * Q_LEN, 8, 128), bits(n * Q_LEN, 16, 128)
+        cu_q = [Q_LEN * i for i in range(n + 1)]
+        return report(lambda th: cref.verify_attention(q, k_res, v_res, ks, vs, list(range(n)), contexts, cu_q,
+                                                       scale=scale, threads=th), n * Q_LEN, layers, reps)
+
+    c3 = [int(x) for x in rng.integers(128, 1025, size=16)]
+    configs = {
+        '1_draft_2_requests': draft_case([128, 96], [[128], [96]], 1, 5),
+        '2_verify_4_requests_1_layer': verify_case([int(x) for x in rng.integers(64, 513, size=4)], 1, 5),
+        '3_draft_5_layers_16_requests_4_blocks': draft_case(
+            c3, [[int(a) for a in rng.integers(0, c + 1, size=4)] for c in c3], 5, 5),
+        '4_verify_28_layers_32_requests': verify_case([int(x) for x in rng.integers(256, 2049, size=32)], 28, 3),
+    }
+    return {'cpu': cpu_model(), 'threads': [threads, 2], 'kind': 'port (oracle/attn_ref.c, FP32, OpenMP)',
+            'configs': configs}
 
 
 def draft_pairs(anchors):
@@ -672,6 +840,7 @@ def cpu_leg(args, pool, bucket, handles, contexts, anchors, qv, qd, bkd, bvd, dc
     slots = [h.index for h in handles]
     cmax = max(ctx)
     t_verify = 0.0
+    two = {}      # per-layer seconds at 2 threads (layer 0 of each kind)
     for layer in range(n_verify):
         kn = torch.randn(B * Q_LEN, 8, 128, generator=gen, device=dev).to(torch.bfloat16)
         vn = torch.randn(B * Q_LEN, 8, 128, generator=gen, device=dev).to(torch.bfloat16)
@@ -684,6 +853,10 @@ def cpu_leg(args, pool, bucket, handles, contexts, anchors, qv, qd, bkd, bvd, dc
         ref = cref.verify_attention(q, kres, vres, ks, vs, slots, ctx, cu_q, scale=SCALE, threads=threads)
         t_verify += time.perf_counter() - t0
         gate(out, ref, 'verify')
+        if layer == 0:
+            t0 = time.perf_counter()
+            cref.verify_attention(q, kres, vres, ks, vs, slots, ctx, cu_q, scale=SCALE, threads=2)
+            two['verify'] = time.perf_counter() - t0
         del kres, vres
     pool.abort(tx)
 
@@ -706,16 +879,27 @@ def cpu_leg(args, pool, bucket, handles, contexts, anchors, qv, qd, bkd, bvd, dc
                                     bits(bvd[layer]), cu_b, flat, scale=SCALE, threads=threads)
         t_draft += time.perf_counter() - t0
         gate(dout, dref, 'draft')
+        if layer == 0:
+            t0 = time.perf_counter()
+            cref.draft_attention(bits(qd[layer]), ck, cv, offs_host, contexts, bits(bkd[layer]), bits(bvd[layer]),
+                                 cu_b, flat, scale=SCALE, threads=2)
+            two['draft'] = time.perf_counter() - t0
     stats['within_tolerance'] = bool(stats['verify_max_abs'] <= 2e-2 and stats['verify_mean_abs'] <= 2e-3
                                      and stats['draft_max_abs'] <= 2e-2 and stats['draft_mean_abs'] <= 2e-3)
     stats['checked_layers'] = {'verify': n_verify, 'draft': n_draft}
     round_s = VERIFY_LAYERS * t_verify / n_verify + DRAFT_LAYERS * t_draft / n_draft
     scaled = '' if (n_verify, n_draft) == (VERIFY_LAYERS, DRAFT_LAYERS) else ', scaled to 28 + 5 layers'
+    round_2 = VERIFY_LAYERS * two['verify'] + DRAFT_LAYERS * two['draft']
     cpu = {
         'value': round(B * Q_LEN / round_s, 3), 'unit': 'tokens/s', 'cores': threads, 'kind': 'port',
         'sample': f'C oracle (oracle/attn_ref.c, FP32, OpenMP, {threads} threads) over one round of the same '
                   f'64-request workload: {n_verify} verification layers ({t_verify:.2f} s) and {n_draft} draft '
                   f'layers ({t_draft:.2f} s){scaled}; round time {round_s:.2f} s; host CPU {cpu_model()}',
+        'two_threads': {'value': round(B * Q_LEN / round_2, 3), 'unit': 'tokens/s', 'cores': 2,
+                        'sample': f'the same C oracle at 2 threads (the reference CI thread count) on the first '
+                                  f'verification layer ({two["verify"]:.2f} s) and the first draft layer '
+                                  f'({two["draft"]:.2f} s) of that round, scaled to 28 + 5 layers: '
+                                  f'{round_2:.2f} s per round'},
     }
     return cpu, stats
 
