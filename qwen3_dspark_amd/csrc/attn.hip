@@ -1,6 +1,7 @@
 // DSpark attention kernels for gfx950 (MI355X).
 //
-// Three entry points share one MFMA inner loop:
+// Three entry points (varlen and verify share one MFMA inner loop; draft has
+// its own 32-row core, described with its section):
 //   * varlen    - packed THD attention over cu_seqlens (exact-K or
 //                 capacity-tail K/V), bottom-right causal or noncausal.
 //                 Replaces aten::_flash_attention_forward as called by
@@ -17,7 +18,7 @@
 //                 (dspark_qwen/model.py:12-19); context is streamed once per
 //                 request for all of its blocks.
 //
-// MFMA mapping (v_mfma_f32_16x16x32_bf16, wave64):
+// varlen / verify MFMA mapping (v_mfma_f32_16x16x32_bf16, wave64):
 //   S^T[key][row] = K[key][:] . Q[row][:]   A = K (16 keys), B = Q^T
 //   O^T[d][row]  += V^T[d][key] P^T[key][row]  A = V^T (via LDS), B = P^T
 // A 16-row tile holds 8 query tokens x the 2 query heads of one KV head
@@ -53,13 +54,13 @@ constexpr int ROWB = HD * 2;           // bytes per LDS K/V row (256)
 constexpr int OPITCH = HD + 4;         // floats per row in the merge buffer
 
 // XOR swizzle of the 16-byte chunk index of LDS row k (rows are 256 B,
-// i.e. 16 chunks spanning all banks).  Conflict-free for the three access
+// i.e. 16 chunks spanning all banks).  Conflict-free for the access
 // patterns on a K/V tile:
 //  - row writes (registers or direct loads): 16 lanes write the 16 chunks
 //    of one row, any per-row XOR keeps them distinct;
-//  - transpose reads (V^T): a 16-lane group reads rows 8grp+r (r<4), chunks
-//    2nb and 2nb+1; swz = 4r + grp moves the 4 rows to distinct chunk
-//    pairs;
+//  - transpose reads (V^T): a 16-lane group reads 4 rows r (r<4) with the
+//    same k>>3, chunks 2c and 2c+1; swz = 4r + ((k>>3)&3) moves the 4 rows
+//    to distinct chunk pairs;
 //  - K fragment reads (draft, from LDS): 16 lanes read rows 8q+4j+e (q<4,
 //    e<4), one chunk; (k&3, (k>>3)&3) takes all 16 values.
 __device__ __forceinline__ int swz(int k) {
@@ -642,28 +643,8 @@ struct DraftArgs {
 };
 
 constexpr int BLOCK_ROWS = 7;
-constexpr int DWAVES = 8;                            // one draft block per wave
-constexpr int DSTEP = 64;                            // context keys per ring stage
-
-// The context ring: each stage holds DSTEP K rows then DSTEP V rows, both
-// XOR-swizzled by 16-byte chunk.  A bf16 K row is 256 B (chunk c at
-// c ^ swz(k)); an fp32 K row (the reference's AMP pool, packed_draft.py:222-235)
-// is 512 B, the low four floats of bf16 chunk c at position c ^ swz(k) and the
-// high four at 16 + (c ^ swz(k)), so that the 16 lanes reading one chunk of
-// 16 rows touch 16 distinct bank groups.  Stages are filled by direct
-// global->LDS loads of 1 KiB pieces, PER_WAVE pieces per wave.
-template <bool KF32>
-struct DraftRing {
-  static constexpr int KROW = KF32 ? 2 * ROWB : ROWB;   // bytes per staged K row
-  static constexpr int STAGES = KF32 ? 3 : 4;            // 144 KiB or 128 KiB of LDS
-  static constexpr int K_BYTES = DSTEP * KROW;
-  static constexpr int STAGE_BYTES = K_BYTES + DSTEP * ROWB;
-  static constexpr int K_PIECES = K_BYTES / 1024;
-  static constexpr int PER_WAVE = STAGE_BYTES / 1024 / DWAVES;
-  static constexpr int SMEM = STAGES * STAGE_BYTES;
-  static_assert(PER_WAVE * DWAVES * 1024 == STAGE_BYTES, "stage pieces must divide evenly over the waves");
-  static_assert(SMEM <= 160 * 1024, "ring exceeds the LDS of a CU");
-};
+constexpr int MAX_BLOCKS = 8;                        // draft blocks per request
+constexpr int CHUNK_ALIGN = 64;                      // fixed chunks are multiples of this many keys
 
 // One context segment of one request: keys [k0, k1) of request r (whose
 // blocks are b0 .. b0+nb, largest anchor amax).  The segment ending the
@@ -675,29 +656,258 @@ struct DraftSeg {
   bool last;
 };
 
-// 8 K values (dims 8c .. 8c+7 of one row) from global memory as bf16.
+// A pair of draft blocks is attended as one 32-row tile: row n is block
+// 2p + n/16 of pair p, token (n%16)/2, query head 2g + n%2 (rows with token
+// 7 and rows of a block the request does not have carry zero Q and are never
+// written).  Wave w of the workgroup takes pair p = w/2 and key half
+// h = w%2: rows 32h .. 32h+31 of every 64-key ring stage (the two halves
+// are merged at the end), so that each wave reads half of each stage from
+// LDS and a request with few blocks still keeps two waves busy.
+//
+// v_mfma_f32_32x32x16_bf16 (wave64): A lane l supplies row l%32 at
+// k = 8(l/32) + i, B lane l supplies column l%32 at the same k, and
+// accumulator register r of lane l is row 8(r/4) + 4(l/32) + r%4, column
+// l%32.  With A = K (rows = key slots) and B = Q^T, lane l holds 16 scores
+// of query row l%32; registers 8t .. 8t+7 are the B operand (P^T) of PV
+// k-step t when the A operand (V^T) of lane l takes slots
+// 8(2t + i/4) + 4(l/32) + i%4, i = 0..7.
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef __attribute__((address_space(3))) bf16x8 lds_bf16x8;
+typedef __attribute__((address_space(3))) f32x4 lds_f32x4;
+
+constexpr int DWAVES = 8;                            // waves per workgroup: 4 pairs x 2 key halves
+constexpr int DSTEP = 64;                            // context keys per ring stage
+static_assert(DWAVES == MAX_BLOCKS, "the pairs cover the most blocks a request may hold");
+static_assert(CHUNK_ALIGN % DSTEP == 0, "fixed chunks hold whole stages");
+
+// The context ring: each stage holds DSTEP K rows then DSTEP V rows, filled
+// by direct global->LDS loads of 1 KiB pieces (PER_WAVE per wave).  Rows are
+// XOR-swizzled by 16-byte chunk: a bf16 row (256 B) holds chunk c at
+// c ^ swz(row); an fp32 K row (the reference's AMP pool,
+// packed_draft.py:222-235; 512 B) holds the low four floats of bf16 chunk c
+// at 16-byte position c ^ swz(row) and the high four at 16 + (c ^ swz(row)).
+// The segment ending a request first stages the blocks' own rows in the last
+// slot (pair p's 16 K rows at rows 16p .. 16p+15, then 64 V rows likewise,
+// swizzled by row % 16), attends them, and only then lets the context stream
+// reuse that slot.  After the stream, the key halves merge through the
+// drained ring.
 template <bool KF32>
-__device__ __forceinline__ bf16x8 ld8_k(const void* base, size_t elem) {
-  if constexpr (KF32) return ld8(static_cast<const float*>(base) + elem);
-  else return ld8(static_cast<const bf16*>(base) + elem);
+struct PairRing {
+  static constexpr int KROW = KF32 ? 2 * ROWB : ROWB;   // bytes per staged K row
+  static constexpr int STAGES = KF32 ? 3 : 4;            // 144 KiB or 128 KiB of LDS
+  static constexpr int K_BYTES = DSTEP * KROW;
+  static constexpr int STAGE_BYTES = K_BYTES + DSTEP * ROWB;
+  static constexpr int K_PIECES = K_BYTES / 1024;
+  static constexpr int PER_WAVE = STAGE_BYTES / 1024 / DWAVES;
+  static constexpr int SMEM = STAGES * STAGE_BYTES;
+  static constexpr int OWN_SLOT = (STAGES - 1) * STAGE_BYTES;
+  static constexpr int MERGE_FLOATS = 64 + 2;              // per lane: O^T, max, sum
+  static constexpr int MERGE_BYTES = MERGE_FLOATS * WAVE * 4;
+  static_assert(PER_WAVE * DWAVES * 1024 == STAGE_BYTES, "stage pieces must divide evenly over the waves");
+  static_assert(SMEM <= 160 * 1024, "ring exceeds the LDS of a CU");
+  static_assert(4 * MERGE_BYTES <= OWN_SLOT, "the half merge must not touch the own rows");
+};
+
+// Staged row of key slot m (0..31).  Rows are permuted so that the 16 lanes
+// of a K-fragment read (slots 16u .. 16u+15) see 16 distinct swizzles.
+__device__ __forceinline__ int slot_row(int m) {
+  return 8 * ((m >> 2) & 3) + (m & 3) + 4 * (m >> 4);
 }
 
-// INDEXED: context rows come through a per-request physical index vector
-// (the append-order pool); otherwise they are consecutive rows.  The
-// non-indexed instance has no ordinary global loads inside the stage loop,
-// so nothing forces a full vmcnt drain between ring stages.
-// KF32: context and block K are fp32 and rounded to bf16 when their MFMA
-// fragments are formed, which gives the same bits as attending a bf16 copy.
-// No early return: every wave reaches the end, so a caller may place
+// Staged row of the key behind accumulator register r of a lane in half hh
+// (= l/32): slot_row(8(r/4) + 4hh + r%4).
+__device__ __forceinline__ int acc_row(int r, int hh) {
+  return 16 * ((r >> 2) & 1) + 8 * hh + 4 * (r >> 3) + (r & 3);
+}
+
+struct PairState {
+  float m;         // running reference max of the lane's row (log2 domain)
+  float l;         // per-lane partial sum (16 of the row's 32 slots per tile)
+  f32x16 o[4];     // O^T accumulators for dims 32D .. 32D+31
+};
+
+// Per-lane LDS byte offsets of a 32-key tile, written so that every read of
+// the tile is the base XOR a constant (plus an immediate):
+//  * K fragment of k-step ks (dims 16ks .. 16ks+15; the lane reads bf16
+//    chunk (2ks + l/32) ^ swz(kr) of staged row kr):  k ^ 32ks (fp32 rows:
+//    the low half there, the high half 256 bytes above);
+//  * V^T of PV k-step t, dims 32D .. 32D+31: two transpose reads (each
+//    16-lane group reads 4 rows x 16 dims; lane 4*row + c supplies dims
+//    4c .. 4c+3 of its row) of the rows behind slots 16t + 4(l/32) + i and
+//    16t + 8 + 4(l/32) + i (i < 4):  (v ^ 64D) + 1024t and
+//    (v ^ 64D ^ V1_XOR) + V1_ADD + 1024t.
+// Swizzles and chunk numbers occupy address bits 4..7 and rows start at
+// multiples of 256 bytes, so the XORs never carry into a row.
+struct TileOffsets {
+  uint32_t k;
+  uint32_t v;
+};
+
+// Context stage: slot m's key is staged row slot_row(m).  The rows behind
+// the V^T reads are 8(l/32) + 4t + i (swizzle 4i + l/32) and 16 more
+// (swizzle ^ 2).
+constexpr uint32_t CTX_V1_XOR = 32;
+constexpr uint32_t CTX_V1_ADD = 16 * ROWB;
+template <int KROW>
+__device__ __forceinline__ TileOffsets ctx_tile_offsets(int lane) {
+  const int hh = lane >> 5;
+  const int rr = (lane >> 2) & 3;
+  const int c4 = lane & 3;
+  const int kr = slot_row(lane & 31);
+  const int vr = 8 * hh + rr;
+  return TileOffsets{(uint32_t)(kr * KROW + ((16 * hh) ^ (16 * swz(kr)))),
+                     (uint32_t)(vr * ROWB + ((32 * ((lane >> 4) & 1) + 16 * (c4 >> 1)) ^ (16 * swz(vr))) + 8 * (c4 & 1))};
+}
+
+// Own rows of a pair: staged row v (0..31) of the tile is row
+// 8(v/16) + v%8 (block v/16 of the pair, token v%8) of the 16 staged K and
+// 16 staged V rows; half 1's slots (v%16 >= 8) repeat half 0's rows.  The
+// rows behind the V^T reads are 4t + i (swizzle 4i) and 8 more (swizzle ^ 1).
+constexpr uint32_t OWN_V1_XOR = 16;
+constexpr uint32_t OWN_V1_ADD = 8 * ROWB;
+template <int KROW>
+__device__ __forceinline__ TileOffsets own_tile_offsets(int lane) {
+  const int hh = lane >> 5;
+  const int rr = (lane >> 2) & 3;
+  const int c4 = lane & 3;
+  const int sr = slot_row(lane & 31);
+  const int kr = 8 * (sr >> 4) + (sr & 7);
+  return TileOffsets{(uint32_t)(kr * KROW + ((16 * hh) ^ (16 * swz(kr)))),
+                     (uint32_t)(rr * ROWB + ((32 * ((lane >> 4) & 1) + 16 * (c4 >> 1)) ^ (16 * swz(rr))) + 8 * (c4 & 1))};
+}
+
+// The K fragment at LDS address `addr`: bf16 as staged, or fp32 rounded to
+// bf16 (round to nearest even, the bits of attending a bf16 copy).
+template <bool KF32>
+__device__ __forceinline__ bf16x8 lds_k_frag(uint32_t addr) {
+  if constexpr (KF32) {
+    const f32x4 lo = *(const lds_f32x4*)(uintptr_t)addr;
+    const f32x4 hi = *(const lds_f32x4*)(uintptr_t)(addr + 256);
+    return to_bf16x8(lo, hi);
+  } else {
+    return *(const lds_bf16x8*)(uintptr_t)addr;
+  }
+}
+
+__device__ __forceinline__ bf16x4 lds_tr4(uint32_t addr) {
+  return __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)(uintptr_t)addr);
+}
+
+// One 32-key tile of a pair: S^T = K Q^T, online softmax, O^T += V^T P^T.
+// ka/va: LDS addresses of the lane's K and V bases (TileOffsets plus the K
+// and V base of the tile).  In a masked tile `visible(r)` says whether the
+// key of accumulator register r is visible to the lane's query row.
+//
+// The running maximum only moves up when a tile's maximum exceeds it by more
+// than RESCALE_SLACK (log2 units), so O and l are rescaled rarely instead of
+// every tile.  Exact for any reference value: O and l always share the same
+// reference max, which the split-K merge carries along; probabilities stay
+// <= 2^RESCALE_SLACK, far from FP32/bf16 overflow.  The rescale branch is
+// wave-uniform.
+template <bool KF32, uint32_t V1_XOR, uint32_t V1_ADD, class Vis>
+__device__ __forceinline__ void pair_tile(PairState& st, const bf16x8 (&qf)[8], uint32_t ka, uint32_t va, bool masked,
+                                          Vis visible, float scale_log2) {
+  // Every LDS read of the tile is issued up front: the K fragments, then
+  // the V^T halves, whose latency the QK chain and the softmax then hide.
+  bf16x8 kf[8];
+  #pragma unroll
+  for (int ks = 0; ks < 8; ++ks) kf[ks] = lds_k_frag<KF32>(ka ^ (32u * ks));
+  __builtin_amdgcn_sched_barrier(0);
+  bf16x4 vlo[2][4], vhi[2][4];
+  #pragma unroll
+  for (int t = 0; t < 2; ++t)
+    #pragma unroll
+    for (int D = 0; D < 4; ++D) {
+      vlo[t][D] = lds_tr4((va ^ (64u * D)) + 1024u * t);
+      vhi[t][D] = lds_tr4((va ^ (64u * D) ^ V1_XOR) + V1_ADD + 1024u * t);
+    }
+  f32x16 s = {};
+  #pragma unroll
+  for (int ks = 0; ks < 8; ++ks) s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[ks], qf[ks], s, 0, 0, 0);
+  #pragma unroll
+  for (int r = 0; r < 16; ++r) s[r] *= scale_log2;
+  if (masked) {
+    #pragma unroll
+    for (int r = 0; r < 16; ++r)
+      if (!visible(r)) s[r] = -INFINITY;
+  }
+  float mx = s[0];
+  #pragma unroll
+  for (int r = 1; r < 16; ++r) mx = fmaxf(mx, s[r]);
+  mx = fmaxf(mx, __shfl_xor(mx, 32));    // lanes l and l^32 hold the same row
+  const bool raise = mx > st.m + RESCALE_SLACK;
+  if (__builtin_amdgcn_ballot_w64(raise)) {
+    // Rows that do not raise keep factor 1 (their max may still be -inf,
+    // and -inf - -inf must not reach exp2).
+    const float alpha = raise ? fast_exp2(st.m - mx) : 1.0f;
+    st.l *= alpha;
+    #pragma unroll
+    for (int D = 0; D < 4; ++D) st.o[D] *= alpha;
+    if (raise) st.m = mx;
+  }
+  const float m_use = (st.m == -INFINITY) ? 0.f : st.m;
+  bf16x8 pb[2];
+  float ps = 0.f;
+  #pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    const float p = fast_exp2(s[r] - m_use);
+    ps += p;
+    pb[r >> 3][r & 7] = (bf16)p;
+  }
+  st.l += ps;
+  #pragma unroll
+  for (int t = 0; t < 2; ++t)
+    #pragma unroll
+    for (int D = 0; D < 4; ++D) {
+      bf16x8 vt;
+      #pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        vt[i] = vlo[t][D][i];
+        vt[4 + i] = vhi[t][D][i];
+      }
+      st.o[D] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vt, pb[t], st.o[D], 0, 0, 0);
+    }
+}
+
+// A wave-uniform read-only kernel input through the constant address space,
+// i.e. a scalar load: it waits on lgkmcnt, never on the vmcnt that orders
+// the ring.
+template <class T>
+__device__ __forceinline__ T ld_const(const T* p) {
+  return *(const __attribute__((address_space(4))) T*)p;
+}
+
+// The register operands must hold their loaded values here: the compiler
+// places its wait for them before this point, while no direct-to-LDS load
+// is in flight yet (a wait placed later would drain the ring).
+template <class T>
+__device__ __forceinline__ void settle_one(const T& x) {
+  asm volatile("" ::"v"(x));
+}
+
+template <class... T>
+__device__ __forceinline__ void settle(const T&... x) {
+  (settle_one(x), ...);
+}
+
+// Wave w of the workgroup attends blocks 2(w/2) and 2(w/2)+1 of the
+// segment's request over key half w%2 of every stage.  INDEXED: context
+// rows come through a per-request physical index vector (the append-order
+// pool), else they are consecutive rows; the non-indexed instance has no
+// ordinary global loads inside the stage loop, so nothing forces a full
+// vmcnt drain between ring stages.  KF32: context and block K are fp32.
+// No early return: every wave reaches the end, so that the caller may place
 // workgroup barriers between items.
 template <bool INDEXED, bool KF32>
-__device__ __forceinline__ void draft_item(const DraftArgs& a, unsigned char* smem, const DraftSeg& sg, int g) {
-  using R = DraftRing<KF32>;
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int wave = tid >> 6;
-  const int col = lane & 15;
-  const int grp = lane >> 4;
+__device__ __forceinline__ void draft_pair_item(const DraftArgs& a, unsigned char* smem, const DraftSeg& sg, int g) {
+  using R = PairRing<KF32>;
+  constexpr int KEL = KF32 ? 4 : 2;                 // bytes per K element
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int pw = wave >> 1;                         // block pair
+  const int kh = wave & 1;                          // key half of each stage
+  const int hh = lane >> 5;
+  const int n = lane & 31;
   const int r = __builtin_amdgcn_readfirstlane(sg.r);
   const int k0 = __builtin_amdgcn_readfirstlane(sg.k0);
   const int k1 = __builtin_amdgcn_readfirstlane(sg.k1);
@@ -707,167 +917,146 @@ __device__ __forceinline__ void draft_item(const DraftArgs& a, unsigned char* sm
   const int amax = __builtin_amdgcn_readfirstlane(sg.amax);
   const bool last = sg.last;
   const int kend = min(k1, amax);
-  // This wave's block (if any): rows = 7 tokens x the 2 query heads of KV head g.
-  const int b = wave;
-  const bool active = b < nb;
-  const int tok = col >> 1;
-  const bool row_ok = tok < BLOCK_ROWS;
-  const int tile_anchor = active ? min(a.anchors[b0 + b], k1) : 0;
-  const int vis = row_ok ? tile_anchor : 0;
-  bf16x8 qf[4];
+  const bool active = 2 * pw < nb;
+  const int bi = n >> 4;
+  const int blk = 2 * pw + bi;
+  const int tok = (n & 15) >> 1;
+  const bool row_ok = blk < nb && tok < BLOCK_ROWS;
+  // Context rows visible to each block of the pair (a missing second block
+  // copies the first's, so that the pair's limits are the first block's).
+  const int anc0 = active ? min(ld_const(a.anchors + b0 + 2 * pw), k1) : 0;
+  const int anc1 = 2 * pw + 1 < nb ? min(ld_const(a.anchors + b0 + 2 * pw + 1), k1) : anc0;
+  const int vis = row_ok ? (bi ? anc1 : anc0) : 0;
+  const int pair_hi = max(anc0, anc1);              // keys at or past this are seen by neither block
+  const int full_lim = min(min(anc0, anc1), kend);  // keys below this need no mask
+  // Q rows of the tile (rows outside the blocks read row 0 and are zeroed);
+  // every load is issued before any is used.
+  bf16x8 qf[8];
   {
-    const size_t qe = (size_t)(BLOCK_ROWS * (b0 + (active ? b : 0)) + (row_ok ? tok : 0)) * Q_ROW +
-                      (size_t)(2 * g + (col & 1)) * HD + 8 * grp;
-    const bool q_ok = active && row_ok;
+    const size_t qe = (size_t)(BLOCK_ROWS * (b0 + (row_ok ? blk : 0)) + (row_ok ? tok : 0)) * Q_ROW +
+                      (size_t)(2 * g + (n & 1)) * HD + 8 * hh;
     if (a.q_f32) {
+      const float* qp = static_cast<const float*>(a.q) + qe;
+      f32x4 lo[8], hi[8];
       #pragma unroll
-      for (int ks = 0; ks < 4; ++ks) qf[ks] = q_ok ? ld8(static_cast<const float*>(a.q) + qe + 32 * ks) : zero8();
+      for (int ks = 0; ks < 8; ++ks) {
+        lo[ks] = *reinterpret_cast<const f32x4*>(qp + 16 * ks);
+        hi[ks] = *reinterpret_cast<const f32x4*>(qp + 16 * ks + 4);
+      }
+      #pragma unroll
+      for (int ks = 0; ks < 8; ++ks) qf[ks] = row_ok ? to_bf16x8(lo[ks], hi[ks]) : zero8();
     } else {
       #pragma unroll
-      for (int ks = 0; ks < 4; ++ks) qf[ks] = q_ok ? ld8(static_cast<const bf16*>(a.q) + qe + 32 * ks) : zero8();
-    }
-  }
-  RowState st;
-  row_init(st);
-  // The segment ending the request also attends the wave's own 7 rows: their
-  // K fragments and V rows are fetched now, so that their latency hides
-  // under the context stream instead of following its drain.  (fp32 K rows
-  // are fetched after the drain: held unconverted through the stream they
-  // would need twice the registers.)
-  const bool own = last && active;
-  const size_t rb = (size_t)BLOCK_ROWS * (b0 + (active ? b : 0));
-  bf16x8 own_k[2][4], own_v[2];
-  auto load_own_k = [&]() {
-    #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int kk = 8 * (col >> 2) + 4 * j + (col & 3);
-      const size_t e = (rb + min(kk, BLOCK_ROWS - 1)) * KV_ROW + (size_t)g * HD + 8 * grp;
+      for (int ks = 0; ks < 8; ++ks) qf[ks] = ld8(static_cast<const bf16*>(a.q) + qe + 16 * ks);
       #pragma unroll
-      for (int ks = 0; ks < 4; ++ks) own_k[j][ks] = ld8_k<KF32>(a.k_blk, e + 32 * ks);
-    }
-  };
-  if (own) {
-    if constexpr (!KF32) load_own_k();
-    #pragma unroll
-    for (int i2 = 0; i2 < 2; ++i2) {
-      const int kk = 4 * i2 + grp;
-      own_v[i2] = (kk < BLOCK_ROWS) ? ld8(a.v_blk + (rb + kk) * KV_ROW + (size_t)g * HD + 8 * col) : zero8();
+      for (int ks = 0; ks < 8; ++ks) qf[ks] = row_ok ? qf[ks] : zero8();
     }
   }
+  const int64_t coff = ld_const(a.ctx_off + r);
+  settle(qf[0], qf[1], qf[2], qf[3], qf[4], qf[5], qf[6], qf[7]);
 
-  // Context row kk of this request for KV head g (clamped into range), as a
-  // byte address.
-  constexpr int KEL = KF32 ? 4 : 2;
-  const int64_t coff = a.ctx_off[r];
   const char* kbase = static_cast<const char*>(a.k_ctx) + (size_t)g * a.head_stride * KEL;
   const char* vbase = reinterpret_cast<const char*>(a.v_ctx) + (size_t)g * a.head_stride * 2;
+  // Context row kk of this request (clamped into range) as a byte address.
   auto ctx_row = [&](const char* base, int el, int kk) -> const char* {
     kk = min(kk, kend - 1);
     const int64_t phys = INDEXED ? a.ctx_idx[coff + kk] : coff + kk;
     return base + (size_t)phys * (size_t)a.tok_stride * el;
   };
+  // Own row `row` (0..63: pair row/16, block 2(row/16) + (row%16)/8, token
+  // min(row%8, 6), clamped to the request's blocks) as an element index.
+  auto own_row = [&](int row) {
+    const int b = min(2 * (row >> 4) + ((row >> 3) & 1), nb - 1);
+    return (size_t)(BLOCK_ROWS * (b0 + b) + min(row & 7, BLOCK_ROWS - 1)) * KV_ROW + (size_t)g * HD;
+  };
   const uint32_t smem_lds = lds_address(smem);
-  // Stage `step` of the ring, pieces of 1 KiB; wave w issues pieces
-  // PER_WAVE*w .. +PER_WAVE-1 (the K/V choice is uniform per piece).
+  // One slot of pieces of 1 KiB; wave w issues pieces PER_WAVE*w ..
+  // +PER_WAVE-1 (the K/V choice is uniform per piece).
   //  * bf16 K / V piece: rows 4*pr .. +3; lane L fetches row 4*pr + L/16,
   //    16-byte chunk (L%16) ^ swz(row).
   //  * fp32 K piece: rows 2*pr, 2*pr+1; lane L fetches row 2*pr + L/32 at
   //    position p = L%32: floats 4*(2*((p%16) ^ swz(row)) + p/16) .. +3.
-  auto issue = [&](int step) {
-    const int ks = k0 + step * DSTEP;
-    const uint32_t stage = smem_lds + (uint32_t)((step % R::STAGES) * R::STAGE_BYTES);
+  // Context stages swizzle by the stage row, the own rows by row % 16.
+  auto fill = [&](uint32_t slot, auto k_src, auto v_src, int sw_mask) {
     #pragma unroll
     for (int i = 0; i < R::PER_WAVE; ++i) {
       const int piece = wave * R::PER_WAVE + i;
       const char* src;
-      uint32_t dst;
       if (piece < R::K_PIECES) {
         if constexpr (KF32) {
           const int k = 2 * piece + (lane >> 5);
           const int p = lane & 31;
-          src = ctx_row(kbase, 4, ks + k) + 16 * (2 * ((p & 15) ^ swz(k)) + (p >> 4));
+          src = k_src(k) + 16 * (2 * ((p & 15) ^ swz(k & sw_mask)) + (p >> 4));
         } else {
-          const int k = 4 * piece + grp;
-          src = ctx_row(kbase, 2, ks + k) + 16 * (col ^ swz(k));
+          const int k = 4 * piece + (lane >> 4);
+          src = k_src(k) + 16 * ((lane & 15) ^ swz(k & sw_mask));
         }
-        dst = stage + (uint32_t)(piece * 1024);
       } else {
-        const int pr = piece - R::K_PIECES;
-        const int k = 4 * pr + grp;
-        src = ctx_row(vbase, 2, ks + k) + 16 * (col ^ swz(k));
-        dst = stage + (uint32_t)(R::K_BYTES + pr * 1024);
+        const int k = 4 * (piece - R::K_PIECES) + (lane >> 4);
+        src = v_src(k) + 16 * ((lane & 15) ^ swz(k & sw_mask));
       }
-      lds_dma16(src, __builtin_amdgcn_readfirstlane(dst));
+      lds_dma16(src, __builtin_amdgcn_readfirstlane(slot + (uint32_t)(piece * 1024)));
     }
   };
-  // Keys below this wave's anchor (and the chunk's end) need no mask; the
-  // test is uniform across the wave.
-  const int full_lim = min(tile_anchor, kend);
-  auto compute_sub = [&](const unsigned char* kt_lds, const unsigned char* vt_lds, int h, int kt, auto masked) {
-    constexpr bool MASKED = decltype(masked)::value;
-    f32x4 s0, s1;
-    if constexpr (KF32) {
-      // Each fp32 fragment is rounded and consumed at once (8 fragments of
-      // 8 floats held together would exceed the register budget).
-      s0 = f32x4{0.f, 0.f, 0.f, 0.f};
-      s1 = s0;
-      #pragma unroll
-      for (int ks = 0; ks < 4; ++ks) {
-        #pragma unroll
-        for (int j = 0; j < 2; ++j) {
-          const int k = KT * h + 8 * (col >> 2) + 4 * j + (col & 3);
-          const unsigned char* row = kt_lds + k * R::KROW;
-          const int p = (4 * ks + grp) ^ swz(k);
-          const bf16x8 kf = to_bf16x8(*reinterpret_cast<const f32x4*>(row + 16 * p),
-                                      *reinterpret_cast<const f32x4*>(row + 16 * (16 + p)));
-          if (j == 0) s0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf, qf[ks], s0, 0, 0, 0);
-          else s1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf, qf[ks], s1, 0, 0, 0);
-        }
-        __builtin_amdgcn_sched_barrier(0);   // at most two fp32 fragments in flight
-      }
-    } else {
-      bf16x8 kf[2][4];
-      #pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        const int k = KT * h + 8 * (col >> 2) + 4 * j + (col & 3);
-        #pragma unroll
-        for (int ks = 0; ks < 4; ++ks)
-          kf[j][ks] = *reinterpret_cast<const bf16x8*>(kt_lds + lds_chunk_off(k, 4 * ks + grp));
-      }
-      qk_tile(kf, qf, s0, s1);
-    }
-    const bf16x8 pb = softmax_update<MASKED>(st, s0, s1, kt + 8 * grp, vis, a.scale_log2);
-    bf16x8 vt[8];
-    #pragma unroll
-    for (int nbk = 0; nbk < 8; ++nbk) vt[nbk] = lds_vt(vt_lds + KT * h * ROWB, nbk, lane);
-    if (MASKED && kt + KT > kend) {
-      // rows past kend hold clamped copies; their weights are 0, keep V finite-safe
-      #pragma unroll
-      for (int nbk = 0; nbk < 8; ++nbk)
-        #pragma unroll
-        for (int e = 0; e < 8; ++e)
-          if (kt + 8 * grp + e >= kend) vt[nbk][e] = (bf16)0.0f;
-    }
-    pv_update(st, pb, vt);
+  auto issue = [&](int step) {
+    const int ks = k0 + step * DSTEP;
+    fill(smem_lds + (uint32_t)((step % R::STAGES) * R::STAGE_BYTES),
+         [&](int k) { return ctx_row(kbase, KEL, ks + k); }, [&](int k) { return ctx_row(vbase, 2, ks + k); }, 63);
   };
-  auto compute = [&](int step) {
-    const unsigned char* kt_lds = smem + (step % R::STAGES) * R::STAGE_BYTES;
-    const unsigned char* vt_lds = kt_lds + R::K_BYTES;
-    #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const int kt = k0 + step * DSTEP + KT * h;
-      if (tile_anchor <= kt) continue;
-      if (kt + KT <= full_lim) compute_sub(kt_lds, vt_lds, h, kt, std::false_type{});
-      else compute_sub(kt_lds, vt_lds, h, kt, std::true_type{});
-    }
-  };
+
+  PairState st;
+  st.m = -INFINITY;
+  st.l = 0.f;
+  #pragma unroll
+  for (int D = 0; D < 4; ++D) st.o[D] = f32x16{};
   const int n_steps = kend > k0 ? (kend - k0 + DSTEP - 1) / DSTEP : 0;
+
+  // Own-block keys (bidirectional within each block), once per request,
+  // ahead of the context (their loads share the ring's latency).  The
+  // kh = 0 wave of each pair attends them.
+  if (last) {
+    fill(smem_lds + (uint32_t)R::OWN_SLOT,
+         [&](int k) {
+           return reinterpret_cast<const char*>(a.k_blk) + own_row(k) * KEL;
+         },
+         [&](int k) { return reinterpret_cast<const char*>(a.v_blk + own_row(k)); }, 15);
+  }
+  if (n_steps > 0) {
+    #pragma unroll
+    for (int p = 0; p < R::STAGES - 1; ++p) issue(p);
+  }
+  if (last) {
+    if (n_steps > 0) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(R::PER_WAVE * (R::STAGES - 1)) : "memory");
+    else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    asm volatile("s_barrier" ::: "memory");
+    if (active && kh == 0) {
+      // Register r of a lane in half hh holds block (r/4)%2 of the pair,
+      // token 4(r/8) + r%4 (token 7: r = 11, 15); half 1 repeats half 0.
+      const TileOffsets oo = own_tile_offsets<R::KROW>(lane);
+      const uint32_t own = smem_lds + (uint32_t)R::OWN_SLOT;
+      pair_tile<KF32, OWN_V1_XOR, OWN_V1_ADD>(
+          st, qf, own + (uint32_t)(16 * pw * R::KROW) + oo.k, own + (uint32_t)(R::K_BYTES + 16 * pw * ROWB) + oo.v,
+          true, [&](int rg) { return row_ok && hh == 0 && ((rg >> 2) & 1) == bi && rg != 11 && rg != 15; },
+          a.scale_log2);
+    }
+  }
+
+  const TileOffsets co = ctx_tile_offsets<R::KROW>(lane);
+  auto compute = [&](int step) {
+    const int kt = k0 + step * DSTEP + 32 * kh;
+    if (kt >= pair_hi) return;
+    const uint32_t stage = smem_lds + (uint32_t)((step % R::STAGES) * R::STAGE_BYTES);
+    // The key of register r is visible iff kt + acc_row(r, hh) < vis.
+    const int lim = vis - kt - 8 * hh;
+    pair_tile<KF32, CTX_V1_XOR, CTX_V1_ADD>(
+        st, qf, stage + (uint32_t)(32 * kh * R::KROW) + co.k, stage + (uint32_t)(R::K_BYTES + 32 * kh * ROWB) + co.v,
+        kt + 32 > full_lim, [&](int rg) { return acc_row(rg, 0) < lim; }, a.scale_log2);
+  };
   if (n_steps > 0) {
     // Every thread issues exactly PER_WAVE loads per stage (stages past the
     // end re-read the clamped last row), so "stage s has landed" is always
-    // vmcnt(PER_WAVE * (STAGES - 2)) at the top of step s.
-    #pragma unroll
-    for (int p = 0; p < R::STAGES - 1; ++p) issue(p);
+    // vmcnt(PER_WAVE * (STAGES - 2)) at the top of step s (the own rows,
+    // issued first, have landed by then too).
     for (int s = 0; s < n_steps; ++s) {
       asm volatile("s_waitcnt vmcnt(%0)" ::"n"(R::PER_WAVE * (R::STAGES - 2)) : "memory");
       asm volatile("s_barrier" ::: "memory");
@@ -878,50 +1067,64 @@ __device__ __forceinline__ void draft_item(const DraftArgs& a, unsigned char* sm
     asm volatile("s_barrier" ::: "memory");
   }
 
-  // Own-block keys (bidirectional within the block), once per request.
-  if (own) {
-    if constexpr (KF32) load_own_k();
-    unsigned char* wv = smem + wave * 8 * ROWB;   // 8 rows per wave
+  // The key halves merge: the kh = 1 wave of each pair leaves its state in
+  // the drained ring (register-major, lane-minor), the kh = 0 wave folds it
+  // in with the online-softmax rule and writes the result.
+  float* mb = reinterpret_cast<float*>(smem + pw * R::MERGE_BYTES);
+  if (active && kh == 1) {
     #pragma unroll
-    for (int i2 = 0; i2 < 2; ++i2)
-      *reinterpret_cast<bf16x8*>(wv + lds_chunk_off(4 * i2 + grp, col)) = own_v[i2];
-    f32x4 s0, s1;
-    qk_tile(own_k, qf, s0, s1);
-    const bf16x8 pb = softmax_update<true>(st, s0, s1, 8 * grp, row_ok ? BLOCK_ROWS : 0, a.scale_log2);
-    wave_lds_sync();
-    bf16x8 vt[8];
-    #pragma unroll
-    for (int nbk = 0; nbk < 8; ++nbk) {
-      // keys 8*grp+s >= 8 do not exist in a 7-row block
-      vt[nbk] = lds_vt(wv, nbk, lane);
-      if (grp != 0) vt[nbk] = zero8();
-    }
-    pv_update(st, pb, vt);
-    wave_lds_sync();
-  }
-
-  if (active) {
-    const float l = wave_sum_across_groups(st.l);
-    const size_t orow0 = (size_t)BLOCK_ROWS * (b0 + b);
-    if (pslot < 0) {
-      if (row_ok) {
-        bf16* op = a.out + (orow0 + tok) * Q_ROW + (size_t)(2 * g + (col & 1)) * HD + 4 * grp;
-        #pragma unroll
-        for (int nbk = 0; nbk < 8; ++nbk) {
-          bf16x4 ov;
-          #pragma unroll
-          for (int e = 0; e < 4; ++e) ov[e] = (bf16)(st.o[nbk][e] / l);
-          *reinterpret_cast<bf16x4*>(op + 16 * nbk) = ov;
-        }
-      }
-    } else {
-      const size_t p = (size_t)(pslot * 8 + g) * a.tmax + b;
-      float* po = a.part_o + (p * 16 + col) * HD + 4 * grp;
+    for (int D = 0; D < 4; ++D)
       #pragma unroll
-      for (int nbk = 0; nbk < 8; ++nbk) *reinterpret_cast<f32x4*>(po + 16 * nbk) = st.o[nbk];
-      if (grp == 0) {
-        a.part_ml[(p * 16 + col) * 2 + 0] = st.m;
-        a.part_ml[(p * 16 + col) * 2 + 1] = l;
+      for (int e = 0; e < 16; ++e) mb[(16 * D + e) * WAVE + lane] = st.o[D][e];
+    mb[64 * WAVE + lane] = st.m;
+    mb[65 * WAVE + lane] = st.l;
+  }
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  __syncthreads();
+  if (active && kh == 0) {
+    const float m1 = mb[64 * WAVE + lane];
+    const float l1 = mb[65 * WAVE + lane];
+    const float mt = fmaxf(st.m, m1);
+    // Scale factors of the two halves; a half with no visible key
+    // (max -inf) contributes nothing.
+    const float a0 = st.m == -INFINITY ? 0.f : fast_exp2(st.m - mt);
+    const float a1 = m1 == -INFINITY ? 0.f : fast_exp2(m1 - mt);
+    st.m = mt;
+    st.l = st.l * a0 + l1 * a1;
+    #pragma unroll
+    for (int D = 0; D < 4; ++D)
+      #pragma unroll
+      for (int e = 0; e < 16; ++e) st.o[D][e] = st.o[D][e] * a0 + mb[(16 * D + e) * WAVE + lane] * a1;
+
+    const float l = st.l + __shfl_xor(st.l, 32);
+    if (blk < nb) {
+      if (pslot < 0) {
+        if (tok < BLOCK_ROWS) {
+          bf16* op = a.out + (size_t)(BLOCK_ROWS * (b0 + blk) + tok) * Q_ROW + (size_t)(2 * g + (n & 1)) * HD + 4 * hh;
+          const float inv = 1.0f / l;
+          #pragma unroll
+          for (int D = 0; D < 4; ++D)
+            #pragma unroll
+            for (int q = 0; q < 4; ++q) {
+              bf16x4 ov;
+              #pragma unroll
+              for (int e = 0; e < 4; ++e) ov[e] = (bf16)(st.o[D][4 * q + e] * inv);
+              *reinterpret_cast<bf16x4*>(op + 32 * D + 8 * q) = ov;
+            }
+        }
+      } else {
+        const size_t p = (size_t)(pslot * 8 + g) * a.tmax + blk;
+        float* po = a.part_o + (p * 16 + (n & 15)) * HD + 4 * hh;
+        #pragma unroll
+        for (int D = 0; D < 4; ++D)
+          #pragma unroll
+          for (int q = 0; q < 4; ++q)
+            *reinterpret_cast<f32x4*>(po + 32 * D + 8 * q) =
+                f32x4{st.o[D][4 * q], st.o[D][4 * q + 1], st.o[D][4 * q + 2], st.o[D][4 * q + 3]};
+        if (hh == 0) {
+          a.part_ml[(p * 16 + (n & 15)) * 2 + 0] = st.m;
+          a.part_ml[(p * 16 + (n & 15)) * 2 + 1] = l;
+        }
       }
     }
   }
@@ -929,19 +1132,31 @@ __device__ __forceinline__ void draft_item(const DraftArgs& a, unsigned char* sm
 
 // With a work list, workgroup (run w, KV head g) runs the segments of run w
 // (blockIdx.x = 8w + g).  Without one, workgroup (chunk, KV head) runs one
-// fixed chunk of `chunk` context rows, chunks in request order.
+// fixed chunk of `chunk` context rows, chunks in request order.  Every
+// branch is uniform across the workgroup.
 template <bool INDEXED, bool KF32>
-__global__ __launch_bounds__(512) void draft_attn_kernel(DraftArgs a) {
-  __shared__ __attribute__((aligned(16))) unsigned char smem[DraftRing<KF32>::SMEM];
+__global__ __launch_bounds__(DWAVES * WAVE) void draft_attn_kernel(DraftArgs a) {
+  // 1 KiB alignment: tile offsets are XORed into LDS addresses.
+  __shared__ __attribute__((aligned(1024))) unsigned char smem[PairRing<KF32>::SMEM];
   const int g = blockIdx.x & 7;
   if (a.work) {
-    const int32_t* range = a.work + WORK_INTS * a.n_work + (blockIdx.x >> 3);
-    const int lo = min(max(range[0], 0), a.n_work);     // clamped: never past the records
-    const int hi = min(max(range[1], lo), a.n_work);
+    // The run's range and (speculatively) record number `run`, which is the
+    // run's only record in a plan of one segment per run, load together.
+    const int run = blockIdx.x >> 3;
+    const int32_t* range = a.work + WORK_INTS * a.n_work + run;
+    const int32_t* spec = a.work + WORK_INTS * min(run, a.n_work - 1);
+    int w[WORK_INTS];
+    #pragma unroll
+    for (int j = 0; j < WORK_INTS; ++j) w[j] = ld_const(spec + j);
+    const int lo = min(max(ld_const(range), 0), a.n_work);     // clamped: never past the records
+    const int hi = min(max(ld_const(range + 1), lo), a.n_work);
     for (int i = lo; i < hi; ++i) {
-      const int32_t* w = a.work + WORK_INTS * i;
+      if (i != run) {
+        #pragma unroll
+        for (int j = 0; j < WORK_INTS; ++j) w[j] = ld_const(a.work + WORK_INTS * i + j);
+      }
       const DraftSeg sg{w[0], w[1], w[2], w[3], w[4], w[5], w[6], w[2] >= w[6]};
-      draft_item<INDEXED, KF32>(a, smem, sg, g);
+      draft_pair_item<INDEXED, KF32>(a, smem, sg, g);
       __syncthreads();   // the next segment refills the ring the last one read
     }
     return;
@@ -958,7 +1173,7 @@ __global__ __launch_bounds__(512) void draft_attn_kernel(DraftArgs a) {
   for (int b = 0; b < nb; ++b) amax = max(amax, a.anchors[b0 + b]);
   const DraftSeg sg{r, c * a.chunk, min(c * a.chunk + a.chunk, ctx), nch > 1 ? first + c : -1, b0, nb, amax,
                     c == nch - 1};
-  draft_item<INDEXED, KF32>(a, smem, sg, g);
+  draft_pair_item<INDEXED, KF32>(a, smem, sg, g);
 }
 
 // ---------------------------------------------------------------------------
@@ -1339,9 +1554,9 @@ extern "C" int dspark_draft_attn_fwd(const void* q, int q_dtype, const void* k_c
                  "context strides must be multiples of 8 elements and >= 128");
   DSPARK_REQUIRE((q_dtype == 0 || q_dtype == 1) && (k_dtype == 0 || k_dtype == 1),
                  "q_dtype and k_dtype must be 0 (bf16) or 1 (fp32)");
-  DSPARK_REQUIRE(max_blocks >= 1 && max_blocks <= DWAVES,
-                 "max_blocks must be in [1, %d] (got %d)", DWAVES, max_blocks);
-  DSPARK_REQUIRE(chunk % DSTEP == 0, "draft chunk must be a multiple of %d", DSTEP);
+  DSPARK_REQUIRE(max_blocks >= 1 && max_blocks <= MAX_BLOCKS,
+                 "max_blocks must be in [1, %d] (got %d)", MAX_BLOCKS, max_blocks);
+  DSPARK_REQUIRE(chunk % CHUNK_ALIGN == 0, "draft chunk must be a multiple of %d", CHUNK_ALIGN);
   DSPARK_REQUIRE(n_req >= 1, "n_req must be >= 1 (got %d)", n_req);
   DSPARK_REQUIRE(!work || (n_work >= 1 && n_groups >= 1 && n_groups <= (1 << 24)),
                  "a work list needs n_work >= 1 and n_groups in [1, 2^24]");
