@@ -699,12 +699,18 @@ struct PairRing {
   static constexpr int STAGE_BYTES = K_BYTES + DSTEP * ROWB;
   static constexpr int K_PIECES = K_BYTES / 1024;
   static constexpr int PER_WAVE = STAGE_BYTES / 1024 / DWAVES;
-  static constexpr int SMEM = STAGES * STAGE_BYTES;
+  // bf16 instance: the segment's bf16 Q rows are loaded into LDS with the
+  // ring (pair p's 32 tile rows at rows 32p .. 32p+31, 256 B each, swizzled
+  // by row), so no ordinary load precedes the ring's loads.
+  static constexpr int Q_OFF = STAGES * STAGE_BYTES;
+  static constexpr int Q_BYTES = KF32 ? 0 : 4 * 32 * ROWB;
+  static constexpr int SMEM = Q_OFF + Q_BYTES;
   static constexpr int OWN_SLOT = (STAGES - 1) * STAGE_BYTES;
   static constexpr int MERGE_FLOATS = 64 + 2;              // per lane: O^T, max, sum
   static constexpr int MERGE_BYTES = MERGE_FLOATS * WAVE * 4;
   static_assert(PER_WAVE * DWAVES * 1024 == STAGE_BYTES, "stage pieces must divide evenly over the waves");
   static_assert(SMEM <= 160 * 1024, "ring exceeds the LDS of a CU");
+  static_assert(Q_BYTES == 0 || Q_BYTES == PER_WAVE * DWAVES * 1024, "a Q load is one piece round");
   static_assert(4 * MERGE_BYTES <= OWN_SLOT, "the half merge must not touch the own rows");
 };
 
@@ -877,6 +883,13 @@ __device__ __forceinline__ T ld_const(const T* p) {
   return *(const __attribute__((address_space(4))) T*)p;
 }
 
+// ld_const of element i (wave-uniform; stated, so that the address stays in
+// scalar registers).
+template <class T>
+__device__ __forceinline__ T ld_const(const T* p, int i) {
+  return ld_const(p + __builtin_amdgcn_readfirstlane(i));
+}
+
 // The register operands must hold their loaded values here: the compiler
 // places its wait for them before this point, while no direct-to-LDS load
 // is in flight yet (a wait placed later would drain the ring).
@@ -931,8 +944,10 @@ __device__ __forceinline__ void draft_pair_item(const DraftArgs& a, unsigned cha
   const int full_lim = min(min(anc0, anc1), kend);  // keys below this need no mask
   // Q rows of the tile (rows outside the blocks read row 0 and are zeroed);
   // every load is issued before any is used.
+  // Q of the tile: bf16 Q through LDS (q_lds), else loaded here.
+  const bool q_lds = R::Q_BYTES > 0 && !a.q_f32;
   bf16x8 qf[8];
-  {
+  if (!q_lds) {
     const size_t qe = (size_t)(BLOCK_ROWS * (b0 + (row_ok ? blk : 0)) + (row_ok ? tok : 0)) * Q_ROW +
                       (size_t)(2 * g + (n & 1)) * HD + 8 * hh;
     if (a.q_f32) {
@@ -951,9 +966,9 @@ __device__ __forceinline__ void draft_pair_item(const DraftArgs& a, unsigned cha
       #pragma unroll
       for (int ks = 0; ks < 8; ++ks) qf[ks] = row_ok ? qf[ks] : zero8();
     }
+    settle(qf[0], qf[1], qf[2], qf[3], qf[4], qf[5], qf[6], qf[7]);
   }
   const int64_t coff = ld_const(a.ctx_off + r);
-  settle(qf[0], qf[1], qf[2], qf[3], qf[4], qf[5], qf[6], qf[7]);
 
   const char* kbase = static_cast<const char*>(a.k_ctx) + (size_t)g * a.head_stride * KEL;
   const char* vbase = reinterpret_cast<const char*>(a.v_ctx) + (size_t)g * a.head_stride * 2;
@@ -1011,6 +1026,36 @@ __device__ __forceinline__ void draft_pair_item(const DraftArgs& a, unsigned cha
   for (int D = 0; D < 4; ++D) st.o[D] = f32x16{};
   const int n_steps = kend > k0 ? (kend - k0 + DSTEP - 1) / DSTEP : 0;
 
+  // Nothing of the compiler's is in flight from here on (a previous item's
+  // stores have completed), so it places no vmcnt wait of its own among the
+  // ring's direct-to-LDS loads below.
+  __builtin_amdgcn_s_waitcnt(0x0f70);   // vmcnt(0)
+  // bf16 Q rows, issued first: slot row R = 32p + n holds tile row n of
+  // pair p (rows with no query read block 0, token 0 and are zeroed later).
+  const uint32_t q_lds_row = smem_lds + (uint32_t)(R::Q_OFF + (32 * pw + n) * ROWB);
+  if (q_lds) {
+    #pragma unroll
+    for (int i = 0; i < R::PER_WAVE; ++i) {
+      const int piece = wave * R::PER_WAVE + i;
+      const int row = 4 * piece + (lane >> 4);
+      const int bq = 2 * (row >> 5) + ((row >> 4) & 1);
+      const int tq = (row & 15) >> 1;
+      const bool ok = bq < nb && tq < BLOCK_ROWS;
+      const bf16* src = static_cast<const bf16*>(a.q) + (size_t)(BLOCK_ROWS * (b0 + (ok ? bq : 0)) + (ok ? tq : 0)) * Q_ROW +
+                        (size_t)(2 * g + (row & 1)) * HD + 8 * ((lane & 15) ^ swz(row));
+      lds_dma16(src, __builtin_amdgcn_readfirstlane(smem_lds + (uint32_t)(R::Q_OFF + piece * 1024)));
+    }
+  }
+  // After a barrier that follows the Q loads' landing.
+  auto read_q = [&]() {
+    const int sw = swz(32 * pw + n);
+    #pragma unroll
+    for (int ks = 0; ks < 8; ++ks) {
+      const bf16x8 x = *(const lds_bf16x8*)(uintptr_t)(q_lds_row + (((2 * ks + hh) ^ sw) << 4));
+      qf[ks] = row_ok ? x : zero8();
+    }
+  };
+
   // Own-block keys (bidirectional within each block), once per request,
   // ahead of the context (their loads share the ring's latency).  The
   // kh = 0 wave of each pair attends them.
@@ -1021,14 +1066,24 @@ __device__ __forceinline__ void draft_pair_item(const DraftArgs& a, unsigned cha
          },
          [&](int k) { return reinterpret_cast<const char*>(a.v_blk + own_row(k)); }, 15);
   }
-  if (n_steps > 0) {
-    #pragma unroll
-    for (int p = 0; p < R::STAGES - 1; ++p) issue(p);
-  }
+  // Only stages that hold context are loaded, so the number of ring loads
+  // still in flight behind a given one is known: all but the newest
+  // `behind` stages of PER_WAVE loads each have landed after wait_stages.
+  auto wait_stages = [](int behind) {
+    if (behind <= 0) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    else if (behind == 1) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(R::PER_WAVE) : "memory");
+    else if (behind == 2 || R::STAGES < 4) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * R::PER_WAVE) : "memory");
+    else asm volatile("s_waitcnt vmcnt(%0)" ::"n"(3 * R::PER_WAVE) : "memory");
+  };
+  static_assert(R::STAGES <= 4, "wait_stages covers at most three stages in flight");
+  const int prologue = min(R::STAGES - 1, n_steps);
+  #pragma unroll
+  for (int p = 0; p < R::STAGES - 1; ++p)
+    if (p < prologue) issue(p);
   if (last) {
-    if (n_steps > 0) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(R::PER_WAVE * (R::STAGES - 1)) : "memory");
-    else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    wait_stages(prologue);   // the Q and own rows, issued first, have landed
     asm volatile("s_barrier" ::: "memory");
+    if (q_lds) read_q();
     if (active && kh == 0) {
       // Register r of a lane in half hh holds block (r/4)%2 of the pair,
       // token 4(r/8) + r%4 (token 7: r = 11, 15); half 1 repeats half 0.
@@ -1053,18 +1108,17 @@ __device__ __forceinline__ void draft_pair_item(const DraftArgs& a, unsigned cha
         kt + 32 > full_lim, [&](int rg) { return acc_row(rg, 0) < lim; }, a.scale_log2);
   };
   if (n_steps > 0) {
-    // Every thread issues exactly PER_WAVE loads per stage (stages past the
-    // end re-read the clamped last row), so "stage s has landed" is always
-    // vmcnt(PER_WAVE * (STAGES - 2)) at the top of step s (the own rows,
-    // issued first, have landed by then too).
+    // Every thread issues exactly PER_WAVE loads per context stage, so at
+    // the top of step s the stages issued after stage s number
+    // min(n_steps - 1 - s, STAGES - 2).
     for (int s = 0; s < n_steps; ++s) {
-      asm volatile("s_waitcnt vmcnt(%0)" ::"n"(R::PER_WAVE * (R::STAGES - 2)) : "memory");
+      wait_stages(min(n_steps - 1 - s, R::STAGES - 2));
       asm volatile("s_barrier" ::: "memory");
-      issue(s + R::STAGES - 1);
+      if (s == 0 && q_lds && !last) read_q();
+      if (s + R::STAGES - 1 < n_steps) issue(s + R::STAGES - 1);
       if (active) compute(s);
     }
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    asm volatile("s_barrier" ::: "memory");
+    asm volatile("s_barrier" ::: "memory");   // every wave is done with the ring
   }
 
   // The key halves merge: the kh = 1 wave of each pair leaves its state in
@@ -1194,7 +1248,8 @@ struct MergeArgs {
   int draft;
 };
 
-// Workgroup (8r + g, t) merges request r, KV head g, row tile t: its id is
+// Workgroup (8r + g, t) merges request r, KV head g, row tile t (draft: block
+// t) of a request held by more than one chunk: its id is
 // g mod 8, so it runs on the XCD whose L2 holds the partials that the chunk
 // kernel's head-g workgroups (ids = g mod 8 as well) just wrote.
 __global__ __launch_bounds__(256) void merge_kernel(MergeArgs a) {
