@@ -68,7 +68,9 @@ int64_t dspark_attn_workspace_bytes(int n_req, int64_t key_rows_bound, int row_t
  * streams (0 .. its largest anchor): workgroup (run w, KV head g) processes
  * the records of run w:
  *   [n_work][8] segment records, grouped by run: request, k0, k1, partial
- *       slot (-1: one segment), first block, block count, largest anchor, 0
+ *       slot (-1: one segment), first block, block count, largest anchor,
+ *       0 or 1 + ctx_off[request] (when given, the kernel starts the
+ *       context loads without reading ctx_off first)
  *   [n_groups + 1] run ranges
  *   [n_req][4] request records: first partial slot, segment count, first
  *       block, block count

@@ -654,6 +654,7 @@ constexpr int CHUNK_ALIGN = 64;                      // fixed chunks are multipl
 struct DraftSeg {
   int r, k0, k1, pslot, b0, nb, amax;
   bool last;
+  int off1;   // 1 + ctx_off[r] when the plan carries it, else 0
 };
 
 // A pair of draft blocks is attended as one 32-row tile: row n is block
@@ -968,7 +969,8 @@ __device__ __forceinline__ void draft_pair_item(const DraftArgs& a, unsigned cha
     }
     settle(qf[0], qf[1], qf[2], qf[3], qf[4], qf[5], qf[6], qf[7]);
   }
-  const int64_t coff = ld_const(a.ctx_off + r);
+  const int off1 = __builtin_amdgcn_readfirstlane(sg.off1);
+  const int64_t coff = off1 > 0 ? (int64_t)(off1 - 1) : ld_const(a.ctx_off + r);
 
   const char* kbase = static_cast<const char*>(a.k_ctx) + (size_t)g * a.head_stride * KEL;
   const char* vbase = reinterpret_cast<const char*>(a.v_ctx) + (size_t)g * a.head_stride * 2;
@@ -1209,7 +1211,7 @@ __global__ __launch_bounds__(DWAVES * WAVE) void draft_attn_kernel(DraftArgs a) 
         #pragma unroll
         for (int j = 0; j < WORK_INTS; ++j) w[j] = ld_const(a.work + WORK_INTS * i + j);
       }
-      const DraftSeg sg{w[0], w[1], w[2], w[3], w[4], w[5], w[6], w[2] >= w[6]};
+      const DraftSeg sg{w[0], w[1], w[2], w[3], w[4], w[5], w[6], w[2] >= w[6], w[7]};
       draft_pair_item<INDEXED, KF32>(a, smem, sg, g);
       __syncthreads();   // the next segment refills the ring the last one read
     }
@@ -1226,7 +1228,7 @@ __global__ __launch_bounds__(DWAVES * WAVE) void draft_attn_kernel(DraftArgs a) 
   int amax = 0;
   for (int b = 0; b < nb; ++b) amax = max(amax, a.anchors[b0 + b]);
   const DraftSeg sg{r, c * a.chunk, min(c * a.chunk + a.chunk, ctx), nch > 1 ? first + c : -1, b0, nb, amax,
-                    c == nch - 1};
+                    c == nch - 1, 0};
   draft_pair_item<INDEXED, KF32>(a, smem, sg, g);
 }
 

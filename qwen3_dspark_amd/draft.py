@@ -117,29 +117,36 @@ class DraftBatch:
                                    physical_context_rows=self.physical_context_rows,
                                    key_element_bytes=key_element_bytes, value_element_bytes=value_element_bytes)
 
-    def device_offsets(self, capacity):
-        """int64 per-request first kernel row: offsets as given, or - for a
+    def kernel_offsets(self, capacity):
+        """Per-request first kernel row: offsets as given, or - for a
         head-major slotted pool of `capacity` positions - slot*8*capacity +
         position, the row index in units of 128 elements."""
+        offs = list(self.context_offsets)
+        if capacity:
+            offs = [o + (KV_HEADS - 1) * capacity * (o // capacity) for o in offs]
+        return offs
+
+    def device_offsets(self, capacity):
+        """kernel_offsets(capacity) as an int64 device vector."""
         if capacity not in self._offsets:
-            offs = list(self.context_offsets)
-            if capacity:
-                offs = [o + (KV_HEADS - 1) * capacity * (o // capacity) for o in offs]
-            self._offsets[capacity] = upload(self.device, offs, torch.int64)
+            self._offsets[capacity] = upload(self.device, self.kernel_offsets(capacity), torch.int64)
         return self._offsets[capacity]
 
-    def work(self, chunk, runs=None):
+    def work(self, chunk, runs=None, capacity=None):
         """(device list, segment count, run count) of the draft plan: fixed
         chunks longest first (runs None), or `runs` balanced runs per KV head
-        (0: one per CU).  Uploaded once per plan."""
-        key = (chunk, runs)
+        (0: one per CU).  With a pool capacity (0: flat rows) the segment
+        records also carry each request's kernel offset.  Uploaded once per
+        plan."""
+        key = (chunk, runs, capacity)
         if key not in self._work:
             flat = [a for b in self.anchors for a in b]
+            offs = None if capacity is None else self.kernel_offsets(capacity)
             if runs is None:
-                plan = draft_work(self.context_lengths, self.cu_blocks_host, flat, chunk=chunk)
+                plan = draft_work(self.context_lengths, self.cu_blocks_host, flat, chunk=chunk, offsets=offs)
             else:
                 runs = runs or draft_run_count(sum(max(b) for b in self.anchors), cu_count(self.device))
-                plan = draft_work(self.context_lengths, self.cu_blocks_host, flat, runs)
+                plan = draft_work(self.context_lengths, self.cu_blocks_host, flat, runs, offsets=offs)
             records, n_seg, n_runs = plan
             self._work[key] = (upload_work(records, self.device), n_seg, n_runs)
         return self._work[key]
@@ -179,24 +186,25 @@ class HipDraftAttention:
         self._geometry = None
 
     def _context_geometry(self, keys, batch):
-        """(kernel offsets, token stride, head stride) for the pool form."""
+        """(offset capacity for DraftBatch.kernel_offsets, token stride, head
+        stride) for the pool form."""
         if keys.ndim == 3 and tuple(keys.shape[1:]) == (KV_HEADS, HEAD_DIM):
             if batch.context_indices is not None:
                 if batch.index_max() >= keys.shape[0]:
                     raise ValueError('Context rows addressed beyond the context tensor')
             elif any(o + c > keys.shape[0] for o, c in zip(batch.context_offsets, batch.context_lengths)):
                 raise ValueError('Context rows addressed beyond the context tensor')
-            return batch.device_offsets(0), KV_HEADS * HEAD_DIM, HEAD_DIM
+            return 0, KV_HEADS * HEAD_DIM, HEAD_DIM
         if keys.ndim == 4 and keys.shape[1] == KV_HEADS and keys.shape[3] == HEAD_DIM:
             slots, cap = keys.shape[0], keys.shape[2]
             if batch.context_indices is not None:
                 if slots != 1 or batch.index_max() >= cap:
                     raise ValueError('An indexed pool must be [1,8,N,128] with indices < N')
-                return batch.device_offsets(0), HEAD_DIM, cap * HEAD_DIM
+                return 0, HEAD_DIM, cap * HEAD_DIM
             for o, c in zip(batch.context_offsets, batch.context_lengths):
                 if o // cap >= slots or (o % cap) + c > cap:
                     raise ValueError('Context rows addressed beyond their pool slot')
-            return batch.device_offsets(cap), HEAD_DIM, cap * HEAD_DIM
+            return cap, HEAD_DIM, cap * HEAD_DIM
         raise ValueError('Context K/V must be [rows,8,128], [slots,8,capacity,128] or [1,8,N,128]')
 
     def __call__(self, query, block_keys, block_values, context_keys, context_values, batch, *, scale):
@@ -231,10 +239,11 @@ class HipDraftAttention:
         if self._geometry_for is None or self._geometry_for[0] is not batch or self._geometry_for[1] != key[1]:
             self._geometry = self._context_geometry(context_keys, batch)
             self._geometry_for = key
-        offsets, tok_stride, head_stride = self._geometry
+        capacity, tok_stride, head_stride = self._geometry
+        offsets = batch.device_offsets(capacity)
         out = torch.empty(query.shape, dtype=torch.bfloat16, device=self.device)
         bound = max(batch.context_rows, 1)
-        work, n_work, n_runs = batch.work(self.chunk, self.runs)
+        work, n_work, n_runs = batch.work(self.chunk, self.runs, capacity)
         need = _native.load().dspark_attn_workspace_bytes(n_work, 0, batch.max_blocks, self.chunk)
         ws = self._workspace.get(need)
         _native.call('dspark_draft_attn_fwd', _native.ptr(query), int(query.dtype == torch.float32),

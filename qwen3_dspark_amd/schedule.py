@@ -243,7 +243,7 @@ def segment_plan(split, query_lengths, key_lengths, starts, groups, chunk, capac
     return padded + out[base + runs + 1:], seg_cap, run_cap
 
 
-def draft_work(context_lengths, cu_blocks, anchors, groups=None, *, chunk=None):
+def draft_work(context_lengths, cu_blocks, anchors, groups=None, *, chunk=None, offsets=None):
     """Draft plan: (flat int32 list, segment count, run count).  Request r
     streams its context up to its largest anchor (the rows any of its blocks
     sees), and the segment ending a request also attends its blocks' own rows.
@@ -258,10 +258,13 @@ def draft_work(context_lengths, cu_blocks, anchors, groups=None, *, chunk=None):
         row).
 
       segment: request, k0, k1, partial slot (-1: one segment), first block,
-               block count, largest anchor, 0
+               block count, largest anchor, 1 + offsets[r] (0 without
+               offsets, or when it does not fit in 31 bits: the kernel then
+               reads ctx_off[r] itself)
       request: first partial slot, segment count, first block, block count
     """
     amax = [max(anchors[cu_blocks[r]:cu_blocks[r + 1]]) for r in range(len(context_lengths))]
+    off1 = [0] * len(amax) if offsets is None else [int(o) + 1 if 0 <= int(o) < 2 ** 31 - 1 else 0 for o in offsets]
     if any(not 0 <= a <= int(c) for a, c in zip(amax, context_lengths)):
         raise ValueError('Anchors must lie in [0, context length]')
     if chunk is not None:
@@ -276,7 +279,8 @@ def draft_work(context_lengths, cu_blocks, anchors, groups=None, *, chunk=None):
         per_run = _balanced_runs(amax, groups, DRAFT_TILE, DRAFT_SEGMENT_COST,
                                  [1.0 + DRAFT_BLOCK_WEIGHT * (b - 1) for b in nb])
     return _flatten(len(amax), per_run,
-                    lambda r, k0, k1, slot: (r, k0, k1, slot, cu_blocks[r], cu_blocks[r + 1] - cu_blocks[r], amax[r], 0),
+                    lambda r, k0, k1, slot: (r, k0, k1, slot, cu_blocks[r], cu_blocks[r + 1] - cu_blocks[r], amax[r],
+                                             off1[r]),
                     lambda r, first, count: (first, count, cu_blocks[r], cu_blocks[r + 1] - cu_blocks[r]))
 
 
