@@ -1012,7 +1012,7 @@ __device__ __forceinline__ void draft_pair_item(const DraftArgs& a, unsigned cha
         const int k = 4 * (piece - R::K_PIECES) + (lane >> 4);
         src = v_src(k) + 16 * ((lane & 15) ^ swz(k & sw_mask));
       }
-      lds_dma16(src, __builtin_amdgcn_readfirstlane(slot + (uint32_t)(piece * 1024)));
+      lds_dma16_nt(src, __builtin_amdgcn_readfirstlane(slot + (uint32_t)(piece * 1024)));
     }
   };
   auto issue = [&](int step) {
