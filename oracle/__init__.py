@@ -16,10 +16,14 @@ and bench.py's cpu_baseline leg use it, and only to check results.
                   q/k RMSNorm, RoPE) in float64.
   draft_proj.py - the draft's context projection (fc, context norm, per-layer
                   k_proj / k_norm / RoPE / v_proj) in float64.
+  draft_model.py - the draft backbone over cached context (every draft
+                  layer: norms, projections, RoPE, multi-block attention,
+                  o_proj, MLP; final norm) in float64.
 
 Pinning (see tests/test_oracle_golden.py): every function is checked against
 the reference tests' literal vectors (tests/golden/reference_vectors.json),
 closed forms (uniform attention, position ramps), invariants, brute force on
 tiny inputs and torch's scaled_dot_product_attention on explicit masks;
-qkv.py and draft_proj.py against transformers' own Qwen3 modules.
+qkv.py, draft_proj.py and draft_model.py against transformers' own Qwen3
+modules (draft_model.py also against torch's SDPA and closed forms).
 """

@@ -192,3 +192,43 @@ def test_poison_isolation_and_contract(dev):
     with pytest.raises(ValueError):
         kernel(c['q'].to(dev), c['bk'].to(dev), c['bv'].to(dev), c['ctx_k'][:10].to(dev), c['ctx_v'][:10].to(dev),
                batch, scale=SCALE)
+
+
+def test_config1_fp32_with_rope_at_absolute_positions(dev):
+    """The single-layer fp32 workload as specified: 2 requests with contexts
+    128 and 96, one 7-row block each at anchor = context length, 16/8 heads,
+    d128.  Seeded CPU FP32 N(0,1) draws in the order K, V, Q
+    (scripts/probe_varlen.py:105-110), RoPE theta 1e6 applied to K at
+    positions 0 .. c+6 and to Q at the block's positions c .. c+6
+    (model.py:22-24 rotate; float32 angles as the model forms them).  Q and
+    K go to the kernel in fp32 (rounded to bf16 as it loads them, the
+    reference's cast at the kernel boundary), V in bf16 as the kernel takes
+    it; the oracle sees the fp32 values."""
+    from oracle import qkv
+    from qwen3_dspark_amd.draft import DraftBatch, HipDraftAttention
+    contexts = [128, 96]
+    gen = torch.Generator().manual_seed(SEED)
+    freqs = qkv.inv_freq()
+    ks, vs, qs = [], [], []
+    for c in contexts:
+        k = torch.randn(c + 7, 8, 128, generator=gen)
+        v = torch.randn(c + 7, 8, 128, generator=gen)
+        q = torch.randn(7, 16, 128, generator=gen)
+        ks.append(torch.from_numpy(qkv.rope(k.numpy(), np.arange(c + 7), freqs)).float())
+        vs.append(v)
+        qs.append(torch.from_numpy(qkv.rope(q.numpy(), np.arange(c, c + 7), freqs)).float())
+    ctx_k = torch.cat([k[:c] for k, c in zip(ks, contexts)])
+    ctx_v = torch.cat([v[:c] for v, c in zip(vs, contexts)]).to(torch.bfloat16)
+    bk = torch.cat([k[c:] for k, c in zip(ks, contexts)])
+    bv = torch.cat([v[c:] for v, c in zip(vs, contexts)]).to(torch.bfloat16)
+    q = torch.cat(qs)
+    batch = DraftBatch(dev, [0, contexts[0]], contexts, [[c] for c in contexts])
+    out = HipDraftAttention(dev)(q.to(dev), bk.to(dev), bv.to(dev), ctx_k.to(dev), ctx_v.to(dev), batch,
+                                 scale=SCALE)
+    torch.cuda.synchronize()
+    ref = np.concatenate([attention.draft_attention(qs[r].double().numpy(), ks[r][:c].double().numpy(),
+                                                    vs[r][:c].double().numpy(), ks[r][c:].double().numpy(),
+                                                    vs[r][c:].double().numpy(), [c], scale=SCALE)
+                          for r, c in enumerate(contexts)])
+    stats = attention_gate(f64(out), ref, [(0, 7), (7, 14)])
+    say(f'[draft config1 rope] max |d| {stats[0]["max_abs"]:.2e} mean {stats[0]["mean_abs"]:.2e}')

@@ -86,8 +86,9 @@ def test_fused_hooks_two_rounds_match_cpu_model():
 
 
 def test_varlen_callback_matches_fused_path():
-    """varlen_attention_forward over the store's materialised gather equals
-    the fused callback bit for bit (same kernel family, same inputs)."""
+    """varlen_attention_forward over a PackedLayout with interleaved
+    physical rows equals a direct kernel call on the gathered K/V bit for
+    bit, and meets the attention gate against the oracle."""
     from qwen3_dspark_amd.hf_hooks import varlen_attention_forward
     from qwen3_dspark_amd.kernels import HipVarlenKernel
     from qwen3_dspark_amd.layout import PackedLayout
@@ -116,6 +117,17 @@ def test_varlen_callback_matches_fused_path():
     k, v = layout.gather_kv(key, value)
     direct = kernel(query[0].transpose(0, 1).contiguous(), k, v, layout, scale=128 ** -0.5)
     assert torch.equal(out[0], direct)
+    # and against the oracle: gather by the reference's physical indices
+    # (varlen_target.py:74-82), bottom-right causal attention per request
+    # (varlen_target.py:98-112)
+    from helpers import attention_gate, f64, segments
+    from oracle import attention as oracle_attention
+    idx = layout.gather_indices.cpu().numpy()
+    kk, vv = f64(key[0].transpose(0, 1))[idx], f64(value[0].transpose(0, 1))[idx]
+    cu_q, cu_k = layout.cu_query.tolist(), layout.cu_key.tolist()
+    ref = oracle_attention.varlen_attention(f64(query[0].transpose(0, 1)), kk, vv, cu_q, cu_k, causal=True,
+                                            scale=128 ** -0.5)
+    attention_gate(f64(out[0]), ref, segments(cu_q))
     with pytest.raises(ValueError, match='metadata-only'):
         varlen_attention_forward(None, query, key, value, torch.ones(1), packed_layout=layout,
                                  packed_varlen_kernel=kernel)

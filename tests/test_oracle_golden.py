@@ -347,3 +347,93 @@ def test_draft_projection_oracle_matches_transformers_qwen3_modules():
     for wrong_ctx in (f, qkv.rms_norm(f.reshape(t, 2, 128), np.ones(128), 1e-6).reshape(t, hidden)):
         v_bad = (wrong_ctx @ layers[0][2].weight.detach().numpy().T).reshape(t, 8, 128)
         assert not np.allclose(v_bad, expect[0][1], atol=1e-3)
+
+
+def test_draft_backbone_oracle_matches_transformers_modules_and_closed_forms():
+    """The draft backbone oracle (oracle/draft_model.py) against an
+    independent float32 evaluation: transformers' Qwen3RMSNorm, Qwen3MLP,
+    Qwen3RotaryEmbedding + apply_rotary_pos_emb and torch's SDPA on the
+    block mask of oracle.semantics.block_mask (itself pinned to the
+    reference's truth table above), 2 layers with 3 blocks over a 40-row
+    context.  Closed forms: with o_proj and the MLP's down projection zero a
+    layer is the identity (residuals), so the output is the final RMSNorm of
+    the block embeddings; a planted mistake (the MLP residual dropped) fails."""
+    from torch import nn
+    from transformers import Qwen3Config
+    from transformers.models.qwen3 import modeling_qwen3 as mq
+
+    from oracle import draft_model, semantics
+    hidden, c, anchors = 256, 40, [40, 0, 17]
+    cfg = Qwen3Config(vocab_size=64, hidden_size=hidden, intermediate_size=384, num_hidden_layers=1,
+                      num_attention_heads=16, num_key_value_heads=8, head_dim=128, rope_theta=1e6)
+    torch.manual_seed(11)
+    eps = cfg.rms_norm_eps
+
+    def norm(n):
+        m = mq.Qwen3RMSNorm(n, eps=eps)
+        with torch.no_grad():
+            m.weight.uniform_(0.5, 1.5)
+        return m
+    layers = []
+    for _ in range(2):
+        layers.append(dict(input_norm=norm(hidden), q=nn.Linear(hidden, 2048, bias=False),
+                           k=nn.Linear(hidden, 1024, bias=False), v=nn.Linear(hidden, 1024, bias=False),
+                           o=nn.Linear(2048, hidden, bias=False), q_norm=norm(128), k_norm=norm(128),
+                           post_norm=norm(hidden), mlp=mq.Qwen3MLP(cfg)))
+    final = norm(hidden)
+    rot = mq.Qwen3RotaryEmbedding(cfg)
+    z0 = torch.randn(1, 21, hidden)
+    ctx_kv = [(torch.randn(1, 8, c, 128), torch.randn(1, 8, c, 128)) for _ in layers]
+    pos = (torch.tensor(anchors)[:, None] + torch.arange(7)).reshape(1, -1)
+    visible = torch.from_numpy(np.asarray(semantics.block_mask(anchors, 7, c))).reshape(21, c + 21)
+
+    def reference(mods, zero=False):
+        z = z0
+        cos, sin = rot(z, pos)
+        with torch.no_grad():
+            for m, (ck, cv) in zip(mods, ctx_kv):
+                x = m['input_norm'](z)
+                q = m['q_norm'](m['q'](x).view(1, 21, 16, 128)).transpose(1, 2)
+                k = m['k_norm'](m['k'](x).view(1, 21, 8, 128)).transpose(1, 2)
+                v = m['v'](x).view(1, 21, 8, 128).transpose(1, 2)
+                q, k = mq.apply_rotary_pos_emb(q, k, cos, sin)
+                kk = torch.cat((ck, k), 2).repeat_interleave(2, 1)
+                vv = torch.cat((cv, v), 2).repeat_interleave(2, 1)
+                o = torch.nn.functional.scaled_dot_product_attention(q, kk, vv, attn_mask=visible)
+                z = z + m['o'](o.transpose(1, 2).reshape(1, 21, -1))
+                z = z + m['mlp'](m['post_norm'](z))
+            return final(z)[0].numpy()
+
+    def weights(m):
+        w = lambda mod: mod.weight.detach().numpy()
+        return dict(input_norm=w(m['input_norm']), q_proj=w(m['q']), k_proj=w(m['k']), v_proj=w(m['v']),
+                    o_proj=w(m['o']), q_norm=w(m['q_norm']), k_norm=w(m['k_norm']), post_norm=w(m['post_norm']),
+                    gate=w(m['mlp'].gate_proj), up=w(m['mlp'].up_proj), down=w(m['mlp'].down_proj))
+    kv = [(k[0].transpose(0, 1).numpy(), v[0].transpose(0, 1).numpy()) for k, v in ctx_kv]
+    out = draft_model.draft_backbone(z0[0].numpy(), [weights(m) for m in layers], kv, anchors,
+                                     final.weight.detach().numpy(), eps=eps)
+    np.testing.assert_allclose(out, reference(layers), rtol=2e-4, atol=2e-4)
+    # closed form: zero o_proj and down projection -> the identity per layer
+    with torch.no_grad():
+        for m in layers:
+            m['o'].weight.zero_()
+            m['mlp'].down_proj.weight.zero_()
+    out = draft_model.draft_backbone(z0[0].numpy(), [weights(m) for m in layers], kv, anchors,
+                                     final.weight.detach().numpy(), eps=eps)
+    z = z0[0].double().numpy()
+    closed = final.weight.detach().double().numpy() * z / np.sqrt((z * z).mean(-1, keepdims=True) + eps)
+    np.testing.assert_allclose(out, closed, rtol=1e-12, atol=1e-12)
+    # a planted mistake in a copy of the layer (MLP residual dropped) fails the library check
+    torch.manual_seed(12)
+    fresh = [dict(m, mlp=mq.Qwen3MLP(cfg), o=nn.Linear(2048, hidden, bias=False)) for m in layers]
+    w = [weights(m) for m in fresh]
+    good = draft_model.draft_backbone(z0[0].numpy(), w, kv, anchors, final.weight.detach().numpy(), eps=eps)
+    ref = reference(fresh)
+    np.testing.assert_allclose(good, ref, rtol=2e-4, atol=2e-4)
+    real_mlp = draft_model.mlp
+    try:
+        draft_model.mlp = lambda y, gate, up, down: np.zeros((y.shape[0], np.asarray(down).shape[0]))
+        bad = draft_model.draft_backbone(z0[0].numpy(), w, kv, anchors, final.weight.detach().numpy(), eps=eps)
+    finally:
+        draft_model.mlp = real_mlp
+    assert not np.allclose(bad, ref, atol=1e-2)
