@@ -67,6 +67,9 @@ def parse():
     ap.add_argument('--traffic-probe', action='store_true',
                     help='untimed run for hardware-counter passes: 3 verification-attention and 3 draft-attention '
                          'layers of the workload, then a 1 GiB device-to-device copy as the counter calibration')
+    ap.add_argument('--stream-probe', action='store_true',
+                    help='only measure the streaming-read ceiling (dspark_stream_read over 16 GiB, default and '
+                         'non-temporal loads, 512-2048 workgroups)')
     ap.add_argument('--mfma-probe', action='store_true',
                     help='only run the draft kernels for a rocprofv3 --pmc MfmaUtil MfmaFlopsBF16 pass')
     ap.add_argument('--cpu-verify-layers', type=int, default=VERIFY_LAYERS, help='verify layers in the CPU sample')
@@ -117,6 +120,8 @@ def main():
         return traffic_probe(args)
     if args.mfma_probe:
         return mfma_probe(args)
+    if args.stream_probe:
+        return stream_probe()
     import numpy as np
     import torch
 
@@ -568,6 +573,43 @@ def traffic_probe(args):
                       'context_rows': sum(contexts),
                       'calibration_copy_bytes': 1 << 30,
                       'streaming_reference': streaming_reference(dev, src, dst)}), flush=True)
+
+
+def stream_probe(gib=16, reps=10):
+    """The streaming-read ceiling: dspark_stream_read over a `gib` GiB
+    buffer (far beyond the last-level cache), each workgroup streaming its
+    own contiguous slice, for the default and the non-temporal cache policy
+    and 512 / 1024 / 2048 workgroups of 256 threads.  Median of `reps`
+    event-timed launches after one warm-up, on the launch stream."""
+    import torch
+
+    from qwen3_dspark_amd import _native
+    dev = torch.device('cuda:0')
+    torch.cuda.set_device(dev)
+    nbytes = gib << 30
+    src = torch.ones(nbytes // 4, dtype=torch.int32, device=dev)
+    out = torch.empty(4096, dtype=torch.int32, device=dev)
+    stream = torch.cuda.current_stream(dev)
+    rows = []
+    for nt in (0, 1):
+        for wgs in (512, 1024, 2048):
+            def launch():
+                _native.call('dspark_stream_read', src.data_ptr(), nbytes, nt, wgs, out.data_ptr(),
+                             stream.cuda_stream)
+            launch()
+            times = []
+            for _ in range(reps):
+                a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                a.record(stream)
+                launch()
+                b.record(stream)
+                b.synchronize()
+                times.append(a.elapsed_time(b))
+            ms = sorted(times)[len(times) // 2]
+            rows.append({'nontemporal': bool(nt), 'workgroups': wgs, 'median_ms': round(ms, 4),
+                         'gbs': round(nbytes / ms / 1e6, 1), 'frac_of_8tbs': round(nbytes / ms / 1e6 / HBM_PEAK_GBS, 4)})
+            log(f'[stream] nt={nt} workgroups={wgs}: {rows[-1]["gbs"]} GB/s')
+    print(json.dumps({'stream_probe': rows, 'bytes': nbytes, 'threads_per_workgroup': 256}), flush=True)
 
 
 def streaming_reference(dev, src, dst, reps=10):

@@ -28,6 +28,16 @@ const char* dspark_last_error(void);
 int dspark_abi_version(void);
 
 /*
+ * Measurement utility, no reference counterpart: reads `bytes` (a multiple
+ * of 16) of device memory at `src` with `workgroups` workgroups of 256
+ * threads, each streaming its own contiguous slice with 16-byte loads
+ * (nontemporal = 1: non-temporal cache policy), and writes one uint32
+ * checksum per workgroup to out[workgroups].  Its rate is the streaming-read
+ * ceiling the attention kernels' bandwidth is compared with.
+ */
+int dspark_stream_read(const void* src, int64_t bytes, int nontemporal, int workgroups, void* out, void* stream);
+
+/*
  * Bytes of split-K workspace needed by an attention call.  Layout: FP32
  * partial outputs, then FP32 (max, sum) pairs, for `n` partial slots of 8 KV
  * heads x `row_tiles` 16-row tiles (row_tiles = ceil(max_q/8) for

@@ -12,7 +12,8 @@ CSRC = os.path.join(HERE, 'csrc')
 BUILD_DIR = os.path.join(HERE, '_build')
 LIB_NAME = 'libdspark_amd.so'
 LIB_PATH = os.path.join(BUILD_DIR, LIB_NAME)
-SOURCES = ('attn.hip', 'kv.hip', 'layout.hip', 'prologue.hip', 'project.hip', 'sample.hip', 'errors.cpp')
+SOURCES = ('attn.hip', 'kv.hip', 'layout.hip', 'prologue.hip', 'project.hip', 'sample.hip', 'measure.hip',
+           'errors.cpp')
 ARCH = 'gfx950'
 # Packed FP32 VALU ops are disabled for all device code.
 FLAGS = ('--offload-arch=' + ARCH, '-O3', '-std=c++17', '-shared', '-fPIC',
