@@ -45,43 +45,86 @@ __device__ __forceinline__ double block_sum(double x, double* buf) {
 // ---------------------------------------------------------------------------
 // Row statistics: per (row, chunk of ST_CHUNK logits) the max of x/T and the
 // sum of exp(x/T - max); a non-finite x or x/T marks the row in `bad`.
-// Division by T > 0 is monotone, so the first pass takes the max of the raw
-// logits and divides once: max(x/T) == max(x)/T exactly.
+// Division by T > 0 is monotone, so the max is taken over the raw logits and
+// divided once: max(x/T) == max(x)/T exactly; T == 1 divides nothing
+// (x/1 == x).  One pass over the logits: each thread keeps its ST_PER
+// values in registers (bf16 and fp32 logits are exact in float) between the
+// max and the sum.  A full chunk of a 16-byte aligned row is read with
+// 16-byte loads (a wave reads 1 KiB contiguous per load); other chunks with
+// element loads.
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void row_stats_kernel(const void* logits, int dtype, int64_t row_stride, int vocab,
-                                                        double temperature, int chunks, double* stats,
-                                                        int32_t* bad) {
+constexpr int ST_THREADS = 256;
+constexpr int ST_PER = ST_CHUNK / ST_THREADS;   // logits per thread
+
+template <int DT>   // 0: bf16 logits, 1: fp32
+__global__ __launch_bounds__(ST_THREADS) void row_stats_kernel(const void* logits, int64_t row_stride, int vocab,
+                                                               double temperature, int chunks, double* stats,
+                                                               int32_t* bad) {
+  constexpr int VEC = DT == 0 ? 8 : 4;                 // logits per 16-byte load
   __shared__ double buf[4];
   const int row = blockIdx.x / chunks;
   const int c = blockIdx.x - row * chunks;
   const int v0 = c * ST_CHUNK;
   const int v1 = min(v0 + ST_CHUNK, vocab);
-  const int64_t base = (int64_t)row * row_stride;
-  double xmax = -INFINITY;
+  const int64_t base = (int64_t)row * row_stride + v0;
+  const int tid = threadIdx.x;
+  const bool vec = v1 - v0 == ST_CHUNK && ((base * (DT == 0 ? 2 : 4)) & 15) == 0 &&
+                   ((uintptr_t)logits & 15) == 0;        // uniform over the workgroup
+  float xs[ST_PER];
+  if (vec) {
+    // value i of this thread: element VEC * (tid + ST_THREADS * (i / VEC)) + i % VEC
+    #pragma unroll
+    for (int j = 0; j < ST_PER / VEC; ++j) {
+      const int64_t e = base + (int64_t)VEC * (tid + ST_THREADS * j);
+      if (DT == 0) {
+        const bf16x8 v = *reinterpret_cast<const bf16x8*>(static_cast<const bf16*>(logits) + e);
+        #pragma unroll
+        for (int u = 0; u < VEC; ++u) xs[VEC * j + u] = (float)v[u];
+      } else {
+        const f32x4 v = *reinterpret_cast<const f32x4*>(static_cast<const float*>(logits) + e);
+        #pragma unroll
+        for (int u = 0; u < VEC; ++u) xs[VEC * j + u] = v[u];
+      }
+    }
+  } else {
+    // value i of this thread: element tid + ST_THREADS * i (when below v1)
+    #pragma unroll
+    for (int i = 0; i < ST_PER; ++i) {
+      const int v = v0 + tid + ST_THREADS * i;
+      xs[i] = v < v1 ? (float)load_logit(logits, DT, (int64_t)row * row_stride + v) : -INFINITY;
+    }
+  }
+  auto held = [&](int i) { return vec || v0 + tid + ST_THREADS * i < v1; };
+  float xmax = -INFINITY;
   bool nonfinite = false;
-  for (int v = v0 + threadIdx.x; v < v1; v += blockDim.x) {
-    const double x = load_logit(logits, dtype, base + v);
-    nonfinite |= !isfinite(x);
-    xmax = fmax(xmax, x);
+  #pragma unroll
+  for (int i = 0; i < ST_PER; ++i) {
+    if (!held(i)) continue;
+    nonfinite |= !isfinite(xs[i]);
+    xmax = fmaxf(xmax, xs[i]);
   }
   #pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) xmax = fmax(xmax, __shfl_xor(xmax, off));
-  const int wave = threadIdx.x >> 6;
-  if ((threadIdx.x & 63) == 0) buf[wave] = xmax;
+  for (int off = 32; off >= 1; off >>= 1) xmax = fmaxf(xmax, __shfl_xor(xmax, off));
+  const int wave = tid >> 6;
+  if ((tid & 63) == 0) buf[wave] = xmax;
   __syncthreads();
-  const double m = fmax(fmax(buf[0], buf[1]), fmax(buf[2], buf[3])) / temperature;
+  const bool unit = temperature == 1.0;
+  const double mx = fmax(fmax(buf[0], buf[1]), fmax(buf[2], buf[3]));
+  const double m = unit ? mx : mx / temperature;
   double sum = 0.0;
-  for (int v = v0 + threadIdx.x; v < v1; v += blockDim.x) {
-    const double y = load_logit(logits, dtype, base + v) / temperature;
+  #pragma unroll
+  for (int i = 0; i < ST_PER; ++i) {
+    if (!held(i)) continue;
+    const double y = unit ? (double)xs[i] : (double)xs[i] / temperature;
     nonfinite |= !isfinite(y);
     sum += exp(y - m);
   }
   sum = block_sum(sum, buf);
-  if (threadIdx.x == 0) {
+  if (tid == 0) {
     stats[2 * ((int64_t)row * chunks + c)] = m;
     stats[2 * ((int64_t)row * chunks + c) + 1] = sum;
   }
-  if (__builtin_amdgcn_ballot_w64(nonfinite) && (threadIdx.x & 63) == 0 && bad) bad[row] = 1;   // vector store
+  if (__builtin_amdgcn_ballot_w64(nonfinite) && (tid & 63) == 0 && bad) bad[row] = 1;   // vector store
 }
 
 // Combined (max, sum) of one row from its chunk statistics.
@@ -487,8 +530,12 @@ extern "C" int dspark_logit_row_stats(const void* logits, int dtype, int rows, i
   DSPARK_REQUIRE(temperature > 0.0 && temperature < DBL_MAX, "temperature must be finite and positive");
   const int64_t grid = (int64_t)rows * stat_chunks(vocab);
   DSPARK_REQUIRE(grid <= 0x7fffffffLL, "too many rows");
-  hipLaunchKernelGGL(row_stats_kernel, dim3((unsigned)grid), dim3(256), 0, static_cast<hipStream_t>(stream), logits,
-                     dtype, row_stride, vocab, temperature, stat_chunks(vocab), stats, bad);
+  if (dtype == 0)
+    hipLaunchKernelGGL(row_stats_kernel<0>, dim3((unsigned)grid), dim3(ST_THREADS), 0, static_cast<hipStream_t>(stream),
+                       logits, row_stride, vocab, temperature, stat_chunks(vocab), stats, bad);
+  else
+    hipLaunchKernelGGL(row_stats_kernel<1>, dim3((unsigned)grid), dim3(ST_THREADS), 0, static_cast<hipStream_t>(stream),
+                       logits, row_stride, vocab, temperature, stat_chunks(vocab), stats, bad);
   return launch_status("row_stats_kernel");
 }
 
