@@ -19,7 +19,7 @@
 //                 request for all of its blocks.
 //
 // varlen / verify MFMA mapping (v_mfma_f32_16x16x32_bf16, wave64):
-//   S^T[key][row] = K[key][:] . Q[row][:]   A = K (16 keys), B = Q^T
+//   S^T[key][row] = K[key][:] . Q[row][:]   A = K (16 keys, via LDS), B = Q^T
 //   O^T[d][row]  += V^T[d][key] P^T[key][row]  A = V^T (via LDS), B = P^T
 // A 16-row tile holds 8 query tokens x the 2 query heads of one KV head
 // (row = 2*token + head_in_group).  The S^T accumulator leaves every lane
@@ -283,8 +283,10 @@ struct VarlenArgs {
   float scale_log2;
 };
 
-constexpr int VARLEN_SMEM = 4 * 16 * OPITCH * 4 + 4 * 16 * 2 * 4;   // 34304 B (>= 4*32*256)
-static_assert(VARLEN_SMEM >= 4 * KT * ROWB, "merge buffer must cover the V tiles");
+// Per wave a 32-key K tile and a 32-key V tile (8 KiB each); the 4-wave
+// merge buffer (34,304 B) reuses the start once the tiles are done.
+constexpr int VARLEN_SMEM = 2 * 4 * KT * ROWB;                      // 65536 B
+static_assert(VARLEN_SMEM >= 4 * 16 * OPITCH * 4 + 4 * 16 * 2 * 4, "the tiles must cover the merge buffer");
 
 // One key segment of one request: keys [k0, k1) of request r, whose
 // queries start at row q0 (ql of them) and whose keys number kl; start is
@@ -371,19 +373,20 @@ __device__ __forceinline__ SegView seg_view(const VarlenArgs& a, const Segment& 
   return v;
 }
 
-// One 32-key tile in registers: K as the S^T A-operand (lane (m, grp) holds
-// key 8*(m/4)+4j+m%4, dims 32ks+8grp..+8), V as 4 full rows per load (lane
-// (col, grp) holds key 4*i2+grp, dims 8col..+8).
+// One 32-key tile in registers as loaded: K and V alike as 4 full rows per
+// load (lane (col, grp) of load i holds key 4*i+grp, dims 8col..+8), so
+// every load instruction reads 4 whole 256-byte rows.  Both go through LDS:
+// K comes back as the S^T A-operand, V as V^T.
 struct Tile {
-  bf16x8 k[2][4];
+  bf16x8 k[8];
   bf16x8 v[8];
 };
 
 // Per-lane byte offsets of the fast (unclamped, part A) tile loads; they
-// depend only on the token stride, so they hold for every segment.
+// depend only on the token stride, so they hold for every segment and for
+// K and V alike.
 struct FastOffsets {
-  uint32_t k[2];
-  uint32_t v[8];
+  uint32_t r[8];
 };
 
 // K/V rows are read once per call: non-temporal loads.
@@ -398,11 +401,10 @@ __device__ __forceinline__ void load_fast(const VarlenArgs& a, const SegView& s,
   const char* kb = reinterpret_cast<const char*>(s.kA + (size_t)kt * a.a_tok_stride);
   const char* vb = reinterpret_cast<const char*>(s.vA + (size_t)kt * a.a_tok_stride);
   #pragma unroll
-  for (int j = 0; j < 2; ++j)
-    #pragma unroll
-    for (int ks = 0; ks < 4; ++ks) T.k[j][ks] = ld8_nt(kb + fo.k[j] + 64 * ks);
-  #pragma unroll
-  for (int i2 = 0; i2 < 8; ++i2) T.v[i2] = ld8_nt(vb + fo.v[i2]);
+  for (int i = 0; i < 8; ++i) {
+    T.k[i] = ld8_nt(kb + fo.r[i]);
+    T.v[i] = ld8_nt(vb + fo.r[i]);
+  }
 }
 
 // Any tile: rows clamped, each from part A or B.
@@ -417,13 +419,10 @@ __device__ __forceinline__ void load_slow(const VarlenArgs& a, const SegView& s,
     return kk < s.a_len ? pa + (size_t)kk * a.a_tok_stride : pb + (size_t)(kk - s.a_len) * KV_ROW;
   };
   #pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    const bf16* p = row(s.kA, s.kB, kt + 8 * (col >> 2) + 4 * j + (col & 3)) + 8 * grp;
-    #pragma unroll
-    for (int ks = 0; ks < 4; ++ks) T.k[j][ks] = ld8_nt(p + 32 * ks);
+  for (int i = 0; i < 8; ++i) {
+    T.k[i] = ld8_nt(row(s.kA, s.kB, kt + 4 * i + grp) + 8 * col);
+    T.v[i] = ld8_nt(row(s.vA, s.vB, kt + 4 * i + grp) + 8 * col);
   }
-  #pragma unroll
-  for (int i2 = 0; i2 < 8; ++i2) T.v[i2] = ld8_nt(row(s.vA, s.vB, kt + 4 * i2 + grp) + 8 * col);
 }
 
 // Q of this lane's row of segment s.
@@ -453,11 +452,10 @@ __device__ __forceinline__ void varlen_run(const VarlenArgs& a, unsigned char* s
   {
     const int64_t ts = a.a_tok_stride;
     #pragma unroll
-    for (int j = 0; j < 2; ++j) fo.k[j] = (uint32_t)(((8 * (col >> 2) + 4 * j + (col & 3)) * ts + 8 * grp) * 2);
-    #pragma unroll
-    for (int i2 = 0; i2 < 8; ++i2) fo.v[i2] = (uint32_t)(((4 * i2 + grp) * ts + 8 * col) * 2);
+    for (int i = 0; i < 8; ++i) fo.r[i] = (uint32_t)(((4 * i + grp) * ts + 8 * col) * 2);
   }
   unsigned char* vs = smem + wave * KT * ROWB;
+  unsigned char* kst = smem + (4 + wave) * KT * ROWB;
   const int tok = 8 * t + (col >> 1);
 
   Segment sg;
@@ -481,13 +479,26 @@ __device__ __forceinline__ void varlen_run(const VarlenArgs& a, unsigned char* s
         for (int i2 = 0; i2 < 8; ++i2)
           if (kt + 4 * i2 + grp >= cur.kend) T.v[i2] = zero8();
       }
-      f32x4 s0, s1;
-      qk_tile(T.k, qf, s0, s1);
       #pragma unroll
-      for (int i2 = 0; i2 < 8; ++i2)
-        *reinterpret_cast<bf16x8*>(vs + lds_chunk_off(4 * i2 + grp, col)) = T.v[i2];
-      const bf16x8 pb = softmax_update<MASKED>(st, s0, s1, kt + 8 * grp, vis, a.scale_log2);
+      for (int i = 0; i < 8; ++i) {
+        *reinterpret_cast<bf16x8*>(kst + lds_chunk_off(4 * i + grp, col)) = T.k[i];
+        *reinterpret_cast<bf16x8*>(vs + lds_chunk_off(4 * i + grp, col)) = T.v[i];
+      }
       wave_lds_sync();
+      // S^T A-operand of sub-tile j, k-step ks: lane (col, grp) takes key
+      // 8*(col/4) + 4j + col%4, dims 32ks + 8grp .. +8, so that each lane's
+      // 8 scores are 8 consecutive keys (the P^T operand of the PV step).
+      // The 16 lanes of a group read 16 rows whose swizzles differ.
+      bf16x8 kf[2][4];
+      #pragma unroll
+      for (int j = 0; j < 2; ++j)
+        #pragma unroll
+        for (int ks = 0; ks < 4; ++ks)
+          kf[j][ks] = *reinterpret_cast<const bf16x8*>(
+              kst + lds_chunk_off(8 * (col >> 2) + 4 * j + (col & 3), 4 * ks + grp));
+      f32x4 s0, s1;
+      qk_tile(kf, qf, s0, s1);
+      const bf16x8 pb = softmax_update<MASKED>(st, s0, s1, kt + 8 * grp, vis, a.scale_log2);
       bf16x8 vt[8];
       #pragma unroll
       for (int nb = 0; nb < 8; ++nb) vt[nb] = lds_vt(vs, nb, lane);
