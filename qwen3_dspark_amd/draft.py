@@ -317,6 +317,16 @@ class DraftKVPool:
     def lengths(self):
         return dict(self._lengths)
 
+    @property
+    def kernel(self):
+        """The pool's HipDraftAttention (None unless the geometry is 8 x 128)."""
+        return self._attention
+
+    def length(self, request):
+        """Committed context rows of a request (KeyError if unknown)."""
+        self._request(request)
+        return self._lengths[request]
+
     def slot(self, request):
         self._request(request)
         return self._slots[request]

@@ -92,7 +92,7 @@ class PackedDraft:
         self.projector = self._projector(draft)
         self.pool = DraftKVPool(layers=len(draft.layers), slots=slots, capacity=capacity, device=self.device,
                                 chunk=chunk, projector=self.projector)
-        self.kernel = self.pool._attention
+        self.kernel = self.pool.kernel
         self.last_projection_work = None
 
     def _projector(self, draft):
@@ -141,10 +141,10 @@ class PackedDraft:
         committed context and its own rows."""
         if not anchors:
             raise ValueError('Require active anchor requests')
-        blocks = {}
-        for request, anchor in anchors.items():
-            self.pool._request(request)
-            blocks[request] = (anchor, (self.pool.lengths[request],))
+        if self.draft.training:
+            raise ValueError('Packed draft is inference-only')
+        self.validate_cache()
+        blocks = {request: (anchor, (self.pool.length(request),)) for request, anchor in anchors.items()}
         return self._run(blocks, one_block=True)
 
     @torch.no_grad()
@@ -166,8 +166,9 @@ class PackedDraft:
         size, vocab = self.block_size, draft.embedding.num_embeddings
         requests = tuple(blocks)
         tokens, positions, anchors = [], [], {}
+        lengths = self.pool.lengths
         for request in requests:
-            self.pool._request(request)
+            length = self.pool.length(request)
             anchor, where = blocks[request]
             where = tuple(int(a) for a in where)
             n = len(where)
@@ -176,7 +177,7 @@ class PackedDraft:
                     or not bool(((anchor >= 0) & (anchor < vocab)).all())):
                 raise ValueError('Require one valid [1,1] long anchor per active request' if one_block else
                                  f'Require [1, n] long anchor tokens for 1..{MAX_BLOCKS} blocks per request')
-            if any(not 0 <= a <= self.pool.lengths[request] for a in where):
+            if any(not 0 <= a <= length for a in where):
                 raise ValueError('Every anchor must lie in [0, committed length]')
             block = anchor.new_full((n, size), self.mask_token_id)
             block[:, 0] = anchor[0]
@@ -215,6 +216,5 @@ class PackedDraft:
             raise RuntimeError('Nonfinite packed draft hidden')
         work = self.pool.counters(batch)
         work.update(mlp_calls=len(draft.layers))
-        lengths = self.pool.lengths
         return PackedDraftFeatures(hidden, requests, size, tuple(lengths[r] for r in requests), work,
                                    tuple(len(anchors[r]) for r in requests))
