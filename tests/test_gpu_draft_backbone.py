@@ -142,13 +142,14 @@ def control_backbone(draft, pd, blocks):
             x = layer.input_norm(z)
             q = rotate(att.q_norm(att.q_proj(x).view(1, -1, 16, 128)).transpose(1, 2), cos, sin)
             kb, vb = att.project_kv(x, cos, sin)
-            k = torch.cat((pd.pool.keys[index, slot, :, :c][None], kb.to(torch.bfloat16)), dim=2).float()
-            v = torch.cat((pd.pool.values[index, slot, :, :c][None], vb), dim=2).float()
-            k = k.repeat_interleave(2, dim=1)
-            v = v.repeat_interleave(2, dim=1).contiguous()
-            s = torch.matmul(q.to(torch.bfloat16).float(), k.transpose(-1, -2).contiguous()) * SCALE
-            o = torch.matmul(s.masked_fill(~visible, float('-inf')).softmax(-1), v)
-            o = o.transpose(1, 2).reshape(1, 7 * n, -1).to(torch.bfloat16)
+            with torch.autocast('cuda', enabled=False):      # float32 attention also under autocast
+                k = torch.cat((pd.pool.keys[index, slot, :, :c][None], kb.to(torch.bfloat16)), dim=2).float()
+                v = torch.cat((pd.pool.values[index, slot, :, :c][None], vb.to(torch.bfloat16)), dim=2).float()
+                k = k.repeat_interleave(2, dim=1)
+                v = v.repeat_interleave(2, dim=1).contiguous()
+                s = torch.matmul(q.to(torch.bfloat16).float(), k.transpose(-1, -2).contiguous()) * SCALE
+                o = torch.matmul(s.masked_fill(~visible, float('-inf')).softmax(-1), v)
+                o = o.transpose(1, 2).reshape(1, 7 * n, -1).to(torch.bfloat16)
             z = z + att.o_proj(o)
             z = z + layer.mlp(layer.post_norm(z))
         outs.append(draft.norm(z)[0])
@@ -283,3 +284,53 @@ def test_one_block_backbone_and_contract():
     with pytest.raises(ValueError, match='inference-only'):
         pd.backbone(anchors)
     draft.eval()
+
+
+@torch.no_grad()
+def test_backbone_under_autocast_with_float32_draft():
+    """The reference's own precision form (model.py:111: float32 trainable
+    weights under bf16 autocast): Q and block K reach the kernel in fp32
+    (q_norm / k_norm run in fp32) and are rounded as it loads them, V in
+    bf16; the context projection runs on bf16 snapshots of the weights.
+    Checked against the float32-attention control under the same autocast,
+    and against the float64 oracle of the whole forward on the float32
+    weights."""
+    from qwen3_dspark_amd import backends
+    from qwen3_dspark_amd.draft_backbone import PackedDraft
+    draft = draft_module(SEED + 2)
+    for m in (draft.fc, draft.context_norm, draft.layers, draft.norm, draft.embedding):
+        m.float()
+    names, lengths = ['a', 'b', 'c', 'd'], [200, 1024, 37, 513]
+    rng = np.random.default_rng(SEED + 2)
+    gen = torch.Generator().manual_seed(SEED + 2)
+    pd = PackedDraft(draft, native_backend=backends.DRAFT_BLOCKS_BACKEND, slots=4, capacity=1024)
+    features = [torch.randn(1, c, 5 * HIDDEN, generator=gen).to(DEV) for c in lengths]
+    for n in names:
+        pd.add_request(n)
+    pd.append_committed(dict(zip(names, features)))
+    anchors = [[c] + sorted(int(a) for a in rng.choice(np.arange(c), size=2, replace=False)) for c in lengths]
+    tokens = {n: torch.tensor([rng.integers(0, 151936, size=3).tolist()], device=DEV) for n in names}
+    blocks = {n: (tokens[n], a) for n, a in zip(names, anchors)}
+    with torch.autocast('cuda', dtype=torch.bfloat16):
+        feats = pd.backbone_blocks(blocks)
+        control = f64(control_backbone(draft, pd, blocks))
+    hidden = f64(feats.hidden)
+    assert np.isfinite(hidden).all()
+    fc_out = f64(pd.projector.fc_forward(torch.cat([f[0] for f in features]).to(torch.bfloat16)))
+    weights = [layer_weights(l) for l in draft.layers]
+    proj = [(w['k_proj'], w['k_norm'], w['v_proj']) for w in weights]
+    first = 0
+    for r, n in enumerate(names):
+        c = lengths[r]
+        kv = draft_proj.project_context_kv(None, f64(draft.fc.weight), f64(draft.context_norm.weight), proj,
+                                           np.arange(c), fc_out=fc_out[first:first + c])
+        first += c
+        toks = torch.full((3, 7), MASK_TOKEN, device=DEV)
+        toks[:, 0] = tokens[n][0]
+        z0 = f64(draft.embedding(toks.reshape(1, -1))[0])
+        ref = draft_model.draft_backbone(z0, weights, kv, anchors[r], f64(draft.norm.weight))
+        lo, hi = 21 * r, 21 * (r + 1)
+        err, drift, ctl_drift = rel(hidden[lo:hi], control[lo:hi]), rel(hidden[lo:hi], ref), rel(control[lo:hi], ref)
+        say(f'[autocast] {n}: rel err vs control {err:.2e}, drift vs float64 {drift:.2e} (control {ctl_drift:.2e})')
+        assert err < 3e-2, (n, err)
+        assert drift <= 1.1 * ctl_drift + 5e-3, (n, drift, ctl_drift)
