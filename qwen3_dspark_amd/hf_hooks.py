@@ -5,11 +5,11 @@
   over the model's [1,Hkv,N,D] cache, HIP gather + HIP varlen kernel,
   [1,Q,Hq,D] out.
 * FusedVerificationCache + fused_verification_attention - the verification
-  hooks of dspark_qwen/persistent_qwen_target.py:45-95 (Cache.update stages
-  the layer, the callback attends).  The reference's update materialises the
-  capacity-length K/V with prepare_attention and hands it to the kernel; here
-  update only stages the new rows and the callback calls
-  PersistentTargetKV.attend, which reads resident + scratch rows in place.
+  hooks of dspark_qwen/persistent_qwen_target.py:45-95.  The reference's
+  update stages the layer and materialises the capacity-length K/V with
+  prepare_attention for the kernel; here update only checks the new rows and
+  the callback passes them to PersistentTargetKV.attend, whose one launch
+  stages them and attends over resident + new rows in place.
 * FusedVerifier - binds a PersistentTargetKV transaction to one model forward
   (the callback finds it through the `fused_verification` forward kwarg, as
   the reference passes `persistent_target`).
@@ -64,9 +64,11 @@ def varlen_attention_forward(module, query, key, value, attention_mask, scaling=
 
 
 class FusedVerificationCache(Cache):
-    """Cache.update for one verification transaction: stage the layer's new
-    K/V rows into the store's scratch and return them unchanged (the fused
-    attention reads the committed rows from the resident store itself)."""
+    """Cache.update for one verification transaction: check the layer's new
+    K/V rows against the transaction and return them unchanged.  The
+    callback hands them to the fused attention, which copies them into the
+    store's scratch in the same launch that attends (and reads the committed
+    rows from the resident store in place)."""
 
     def __init__(self, verifier):
         super().__init__(layers=[])
@@ -85,8 +87,6 @@ class FusedVerificationCache(Cache):
         expected = (1, v.store.heads, q, v.store.dim)
         if tuple(key_states.shape) != expected or value_states.shape != key_states.shape:
             raise ValueError('HF layer KV differs from exact packed query shape')
-        v.store.stage_layer(tx, layer_idx, key_states[0].transpose(0, 1).contiguous(),
-                            value_states[0].transpose(0, 1).contiguous())
         return key_states, value_states
 
     def get_seq_length(self, layer_idx=0):
@@ -108,7 +108,8 @@ def fused_verification_attention(module, query, key, value, attention_mask, scal
     if attention_mask is not None or dropout or v.attention_module(module.layer_idx) is not module:
         raise ValueError('Unexpected mask/dropout/foreign model attention')
     q = query[0].transpose(0, 1).contiguous()
-    out = v.store.attend(v.transaction, module.layer_idx, q, scale=scaling)
+    out = v.store.attend(v.transaction, module.layer_idx, q, scale=scaling,
+                         keys=key[0].transpose(0, 1).contiguous(), values=value[0].transpose(0, 1).contiguous())
     if not isinstance(out, torch.Tensor) or out.shape != q.shape or out.dtype != q.dtype or out.device != q.device:
         raise ValueError('Persistent attention returned incompatible output')
     return out[None], None

@@ -181,3 +181,45 @@ def test_persistent_qwen_target_prefill_verify_commit_features():
         assert target.lengths == {n: len(s) for n, s in zip(names, seqs)}
     k, v = target.request_kv('b')[0]
     assert k.shape == (1, 8, len(seqs[1]), 128)
+
+
+def test_one_attention_launch_per_layer_in_the_trace():
+    """The device trace of one verification forward through the fused hooks
+    (the tracing check of scripts/probe_varlen.py:126-136, which counts one
+    aten::_flash_attention_forward per native call and layer): per layer one
+    fused attention chunk launch and one split-K merge, no separate staging
+    or gather launch, and no torch attention or softmax kernel."""
+    from torch.profiler import ProfilerActivity, profile
+
+    from qwen3_dspark_amd.hf_hooks import FusedVerifier
+    from qwen3_dspark_amd.persistent_kv import Bucket, PersistentTargetKV
+    cpu, gpu = tiny_qwen3()
+    rng = np.random.default_rng(9)
+    store = PersistentTargetKV(layers=2, slots=2, context_capacity=512, max_query_tokens=2 * NEW, heads=8,
+                               dim=128, device=DEV)
+    handles = [store.add_request(f'r{i}') for i in range(2)]
+    for h, c in zip(handles, (90, 200)):
+        k, v = cpu_prefix_kv(cpu, rng.integers(0, 512, size=c).tolist())
+        store.load_prefix(h, k.to(DEV), v.to(DEV))
+    bucket = Bucket((NEW,) * 2, (512 - NEW,) * 2, 'trace')
+    store.register_bucket(bucket)
+    verifier = FusedVerifier(gpu, store)
+    ids = torch.tensor([rng.integers(0, 512, size=2 * NEW).tolist()], device=DEV)
+    pos = torch.tensor([[90 + i for i in range(NEW)] + [200 + i for i in range(NEW)]], device=DEV)
+    for attempt in range(2):          # the first forward warms up the libraries outside the trace
+        with verifier.transaction_for(handles, bucket) as tx:
+            if attempt == 0:
+                verifier.forward(ids, pos)
+                store.abort(tx)
+                continue
+            with profile(activities=[ProfilerActivity.CPU, ProfilerActivity.CUDA]) as prof:
+                verifier.forward(ids, pos)
+                torch.cuda.synchronize()
+            store.abort(tx)
+    names = [e.name for e in prof.events() if e.device_type.name == 'CUDA']
+    count = lambda key: sum(key in n for n in names)
+    assert names, 'the profiler recorded no device activity'
+    assert count('varlen_attn_kernel') == 2, names
+    assert count('merge_kernel') == 2, names
+    assert count('kv_stage_kernel') == 0 and count('kv_gather_kernel') == 0, names
+    assert not any('softmax' in n.lower() or 'flash' in n.lower() or 'attention' in n.lower() for n in names), names
