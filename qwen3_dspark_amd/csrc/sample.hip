@@ -31,6 +31,103 @@ __device__ __forceinline__ double load_logit(const void* logits, int dtype, int6
   return (double)static_cast<const float*>(logits)[idx];
 }
 
+// ---------------------------------------------------------------------------
+// Float64 law arithmetic, shared by every kernel below, so that the row
+// statistics and every p value come from the same operations.
+//
+// LawScale, x / T: for T in [2^-100, 2^100] the quotient q = x * (1/T) gets
+// one correction, q + fma(-q, T, x) * (1/T) with fused operations
+// (Markstein's correction step), which yields the correctly rounded x / T:
+// for finite float or bf16 x (|x| < 2^128) no step overflows or underflows.
+// The oracle's tests compare it with true division over every finite bf16
+// value at 17 temperatures and over 2e7 random fp32 values and temperatures
+// in [2^-50, 2^50].  Other T divide.
+//
+// law_exp, exp(z) for z <= 0, by Tang's table-driven method: z = k ln2/32 + r
+// with k = rint(32 z / ln2), |r| <= ln2/64 (Cody-Waite reduction; ln2/32 =
+// L1 + L2 with L1 on 37 bits, so that k L1 is exact for |k| < 2^16);
+// exp(r) - 1 by its degree-6 Taylor polynomial (truncation < 4e-18
+// relative); exp(z) = 2^(k >> 5) (t_j + (t_j p + l_j)), j = k & 31, where
+// 2^(j/32) = t_j + l_j to twice double precision.  Measured error <= 0.56
+// ulp over 2e7 arguments in [-746, 0].  z below -746, -inf and NaN give 0
+// (a row holding a non-finite logit is flagged by the row statistics).
+// ---------------------------------------------------------------------------
+__constant__ __attribute__((aligned(16))) double LAW_EXP_TAB[64] = {
+    0x1.0000000000000p+0, 0x0.0p+0,
+    0x1.059b0d3158574p+0, 0x1.d73e2a475b465p-55,
+    0x1.0b5586cf9890fp+0, 0x1.8a62e4adc610bp-54,
+    0x1.11301d0125b51p+0, -0x1.6c51039449b3ap-54,
+    0x1.172b83c7d517bp+0, -0x1.19041b9d78a76p-55,
+    0x1.1d4873168b9aap+0, 0x1.e016e00a2643cp-54,
+    0x1.2387a6e756238p+0, 0x1.9b07eb6c70573p-54,
+    0x1.29e9df51fdee1p+0, 0x1.612e8afad1255p-55,
+    0x1.306fe0a31b715p+0, 0x1.6f46ad23182e4p-55,
+    0x1.371a7373aa9cbp+0, -0x1.63aeabf42eae2p-54,
+    0x1.3dea64c123422p+0, 0x1.ada0911f09ebcp-55,
+    0x1.44e086061892dp+0, 0x1.89b7a04ef80d0p-59,
+    0x1.4bfdad5362a27p+0, 0x1.d4397afec42e2p-56,
+    0x1.5342b569d4f82p+0, -0x1.07abe1db13cadp-55,
+    0x1.5ab07dd485429p+0, 0x1.6324c054647adp-54,
+    0x1.6247eb03a5585p+0, -0x1.383c17e40b497p-54,
+    0x1.6a09e667f3bcdp+0, -0x1.bdd3413b26456p-54,
+    0x1.71f75e8ec5f74p+0, -0x1.16e4786887a99p-55,
+    0x1.7a11473eb0187p+0, -0x1.41577ee04992fp-55,
+    0x1.82589994cce13p+0, -0x1.d4c1dd41532d8p-54,
+    0x1.8ace5422aa0dbp+0, 0x1.6e9f156864b27p-54,
+    0x1.93737b0cdc5e5p+0, -0x1.75fc781b57ebcp-57,
+    0x1.9c49182a3f090p+0, 0x1.c7c46b071f2bep-56,
+    0x1.a5503b23e255dp+0, -0x1.d2f6edb8d41e1p-54,
+    0x1.ae89f995ad3adp+0, 0x1.7a1cd345dcc81p-54,
+    0x1.b7f76f2fb5e47p+0, -0x1.5584f7e54ac3bp-56,
+    0x1.c199bdd85529cp+0, 0x1.11065895048ddp-55,
+    0x1.cb720dcef9069p+0, 0x1.503cbd1e949dbp-56,
+    0x1.d5818dcfba487p+0, 0x1.2ed02d75b3707p-55,
+    0x1.dfc97337b9b5fp+0, -0x1.1a5cd4f184b5cp-54,
+    0x1.ea4afa2a490dap+0, -0x1.e9c23179c2893p-54,
+    0x1.f50765b6e4540p+0, 0x1.9d3e12dd8a18bp-54};
+constexpr double EXP_INV_L = 0x1.71547652b82fep+5;   // 32 / ln2
+constexpr double EXP_L1 = 0x1.62e42fefa0000p-6;      // ln2/32, high 37 bits
+constexpr double EXP_L2 = 0x1.cf79abc9e3b3ap-45;      // ln2/32 - L1
+
+struct LawScale {
+  double T, rT;
+  bool fast;
+  __device__ __forceinline__ double operator()(double x) const {
+    if (!fast) return x / T;
+    const double q = __dmul_rn(x, rT);
+    return __fma_rn(__fma_rn(-q, T, x), rT, q);
+  }
+};
+
+inline LawScale law_scale(double T) {
+  return LawScale{T, 1.0 / T, T >= 0x1p-100 && T <= 0x1p100};
+}
+
+// tab: LAW_EXP_TAB, or a copy of it in LDS (stage_exp_table).
+__device__ __forceinline__ double law_exp(double z, const double* tab) {
+  z = fmax(z, -746.0);
+  const double k = rint(__dmul_rn(z, EXP_INV_L));
+  const int n = (int)k;
+  const double r = __fma_rn(-k, EXP_L2, __fma_rn(-k, EXP_L1, z));
+  double c = __fma_rn(r, 1.0 / 720, 1.0 / 120);
+  c = __fma_rn(r, c, 1.0 / 24);
+  c = __fma_rn(r, c, 1.0 / 6);
+  c = __fma_rn(r, c, 0.5);
+  const double p = __fma_rn(__dmul_rn(r, r), c, r);
+  const double2 t = *reinterpret_cast<const double2*>(tab + 2 * (n & 31));
+  return ldexp(__dadd_rn(t.x, __fma_rn(t.x, p, t.y)), n >> 5);
+}
+
+// Copies the table into LDS; the caller's next barrier publishes it.
+__device__ __forceinline__ void stage_exp_table(double* lds) {
+  if (threadIdx.x < 64) lds[threadIdx.x] = LAW_EXP_TAB[threadIdx.x];
+}
+
+// p(v) = exp(x_v / T - M) / S.
+__device__ __forceinline__ double law_p(double x, const LawScale& sc, double M, double S, const double* tab) {
+  return law_exp(sc(x) - M, tab) / S;
+}
+
 // Block-wide sum for 256 threads (4 waves); `buf` holds 4 doubles.
 __device__ __forceinline__ double block_sum(double x, double* buf) {
   #pragma unroll
@@ -58,10 +155,11 @@ constexpr int ST_PER = ST_CHUNK / ST_THREADS;   // logits per thread
 
 template <int DT>   // 0: bf16 logits, 1: fp32
 __global__ __launch_bounds__(ST_THREADS) void row_stats_kernel(const void* logits, int64_t row_stride, int vocab,
-                                                               double temperature, int chunks, double* stats,
+                                                               LawScale sc, int chunks, double* stats,
                                                                int32_t* bad) {
   constexpr int VEC = DT == 0 ? 8 : 4;                 // logits per 16-byte load
   __shared__ double buf[4];
+  __shared__ __attribute__((aligned(16))) double tab[64];
   const int row = blockIdx.x / chunks;
   const int c = blockIdx.x - row * chunks;
   const int v0 = c * ST_CHUNK;
@@ -70,7 +168,11 @@ __global__ __launch_bounds__(ST_THREADS) void row_stats_kernel(const void* logit
   const int tid = threadIdx.x;
   const bool vec = v1 - v0 == ST_CHUNK && ((base * (DT == 0 ? 2 : 4)) & 15) == 0 &&
                    ((uintptr_t)logits & 15) == 0;        // uniform over the workgroup
+  stage_exp_table(tab);
+  // Values this thread does not hold are -inf: they leave the max alone and
+  // add exp(-inf) = 0 to the sum.
   float xs[ST_PER];
+  bool nonfinite = false;
   if (vec) {
     // value i of this thread: element VEC * (tid + ST_THREADS * (i / VEC)) + i % VEC
     #pragma unroll
@@ -86,38 +188,39 @@ __global__ __launch_bounds__(ST_THREADS) void row_stats_kernel(const void* logit
         for (int u = 0; u < VEC; ++u) xs[VEC * j + u] = v[u];
       }
     }
+    #pragma unroll
+    for (int i = 0; i < ST_PER; ++i) nonfinite |= !isfinite(xs[i]);
   } else {
     // value i of this thread: element tid + ST_THREADS * i (when below v1)
     #pragma unroll
     for (int i = 0; i < ST_PER; ++i) {
       const int v = v0 + tid + ST_THREADS * i;
-      xs[i] = v < v1 ? (float)load_logit(logits, DT, (int64_t)row * row_stride + v) : -INFINITY;
+      const bool held = v < v1;
+      xs[i] = held ? (float)load_logit(logits, DT, (int64_t)row * row_stride + v) : -INFINITY;
+      nonfinite |= held && !isfinite(xs[i]);
     }
   }
-  auto held = [&](int i) { return vec || v0 + tid + ST_THREADS * i < v1; };
   float xmax = -INFINITY;
-  bool nonfinite = false;
   #pragma unroll
-  for (int i = 0; i < ST_PER; ++i) {
-    if (!held(i)) continue;
-    nonfinite |= !isfinite(xs[i]);
-    xmax = fmaxf(xmax, xs[i]);
-  }
+  for (int i = 0; i < ST_PER; ++i) xmax = fmaxf(xmax, xs[i]);
   #pragma unroll
   for (int off = 32; off >= 1; off >>= 1) xmax = fmaxf(xmax, __shfl_xor(xmax, off));
   const int wave = tid >> 6;
   if ((tid & 63) == 0) buf[wave] = xmax;
-  __syncthreads();
-  const bool unit = temperature == 1.0;
-  const double mx = fmax(fmax(buf[0], buf[1]), fmax(buf[2], buf[3]));
-  const double m = unit ? mx : mx / temperature;
+  __syncthreads();   // also publishes the exp table
+  const double m = sc((double)fmaxf(fmaxf(buf[0], buf[1]), fmaxf(buf[2], buf[3])));
   double sum = 0.0;
-  #pragma unroll
-  for (int i = 0; i < ST_PER; ++i) {
-    if (!held(i)) continue;
-    const double y = unit ? (double)xs[i] : (double)xs[i] / temperature;
-    nonfinite |= !isfinite(y);
-    sum += exp(y - m);
+  if (sc.fast) {
+    // finite x / T stays finite: only the logits need the check
+    #pragma unroll
+    for (int i = 0; i < ST_PER; ++i) sum += law_exp(sc((double)xs[i]) - m, tab);
+  } else {
+    #pragma unroll
+    for (int i = 0; i < ST_PER; ++i) {
+      const double y = (double)xs[i] / sc.T;
+      nonfinite |= (vec || v0 + tid + ST_THREADS * i < v1) && !isfinite(y);
+      sum += law_exp(y - m, tab);
+    }
   }
   sum = block_sum(sum, buf);
   if (tid == 0) {
@@ -133,7 +236,7 @@ __device__ __forceinline__ void row_law(const double* stats, int row, int chunks
   M = -INFINITY;
   for (int c = 0; c < chunks; ++c) M = fmax(M, st[2 * c]);
   S = 0.0;
-  for (int c = 0; c < chunks; ++c) S += st[2 * c + 1] * exp(st[2 * c] - M);
+  for (int c = 0; c < chunks; ++c) S += st[2 * c + 1] * law_exp(st[2 * c] - M, LAW_EXP_TAB);
 }
 
 // ---------------------------------------------------------------------------
@@ -172,15 +275,15 @@ static_assert(sizeof(DrawJob) == 64, "draw job layout");
 struct DrawSrc {
   const void* logits;
   int dtype;
-  double temperature;
+  LawScale sc;
   const double* q;
   const double* probs;
   int vocab;
 };
 
-__device__ __forceinline__ double draw_value(const DrawSrc& s, const DrawJob& j, int v) {
+__device__ __forceinline__ double draw_value(const DrawSrc& s, const DrawJob& j, int v, const double* tab) {
   if (j.kind == DK_PROBS) return s.probs[j.src + v];
-  const double p = exp(load_logit(s.logits, s.dtype, j.src + v) / s.temperature - j.M) / j.S;
+  const double p = law_p(load_logit(s.logits, s.dtype, j.src + v), s.sc, j.M, j.S, tab);
   return j.kind == DK_RESIDUAL ? fmax(p - s.q[j.qrow + v], 0.0) : p;
 }
 
@@ -193,10 +296,13 @@ __device__ __forceinline__ void segment_bounds(int seg, int vocab, int& s0, int&
 // grid: jobs x SEG_SLICES; each wave sums SEG_PER_SLICE / 4 segments.
 __global__ __launch_bounds__(256) void segment_sums_kernel(DrawSrc src, const DrawJob* jobs, double* segsum,
                                                            int32_t* seglast) {
+  __shared__ __attribute__((aligned(16))) double tab[64];
   const int job = blockIdx.x / SEG_SLICES;
   const int slice = blockIdx.x - job * SEG_SLICES;
   const DrawJob j = jobs[job];
-  if (j.kind == DK_NONE) return;
+  if (j.kind == DK_NONE) return;                    // uniform across the workgroup
+  stage_exp_table(tab);
+  __syncthreads();
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   for (int i = 0; i < SEG_PER_SLICE / 4; ++i) {
@@ -206,7 +312,7 @@ __global__ __launch_bounds__(256) void segment_sums_kernel(DrawSrc src, const Dr
     double part = 0.0;
     int last = -1;
     for (int v = s0 + lane; v < s1; v += WAVE) {
-      const double r = draw_value(src, j, v);
+      const double r = draw_value(src, j, v, tab);
       part += r;
       if (r > 0.0) last = v;
     }
@@ -299,7 +405,7 @@ __global__ __launch_bounds__(256) void draw_kernel(DrawSrc src, const DrawJob* j
       int hit = INT32_MAX, pos = -1;
       for (int v0 = s0; v0 < s1 && hit == INT32_MAX; v0 += WAVE) {
         const int v = v0 + lane;
-        const double r = v < s1 ? draw_value(src, j, v) / norm : 0.0;
+        const double r = v < s1 ? draw_value(src, j, v, LAW_EXP_TAB) / norm : 0.0;
         if (r > 0.0) pos = v;
         const double incl = run + wave_inclusive_scan(r, lane);
         const unsigned long long over = __builtin_amdgcn_ballot_w64(v < s1 && incl > j.u);
@@ -339,7 +445,7 @@ struct VerifyArgs {
   int dtype;                 // 0 bf16, 1 fp32
   int64_t row_stride;
   int vocab;
-  double temperature;
+  LawScale sc;               // division by the temperature
   const double* stats;       // row statistics, `chunks` (max, sum) pairs per row
   int chunks;
   const int32_t* bad;        // [rows] non-finite flags
@@ -370,7 +476,6 @@ __global__ __launch_bounds__(64) void verify_plan_kernel(VerifyArgs a) {
   const int n = a.cu_rows[r + 1] - row0 - 1;
   const int d0 = row0 - r;
   const int V = a.vocab;
-  const double T = a.temperature;
   if (n < 0 || n > MAX_PROPOSAL) {                       // wave-uniform; nothing else is read
     if (lane == 0) {
       DrawJob job{};
@@ -408,7 +513,8 @@ __global__ __launch_bounds__(64) void verify_plan_kernel(VerifyArgs a) {
       law[2 * j + 1] = S;
       if (j < n) {
         const int64_t tok = a.tokens[d0 + j];
-        const double p = exp(load_logit(a.logits, a.dtype, (int64_t)(row0 + j) * a.row_stride + tok) / T - M) / S;
+        const double p = law_p(load_logit(a.logits, a.dtype, (int64_t)(row0 + j) * a.row_stride + tok), a.sc, M, S,
+                               LAW_EXP_TAB);
         alpha[j] = fmin(p / a.q[(int64_t)(d0 + j) * V + tok], 1.0);
       }
     }
@@ -486,14 +592,16 @@ __global__ __launch_bounds__(64) void verify_plan_kernel(VerifyArgs a) {
 // Materialised laws and plain categorical draws (the draft's proposal side).
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void probs_kernel(const void* logits, int dtype, int64_t row_stride, int vocab,
-                                                    double temperature, const double* stats, int chunks,
-                                                    double* probs) {
+                                                    LawScale sc, const double* stats, int chunks, double* probs) {
+  __shared__ __attribute__((aligned(16))) double tab[64];
+  stage_exp_table(tab);
+  __syncthreads();
   const int row = blockIdx.y;
   double M, S;
   row_law(stats, row, chunks, M, S);
   const int64_t base = (int64_t)row * row_stride;
   for (int v = blockIdx.x * blockDim.x + threadIdx.x; v < vocab; v += gridDim.x * blockDim.x)
-    probs[(int64_t)row * vocab + v] = exp(load_logit(logits, dtype, base + v) / temperature - M) / S;
+    probs[(int64_t)row * vocab + v] = law_p(load_logit(logits, dtype, base + v), sc, M, S, tab);
 }
 
 __global__ __launch_bounds__(256) void row_jobs_kernel(int rows, int vocab, const double* uniforms, DrawJob* jobs) {
@@ -532,10 +640,10 @@ extern "C" int dspark_logit_row_stats(const void* logits, int dtype, int rows, i
   DSPARK_REQUIRE(grid <= 0x7fffffffLL, "too many rows");
   if (dtype == 0)
     hipLaunchKernelGGL(row_stats_kernel<0>, dim3((unsigned)grid), dim3(ST_THREADS), 0, static_cast<hipStream_t>(stream),
-                       logits, row_stride, vocab, temperature, stat_chunks(vocab), stats, bad);
+                       logits, row_stride, vocab, law_scale(temperature), stat_chunks(vocab), stats, bad);
   else
     hipLaunchKernelGGL(row_stats_kernel<1>, dim3((unsigned)grid), dim3(ST_THREADS), 0, static_cast<hipStream_t>(stream),
-                       logits, row_stride, vocab, temperature, stat_chunks(vocab), stats, bad);
+                       logits, row_stride, vocab, law_scale(temperature), stat_chunks(vocab), stats, bad);
   return launch_status("row_stats_kernel");
 }
 
@@ -577,13 +685,13 @@ extern "C" int dspark_spec_verify(const void* logits, int dtype, int64_t row_str
   DSPARK_REQUIRE(workspace_bytes >= draw_workspace(n_req) && (reinterpret_cast<uintptr_t>(workspace) & 63) == 0,
                  "workspace must be 64-byte aligned and hold dspark_draw_workspace_bytes(n_req) bytes");
   DrawJob* jobs = static_cast<DrawJob*>(workspace);
-  VerifyArgs a{logits, dtype, row_stride, vocab, temperature, stats, stat_chunks(vocab), bad, cu_rows, tokens, q,
+  VerifyArgs a{logits, dtype, row_stride, vocab, law_scale(temperature), stats, stat_chunks(vocab), bad, cu_rows, tokens, q,
                uniforms, budget, stops, n_stops, n_req, out_tokens, out_meta, jobs};
   hipStream_t s = static_cast<hipStream_t>(stream);
   hipLaunchKernelGGL(verify_plan_kernel, dim3(n_req), dim3(64), 0, s, a);
   int rc = launch_status("verify_plan_kernel");
   if (rc != OK) return rc;
-  const DrawSrc src{logits, dtype, temperature, q, nullptr, vocab};
+  const DrawSrc src{logits, dtype, law_scale(temperature), q, nullptr, vocab};
   const DrawOut o{out_tokens, out_meta, budget, stops, n_stops};
   return launch_draws(src, jobs, n_req, o, s);
 }
@@ -598,7 +706,7 @@ extern "C" int dspark_logits_to_probs(const void* logits, int dtype, int rows, i
   DSPARK_REQUIRE(temperature > 0.0 && temperature < DBL_MAX, "temperature must be finite and positive");
   const unsigned gx = (unsigned)std::min<int64_t>((vocab + 255) / 256, 64);
   hipLaunchKernelGGL(probs_kernel, dim3(gx, rows), dim3(256), 0, static_cast<hipStream_t>(stream), logits, dtype,
-                     row_stride, vocab, temperature, stats, stat_chunks(vocab), probs);
+                     row_stride, vocab, law_scale(temperature), stats, stat_chunks(vocab), probs);
   return launch_status("probs_kernel");
 }
 
@@ -614,7 +722,7 @@ extern "C" int dspark_sample_rows(const double* probs, int rows, int vocab, cons
   hipLaunchKernelGGL(row_jobs_kernel, dim3((rows + 255) / 256), dim3(256), 0, s, rows, vocab, uniforms, jobs);
   int rc = launch_status("row_jobs_kernel");
   if (rc != OK) return rc;
-  const DrawSrc src{nullptr, 0, 1.0, nullptr, probs, vocab};
+  const DrawSrc src{nullptr, 0, law_scale(1.0), nullptr, probs, vocab};
   const DrawOut o{out, nullptr, nullptr, nullptr, 0};
   return launch_draws(src, jobs, rows, o, s);
 }
