@@ -293,6 +293,39 @@ __device__ __forceinline__ void segment_bounds(int seg, int vocab, int& s0, int&
   s1 = min(s0 + per, vocab);
 }
 
+// This lane's share of one segment's sum and last index of positive mass:
+// values v = s0 + lane + 64 i in increasing order (the order of a plain
+// strided loop), their loads issued SEG_BATCH strips at a time (indices
+// clamped into the segment, values past it dropped) so that a wave waits
+// for one round trip per batch instead of one per strip.
+constexpr int SEG_BATCH = 8;
+
+template <int KIND, int DT>
+__device__ __forceinline__ void segment_part(const DrawSrc& src, const DrawJob& j, int s0, int s1, int lane,
+                                             const double* tab, double& part, int& last) {
+  for (int v0 = s0 + lane; v0 < s1; v0 += WAVE * SEG_BATCH) {
+    double x[SEG_BATCH], qv[SEG_BATCH];
+    #pragma unroll
+    for (int u = 0; u < SEG_BATCH; ++u) {
+      const int v = min(v0 + WAVE * u, s1 - 1);
+      if (KIND == DK_PROBS) x[u] = src.probs[j.src + v];
+      else x[u] = DT == 0 ? (double)(float)static_cast<const bf16*>(src.logits)[j.src + v]
+                          : (double)static_cast<const float*>(src.logits)[j.src + v];
+      if (KIND == DK_RESIDUAL) qv[u] = src.q[j.qrow + v];
+    }
+    #pragma unroll
+    for (int u = 0; u < SEG_BATCH; ++u) {
+      const int v = v0 + WAVE * u;
+      double r = KIND == DK_PROBS ? x[u] : law_p(x[u], src.sc, j.M, j.S, tab);
+      if (KIND == DK_RESIDUAL) r = fmax(r - qv[u], 0.0);
+      if (v < s1) {
+        part += r;
+        if (r > 0.0) last = v;
+      }
+    }
+  }
+}
+
 // grid: jobs x SEG_SLICES; each wave sums SEG_PER_SLICE / 4 segments.
 __global__ __launch_bounds__(256) void segment_sums_kernel(DrawSrc src, const DrawJob* jobs, double* segsum,
                                                            int32_t* seglast) {
@@ -311,11 +344,14 @@ __global__ __launch_bounds__(256) void segment_sums_kernel(DrawSrc src, const Dr
     segment_bounds(seg, src.vocab, s0, s1);
     double part = 0.0;
     int last = -1;
-    for (int v = s0 + lane; v < s1; v += WAVE) {
-      const double r = draw_value(src, j, v, tab);
-      part += r;
-      if (r > 0.0) last = v;
-    }
+    if (j.kind == DK_PROBS)
+      segment_part<DK_PROBS, 0>(src, j, s0, s1, lane, tab, part, last);
+    else if (src.dtype == 0)
+      j.kind == DK_LAW ? segment_part<DK_LAW, 0>(src, j, s0, s1, lane, tab, part, last)
+                       : segment_part<DK_RESIDUAL, 0>(src, j, s0, s1, lane, tab, part, last);
+    else
+      j.kind == DK_LAW ? segment_part<DK_LAW, 1>(src, j, s0, s1, lane, tab, part, last)
+                       : segment_part<DK_RESIDUAL, 1>(src, j, s0, s1, lane, tab, part, last);
     #pragma unroll
     for (int off = 32; off >= 1; off >>= 1) {
       part += __shfl_xor(part, off);
