@@ -165,3 +165,37 @@ def test_verification_errors_and_stops():
     assert (r.tokens.tolist(), r.accepted_draft_tokens, r.stop_reason, r.draws) == ([3], 1, 'eos', 1)
     r = call(3, budget=1)
     assert (r.tokens.tolist(), r.stop_reason, r.draws) == ([3], 'budget', 1)
+
+
+def test_laws_and_verification_outside_the_corrected_quotient_range():
+    """The sampling kernels divide by T through a corrected reciprocal
+    product for T in [2^-100, 2^100] and by IEEE division outside it: at
+    temperatures on both sides of each bound, the laws against the oracle
+    to 1e-12 and every integer outcome of a verification batch identical.
+    The fp32 logits are scaled by T so that the laws stay spread."""
+    from qwen3_dspark_amd.sampling import logits_to_probabilities, sample_categorical, verify_proposals
+    V, R, N = 2000, 8, 3
+    gen = torch.Generator(device=DEV).manual_seed(SEED + 7)
+    rows = torch.arange(R * (N + 1), device=DEV).reshape(R, N + 1)[:, :N].reshape(-1)
+    for T in (2.0 ** -101, 2.0 ** -99, 2.0 ** 99, 3 * 2.0 ** 100, 2.0 ** 101):
+        say(f'[sampling] temperature {T!r}')
+        base = torch.randn(R * (N + 1), V, generator=gen, device=DEV, dtype=torch.float64) * 2.0
+        target = (base * T).float()
+        draft_logits = (target[rows].double() + torch.randn(R * N, V, generator=gen, device=DEV,
+                                                            dtype=torch.float64) * T).float()
+        q = logits_to_probabilities(draft_logits, T)
+        np.testing.assert_allclose(q.cpu().numpy(), oracle.logits_to_probabilities(draft_logits.cpu().numpy(), T),
+                                   rtol=1e-12, atol=1e-300)
+        tokens = sample_categorical(q, torch.rand(R * N, generator=gen, device=DEV, dtype=torch.float64))
+        uniforms = torch.rand(R * (N + 1), generator=gen, device=DEV, dtype=torch.float64)
+        got = verify_proposals(target, tokens, q, uniforms, counts=[N] * R, temperature=T,
+                               max_new_tokens=[N + 1] * R)
+        p_h = oracle.logits_to_probabilities(target.cpu().numpy(), T)
+        q_h, t_h, u_h = q.cpu().numpy(), tokens.cpu().numpy(), uniforms.cpu().numpy()
+        for r in range(R):
+            ref = oracle.verify_proposal(t_h[N * r:N * r + N], q_h[N * r:N * r + N],
+                                         p_h[(N + 1) * r:(N + 1) * (r + 1)], u_h[(N + 1) * r:(N + 1) * (r + 1)],
+                                         max_new_tokens=N + 1)
+            assert as_tuple(got[r]) == (ref.tokens, ref.accepted_draft_tokens, ref.rejected_index,
+                                        ref.extra_token_kind, ref.stop_reason), (T, r)
+            assert got[r].draws == ref.draws
