@@ -62,6 +62,8 @@ def parse():
     ap.add_argument('--chunk', type=int, default=None, help='keys per split-K verification work item')
     ap.add_argument('--draft-chunk', type=int, default=None, help='keys per split-K draft work item')
     ap.add_argument('--no-cpu-baseline', action='store_true', help='skip the CPU oracle leg (profiling runs)')
+    ap.add_argument('--equal-runs', action='store_true',
+                    help='verification plans with equal runs on every XCD (no XCD speed calibration)')
     ap.add_argument('--traffic-summary', nargs=2, metavar=('FETCH_DIR', 'WRITE_DIR'),
                     help='turn the FETCH_SIZE and WRITE_SIZE passes of --traffic-probe into profiles/*_traffic.json')
     ap.add_argument('--traffic-probe', action='store_true',
@@ -151,6 +153,10 @@ def main():
         pool.load_prefix(h, pool.keys[:, h.index, :c], pool.values[:, h.index, :c])
     bucket = Bucket((Q_LEN,) * B, (CAPACITY - Q_LEN,) * B, '64-request stress shape')
     pool.register_bucket(bucket)
+    # XCD-balanced plans: measure once, at set-up, how fast each XCD reads the
+    # store (as a server would at start-up); later plans size each XCD's runs.
+    xcd_speed = pool.calibrate_xcd() if not args.equal_runs else None
+    log(f'[bench] XCD speeds: {None if xcd_speed is None else [round(x, 3) for x in xcd_speed]}')
     qv = torch.randn(VERIFY_LAYERS, B * Q_LEN, 16, 128, generator=gen, device=dev).to(torch.bfloat16)
     kn = torch.randn(VERIFY_LAYERS, B * Q_LEN, 8, 128, generator=gen, device=dev).to(torch.bfloat16)
     vn = torch.randn(VERIFY_LAYERS, B * Q_LEN, 8, 128, generator=gen, device=dev).to(torch.bfloat16)
@@ -290,6 +296,7 @@ def main():
             'draft_attn_tokens_per_s': round(nq_d / (float(np.median(d_ms)) * 1e-3), 1),
             'round_algorithmic_bytes': int(round_bytes), 'round_gbs': round(round_gbs, 1),
             'round_frac': round(round_gbs / HBM_PEAK_GBS, 4),
+            'xcd_speed': None if xcd_speed is None else [round(x, 4) for x in xcd_speed],
         },
     }
 
@@ -546,6 +553,8 @@ def traffic_probe(args):
         pool.load_prefix(h, pool.keys[:, h.index, :c], pool.values[:, h.index, :c])
     bucket = Bucket((Q_LEN,) * B, (CAPACITY - Q_LEN,) * B, '64-request stress shape')
     pool.register_bucket(bucket)
+    if not args.equal_runs:
+        pool.calibrate_xcd()          # the plan of the timed rounds
     q = torch.zeros(B * Q_LEN, 16, 128, dtype=torch.bfloat16, device=dev)
     kn = torch.zeros(B * Q_LEN, 8, 128, dtype=torch.bfloat16, device=dev)
     tx = pool.begin(handles, bucket)

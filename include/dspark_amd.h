@@ -38,6 +38,18 @@ int dspark_abi_version(void);
 int dspark_stream_read(const void* src, int64_t bytes, int nontemporal, int workgroups, void* out, void* stream);
 
 /*
+ * Measurement utility, no reference counterpart: the read bandwidth each XCD
+ * gets from a region.  `workgroups` (a multiple of 8) workgroups of 256
+ * threads each stream their own contiguous slice of `bytes` at `src` with
+ * non-temporal 16-byte loads; workgroup w (which runs on XCD w mod 8)
+ * writes stamps[3w] = start and stamps[3w+1] = end (a 100 MHz constant
+ * clock) and stamps[3w+2] = its XCD id (low 32 bits) with the slice's
+ * checksum (high 32 bits).  The caller derives per-XCD speeds, e.g. for the
+ * xcd-weighted plans of the varlen / verify work lists.
+ */
+int dspark_xcd_read_stamps(const void* src, int64_t bytes, int workgroups, void* stamps, void* stream);
+
+/*
  * Bytes of split-K workspace needed by an attention call.  Layout: FP32
  * partial outputs, then FP32 (max, sum) pairs, for `n` partial slots of 8 KV
  * heads x `row_tiles` 16-row tiles (row_tiles = ceil(max_q/8) for
@@ -56,7 +68,9 @@ int64_t dspark_attn_workspace_bytes(int n_req, int64_t key_rows_bound, int row_t
  * the device beyond clamping the run ranges to [0, n_work]).
  *
  * varlen / verify: segment lists.  A segment is keys [k0, k1) of one
- * request.  Workgroup (run w, KV head g) processes the records of run w:
+ * request.  Workgroup (run w, KV head g) processes the records of run w;
+ * n_groups must be a multiple of 8, and the 8 workgroups of run w run on
+ * XCD w mod 8 (so a plan can size each XCD's runs to its measured speed):
  *   [n_work][8] segment records, grouped by run:
  *       request, k0, k1, partial slot (-1 when the request has one segment,
  *       which then writes the output), first query row, query length,

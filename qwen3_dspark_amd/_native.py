@@ -24,6 +24,7 @@ SIGNATURES = {
     'dspark_last_error': (ctypes.c_char_p, []),
     'dspark_abi_version': (_I, []),
     'dspark_stream_read': (_I, [_P, _L, _I, _I, _P, _P]),
+    'dspark_xcd_read_stamps': (_I, [_P, _L, _I, _P, _P]),
     'dspark_attn_workspace_bytes': (_L, [_I, _L, _I, _I]),
     'dspark_varlen_attn_fwd': (_I, [_P, _P, _P, _P, _P, _I, _L, _L, _I, _I, _F, _I, _P, _I, _I, _P, _P, _L, _P]),
     'dspark_verify_attn_fwd': (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _I, _L, _L, _L, _L, _I, _F, _I, _P, _I, _I,

@@ -599,16 +599,21 @@ __device__ __forceinline__ void varlen_run(const VarlenArgs& a, unsigned char* s
   }
 }
 
-// With a work list, workgroup (w, g) runs the segments w's range of records
-// names, for KV head g (blockIdx.x = 8w + g).  Without one, a persistent
-// grid walks the fixed chunks (item, KV head) with a stride of the grid
-// size, so per-workgroup start-up is paid once per CU slot.
+// With a work list, the 8 workgroups of run w (one per KV head g) all run
+// on XCD w mod 8: workgroups are dealt round-robin over the 8 XCDs, so
+// blockIdx.x = 8 (8 (w / 8) + g) + w mod 8 (the run count is a multiple of
+// 8).  A plan can then size the runs of each XCD to its measured speed.
+// Without a list, a persistent grid walks the fixed chunks (item, KV head)
+// with a stride of the grid size, so per-workgroup start-up is paid once
+// per CU slot.
 template <bool VERIFY>
 __global__ __launch_bounds__(256, 2) void varlen_attn_kernel(VarlenArgs a) {
   __shared__ __attribute__((aligned(16))) unsigned char smem[VARLEN_SMEM];
-  const int g = blockIdx.x & 7;
+  const int slot = blockIdx.x >> 3;
+  const int g = a.work ? (slot & 7) : (blockIdx.x & 7);
   if (a.work) {
-    const int32_t* range = a.work + WORK_INTS * a.n_work + (blockIdx.x >> 3);
+    const int run = ((slot >> 3) << 3) | (blockIdx.x & 7);
+    const int32_t* range = a.work + WORK_INTS * a.n_work + run;
     const int b = min(max(range[0], 0), a.n_work);      // clamped: never past the records
     const int e = min(max(range[1], b), a.n_work);
     varlen_run<VERIFY>(a, smem, g, blockIdx.y, [&](int n, Segment& sg) {
@@ -1412,8 +1417,8 @@ template <bool VERIFY>
 int varlen_launch(VarlenArgs& a, int64_t key_rows_bound, int max_q, float scale, int chunk, const int32_t* work,
                   int n_work, int n_groups, void* workspace, int64_t workspace_bytes_, void* stream, const char* what) {
   DSPARK_REQUIRE(max_q >= 1, "max_q must be >= 1");
-  DSPARK_REQUIRE(!work || (n_work >= 1 && n_groups >= 1 && n_groups <= (1 << 24)),
-                 "a work list needs n_work >= 1 and n_groups in [1, 2^24]");
+  DSPARK_REQUIRE(!work || (n_work >= 1 && n_groups >= 8 && n_groups <= (1 << 24) && n_groups % 8 == 0),
+                 "a work list needs n_work >= 1 and n_groups a multiple of 8 in [8, 2^24]");
   const int tiles = (max_q + 7) / 8;
   int rc = check_shape(work ? n_work : a.n_req, work ? 0 : key_rows_bound, tiles, chunk, scale);
   if (rc != OK) return rc;

@@ -98,6 +98,7 @@ class HipKVDevice:
         self.layers, self.slots, self.capacity = layers, slots, context_capacity
         self.max_rows, self.heads, self.dim, self.dtype = max_query_tokens, heads, dim, dtype
         self.chunk, self.split = chunk, split
+        self.xcd_speed = None          # relative speed of each XCD for balanced plans (None: equal runs)
         self.elem = torch.empty((), dtype=dtype).element_size()
         self._keys = torch.zeros((layers, slots, heads, context_capacity, dim), dtype=dtype, device=self.device)
         self._values = torch.zeros_like(self._keys)
@@ -148,6 +149,33 @@ class HipKVDevice:
         return (kv + 18 * n + 8 * (r + 1) + 8 * q + 12 * r + 4 * _list_ints(shape, self.device, self.chunk, self.split)
                 + _partials_bytes(shape, self.device, self.chunk, self.split))
 
+    # -- XCD calibration -------------------------------------------------------
+    def measure_xcd_speed(self, workgroups=1024, passes=2):
+        """Relative read bandwidth of the 8 XCDs over this store's resident
+        K and V (dspark_xcd_read_stamps over every layer's K and V region,
+        `passes` times, one host synchronisation at the end): each XCD's
+        mean per-workgroup rate over the mean of the 8."""
+        import numpy as np
+        region = self._keys[0].numel() * self.elem
+        workgroups = max(8, min(int(workgroups), region // (64 << 10)) // 8 * 8)
+        launches = 2 * self.layers * int(passes)
+        stamps = torch.zeros((launches, workgroups, 3), dtype=torch.int64, device=self.device)
+        stream = _native.stream_handle(self.device)
+        i = 0
+        for _ in range(int(passes)):
+            for layer in range(self.layers):
+                for t in (self._keys[layer], self._values[layer]):
+                    _native.call('dspark_xcd_read_stamps', t.data_ptr(), region, workgroups, stamps[i].data_ptr(),
+                                 stream)
+                    i += 1
+        st = stamps.cpu().numpy()
+        per = -(-(region // 16) // workgroups) * 16
+        size = np.minimum(per, np.maximum(region - per * np.arange(workgroups), 0))     # bytes of each slice
+        rate = size / np.maximum(st[..., 1] - st[..., 0], 1)
+        xcd = st[..., 2] & 15
+        mean = np.array([rate[xcd == x].mean() for x in range(8)])
+        return [float(x) for x in mean / mean.mean()]
+
     # -- resident rows --------------------------------------------------------
     def write_prefix(self, slot, keys, values):
         n = keys.shape[1]
@@ -166,7 +194,7 @@ class HipKVDevice:
         key_lengths = [c + q for c, q in zip(contexts, query_lengths)]
         runs = run_count(sum(key_lengths), cu_count(self.device), (shape.maximum_query_length + 7) // 8)
         records, _, _ = segment_plan(self.split, query_lengths, key_lengths, slots, runs, self.chunk,
-                                     self.launch_shape(shape))
+                                     self.launch_shape(shape), xcd_speed=self.xcd_speed)
         if len(records) > ws.work.numel():
             raise ValueError('Work list exceeds the bucket workspace')
         r = len(slots)

@@ -24,6 +24,7 @@ launch lives in an injected device half (kv_device.HipKVDevice):
 """
 import enum
 import heapq
+import math
 from dataclasses import dataclass
 from types import SimpleNamespace
 from typing import Mapping
@@ -420,6 +421,39 @@ class PersistentTargetKV:
     def workspace(self, bucket):
         """Device buffers of a registered bucket or family."""
         return self._workspaces[bucket]
+
+    # -- XCD-balanced plans (no reference counterpart) -------------------------
+    @property
+    def xcd_speed(self):
+        """Relative speeds of the 8 XCDs that size the runs of later balanced
+        plans (run w executes on XCD w mod 8), or None for equal runs."""
+        return self.kv_device.xcd_speed
+
+    def set_xcd_speed(self, speed):
+        """Use the given 8 relative XCD speeds (positive, finite; None: equal
+        runs) for the plans of later transactions."""
+        self._permit('admin')
+        if speed is not None:
+            speed = tuple(float(x) for x in speed)
+            if len(speed) != 8 or not all(math.isfinite(x) and x > 0 for x in speed):
+                raise ValueError('xcd_speed must give 8 positive finite relative speeds')
+            mean = sum(speed) / 8
+            speed = tuple(x / mean for x in speed)
+        self.kv_device.xcd_speed = speed
+
+    def calibrate_xcd(self, *, workgroups=1024, passes=2, clip=0.25):
+        """Measure the read bandwidth each XCD gets from this store's resident
+        K/V and size the runs of later balanced plans to it, so that the
+        XCDs finish together: the 8 XCDs of an MI355X do not read a given
+        allocation equally fast, and which are slower depends on where it
+        landed.  Relative speeds are clipped to 1 +- clip.  Opt-in: cut
+        points then depend on the measurement, so outputs can differ in the
+        last bits between processes (as between batches).  Returns the
+        speeds in use."""
+        self._permit('admin')
+        raw = self.kv_device.measure_xcd_speed(workgroups=workgroups, passes=passes)
+        self.set_xcd_speed([min(1.0 + clip, max(1.0 - clip, x)) for x in raw])
+        return self.xcd_speed
 
     def register_bucket(self, bucket):
         self._permit('admin')

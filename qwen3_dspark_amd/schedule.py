@@ -3,7 +3,8 @@
 Varlen / verification attention: balanced key segments.  The keys of all
 requests, laid end to end in request order, are cut into `groups` runs of
 (nearly) equal length, each cut moved to a 32-key tile boundary of the
-request it falls in; workgroup (w, KV head g) streams run w.  A run may end
+request it falls in; the 8 workgroups of run w (one per KV head) run on
+XCD w mod 8 (see XCDS).  A run may end
 inside one request and start inside the next, so a request is held by one
 or more segments (one per run it meets).  Every workgroup therefore reads
 the same number of key rows, whatever the mix of context lengths, and a
@@ -20,6 +21,9 @@ the merge.
            length, key length, first key row (varlen) or resident slot (verify)
   request: first partial slot, segment count, first query row, query length
 
+With measured per-XCD speeds (xcd_speed), run w's share of the cost is
+proportional to the speed of its XCD, so that the XCDs finish together.
+
 Draft attention: the same balanced segments over the context rows each
 request streams (up to its largest anchor), one run per (workgroup, KV
 head), cuts on 64-row ring-stage boundaries (draft_work).
@@ -33,6 +37,7 @@ DEFAULT_CHUNK = 1024          # verification / varlen: fixed chunks when no list
 TILE = 32                     # segment cuts fall on multiples of this many keys
 MIN_SEGMENT = 256             # fewest keys a run is given (tiny calls use fewer runs)
 RESIDENT_PER_CU = 2           # varlen/verify workgroups resident per CU (register budget)
+XCDS = 8                      # MI355X: workgroup b runs on XCD b mod 8; varlen runs come in whole rounds of 8
 SEGMENT_COST = 64             # keys' worth of fixed work per segment in balanced varlen plans (measured)
 DRAFT_TILE = 64               # draft cuts fall on multiples of the ring stage
 DRAFT_SEGMENT_COST = 512      # balanced draft plans: fixed cost of a segment, in context rows (measured)
@@ -76,9 +81,11 @@ def _bases(lengths, chunk):
 
 def run_count(total_keys, n_cu, row_tiles=1):
     """Runs for a balanced list: one workgroup per CU slot and KV head when
-    there is enough work, never fewer than MIN_SEGMENT keys per run."""
-    slots = max(1, (int(n_cu) * RESIDENT_PER_CU) // (8 * max(1, int(row_tiles))))
-    return max(1, min(slots, -(-int(total_keys) // MIN_SEGMENT)))
+    there is enough work, about MIN_SEGMENT keys per run at least, in whole
+    rounds of XCDS runs (run w executes on XCD w mod XCDS)."""
+    slots = max(XCDS, (int(n_cu) * RESIDENT_PER_CU) // (8 * max(1, int(row_tiles))) // XCDS * XCDS)
+    runs = max(1, min(slots, -(-int(total_keys) // MIN_SEGMENT)))
+    return -(-runs // XCDS) * XCDS
 
 
 def _flatten(n, per_run, record, request):
@@ -126,15 +133,25 @@ def _segment_list(query_lengths, key_lengths, starts, per_run):
                     lambda r, first, count: (first, count, q0[r], int(query_lengths[r])))
 
 
-def _balanced_runs(key_lengths, groups, tile, seg_cost=0, weights=None):
+def _balanced_runs(key_lengths, groups, tile, seg_cost=0, weights=None, shares=None):
     """Per-run [(request, k0, k1)] lists: the keys of all requests end to end,
     cut into `groups` runs of (nearly) equal cost, each cut moved down to a
     `tile` boundary of the request holding it.  A request costs seg_cost
     (the fixed work of starting a segment, in keys) plus its keys, each
     weighted by weights[r] (default 1), so runs that hold more request
-    starts or heavier keys get fewer keys."""
+    starts or heavier keys get fewer keys.  shares (one positive number per
+    run) makes run w's cost proportional to shares[w] instead of equal."""
     n = len(key_lengths)
     groups = max(1, int(groups))
+    if shares is None:
+        bound = [w / groups for w in range(groups + 1)]
+    else:
+        if len(shares) != groups or min(shares) <= 0:
+            raise ValueError('shares must give one positive number per run')
+        bound, acc, tot = [0.0], 0.0, float(sum(shares))
+        for x in shares:
+            acc += float(x)
+            bound.append(acc / tot)
     seg_cost = max(0.0, float(seg_cost))
     wt = [1.0] * n if weights is None else [max(1e-3, float(x)) for x in weights]
     begin, vbegin, total, vtotal = [], [], 0, 0.0
@@ -145,7 +162,7 @@ def _balanced_runs(key_lengths, groups, tile, seg_cost=0, weights=None):
         vtotal += seg_cost + w * int(k)
     cuts, r = [0], 0
     for w in range(1, groups):
-        x = w * vtotal / groups                       # cut in cost space
+        x = bound[w] * vtotal                         # cut in cost space
         while r + 1 < n and vbegin[r + 1] <= x:
             r += 1
         into = int(max(0.0, (x - vbegin[r] - seg_cost) / wt[r]))   # keys of request r before the cut
@@ -171,15 +188,29 @@ def _balanced_runs(key_lengths, groups, tile, seg_cost=0, weights=None):
     return per_run
 
 
-def varlen_work(query_lengths, key_lengths, starts, groups, seg_cost=None):
+def xcd_shares(groups, xcd_speed):
+    """Cost share of each of `groups` runs: the speed of the XCD it runs on
+    (run w on XCD w mod XCDS), or None for equal runs."""
+    if xcd_speed is None:
+        return None
+    speed = [float(x) for x in xcd_speed]
+    if len(speed) != XCDS or min(speed) <= 0:
+        raise ValueError(f'xcd_speed must give {XCDS} positive relative speeds')
+    return [speed[w % XCDS] for w in range(int(groups))]
+
+
+def varlen_work(query_lengths, key_lengths, starts, groups, seg_cost=None, xcd_speed=None):
     """Balanced plan: (flat int32 list, segment count, run count) for varlen (starts =
     first key row of each request) or verify (starts = resident slot of each
     request); groups = number of runs (workgroups per KV head); seg_cost
-    (default SEGMENT_COST) the fixed cost of a segment in keys.  The cut
-    points depend on every request's length, so a request's output can
-    differ in the last bits between batches; request_work keeps them apart."""
+    (default SEGMENT_COST) the fixed cost of a segment in keys; xcd_speed
+    (8 relative speeds) weights each run by the speed of its XCD.  The cut
+    points depend on every request's length (and on xcd_speed), so a
+    request's output can differ in the last bits between batches;
+    request_work keeps them apart."""
     cost = SEGMENT_COST if seg_cost is None else seg_cost
-    return _segment_list(query_lengths, key_lengths, starts, _balanced_runs(key_lengths, groups, TILE, cost))
+    return _segment_list(query_lengths, key_lengths, starts,
+                         _balanced_runs(key_lengths, groups, TILE, cost, shares=xcd_shares(groups, xcd_speed)))
 
 
 def request_work(query_lengths, key_lengths, starts, chunk, groups):
@@ -195,7 +226,7 @@ def request_work(query_lengths, key_lengths, starts, chunk, groups):
             k0 = c * chunk
             segs.append((min(chunk, kl - k0) if kl > 0 else 0, r, k0, min(kl, k0 + chunk)))
     segs.sort(key=lambda x: (-x[0], x[1], x[2]))
-    groups = max(1, min(int(groups), len(segs)))
+    groups = -(-max(1, min(int(groups), len(segs))) // XCDS) * XCDS     # whole rounds over the XCDs
     heap = [(0, w) for w in range(groups)]
     per_run = [[] for _ in range(groups)]
     for size, r, k0, k1 in segs:
@@ -218,16 +249,17 @@ def varlen_list_bound(n_req, groups, rows_bound=0, chunk=None):
 SPLITS = ('balanced', 'request')
 
 
-def segment_plan(split, query_lengths, key_lengths, starts, groups, chunk, capacity=None):
+def segment_plan(split, query_lengths, key_lengths, starts, groups, chunk, capacity=None, xcd_speed=None):
     """(flat int32 list, segment count, run count) of the named plan; the
-    launch must pass the returned counts (n_work, n_groups).
+    launch must pass the returned counts (n_work, n_groups).  xcd_speed:
+    see varlen_work (balanced plans only).
 
     capacity = (segments, runs) lays the list out in regions of fixed size:
     the records padded to `segments`, the run ranges to `runs` (trailing runs
     empty).  Every transaction of a bucket then launches with the same
     arguments and grid, which a captured graph replays."""
     if split == 'balanced':
-        out, n_seg, runs = varlen_work(query_lengths, key_lengths, starts, groups)
+        out, n_seg, runs = varlen_work(query_lengths, key_lengths, starts, groups, xcd_speed=xcd_speed)
     elif split == 'request':
         out, n_seg, runs = request_work(query_lengths, key_lengths, starts, chunk, groups)
     else:

@@ -23,6 +23,11 @@ class CpuKVDevice:
         self.scratch_values = torch.zeros_like(self.scratch_keys)
         self.calls = []            # device-call names, in order
         self.fail = None           # name of a device call to fail once (injected fault)
+        self.xcd_speed = None      # relative XCD speeds for balanced plans (the device half holds them)
+
+    def measure_xcd_speed(self, workgroups=1024, passes=2):
+        self._enter('measure_xcd_speed')
+        return [1.3, 0.7, 1.0, 1.0, 1.0, 1.0, 1.0, 1.0]
 
     def _enter(self, name):
         self.calls.append(name)

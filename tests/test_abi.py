@@ -93,6 +93,9 @@ def test_invalid_sizes_are_rejected_before_any_launch():
     rc = lib.dspark_varlen_attn_fwd(fake, fake, fake, fake, fake, 2, 8, 8, 1, 1, 0.088, 512, fake, 0, 1, fake, fake,
                                     1 << 20, None)
     assert rc == -1 and 'n_work' in lib.dspark_last_error().decode()
+    rc = lib.dspark_varlen_attn_fwd(fake, fake, fake, fake, fake, 2, 8, 8, 1, 1, 0.088, 512, fake, 3, 12, fake, fake,
+                                    1 << 20, None)
+    assert rc == -1 and 'multiple of 8' in lib.dspark_last_error().decode()
     rc = lib.dspark_draft_attn_fwd(fake, 0, fake, fake, 0, None, fake, fake, 1024, 128, fake, fake, fake, fake,
                                    2, 100, 9, 0.088, 512, None, 0, 0, fake, fake, 1 << 24, None)
     assert rc == -1 and 'max_blocks' in lib.dspark_last_error().decode()

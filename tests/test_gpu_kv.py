@@ -367,6 +367,47 @@ def test_fused_verify_attention_parity_commit_and_second_round(dev):
             assert torch.isnan(pool.keys[:, h.index, ctx[i] + n:]).all()
 
 
+def test_xcd_calibration_and_skewed_plans_meet_the_oracle(dev):
+    """XCD-balanced plans (no reference counterpart): calibrate_xcd on a
+    real store gives 8 speeds of mean 1 within 1 +- 0.25, and with strongly
+    skewed speeds (runs of one XCD carrying 2.5x the cost of another's) the
+    fused verification attention still meets the oracle; the work list's
+    cuts move, the cover stays exact."""
+    from qwen3_dspark_amd.persistent_kv import Bucket, PersistentTargetKV
+    rng = np.random.default_rng(SEED + 3)
+    gen = torch.Generator().manual_seed(SEED + 3)
+    B, C = 6, 4096
+    pool = PersistentTargetKV(layers=1, slots=B, context_capacity=C, max_query_tokens=7 * B, heads=8, dim=128,
+                              device=dev)
+    handles = [pool.add_request(f'r{i}') for i in range(B)]
+    for h in handles:
+        n = int(rng.integers(256, C - 7))
+        kv = randn_bf16(gen, 2, 1, n, 8, 128).to(dev)
+        pool.load_prefix(h, kv[0], kv[1])
+    speed = pool.calibrate_xcd()
+    say(f'[xcd] calibrated speeds {[round(x, 3) for x in speed]}')
+    assert len(speed) == 8 and abs(sum(speed) / 8 - 1) < 1e-9 and all(0.75 <= x <= 1.25 for x in speed)
+    bucket = Bucket((7,) * B, (C - 7,) * B, 'xcd plans')
+    pool.register_bucket(bucket)
+    ctx = [pool.length(h) for h in handles]
+    cu_q = list(range(0, 7 * B + 1, 7))
+    lists = []
+    for skew in (None, (2.0, 0.8, 1.4, 1.0, 1.2, 0.9, 1.1, 1.0)):
+        pool.set_xcd_speed(skew)
+        tx = pool.begin(handles, bucket)
+        lists.append(pool.workspace(bucket).work.clone())
+        q = randn_bf16(gen, 7 * B, 16, 128).to(dev)
+        nk = randn_bf16(gen, 7 * B, 8, 128).to(dev)
+        nv = randn_bf16(gen, 7 * B, 8, 128).to(dev)
+        out = pool.attend(tx, 0, q, keys=nk, values=nv)
+        torch.cuda.synchronize()
+        ref = cref.verify_attention(bits(q), bits(pool.keys[0]), bits(pool.values[0]), bits(pool.scratch_keys[0]),
+                                    bits(pool.scratch_values[0]), [h.index for h in handles], ctx, cu_q, scale=SCALE)
+        attention_gate(f64(out), ref, segments(cu_q))
+        pool.abort(tx)
+    assert not torch.equal(lists[0], lists[1])      # the skewed speeds moved the cuts
+
+
 def test_verify_rows_without_visible_keys_in_a_tile(dev):
     """Contexts whose last key tile holds new rows visible to the later
     query rows only (c + 7 just past a 32-key or chunk boundary): every

@@ -20,13 +20,13 @@ def decode(out, n_seg, groups, n_req):
     return rec, ranges, reqs
 
 
-def check(query_lengths, key_lengths, starts, groups, chunk=None, seg_cost=None):
+def check(query_lengths, key_lengths, starts, groups, chunk=None, seg_cost=None, xcd_speed=None):
     if chunk is None:
-        out, n_seg, runs = varlen_work(query_lengths, key_lengths, starts, groups, seg_cost)
+        out, n_seg, runs = varlen_work(query_lengths, key_lengths, starts, groups, seg_cost, xcd_speed=xcd_speed)
         assert runs == groups
     else:
         out, n_seg, runs = request_work(query_lengths, key_lengths, starts, chunk, groups)
-        assert runs == max(1, min(groups, n_seg))
+        assert runs == -(-max(1, min(groups, n_seg)) // 8) * 8 and runs % 8 == 0
         groups = runs
     n = len(key_lengths)
     rec, ranges, reqs = decode(out, n_seg, groups, n)
@@ -90,11 +90,14 @@ def test_edge_shapes(kl, groups):
 
 
 def test_run_count_bounds():
-    assert run_count(10, 256) == 1
-    assert run_count(MIN_SEGMENT * 3, 256) == 3
+    # whole rounds of 8 runs (run w executes on XCD w mod 8)
+    assert run_count(10, 256) == 8
+    assert run_count(MIN_SEGMENT * 3, 256) == 8
+    assert run_count(MIN_SEGMENT * 12, 256) == 16
     assert run_count(10 ** 7, 256) == 64
     assert run_count(10 ** 7, 256, row_tiles=2) == 32
-    assert run_count(10 ** 7, 304) == 76
+    assert run_count(10 ** 7, 304) == 72
+    assert run_count(10 ** 7, 8, row_tiles=4) == 8
 
 
 def test_random_shapes_cover_exactly():
@@ -201,3 +204,27 @@ def test_draft_plan_covers_each_streamed_context_once():
             assert max(cost) - min(cost) <= 2 * (DRAFT_TILE * (1 + 7 * DRAFT_BLOCK_WEIGHT) + DRAFT_SEGMENT_COST) + 1
         else:
             assert loads == sorted(loads, reverse=True) and max(loads) <= 1024   # longest first
+
+
+def test_xcd_speeds_size_the_runs_of_each_xcd():
+    """Run w executes on XCD w mod 8: with measured XCD speeds, each XCD's
+    runs carry cost in proportion to its speed (the cover stays exact)."""
+    rng = np.random.default_rng(20261009)
+    ctx = np.floor(np.exp(rng.uniform(np.log(256), np.log(8192), size=64))).astype(int)
+    kl = [int(c) + 7 for c in ctx]
+    groups = run_count(sum(kl), 256)
+    speed = [1.05, 0.95, 1.03, 0.97, 1.04, 0.96, 1.02, 0.98]
+    loads, _ = check([7] * 64, kl, list(range(64)), groups, xcd_speed=speed)
+    cost = [k + SEGMENT_COST * n for k, n in zip(loads, check.starts)]
+    total = sum(cost)
+    for w in range(groups):   # every run within two cuts' rounding of its share
+        assert abs(cost[w] - total * speed[w % 8] / (sum(speed) * groups / 8)) <= 2 * (TILE + SEGMENT_COST)
+    per_xcd = [sum(cost[w] for w in range(x, groups, 8)) for x in range(8)]
+    ratios = [c / v for c, v in zip(per_xcd, speed)]
+    assert max(ratios) / min(ratios) < 1.02
+    assert sum(loads) == sum(kl)
+    # equal speeds give the equal plan
+    assert varlen_work([7] * 64, kl, list(range(64)), groups, xcd_speed=[2.0] * 8) == \
+        varlen_work([7] * 64, kl, list(range(64)), groups)
+    with pytest.raises(ValueError, match='8 positive'):
+        varlen_work([7] * 64, kl, list(range(64)), groups, xcd_speed=[1.0] * 7)

@@ -193,6 +193,33 @@ def test_ordered_shape_bounds_and_active_subset(golden):
         pool.register_bucket(Bucket((8, 8), (8, 8), 'fixture'))
 
 
+def test_xcd_speeds_are_validated_normalised_clipped_and_admin_only():
+    """XCD-balanced plans (no reference counterpart): explicit speeds are
+    checked and normalised to mean 1, calibration clips the measured
+    speeds to 1 +- clip, and neither may change during a transaction."""
+    pool = store()
+    assert pool.xcd_speed is None
+    pool.set_xcd_speed([2.0, 2.0, 2.0, 2.0, 4.0, 4.0, 4.0, 4.0])
+    assert pool.xcd_speed == (2 / 3,) * 4 + (4 / 3,) * 4
+    for bad in ([1.0] * 7, [1.0] * 7 + [0.0], [1.0] * 7 + [float('nan')], [1.0] * 7 + [-1.0]):
+        with pytest.raises(ValueError, match='8 positive finite'):
+            pool.set_xcd_speed(bad)
+    pool.set_xcd_speed(None)
+    assert pool.xcd_speed is None
+    got = pool.calibrate_xcd(clip=0.1)                       # the stand-in measures 1.3, 0.7, 1, ...
+    assert pool.kv_device.calls[-1] == 'measure_xcd_speed'
+    assert got == pytest.approx([1.1, 0.9, 1.0, 1.0, 1.0, 1.0, 1.0, 1.0])
+    h = pool.add_request('a')
+    bucket = Bucket((1,), (4,), 'xcd')
+    pool.register_bucket(bucket)
+    tx = pool.begin([h], bucket)
+    with pytest.raises(RuntimeError, match='Outstanding verification transaction'):
+        pool.set_xcd_speed(None)
+    with pytest.raises(RuntimeError, match='Outstanding verification transaction'):
+        pool.calibrate_xcd()
+    pool.abort(tx)
+
+
 def test_attention_staging_matches_independent_variable_prefix_sdpa():
     """tests/test_persistent_target_kv.py:133-147: each request's slice of the
     materialised K/V gives exactly the attention over its true rows."""
