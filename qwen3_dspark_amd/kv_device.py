@@ -152,29 +152,10 @@ class HipKVDevice:
     # -- XCD calibration -------------------------------------------------------
     def measure_xcd_speed(self, workgroups=1024, passes=2):
         """Relative read bandwidth of the 8 XCDs over this store's resident
-        K and V (dspark_xcd_read_stamps over every layer's K and V region,
-        `passes` times, one host synchronisation at the end): each XCD's
-        mean per-workgroup rate over the mean of the 8."""
-        import numpy as np
-        region = self._keys[0].numel() * self.elem
-        workgroups = max(8, min(int(workgroups), region // (64 << 10)) // 8 * 8)
-        launches = 2 * self.layers * int(passes)
-        stamps = torch.zeros((launches, workgroups, 3), dtype=torch.int64, device=self.device)
-        stream = _native.stream_handle(self.device)
-        i = 0
-        for _ in range(int(passes)):
-            for layer in range(self.layers):
-                for t in (self._keys[layer], self._values[layer]):
-                    _native.call('dspark_xcd_read_stamps', t.data_ptr(), region, workgroups, stamps[i].data_ptr(),
-                                 stream)
-                    i += 1
-        st = stamps.cpu().numpy()
-        per = -(-(region // 16) // workgroups) * 16
-        size = np.minimum(per, np.maximum(region - per * np.arange(workgroups), 0))     # bytes of each slice
-        rate = size / np.maximum(st[..., 1] - st[..., 0], 1)
-        xcd = st[..., 2] & 15
-        mean = np.array([rate[xcd == x].mean() for x in range(8)])
-        return [float(x) for x in mean / mean.mean()]
+        K and V (every layer's K and V region; xcd.measure_read_speed)."""
+        from .xcd import measure_read_speed
+        return measure_read_speed([t for layer in range(self.layers) for t in (self._keys[layer], self._values[layer])],
+                                  workgroups=workgroups, passes=passes)
 
     # -- resident rows --------------------------------------------------------
     def write_prefix(self, slot, keys, values):

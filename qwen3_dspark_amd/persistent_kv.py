@@ -24,7 +24,6 @@ launch lives in an injected device half (kv_device.HipKVDevice):
 """
 import enum
 import heapq
-import math
 from dataclasses import dataclass
 from types import SimpleNamespace
 from typing import Mapping
@@ -34,6 +33,7 @@ import torch
 from .kernels import HEAD_DIM, KV_HEADS, Q_HEADS, SCALE, _check_scale
 from .kv_device import MAX_BUCKET_REQUESTS, HipKVDevice
 from .schedule import DEFAULT_CHUNK, SPLITS
+from .xcd import clipped, normalised
 
 
 @dataclass(frozen=True)
@@ -433,13 +433,7 @@ class PersistentTargetKV:
         """Use the given 8 relative XCD speeds (positive, finite; None: equal
         runs) for the plans of later transactions."""
         self._permit('admin')
-        if speed is not None:
-            speed = tuple(float(x) for x in speed)
-            if len(speed) != 8 or not all(math.isfinite(x) and x > 0 for x in speed):
-                raise ValueError('xcd_speed must give 8 positive finite relative speeds')
-            mean = sum(speed) / 8
-            speed = tuple(x / mean for x in speed)
-        self.kv_device.xcd_speed = speed
+        self.kv_device.xcd_speed = normalised(speed)
 
     def calibrate_xcd(self, *, workgroups=1024, passes=2, clip=0.25):
         """Measure the read bandwidth each XCD gets from this store's resident
@@ -451,8 +445,7 @@ class PersistentTargetKV:
         last bits between processes (as between batches).  Returns the
         speeds in use."""
         self._permit('admin')
-        raw = self.kv_device.measure_xcd_speed(workgroups=workgroups, passes=passes)
-        self.set_xcd_speed([min(1.0 + clip, max(1.0 - clip, x)) for x in raw])
+        self.set_xcd_speed(clipped(self.kv_device.measure_xcd_speed(workgroups=workgroups, passes=passes), clip))
         return self.xcd_speed
 
     def register_bucket(self, bucket):
