@@ -38,7 +38,7 @@ TILE = 32                     # segment cuts fall on multiples of this many keys
 MIN_SEGMENT = 256             # fewest keys a run is given (tiny calls use fewer runs)
 RESIDENT_PER_CU = 2           # varlen/verify workgroups resident per CU (register budget)
 XCDS = 8                      # MI355X: workgroup b runs on XCD b mod 8; varlen runs come in whole rounds of 8
-SEGMENT_COST = 64             # keys' worth of fixed work per segment in balanced varlen plans (measured)
+SEGMENT_COST = 96             # keys' worth of fixed work per segment in balanced varlen plans (measured)
 DRAFT_TILE = 64               # draft cuts fall on multiples of the ring stage
 DRAFT_SEGMENT_COST = 512      # balanced draft plans: fixed cost of a segment, in context rows (measured)
 DRAFT_BLOCK_WEIGHT = 0.055    # balanced draft plans: extra cost of a row per block beyond the first (measured)
