@@ -219,7 +219,7 @@ int dspark_draft_attn_fwd(const void* q, int q_dtype, const void* k_ctx, const v
  * [tokens, 16, 128]; k_out/v_out token rows of 8*128 elements,
  * kv_row_stride apart (1024 writes a [tokens, 8, 128] tensor, e.g. the
  * transaction scratch layer, replacing stage_layer's copy).  hidden must be
- * a multiple of 64.  FP32 accumulation, bf16 outputs.
+ * a multiple of 128.  FP32 accumulation, bf16 outputs.
  */
 int dspark_qkv_prologue(const void* x, const void* wq, const void* wk, const void* wv,
                         const void* q_norm, const void* k_norm, const float* inv_freq,

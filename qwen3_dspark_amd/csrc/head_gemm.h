@@ -15,10 +15,12 @@
 // (d + 64 = tile mt + 4) sits in the same lane.
 //
 // The head's weight slice [128, hidden] and the workgroup's token rows
-// stream through a 6-stage LDS ring fed by direct-to-LDS loads: every thread
-// issues exactly 3 loads per stage (2 weight pieces, 1 token piece), so the
-// weights are read once per workgroup and shared by the 8 waves, with 5
-// stages in flight.
+// stream through a 3-stage LDS ring fed by direct-to-LDS loads.  A stage is
+// two 64-column sub-stages (128 hidden columns, one barrier): every thread
+// issues exactly 3 loads per sub-stage (2 weight pieces, 1 token piece), so
+// the weights are read once per workgroup and shared by the 8 waves, with 2
+// stages in flight.  (Six single sub-stage stages, 5 in flight, took ≈0.5 us
+// more per 448-token prologue: twice the barriers.)
 #pragma once
 #include "common.h"
 
@@ -26,12 +28,15 @@ namespace dspark {
 
 constexpr int HG_TOKENS = 64;                    // tokens per workgroup, 16 per token group
 constexpr int HG_WAVES = 8;                      // 4 token groups x 2 column halves
-constexpr int HG_KB = 64;                        // hidden columns per ring stage
-constexpr int HG_STAGES = 6;                     // ring depth (5 stages in flight)
+constexpr int HG_KB = 64;                        // hidden columns per sub-stage
+constexpr int HG_SUB = 2;                        // sub-stages per ring stage (one barrier each)
+constexpr int HG_STAGES = 3;                     // ring depth (2 stages in flight)
 constexpr int HG_W_BYTES = HD * HG_KB * 2;       // 128 weight rows x 128 B = 16 KiB
 constexpr int HG_X_BYTES = 16 * HG_KB * 2;       // 16 token rows x 128 B per token group
-constexpr int HG_STAGE_BYTES = HG_W_BYTES + 4 * HG_X_BYTES;   // 24 KiB
+constexpr int HG_SUB_BYTES = HG_W_BYTES + 4 * HG_X_BYTES;     // 24 KiB
+constexpr int HG_STAGE_BYTES = HG_SUB * HG_SUB_BYTES;         // 48 KiB
 constexpr int HG_SMEM = HG_STAGES * HG_STAGE_BYTES;            // 144 KiB
+constexpr int HG_COLS = HG_KB * HG_SUB;          // hidden columns per ring stage (hidden must be a multiple)
 
 // 16-byte chunk swizzle of a 128-byte LDS row: the 16 rows 16*mt + col that
 // one fragment read touches land on 16 distinct bank groups.
@@ -54,7 +59,7 @@ __device__ __forceinline__ void head_tile_gemm(const bf16* __restrict__ w, const
   const int grp = lane >> 4;
   const int tg = wave & 3;
   const int kh = wave >> 2;
-  const int steps = hidden / HG_KB;
+  const int steps = hidden / HG_COLS;
 
   // Direct loads: lane L of a 1 KiB piece (8 rows x 128 B) fetches row
   // 8*piece + L/8, global chunk (L%8) ^ swz(row), landing at LDS chunk L%8.
@@ -63,19 +68,22 @@ __device__ __forceinline__ void head_tile_gemm(const bf16* __restrict__ w, const
   const int prow = lane >> 3;
   auto issue = [&](int step) {
     const int st = min(step, steps - 1);   // past the end: re-read the last stage (never used)
-    const uint32_t base = smem_lds + (uint32_t)((step % HG_STAGES) * HG_STAGE_BYTES);
-    const int k0 = st * HG_KB;
     #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const int piece = 2 * wave + i;
-      const int row = 8 * piece + prow;
-      const bf16* src = w + (size_t)row * hidden + k0 + 8 * ((lane & 7) ^ hg_swz(row));
-      lds_dma16(src, __builtin_amdgcn_readfirstlane(base + (uint32_t)(piece * 1024)));
+    for (int sub = 0; sub < HG_SUB; ++sub) {
+      const uint32_t base = smem_lds + (uint32_t)((step % HG_STAGES) * HG_STAGE_BYTES + sub * HG_SUB_BYTES);
+      const int k0 = (st * HG_SUB + sub) * HG_KB;
+      #pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        const int piece = 2 * wave + i;
+        const int row = 8 * piece + prow;
+        const bf16* src = w + (size_t)row * hidden + k0 + 8 * ((lane & 7) ^ hg_swz(row));
+        lds_dma16(src, __builtin_amdgcn_readfirstlane(base + (uint32_t)(piece * 1024)));
+      }
+      const int row = 8 * wave + prow;      // token row of the tile; row % 16 within its group
+      const int tok = min(t0 + row, tokens - 1);
+      const bf16* src = x + (size_t)tok * hidden + k0 + 8 * ((lane & 7) ^ hg_swz(row & 15));
+      lds_dma16(src, __builtin_amdgcn_readfirstlane(base + (uint32_t)(HG_W_BYTES + wave * 1024)));
     }
-    const int row = 8 * wave + prow;      // token row of the tile; row % 16 within its group
-    const int tok = min(t0 + row, tokens - 1);
-    const bf16* src = x + (size_t)tok * hidden + k0 + 8 * ((lane & 7) ^ hg_swz(row & 15));
-    lds_dma16(src, __builtin_amdgcn_readfirstlane(base + (uint32_t)(HG_W_BYTES + wave * 1024)));
   };
 
   #pragma unroll
@@ -84,24 +92,27 @@ __device__ __forceinline__ void head_tile_gemm(const bf16* __restrict__ w, const
   #pragma unroll
   for (int p = 0; p < HG_STAGES - 1; ++p) issue(p);
   for (int s = 0; s < steps; ++s) {
-    // this thread's stage-s loads landed: the 3 loads of each of the
-    // HG_STAGES - 2 later stages may still be in flight
-    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(3 * (HG_STAGES - 2)) : "memory");
+    // this thread's stage-s loads landed: the 3 loads per sub-stage of each
+    // of the HG_STAGES - 2 later stages may still be in flight
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(3 * HG_SUB * (HG_STAGES - 2)) : "memory");
     asm volatile("s_barrier" ::: "memory");            // ... and everyone else's
     issue(s + HG_STAGES - 1);
-    const unsigned char* wst = smem + (s % HG_STAGES) * HG_STAGE_BYTES;
-    const unsigned char* xst = wst + HG_W_BYTES + tg * HG_X_BYTES;
-    const int c = 4 * kh + grp;
-    const bf16x8 xb = *reinterpret_cast<const bf16x8*>(xst + col * 128 + ((c ^ hg_swz(col)) << 4));
-    if (SUMSQ) {
-      #pragma unroll
-      for (int i = 0; i < 8; ++i) ss += (float)xb[i] * (float)xb[i];
-    }
     #pragma unroll
-    for (int mt = 0; mt < 8; ++mt) {
-      const int row = 16 * mt + col;
-      const bf16x8 wa = *reinterpret_cast<const bf16x8*>(wst + row * 128 + ((c ^ hg_swz(row)) << 4));
-      acc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wa, xb, acc[mt], 0, 0, 0);
+    for (int sub = 0; sub < HG_SUB; ++sub) {
+      const unsigned char* wst = smem + (s % HG_STAGES) * HG_STAGE_BYTES + sub * HG_SUB_BYTES;
+      const unsigned char* xst = wst + HG_W_BYTES + tg * HG_X_BYTES;
+      const int c = 4 * kh + grp;
+      const bf16x8 xb = *reinterpret_cast<const bf16x8*>(xst + col * 128 + ((c ^ hg_swz(col)) << 4));
+      if (SUMSQ) {
+        #pragma unroll
+        for (int i = 0; i < 8; ++i) ss += (float)xb[i] * (float)xb[i];
+      }
+      #pragma unroll
+      for (int mt = 0; mt < 8; ++mt) {
+        const int row = 16 * mt + col;
+        const bf16x8 wa = *reinterpret_cast<const bf16x8*>(wst + row * 128 + ((c ^ hg_swz(row)) << 4));
+        acc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wa, xb, acc[mt], 0, 0, 0);
+      }
     }
   }
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");

@@ -119,8 +119,8 @@ extern "C" int dspark_draft_kv_project(const void* x, int tokens, int hidden, co
                                        int64_t slot_stride, int64_t head_stride, int32_t* flag, void* stream) {
   clear_error();
   DSPARK_REQUIRE(x && w && k_norm && inv_freq && req && k_pool && v_pool, "null pointer argument");
-  DSPARK_REQUIRE(tokens >= 1 && hidden >= HG_KB && hidden % HG_KB == 0, "need tokens >= 1 and hidden a multiple of %d",
-                 HG_KB);
+  DSPARK_REQUIRE(tokens >= 1 && hidden >= HG_COLS && hidden % HG_COLS == 0, "need tokens >= 1 and hidden a multiple of %d",
+                 HG_COLS);
   DSPARK_REQUIRE(layers >= 1 && layers <= 64, "layers must be in [1, 64] (got %d)", layers);
   DSPARK_REQUIRE(n_req >= 1 && n_req <= tokens, "n_req must be in [1, tokens]");
   DSPARK_REQUIRE(eps_ctx > 0.f && eps_k > 0.f, "eps must be positive");

@@ -90,8 +90,8 @@ extern "C" int dspark_qkv_prologue(const void* x, const void* wq, const void* wk
   clear_error();
   DSPARK_REQUIRE(x && wq && wk && wv && q_norm && k_norm && inv_freq && positions && q_out && k_out && v_out,
                  "null pointer argument");
-  DSPARK_REQUIRE(tokens >= 1 && hidden >= HG_KB && hidden % HG_KB == 0, "need tokens >= 1 and hidden a multiple of %d",
-                 HG_KB);
+  DSPARK_REQUIRE(tokens >= 1 && hidden >= HG_COLS && hidden % HG_COLS == 0, "need tokens >= 1 and hidden a multiple of %d",
+                 HG_COLS);
   DSPARK_REQUIRE(kv_row_stride >= KV_ROW && kv_row_stride % 8 == 0, "kv_row_stride must be >= 1024 and a multiple of 8");
   DSPARK_REQUIRE(eps > 0.f, "eps must be positive");
   const uintptr_t any = (uintptr_t)x | (uintptr_t)wq | (uintptr_t)wk | (uintptr_t)wv | (uintptr_t)q_out |

@@ -58,8 +58,8 @@ class DraftContextProjector:
                                  'k_proj/v_proj [8*128, hidden] and k_norm [128] on one gfx950 device')
         if not 1 <= len(layers) <= 64:
             raise ValueError('Between 1 and 64 draft layers')
-        if hidden < 64 or hidden % 64:
-            raise ValueError('Hidden size must be a positive multiple of 64')
+        if hidden < 128 or hidden % 128:
+            raise ValueError('Hidden size must be a positive multiple of 128')
         if not (eps > 0 and theta > 0):
             raise ValueError('eps and theta must be positive')
         self.hidden, self.features, self.layers = hidden, features, len(layers)

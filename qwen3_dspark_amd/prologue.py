@@ -36,8 +36,8 @@ class QKVPrologue:
                     or tuple(t.shape) != shape):
                 raise ValueError('Prologue weights must be bf16 q/k/v projections [Hq*128|Hkv*128, H] and '
                                  '[128] norms on one gfx950 device')
-        if hidden < 64 or hidden % 64:
-            raise ValueError('Hidden size must be a positive multiple of 64')
+        if hidden < 128 or hidden % 128:
+            raise ValueError('Hidden size must be a positive multiple of 128')
         if not (eps > 0 and theta > 0):
             raise ValueError('eps and theta must be positive')
         self.hidden = hidden
