@@ -72,6 +72,9 @@ def parse():
     ap.add_argument('--stream-probe', action='store_true',
                     help='only measure the streaming-read ceiling (dspark_stream_read over 16 GiB, default and '
                          'non-temporal loads, 512-2048 workgroups)')
+    ap.add_argument('--xcd-ab', action='store_true',
+                    help='only compare verification plans with equal runs and with XCD-calibrated runs on one store '
+                         '(alternating transactions of 28 layers), and report the measured XCD speeds')
     ap.add_argument('--mfma-probe', action='store_true',
                     help='only run the draft kernels for a rocprofv3 --pmc MfmaUtil MfmaFlopsBF16 pass')
     ap.add_argument('--cpu-verify-layers', type=int, default=VERIFY_LAYERS, help='verify layers in the CPU sample')
@@ -101,6 +104,56 @@ def verify_bytes(contexts):
     return sum(c + Q_LEN for c in contexts) * 2 * ROW_BYTES + 2 * B * Q_LEN * Q_ROW_BYTES
 
 
+def xcd_ab(args, rounds=14):
+    """Verification attention of the first round of the workload on one
+    28-layer store: transactions planned with equal runs and with runs sized
+    to the XCD speeds calibrate_xcd measures, alternating, median per call."""
+    import numpy as np
+    import torch
+
+    from qwen3_dspark_amd.persistent_kv import Bucket, PersistentTargetKV
+    dev = torch.device('cuda:0')
+    torch.cuda.set_device(dev)
+    contexts, _, _ = workload(args.warmup + args.steps)
+    gen = torch.Generator(device=dev).manual_seed(SEED)
+    pool = PersistentTargetKV(layers=VERIFY_LAYERS, slots=B, context_capacity=CAPACITY, max_query_tokens=B * Q_LEN,
+                              heads=8, dim=128, device=dev)
+    handles = [pool.add_request(f'req{i}') for i in range(B)]
+    for layer in range(VERIFY_LAYERS):
+        pool.keys[layer].normal_(generator=gen)
+        pool.values[layer].normal_(generator=gen)
+    for h, c in zip(handles, contexts):
+        pool.load_prefix(h, pool.keys[:, h.index, :c], pool.values[:, h.index, :c])
+    bucket = Bucket((Q_LEN,) * B, (CAPACITY - Q_LEN,) * B, '64-request stress shape')
+    pool.register_bucket(bucket)
+    speed = pool.calibrate_xcd()
+    qv = torch.randn(VERIFY_LAYERS, B * Q_LEN, 16, 128, generator=gen, device=dev).to(torch.bfloat16)
+    kn = torch.randn(VERIFY_LAYERS, B * Q_LEN, 8, 128, generator=gen, device=dev).to(torch.bfloat16)
+    vn = torch.randn(VERIFY_LAYERS, B * Q_LEN, 8, 128, generator=gen, device=dev).to(torch.bfloat16)
+    out = torch.empty_like(qv)
+    plans = {'equal': None, 'calibrated': speed}
+    times = {n: [] for n in plans}
+    for r in range(rounds):
+        for name in (('equal', 'calibrated') if r % 2 == 0 else ('calibrated', 'equal')):
+            pool.set_xcd_speed(plans[name])
+            tx = pool.begin(handles, bucket)
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for layer in range(VERIFY_LAYERS):
+                pool.attend(tx, layer, qv[layer], keys=kn[layer], values=vn[layer], out=out[layer])
+            e1.record()
+            pool.abort(tx)
+            if r >= 2:
+                times[name].append((e0, e1))
+    torch.cuda.synchronize()
+    res = {'xcd_speed': [round(x, 4) for x in speed], 'rounds': rounds - 2, 'calls_per_round': VERIFY_LAYERS}
+    for name in plans:
+        us = np.array([a.elapsed_time(b) / VERIFY_LAYERS for a, b in times[name]]) * 1e3
+        res[name] = {'median_us': round(float(np.median(us)), 2), 'p10_us': round(float(np.percentile(us, 10)), 2),
+                     'p90_us': round(float(np.percentile(us, 90)), 2)}
+    print(json.dumps({'xcd_ab': res}), flush=True)
+
+
 def draft_bytes(anchors):
     """Algorithmic bytes of one draft-attention layer: context rows up to the
     largest anchor read once per request, block K/V, Q and O."""
@@ -122,6 +175,8 @@ def main():
         return traffic_probe(args)
     if args.mfma_probe:
         return mfma_probe(args)
+    if args.xcd_ab:
+        return xcd_ab(args)
     if args.stream_probe:
         return stream_probe()
     import numpy as np
