@@ -111,6 +111,26 @@ class DraftBatch:
         self._index_max = None
         self.physical_context_rows = self.context_rows
 
+    @classmethod
+    def from_packed_layout(cls, layout, *, block_size=BLOCK_SIZE):
+        """The batch of the reference's one-block backbone call
+        (packed_draft.py:205-226), from the PackedLayout it builds over the
+        metadata of cat(pool, block): request r's keys are its c_r context
+        rows (pool rows in position order) followed by its own block_size
+        rows, and its queries are those block rows.  The batch reads the
+        context through layout.gather_indices from the [1, 8, N, 128] pool
+        in place (one block per request at anchor c_r); the block's own rows
+        come as separate block K/V."""
+        qs, ks = tuple(layout.query_lengths), tuple(layout.key_lengths)
+        if not qs or len(qs) != len(ks) or any(q != block_size for q in qs) or any(k < block_size for k in ks):
+            raise ValueError('Each request must query exactly its own draft block')
+        first = [0]
+        for k in ks[:-1]:
+            first.append(first[-1] + k)
+        contexts = [k - block_size for k in ks]
+        indices = layout.gather_indices
+        return cls(indices.device, first, contexts, [[c] for c in contexts], context_indices=indices)
+
     def counters(self, layers=1, *, key_element_bytes=2, value_element_bytes=2):
         """draft_work_counters of this batch over `layers` attention calls."""
         return draft_work_counters(self.context_lengths, self.anchors, layers=layers,
@@ -184,6 +204,7 @@ class HipDraftAttention:
         self._workspace = Workspace(self.device)
         self._geometry_for = None
         self._geometry = None
+        self._packed = None         # (layout, DraftBatch) of over_append_order_pool
 
     def _context_geometry(self, keys, batch):
         """(offset capacity for DraftBatch.kernel_offsets, token stride, head
@@ -256,6 +277,33 @@ class HipDraftAttention:
         return out
 
 
+    def over_append_order_pool(self, query, block_keys, block_values, pool_keys, pool_values, layout, *, scale):
+        """The attention of the reference's backbone layer over its own
+        append-order pool (packed_draft.py:219-236 in one call): query
+        [7B, 16, 128]; block K/V as project_kv returns them, [1, 8, 7B, 128]
+        (or [7B, 8, 128]); pool K/V the layer's [1, 8, N, 128] tensors (None
+        before the first append); layout the PackedLayout of that backbone
+        call.  The context is read through the layout's gather indices in
+        place: no cat, no gather copy and no cast copy of the pool.  V must
+        be bf16; fp32 Q/K (the AMP pool) are rounded as they are loaded."""
+        if self._packed is None or self._packed[0] is not layout:
+            self._packed = (layout, DraftBatch.from_packed_layout(layout))
+        batch = self._packed[1]
+
+        def rows(t):
+            if isinstance(t, torch.Tensor) and t.ndim == 4 and t.shape[0] == 1:
+                t = t[0].transpose(0, 1)
+            return t.contiguous() if isinstance(t, torch.Tensor) else t
+        block_keys, block_values = rows(block_keys), rows(block_values)
+        if pool_keys is None and pool_values is None:
+            if batch.context_rows:
+                raise ValueError('Context rows addressed beyond the context tensor')
+            kdt = block_keys.dtype if isinstance(block_keys, torch.Tensor) else torch.bfloat16
+            pool_keys = torch.zeros((1, KV_HEADS, 1, HEAD_DIM), dtype=kdt, device=self.device)
+            pool_values = torch.zeros((1, KV_HEADS, 1, HEAD_DIM), dtype=torch.bfloat16, device=self.device)
+        return self(query, block_keys, block_values, pool_keys, pool_values, batch, scale=scale)
+
+
 class DraftKVPool:
     """Projected draft context per request: the cache state of PackedDraft
     (dspark_qwen/packed_draft.py:63-185) without the model.
@@ -279,10 +327,22 @@ class DraftKVPool:
     The reference's pool under bf16 autocast holds FP32 K (its k_norm runs in
     FP32) and BF16 V (packed_draft.py:222-235); attention reads such a pool in
     place and rounds K to bf16 in registers.
+
+    With growable=True the slot count and per-slot capacity are starting
+    sizes: a request admitted with every slot taken doubles the slots, an
+    append beyond a slot's capacity at least doubles the capacity (rounded up
+    to GROW_ALIGN rows).  A resize allocates the new pool and copies every
+    committed row once, so n appends cost O(log n) copies of the pool where
+    the reference's append-order pool concatenates all of it on every append
+    (packed_draft.py:157-158).  Without growable the sizes are fixed and an
+    overflow raises.
     """
 
+    GROW_ALIGN = 256
+
     def __init__(self, *, layers, slots, capacity, heads=KV_HEADS, dim=HEAD_DIM, dtype=torch.bfloat16,
-                 key_dtype=None, value_dtype=None, device='cuda', chunk=DRAFT_CHUNK, projector=None):
+                 key_dtype=None, value_dtype=None, device='cuda', chunk=DRAFT_CHUNK, projector=None,
+                 growable=False):
         if any(type(n) is not int or n < 1 for n in (layers, slots, capacity, heads, dim)):
             raise ValueError('All pool sizes must be positive integers')
         key_dtype = dtype if key_dtype is None else key_dtype
@@ -302,6 +362,8 @@ class DraftKVPool:
             raise ValueError('A KV head row must be a multiple of 16 bytes')
         self.keys = torch.zeros((layers, slots, heads, capacity, dim), dtype=key_dtype, device=self.device)
         self.values = torch.zeros((layers, slots, heads, capacity, dim), dtype=value_dtype, device=self.device)
+        self.growable = bool(growable)
+        self.resizes = 0
         self._lengths = {}
         self._slots = {}
         self._free = list(range(slots))
@@ -335,9 +397,37 @@ class DraftKVPool:
         if not isinstance(request, str) or not request or request in self._lengths:
             raise ValueError('Require a fresh nonempty request name')
         if not self._free:
-            raise ValueError('Draft pool slot capacity exhausted')
+            if not self.growable:
+                raise ValueError('Draft pool slot capacity exhausted')
+            self._resize(2 * self.slot_capacity, self.capacity)
         self._slots[request] = self._free.pop(0)
         self._lengths[request] = 0
+
+    def _resize(self, slots, capacity):
+        """Reallocate the pool as [layers, slots, heads, capacity, dim] and
+        copy every slot's committed rows to the same slot and positions."""
+        old_k, old_v, old_s, old_c = self.keys, self.values, self.slot_capacity, self.capacity
+        shape = (self.layers, slots, self.heads, capacity, self.dim)
+        keys = torch.zeros(shape, dtype=self.key_dtype, device=self.device)
+        values = torch.zeros(shape, dtype=self.value_dtype, device=self.device)
+        used = max(self._lengths.values(), default=0)
+        if used:
+            keys[:, :old_s, :, :used].copy_(old_k[:, :, :, :used])
+            values[:, :old_s, :, :used].copy_(old_v[:, :, :, :used])
+        self.keys, self.values = keys, values
+        self._free += list(range(old_s, slots))
+        self.slot_capacity, self.capacity = slots, capacity
+        self.resizes += 1
+
+    def _reserve(self, needed):
+        """Make room for `needed` committed rows in a slot: grow the capacity
+        of a growable pool, else raise."""
+        if needed <= self.capacity:
+            return
+        if not self.growable:
+            raise ValueError('Committed draft context exceeds the pool capacity')
+        align = self.GROW_ALIGN
+        self._resize(self.slot_capacity, max(2 * self.capacity, -(-needed // align) * align))
 
     def _request(self, request):
         if request not in self._lengths:
@@ -385,7 +475,7 @@ class DraftKVPool:
             self._request(request)
             if type(n) is not int or n < 1:
                 raise ValueError('Each committed chunk needs a positive row count')
-            if self._lengths[request] + n > self.capacity:
+            if self._lengths[request] + n > self.capacity and not self.growable:
                 raise ValueError('Committed draft context exceeds the pool capacity')
         rows = sum(n for _, n in order)
         if len(projected) != self.layers:
@@ -397,6 +487,7 @@ class DraftKVPool:
                 if strides[i] is not None and st != strides[i]:
                     raise ValueError('Projected K/V must share one layout across layers')
                 strides[i] = st
+        self._reserve(max(self._lengths[r] + n for r, n in order))
         req, offset = [[], [], [], []], 0
         for request, n in order:
             req[0].append(self._slots[request])
@@ -453,9 +544,10 @@ class DraftKVPool:
                     or value.shape[2] != proj.features or value.device != self.device
                     or not value.is_floating_point()):
                 raise ValueError('Expected finite nonempty [1, tokens, target_features] on draft device')
-            if self._lengths[request] + value.shape[1] > self.capacity:
+            if self._lengths[request] + value.shape[1] > self.capacity and not self.growable:
                 raise ValueError('Committed draft context exceeds the pool capacity')
             feats.append(value[0])
+        self._reserve(max(self._lengths[r] + f.shape[0] for (r, _), f in zip(order, feats)))
         x = (torch.cat(feats) if len(feats) > 1 else feats[0]).to(torch.bfloat16).contiguous()
         rec, first = [], 0
         for (request, _), f in zip(order, feats):

@@ -59,27 +59,45 @@ class PackedDraftFeatures:
 class PackedDraft:
     """Drop-in for dspark_qwen/packed_draft.py:PackedDraft.
 
-    Same methods, argument meaning and errors: add_request / append_committed
-    / crop / remove_request / request_kv / lengths / validate_cache /
-    backbone.  Differences:
-      * storage is a slotted pool: `slots` requests of up to `capacity`
-        committed context rows each (the reference grows one append-order
-        tensor without bound);
+    Constructed like the reference, PackedDraft(draft, native_backend=...,
+    test_kernel=None), with the same methods, argument meaning and errors:
+    add_request / append_committed / crop / remove_request / request_kv /
+    lengths / validate_cache / backbone.  Differences:
+      * storage is a slotted pool that grows on demand (DraftKVPool with
+        growable=True: slots double when every slot is taken, a slot's
+        capacity at least doubles when an append overflows it); passing
+        `slots` and `capacity` fixes the sizes instead, and an overflow
+        then raises;
       * native_backend must name this build's multi-block draft kernel
-        (backends.DRAFT_BLOCKS_BACKEND); there is no CPU test_kernel;
+        (backends.DRAFT_BLOCKS_BACKEND); a CPU test_kernel is refused with
+        the reference's message, since every draft here is on the GPU;
       * backbone_blocks adds 1..8 blocks per request at any anchors
         (DSparkDraft.backbone's multi-anchor form, model.py:101-119);
         backbone is its one-block form at anchor = committed length.
     Draft weights in float32 (the reference's autocast form) are snapshotted
     to bf16 for the context projection, whose GEMMs the reference's autocast
-    runs in bf16 as well.
+    runs in bf16 as well.  The attention takes bf16 Q/K/V, or FP32 Q/K under
+    bf16 autocast (rounded as the kernel loads them); a float32 draft run
+    without autocast is refused with the ValueError of the reference's native
+    kernel (rocm_varlen.py:65-70), which takes BF16 tensors only.
     """
 
-    def __init__(self, draft, *, native_backend=None, slots, capacity, chunk=DRAFT_CHUNK):
+    # Starting sizes of the growable pool.
+    INITIAL_SLOTS = 8
+    INITIAL_CAPACITY = 1024
+
+    def __init__(self, draft, *, native_backend=None, test_kernel=None, slots=None, capacity=None,
+                 chunk=DRAFT_CHUNK):
         if draft.training:
             raise ValueError('Packed draft is inference-only; call eval first')
+        if test_kernel is not None:
+            # The reference admits an injected kernel only on a CPU draft with
+            # no native backend (packed_draft.py:75-78); drafts here are GPU.
+            raise ValueError('CPU-only test injection cannot select a native backend')
         if native_backend != backends.DRAFT_BLOCKS_BACKEND:
             raise ValueError('Select explicit noncausal draft backend; no default/fallback')
+        if (slots is None) != (capacity is None):
+            raise ValueError('Give both slots and capacity for a fixed pool, or neither for a growable one')
         self.draft = draft
         self.device = require_gfx950(draft.embedding.weight.device)
         attn = [layer.attention for layer in draft.layers]
@@ -90,8 +108,10 @@ class PackedDraft:
             raise ValueError(f'HIP packed draft supports {BLOCK_SIZE}-row blocks only')
         self.mask_token_id = int(draft.spec.mask_token_id)
         self.projector = self._projector(draft)
-        self.pool = DraftKVPool(layers=len(draft.layers), slots=slots, capacity=capacity, device=self.device,
-                                chunk=chunk, projector=self.projector)
+        growable = slots is None
+        self.pool = DraftKVPool(layers=len(draft.layers), slots=self.INITIAL_SLOTS if growable else slots,
+                                capacity=self.INITIAL_CAPACITY if growable else capacity, device=self.device,
+                                chunk=chunk, projector=self.projector, growable=growable)
         self.kernel = self.pool.kernel
         self.last_projection_work = None
 
@@ -191,6 +211,7 @@ class PackedDraft:
         cos, sin = draft.rotary(z, query_positions[None])
         nq = z.shape[1]
         autocast = torch.is_autocast_enabled(self.device.type)
+        bad = torch.zeros((), dtype=torch.bool, device=self.device)
         for index, layer in enumerate(draft.layers):
             attention = layer.attention
             normalized = layer.input_norm(z)
@@ -199,20 +220,27 @@ class PackedDraft:
             kb, vb = attention.project_kv(normalized, cos, sin)
             kb = kb.squeeze(0).transpose(0, 1)
             vb = vb.squeeze(0).transpose(0, 1)
-            # The kernel rounds fp32 Q/K to bf16 as it loads them: the cast the
-            # reference applies at its kernel boundary (packed_draft.py:229-235).
+            if not autocast and any(t.dtype != torch.bfloat16 for t in (q, kb, vb)):
+                raise ValueError('Pinned varlen requires no-autograd contiguous BF16 THD tensors on its selected GPU')
+            # Under autocast the kernel rounds fp32 Q/K to bf16 as it loads
+            # them: the cast the reference applies at its kernel boundary
+            # (packed_draft.py:229-235).  V arrives in bf16 there.
             q = (q if q.dtype == torch.float32 else q.to(torch.bfloat16)).contiguous()
             kb = kb.to(self.pool.key_dtype).contiguous()
             vb = vb.to(torch.bfloat16).contiguous()
             output = self.pool.attention(index, q, kb, vb, batch, scale=attention.dim ** -.5)
             if output.shape != (nq, attention.heads, attention.dim) or output.device != self.device:
                 raise RuntimeError('Invalid packed draft attention output')
-            if not autocast:
-                output = output.to(attention.o_proj.weight.dtype)
+            # The reference's per-layer finiteness check (packed_draft.py:237-239),
+            # kept on the device and read once after the last layer.
+            bad = bad | ~torch.isfinite(output).all()
             z = z + attention.o_proj(output.reshape(1, nq, -1))
             z = z + layer.mlp(layer.post_norm(z))
         hidden = draft.norm(z).squeeze(0)
-        if not bool(torch.isfinite(hidden).all()):
+        bad_attention, bad_hidden = torch.stack((bad, ~torch.isfinite(hidden).all())).tolist()
+        if bad_attention:
+            raise RuntimeError('Invalid packed draft attention output')
+        if bad_hidden:
             raise RuntimeError('Nonfinite packed draft hidden')
         work = self.pool.counters(batch)
         work.update(mlp_calls=len(draft.layers))

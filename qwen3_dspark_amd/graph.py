@@ -25,6 +25,97 @@ import torch
 from .kernels import HEAD_DIM, KV_HEADS, Q_HEADS
 
 
+def _private_pool_bytes(pool_id, device):
+    """Reserved bytes of a graph's private memory pool: the sum of the
+    segments torch's allocator snapshot lists for that pool on `device`
+    (inactive retained blocks included)."""
+    total = 0
+    for seg in torch.cuda.memory.memory_snapshot(mempool_id=pool_id):
+        if seg.get('device', device.index) != device.index:
+            continue
+        if 'segment_pool_id' in seg and tuple(seg['segment_pool_id']) != tuple(pool_id):
+            continue
+        total += int(seg['total_size'])
+    return total
+
+
+@dataclass(frozen=True)
+class ReplayEvent:
+    """The completion handle of one replay: the event recorded after it on
+    the caller's stream and the program it belongs to."""
+    event: object
+    graph: object
+
+
+class TorchGraphBackend:
+    """Graph backend object of the persistent target's captured buckets (the
+    role of TorchGraphBackend, persistent_qwen_graph.py:97-138): captures a
+    body into a HIP graph (torch's CUDAGraph on ROCm) on a side stream,
+    replays it on the caller's stream and reports completion only for the
+    events it recorded itself.
+
+    Each capture gets a private memory pool.  Its reserved bytes are counted
+    from the allocator's snapshot and must stay within the caller's
+    reservation; one backend never shares a pool between captures."""
+    kind = 'mi355x_hip_full_model_graph'
+
+    def __init__(self):
+        self._pools = set()
+        self._issued = weakref.WeakValueDictionary()
+
+    def capture(self, body, device, reserve_bytes):
+        """Capture `body` (no execution); returns (graph, memory accounting)."""
+        if device.type != 'cuda':
+            raise ValueError('Actual CUDA/ROCm device required for graph capture')
+        before = torch.cuda.memory_reserved(device)
+        stream = torch.cuda.Stream(device=device)
+        stream.wait_stream(torch.cuda.current_stream(device))
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=stream):
+            body()
+        torch.cuda.current_stream(device).wait_stream(stream)
+        stream.synchronize()
+        pool = graph.pool()
+        if pool in self._pools:
+            raise RuntimeError('Graph pool sharing is not registered or budgeted')
+        self._pools.add(pool)
+        reserved = _private_pool_bytes(pool, device)
+        after = torch.cuda.memory_reserved(device)
+        memory = dict(kind='graph_private_pool_reserved_segments', pool_id=list(pool),
+                      private_pool_reserved_bytes=reserved, global_reserved_before=before,
+                      global_reserved_after=after, global_reserved_delta=after - before,
+                      reservation_bytes=reserve_bytes, includes_inactive_blocks=True)
+        if reserved > reserve_bytes:
+            raise RuntimeError('Graph private-pool reserved bytes exceed registered reservation: '
+                               f'measured={reserved}, reservation={reserve_bytes}')
+        return graph, memory
+
+    def replay(self, graph, device):
+        """Replay on the current stream; returns a ReplayEvent."""
+        graph.replay()
+        event = torch.cuda.Event()
+        event.record(torch.cuda.current_stream(device))
+        handle = ReplayEvent(event, graph)
+        self._issued[id(handle)] = handle
+        return handle
+
+    def _own(self, handle):
+        if not isinstance(handle, ReplayEvent) or self._issued.get(id(handle)) is not handle:
+            raise ValueError('Foreign completion event')
+
+    def wait(self, handle):
+        self._own(handle)
+        handle.event.synchronize()
+
+    def complete(self, handle):
+        """True iff `handle` is a replay this backend issued and it finished."""
+        try:
+            self._own(handle)
+        except ValueError:
+            return False
+        return bool(handle.event.query())
+
+
 @dataclass(frozen=True)
 class GraphCompletion:
     """A submitted replay: the store's external-write receipt and the event

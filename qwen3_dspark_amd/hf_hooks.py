@@ -13,9 +13,10 @@
 * FusedVerifier - binds a PersistentTargetKV transaction to one model forward
   (the callback finds it through the `fused_verification` forward kwarg, as
   the reference passes `persistent_target`).
-* PersistentQwenTarget - the full-model transaction adapter of
-  dspark_qwen/persistent_qwen_target.py:100-472 (verify / commit / abort /
-  prefill / predict / request_kv, captured layer features) on that path.
+* PackedFeatures / CachedFeatures - the hidden states of one packed forward
+  (packed_target.py:18-28, cached_target.py:15-22).  The full-model
+  transaction adapter over FusedVerifier is
+  persistent_target.PersistentQwenTarget (also importable from here).
 * VarlenPackedTarget + PackedVarlenCache - the append-order adapter of
   dspark_qwen/varlen_target.py:132-167 over PackedTarget
   (packed_target.py:30-200): one packed forward per append over an
@@ -26,7 +27,6 @@ The callbacks keep the reference's contract: no attention mask or dropout,
 the module must belong to the bound model, ValueError otherwise.
 """
 import contextlib
-import weakref
 from collections.abc import Mapping
 from dataclasses import dataclass
 
@@ -36,11 +36,10 @@ from transformers.modeling_utils import ALL_ATTENTION_FUNCTIONS
 
 from . import backends
 from ._device import upload
-from .kernels import HEAD_DIM, KV_HEADS, Q_HEADS, HipCapacityKernel
+from .kernels import HEAD_DIM, KV_HEADS, Q_HEADS
 from .layout import PackedLayout
 from .packed_kv import AppendOrderKV
-from .persistent_kv import Bucket, PersistentTargetKV, QueryFamily
-from .schedule import DEFAULT_CHUNK
+from .persistent_kv import PersistentTargetKV
 
 VARLEN_BACKEND = 'dspark_mi355x_varlen'
 FUSED_BACKEND = 'dspark_mi355x_fused_verify'
@@ -166,7 +165,7 @@ class FusedVerifier:
 
 
 # ---------------------------------------------------------------------------
-# Full-model transaction adapter (dspark_qwen/persistent_qwen_target.py:100-472)
+# Packed forward outputs (packed_target.py:18-28)
 # ---------------------------------------------------------------------------
 
 @dataclass(frozen=True)
@@ -195,522 +194,6 @@ class PackedFeatures:
         offset, count, start = self.spans[request_id]
         return CachedFeatures(start, self.last[:, offset:offset + count],
                               None if self.context is None else self.context[:, offset:offset + count])
-
-
-GRAPH_BACKEND = 'mi355x_hip_full_model_graph'
-
-
-@dataclass(frozen=True)
-class GraphTicket:
-    """A prepared graph verification: the open transaction, the store's
-    external-write receipt, the captured program and the request spans."""
-    transaction: object
-    receipt: object
-    execution: object
-    spans: dict
-
-
-@dataclass(frozen=True)
-class GraphCompletion:
-    """A submitted replay and the event recorded after it on the owner stream."""
-    ticket: GraphTicket
-    event: object
-
-
-class FullModelGraph:
-    """One captured verification forward of a registered bucket: the
-    embedding, every decoder layer (with its fused stage + attention
-    launches) and the final norm, replayed under the store's external-write
-    receipts (FullTargetExecution + TorchGraphBackend,
-    persistent_qwen_graph.py:97-275).  Token ids go into a fixed buffer; the
-    positions come from the bucket's fixed workspace; the last hidden states
-    and captured layer features live in the graph's memory and are
-    overwritten by the next replay (hence the target's feature lease)."""
-    kind = GRAPH_BACKEND
-
-    def __init__(self, target, bucket, reserve_bytes):
-        self.target, self.bucket, self.reserve_bytes = target, bucket, reserve_bytes
-        self.ids = torch.zeros((1, bucket.query_tokens), dtype=torch.long, device=target.device)
-        self.writer = target.store.register_external_writer(bucket, range(target.store.layers), self.complete)
-        self.graph = None
-        self.last = self.context = None
-        self.invalid = False
-        self._submitted = {}      # id(receipt) -> (receipt, event)
-        self._addresses = None
-
-    @staticmethod
-    def output_buffer_bytes(target, bucket):
-        """Fixed buffers a capture keeps besides the graph's own pool: ids,
-        last hidden states and captured features."""
-        hidden = target.model.config.hidden_size
-        return bucket.query_tokens * (8 + 2 * hidden * (1 + len(target.layer_ids)))
-
-    def pointers(self):
-        return dict(ids=self.ids.data_ptr(), last=None if self.last is None else self.last.data_ptr(),
-                    context=None if self.context is None else self.context.data_ptr(),
-                    **self.target.store.pointers(self.bucket))
-
-    def validate(self):
-        if self.invalid or self.target.store.failed:
-            raise RuntimeError('Captured program invalidated')
-        if self._addresses is not None and self.pointers() != self._addresses:
-            raise RuntimeError('Captured buffer addresses changed')
-
-    def load(self, chunks):
-        self.ids.copy_(torch.cat(tuple(chunks.values()), dim=1))
-
-    def _forward(self):
-        t = self.target
-        out = t.model.model(input_ids=self.ids, position_ids=t.store.workspace(self.bucket).positions[None],
-                            attention_mask=None, past_key_values=t.verifier.cache, use_cache=True, return_dict=True,
-                            fused_verification=t.verifier)
-        if t.store.staged_layers() != t.store.layers or set(t._captured) != set(t.layer_ids):
-            raise RuntimeError('Full layer cache update or selected feature capture missing')
-        context = torch.cat([t._captured[i] for i in t.layer_ids], dim=-1) if t.layer_ids else None
-        t._captured = {}
-        return out.last_hidden_state, context
-
-    @torch.no_grad()
-    def capture(self, handles, query_lengths):
-        """One eager forward (lazy library state settles), then the capture,
-        each in a transaction of its own that is aborted: nothing runs
-        during capture and nothing is committed."""
-        t = self.target
-        if self.graph is not None:
-            raise ValueError('Bucket already captured')
-        for capture in (False, True):
-            with t.verifier.transaction_for(handles, self.bucket, query_lengths=query_lengths) as tx:
-                try:
-                    if not capture:
-                        self._forward()
-                    else:
-                        device = t.device
-                        stream = torch.cuda.Stream(device=device)
-                        stream.wait_stream(torch.cuda.current_stream(device))
-                        graph = torch.cuda.CUDAGraph()
-                        with torch.cuda.graph(graph, stream=stream):
-                            self.last, self.context = self._forward()
-                        torch.cuda.current_stream(device).wait_stream(stream)
-                        stream.synchronize()
-                        self.graph = graph
-                finally:
-                    t._captured = {}
-                    t.store.abort(tx)
-        self._addresses = self.pointers()
-
-    def submit(self, receipt):
-        """Replay on the current stream; returns the event recorded after it."""
-        self.validate()
-        self.graph.replay()
-        event = torch.cuda.Event()
-        event.record(torch.cuda.current_stream(self.target.device))
-        self._submitted = {id(receipt): (receipt, event)}
-        return event
-
-    def complete(self, event, receipt):
-        """The store's completion check: this program's event for this
-        receipt, observed complete."""
-        entry = self._submitted.get(id(receipt))
-        return entry is not None and entry[0] is receipt and entry[1] is event and event.query()
-
-
-class PersistentQwenTarget:
-    """HF Qwen3 target over a PersistentTargetKV with the fused MI355X
-    attention: the API of persistent_qwen_target.py:100-472.
-
-    verify() runs one packed forward whose layers stage their new K/V rows
-    into scratch and attend over resident + scratch rows in place; nothing is
-    committed until commit() keeps the caller's accepted prefixes (the rest
-    is rolled back by omission).  prefill() = verify + commit of every row.
-    Decoder outputs of `layer_ids` are captured as draft context features.
-    A registered graph bucket (register_graph_bucket + capture_graph) is
-    verified by replaying the captured full-model forward under the store's
-    external-write receipts; verify_eager() remains the explicit eager path.
-    Every call comes from the stream current at construction (the owner
-    stream); features are leases that predict() checks by identity.
-    """
-    BACKEND_NAME = FUSED_BACKEND
-
-    def __init__(self, model, layer_ids=(), *, slots, context_capacity, max_query_tokens, chunk=DEFAULT_CHUNK,
-                 graph_backend=None, max_buckets=32, workspace_byte_budget=256 * 1024 ** 2, max_graph_buckets=0,
-                 graph_byte_budget=0):
-        cfg = model.config
-        if (cfg.model_type != 'qwen3' or getattr(cfg, 'use_sliding_window', False)
-                or any(kind != 'full_attention' for kind in cfg.layer_types)
-                or (cfg.rope_parameters or {}).get('rope_type', 'default') != 'default'):
-            raise ValueError('Owned dense Qwen3 with default RoPE required')
-        if (cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim) != (16, 8, 128):
-            raise ValueError('The MI355X attention path requires 16 query heads, 8 KV heads, head dim 128')
-        self.layer_ids = tuple(layer_ids)
-        if (tuple(sorted(set(self.layer_ids))) != self.layer_ids
-                or any(type(i) is not int or not 0 <= i < cfg.num_hidden_layers for i in self.layer_ids)):
-            raise ValueError('Unique increasing valid decoder layer IDs required')
-        device = model.get_input_embeddings().weight.device
-        dtype = model.get_input_embeddings().weight.dtype
-        if dtype != torch.bfloat16:
-            raise ValueError('The MI355X attention path requires a bf16 model')
-        if any(type(x) is not int or x < 1 for x in (max_buckets, workspace_byte_budget)):
-            raise ValueError('Positive finite bucket/workspace budget required')
-        if graph_backend is not None:
-            if graph_backend != GRAPH_BACKEND:
-                raise ValueError('Explicit device-compatible graph backend required')
-            if any(type(x) is not int or x < 1 for x in (max_graph_buckets, graph_byte_budget)):
-                raise ValueError('Positive finite graph count and byte budget required')
-        self._old_backend = cfg._attn_implementation
-        self.store = PersistentTargetKV(layers=cfg.num_hidden_layers, slots=slots, context_capacity=context_capacity,
-                                        max_query_tokens=max_query_tokens, heads=cfg.num_key_value_heads,
-                                        dim=cfg.head_dim, dtype=dtype, device=device, chunk=chunk)
-        self.verifier = FusedVerifier(model, self.store)
-        self.model = self.verifier.model
-        # The kernel identity the reference's session guard reads
-        # (packed_sampling.py:110-115): the capacity-tail drop-in of
-        # _native_attention.  verify() itself runs the fused store attention.
-        self._varlen_kernel = HipCapacityKernel(device)
-        self._graph_backend = graph_backend
-        self._max_buckets, self._workspace_budget = max_buckets, workspace_byte_budget
-        self._max_graph_buckets, self._graph_budget = max_graph_buckets, graph_byte_budget
-        self._workspace_bytes = self._graph_reserved_bytes = 0
-        self._handles = {}
-        self._pending = None
-        self._captured = {}
-        self._graphs = {}
-        self._graph_ticket = self._graph_completion = self._feature_lease = None
-        self._features = weakref.WeakValueDictionary()
-        self._closed = False
-        self._owner_stream = torch.cuda.current_stream(device).cuda_stream
-        self._hooks = [self.model.model.layers[i].register_forward_hook(self._hook(i)) for i in self.layer_ids]
-
-    @property
-    def device(self):
-        return self.store.device
-
-    @property
-    def lengths(self):
-        return {r: self.store.length(h) for r, h in self._handles.items()}
-
-    def _hook(self, index):
-        def capture(_module, _inputs, output):
-            if self.verifier.transaction is None:
-                raise RuntimeError('Foreign model forward while the adapter owns the model')
-            self._captured[index] = output[0] if isinstance(output, tuple) else output
-        return capture
-
-    # -- ownership -------------------------------------------------------------
-    def _check_stream(self):
-        if torch.cuda.current_stream(self.device).cuda_stream != self._owner_stream:
-            raise RuntimeError('Target, head, draft feature consumers and release must use the owner stream')
-
-    def _idle(self):
-        self._check_stream()
-        if self._closed:
-            raise RuntimeError('Target adapter closed')
-        if self._pending is not None or self.verifier.transaction is not None:
-            raise RuntimeError('Finish existing verification transaction first')
-        if self._graph_ticket is not None or self._feature_lease is not None:
-            raise RuntimeError('Finish graph submission and release feature lease first')
-        if self.store.failed:
-            raise RuntimeError('Store invalidated by copy failure; construct a new store')
-        if self.store.open_transaction is not None:
-            raise RuntimeError('Outstanding verification transaction')
-
-    def invalidate(self):
-        """Fail closed after an uncertain asynchronous or device failure."""
-        self.store.invalidate()
-        for graph in self._graphs.values():
-            graph.invalid = True
-        self._pending = self._graph_ticket = self._graph_completion = None
-
-    def release_features(self, features):
-        self._check_stream()
-        if self._features.get(id(features)) is not features:
-            raise ValueError('Foreign, copied or already released features')
-        if self._pending is not None and self._pending[0] is features:
-            raise RuntimeError('Commit or abort before releasing feature lease')
-        if self._feature_lease is features:
-            self._feature_lease = None
-        del self._features[id(features)]
-
-    # -- requests and buckets ---------------------------------------------------------
-    def add_request(self, request):
-        self._idle()
-        handle = self.store.add_request(request)
-        self._handles[request] = handle
-        return handle
-
-    def remove_request(self, request):
-        self._idle()
-        self.store.remove_request(self._handles[request])
-        del self._handles[request]
-
-    def reset(self):
-        """Release every request incarnation; bucket addresses stay."""
-        self._idle()
-        for request in tuple(self._handles):
-            self.remove_request(request)
-
-    def close(self):
-        self._idle()
-        for hook in self._hooks:
-            hook.remove()
-        self._hooks = []
-        self.model.config._attn_implementation = self._old_backend
-        self._closed = True
-
-    def _fits(self, size, count):
-        if len(self._registered()) + count > self._max_buckets or self._workspace_bytes + size > self._workspace_budget:
-            raise ValueError('Finite bucket/workspace budget exceeded')
-        if self._graph_backend is not None and self._workspace_bytes + size + self._graph_reserved_bytes > self._graph_budget:
-            raise ValueError('Combined graph/workspace byte budget exceeded')
-
-    def _registered(self):
-        return self.store.registered()
-
-    def register_bucket(self, bucket):
-        self._idle()
-        if isinstance(bucket, QueryFamily):
-            self.store.register_bucket(bucket)
-            return
-        if not isinstance(bucket, Bucket):
-            raise ValueError('Explicit Bucket or QueryFamily required')
-        if not self.store.is_registered(bucket):
-            size = self.store.workspace_bytes(bucket)
-            self._fits(size, 1)
-            self.store.register_bucket(bucket)
-            self._workspace_bytes += size
-
-    def register_families(self, families):
-        """One finite family declaration sharing one workspace."""
-        self._idle()
-        size = self.store.workspace_bytes(self.store.family_arena_shape(families))
-        self._fits(size, len(families))
-        self.store.register_families(families)
-        self._workspace_bytes += size
-
-    def _validate_chunks(self, chunks, bucket):
-        if not isinstance(chunks, Mapping) or not chunks or not isinstance(bucket, (Bucket, QueryFamily)):
-            raise ValueError('Nonempty ordered token mapping and explicit bucket required')
-        queries = tuple(x.shape[1] if isinstance(x, torch.Tensor) and x.ndim == 2 else -1 for x in chunks.values())
-        lengths = self.lengths
-        if not bucket.accepts(queries, tuple(lengths.get(r, -1) for r in chunks)):
-            raise ValueError('Ordered query lengths and contexts must match the chosen bucket or family')
-        for request, ids in chunks.items():
-            if request not in self._handles:
-                raise ValueError('Request not resident')
-            if ids.shape[0] != 1 or ids.dtype != torch.long or ids.device != self.device:
-                raise ValueError('Each token chunk must be [1,Q] long on target device')
-            if bool(((ids < 0) | (ids >= self.model.config.vocab_size)).any()):
-                raise ValueError('Token outside vocabulary')
-
-    @staticmethod
-    def _spans(chunks, tx):
-        spans, offset = {}, 0
-        for request, c, q in zip(chunks, tx.context_lengths, tx.query_lengths):
-            spans[request] = (offset, q, c)
-            offset += q
-        return spans
-
-    def _publish(self, features, tx, *, lease):
-        self._pending = (features, tx)
-        self._features[id(features)] = features
-        if lease:
-            self._feature_lease = features
-        return features
-
-    # -- graph buckets (persistent_qwen_target.py:243-336) ------------------------------
-    def register_graph_bucket(self, bucket, *, reserve_bytes):
-        """Explicit registration; reserve_bytes covers the capture's own pool."""
-        self._idle()
-        if self._graph_backend is None or type(reserve_bytes) is not int or reserve_bytes < 1:
-            raise ValueError('Graph backend and positive allocation reservation required')
-        if bucket in self._graphs or len(self._graphs) >= self._max_graph_buckets:
-            raise ValueError('Duplicate graph bucket or finite graph count exceeded')
-        workspace = 0 if self.store.is_registered(bucket) else self.store.workspace_bytes(bucket)
-        extra = FullModelGraph.output_buffer_bytes(self, bucket) + reserve_bytes
-        if self._workspace_bytes + workspace + self._graph_reserved_bytes + extra > self._graph_budget:
-            raise ValueError('Combined graph/workspace byte budget exceeded')
-        self.register_bucket(bucket)
-        self._graphs[bucket] = FullModelGraph(self, bucket, reserve_bytes)
-        self._graph_reserved_bytes += extra
-
-    @torch.no_grad()
-    def capture_graph(self, chunks, *, bucket):
-        """Set-up only: capture the bucket's full-model forward (token ids and
-        query lengths of `chunks` shape the capture; nothing is committed)."""
-        self._idle()
-        self._validate_chunks(chunks, bucket)
-        if bucket not in self._graphs:
-            raise ValueError('Explicit registered graph bucket required')
-        ex = self._graphs[bucket]
-        try:
-            ex.load(chunks)
-            ex.capture(tuple(self._handles[r] for r in chunks), tuple(ids.shape[1] for ids in chunks.values()))
-        except BaseException:
-            self.invalidate()
-            raise
-
-    @torch.no_grad()
-    def prepare_graph_verify(self, chunks, *, bucket):
-        self._idle()
-        self._validate_chunks(chunks, bucket)
-        ex = self._graphs.get(bucket)
-        if ex is None or ex.graph is None:
-            raise ValueError('Explicitly captured bucket required; no capture-on-miss')
-        ex.validate()
-        tx = self.store.begin(tuple(self._handles[r] for r in chunks), bucket,
-                              query_lengths=tuple(ids.shape[1] for ids in chunks.values()))
-        try:
-            ex.load(chunks)
-            receipt = self.store.prepare_external_write(tx, ex.writer)
-            self._graph_ticket = GraphTicket(tx, receipt, ex, self._spans(chunks, tx))
-            return self._graph_ticket
-        except BaseException:
-            self.store.abort(tx)
-            raise
-
-    @torch.no_grad()
-    def submit_graph(self, ticket):
-        self._check_stream()
-        if ticket is not self._graph_ticket or self._graph_completion is not None:
-            raise ValueError('Exact unsubmitted graph ticket required')
-        try:
-            event = ticket.execution.submit(ticket.receipt)
-            self.store.submit_external_write(ticket.receipt, event)
-            self._graph_completion = GraphCompletion(ticket, event)
-            return self._graph_completion
-        except BaseException:
-            self.invalidate()
-            raise
-
-    @torch.no_grad()
-    def finish_graph(self, completion, *, wait=True):
-        self._check_stream()
-        if completion is None or completion is not self._graph_completion:
-            raise ValueError('Exact submitted graph completion required')
-        ticket = completion.ticket
-        ex = ticket.execution
-        try:
-            if wait:
-                completion.event.synchronize()
-            ready = ex.complete(completion.event, ticket.receipt)
-        except BaseException:
-            self.invalidate()
-            raise
-        if not ready:
-            raise RuntimeError('Graph completion has not been observed')
-        try:
-            self.store.complete_external_write(ticket.receipt)
-            ex.validate()
-            work = self.store.work(ticket.transaction)
-            work.update(model_forward_calls=1, layers=self.store.layers, selected_layer_ids=list(self.layer_ids),
-                        attention_backend=self.BACKEND_NAME, execution_kind=ex.kind,
-                        committed_write_policy='scratch_only_until_explicit_commit',
-                        graph_scope='HF embedding, every decoder layer with the fused stage + attention, final '
-                                    'norm; head and sampling outside',
-                        graph_reserved_bytes=self._graph_reserved_bytes, workspace_bytes=self._workspace_bytes)
-            features = PackedFeatures(ex.last, ex.context, ticket.spans, work)
-            self._graph_ticket = self._graph_completion = None
-            return self._publish(features, ticket.transaction, lease=True)
-        except BaseException:
-            self.invalidate()
-            raise
-
-    def cancel_graph(self, ticket):
-        self._check_stream()
-        if ticket is not self._graph_ticket:
-            raise ValueError('Exact graph ticket required')
-        try:
-            self.store.abort(ticket.transaction)      # refuses an unfinished external write
-        except BaseException:
-            if self.store.failed:
-                self.invalidate()
-            raise
-        self._graph_ticket = self._graph_completion = None
-
-    # -- verification ------------------------------------------------------------
-    @torch.no_grad()
-    def verify(self, chunks, *, bucket):
-        """One packed forward over {request: ids [1, q]} in bucket order:
-        the captured program for a registered graph bucket, else eager."""
-        if bucket in self._graphs:
-            return self.finish_graph(self.submit_graph(self.prepare_graph_verify(chunks, bucket=bucket)))
-        return self.verify_eager(chunks, bucket=bucket)
-
-    @torch.no_grad()
-    def verify_eager(self, chunks, *, bucket):
-        """The explicit eager forward, also on registered graph buckets."""
-        self._idle()
-        self._validate_chunks(chunks, bucket)
-        handles = tuple(self._handles[r] for r in chunks)
-        query_lengths = tuple(ids.shape[1] for ids in chunks.values())
-        self._captured = {}
-        with self.verifier.transaction_for(handles, bucket, query_lengths=query_lengths) as tx:
-            try:
-                out = self.model.model(input_ids=torch.cat(tuple(chunks.values()), dim=1),
-                                       position_ids=self.store.workspace(tx.bucket).positions[None],
-                                       attention_mask=None, past_key_values=self.verifier.cache, use_cache=True,
-                                       return_dict=True, fused_verification=self.verifier)
-                if self.store.staged_layers() != self.store.layers or set(self._captured) != set(self.layer_ids):
-                    raise RuntimeError('Full layer cache update or selected feature capture missing')
-            except BaseException:
-                if self.store.open_transaction is tx and not self.store.failed:
-                    self.store.abort(tx)
-                raise
-            finally:
-                captured, self._captured = self._captured, {}
-        context = torch.cat([captured[i] for i in self.layer_ids], dim=-1) if self.layer_ids else None
-        work = self.store.work(tx)
-        work.update(model_forward_calls=1, layers=self.store.layers, selected_layer_ids=list(self.layer_ids),
-                    attention_backend=self.BACKEND_NAME, workspace_bytes=self._workspace_bytes,
-                    committed_write_policy='scratch_only_until_explicit_commit')
-        if isinstance(bucket, QueryFamily):
-            work['execution_kind'] = 'explicit_eager'
-        features = PackedFeatures(out.last_hidden_state.detach(), None if context is None else context.detach(),
-                                  self._spans(chunks, tx), work)
-        return self._publish(features, tx, lease=False)
-
-    @torch.no_grad()
-    def commit(self, features, committed_query_lengths):
-        self._check_stream()
-        if self._pending is None or self._pending[0] is not features:
-            raise ValueError('Only the outstanding verification features can commit')
-        if not isinstance(committed_query_lengths, Mapping) or set(committed_query_lengths) != set(features.spans):
-            raise ValueError('One committed query prefix per verified request required')
-        _, tx = self._pending
-        result = self.store.commit(tx, {self._handles[r]: n for r, n in committed_query_lengths.items()})
-        self._pending = None
-        return result
-
-    def abort(self, features):
-        self._check_stream()
-        if self._pending is None or self._pending[0] is not features:
-            raise ValueError('Only outstanding verification features can abort')
-        self.store.abort(self._pending[1])
-        self._pending = None
-
-    @torch.no_grad()
-    def prefill(self, chunks, *, bucket):
-        self._idle()
-        if any(self.lengths.get(r) != 0 for r in chunks):
-            raise ValueError('Prefill is only for newly admitted empty requests')
-        features = (self.verify_eager(chunks, bucket=bucket) if bucket in self._graphs
-                    else self.verify(chunks, bucket=bucket))
-        self.commit(features, {r: ids.shape[1] for r, ids in chunks.items()})
-        return features
-
-    @torch.no_grad()
-    def predict(self, features, last_only=False):
-        """The model's LM head over the verified rows (after its final norm)."""
-        self._check_stream()
-        if self._features.get(id(features)) is not features:
-            raise ValueError('Foreign or released features')
-        logits = self.model.get_output_embeddings()(features.last)
-        return {r: (logits[:, offset + count - 1] if last_only else logits[:, offset:offset + count])
-                for r, (offset, count, _) in features.spans.items()}
-
-    def request_kv(self, request):
-        """Per layer (keys, values) [1, Hkv, C, D] copies of a request's committed rows."""
-        keys, values = self.store.request_kv(self._handles[request])
-        return tuple((k.transpose(0, 1)[None], v.transpose(0, 1)[None]) for k, v in zip(keys, values))
 
 
 # ---------------------------------------------------------------------------
@@ -791,8 +274,18 @@ class VarlenPackedTarget:
         self.kv = AppendOrderKV(layers=cfg.num_hidden_layers, heads=KV_HEADS, dim=HEAD_DIM, dtype=torch.bfloat16,
                                 device=device)
         self.cache = PackedVarlenCache(self)
+        self._closed = False
+        self._old_backend = cfg._attn_implementation
         ALL_ATTENTION_FUNCTIONS.register(VARLEN_BACKEND, varlen_attention_forward)
         cfg._attn_implementation = VARLEN_BACKEND
+
+    def close(self):
+        """Give the model its previous attention implementation back; the
+        target is unusable afterwards."""
+        if self.model.config._attn_implementation == VARLEN_BACKEND:
+            self.model.config._attn_implementation = self._old_backend
+        self.kv.reset()
+        self._closed = True
 
     @property
     def device(self):
@@ -864,6 +357,8 @@ class VarlenPackedTarget:
         """One packed forward over the ordered {request: ids [1, q]}; returns
         PackedFeatures (last hidden states, captured layer outputs, spans,
         work counters).  Invalid inputs fail before any mutation."""
+        if self._closed:
+            raise RuntimeError('Target adapter closed')
         self._validate_chunks(chunks)
         lengths = self.kv.lengths
         spans, markers, positions, offset = {}, [], [], 0
@@ -909,3 +404,15 @@ class VarlenPackedTarget:
         logits = self.model.get_output_embeddings()(features.last)
         return {r: (logits[:, offset + count - 1] if last_only else logits[:, offset:offset + count])
                 for r, (offset, count, _) in features.spans.items()}
+
+
+def __getattr__(name):
+    # The full-model adapter lives in persistent_target (which imports this
+    # module); resolve its names here lazily.
+    if name in ('PersistentQwenTarget', 'FullModelGraph', 'GraphTicket', 'GraphCompletion'):
+        from . import persistent_target
+        return getattr(persistent_target, name)
+    if name == 'GRAPH_BACKEND':
+        from .graph import TorchGraphBackend
+        return TorchGraphBackend.kind
+    raise AttributeError(name)

@@ -443,7 +443,8 @@ class PersistentTargetKV:
         landed.  Relative speeds are clipped to 1 +- clip.  Opt-in: cut
         points then depend on the measurement, so outputs can differ in the
         last bits between processes (as between batches).  Returns the
-        speeds in use."""
+        speeds in use: None (equal runs) when the measurement does not
+        cover all 8 XCDs."""
         self._permit('admin')
         self.set_xcd_speed(clipped(self.kv_device.measure_xcd_speed(workgroups=workgroups, passes=passes), clip))
         return self.xcd_speed

@@ -18,7 +18,8 @@ def measure_read_speed(tensors, *, workgroups=1024, passes=2):
     """Relative read bandwidth of the 8 XCDs over the given device tensors
     (each contiguous, same device): dspark_xcd_read_stamps over every tensor
     `passes` times, one host synchronisation at the end.  Returns each XCD's
-    mean per-workgroup rate over the mean of the 8."""
+    mean per-workgroup rate over the mean of the 8 (xcd_rates), or None if
+    the stamps do not cover every XCD."""
     tensors = [t for t in tensors if t.numel()]
     if not tensors or any(not t.is_contiguous() or t.device != tensors[0].device for t in tensors):
         raise ValueError('Contiguous device tensors on one device required')
@@ -42,10 +43,29 @@ def measure_read_speed(tensors, *, workgroups=1024, passes=2):
         per = -(-(n // 16) // wgs) * 16
         return [min(per, max(n - per * w, 0)) for w in range(wgs)]
     slice_bytes = np.array([slices(n) for _ in range(int(passes)) for n in sizes], dtype=np.float64)
-    rate = slice_bytes / np.maximum(st[..., 1] - st[..., 0], 1)
-    xcd = st[..., 2] & (XCDS - 1)
-    mean = np.array([rate[xcd == x].mean() for x in range(XCDS)])
-    return [float(x) for x in mean / mean.mean()]
+    return xcd_rates(slice_bytes, st[..., 1] - st[..., 0], st[..., 2])
+
+
+def xcd_rates(slice_bytes, ticks, xcc):
+    """Each XCD's mean read rate over its workgroups' nonempty slices,
+    relative to the mean of the 8; None when some XCD has no nonempty slice
+    or a rate is not finite and positive (a partitioned mode, or a region
+    too small to spread over every XCD), so that plans then use equal runs."""
+    slice_bytes = np.asarray(slice_bytes, dtype=np.float64)
+    ticks = np.asarray(ticks, dtype=np.float64)
+    xcd = np.asarray(xcc, dtype=np.int64) & (XCDS - 1)
+    used = slice_bytes > 0
+    rate = slice_bytes / np.maximum(ticks, 1)
+    means = []
+    for x in range(XCDS):
+        mine = rate[used & (xcd == x)]
+        if mine.size == 0:
+            return None
+        means.append(mine.mean())
+    means = np.array(means)
+    if not (np.isfinite(means).all() and (means > 0).all()):
+        return None
+    return [float(x) for x in means / means.mean()]
 
 
 def normalised(speed, what='xcd_speed'):
@@ -60,5 +80,11 @@ def normalised(speed, what='xcd_speed'):
 
 
 def clipped(speed, clip):
-    """Speeds limited to 1 +- clip (a measurement's noise never skews a plan further)."""
-    return [min(1.0 + clip, max(1.0 - clip, float(x))) for x in speed]
+    """Speeds limited to 1 +- clip (a measurement's noise never skews a plan
+    further); None stays None.  A speed that is not finite is refused."""
+    if speed is None:
+        return None
+    speed = [float(x) for x in speed]
+    if not all(np.isfinite(x) for x in speed):
+        raise ValueError('Relative XCD speeds must be finite')
+    return [min(1.0 + clip, max(1.0 - clip, x)) for x in speed]

@@ -85,7 +85,8 @@ def rel_err(got, want):
 
 @torch.no_grad()
 def test_config4_verification_round_full_size():
-    from qwen3_dspark_amd.hf_hooks import PersistentQwenTarget
+    from qwen3_dspark_amd import backends
+    from qwen3_dspark_amd.persistent_target import PersistentQwenTarget
     from qwen3_dspark_amd.persistent_kv import Bucket
     ref, control, model = qwen3_06b_models()
     rng = np.random.default_rng(SEED)
@@ -93,7 +94,7 @@ def test_config4_verification_round_full_size():
     seqs = [rng.integers(0, 151936, size=n).tolist() for n in lengths]
     names = [f'r{i}' for i in range(REQUESTS)]
     capacity = HI + 2 * NEW
-    target = PersistentQwenTarget(model, slots=REQUESTS, context_capacity=capacity, max_query_tokens=sum(lengths),
+    target = PersistentQwenTarget(model, native_backend=backends.CAPACITY_BACKEND, slots=REQUESTS, context_capacity=capacity, max_query_tokens=sum(lengths),
                                   workspace_byte_budget=1 << 31)
     for n in names:
         target.add_request(n)

@@ -138,12 +138,14 @@ def test_persistent_qwen_target_prefill_verify_commit_features():
     prefill ragged prompts, verify 7 tokens per request, commit a prefix,
     verify again; logits via predict() and captured layer features match the
     CPU float32 model over each request's full sequence."""
-    from qwen3_dspark_amd.hf_hooks import PersistentQwenTarget
+    from qwen3_dspark_amd import backends
     from qwen3_dspark_amd.persistent_kv import Bucket
+    from qwen3_dspark_amd.persistent_target import PersistentQwenTarget
     cpu, gpu = tiny_qwen3()
     rng = np.random.default_rng(11)
     prompts = [rng.integers(0, 512, size=n).tolist() for n in (20, 65, 9)]
-    target = PersistentQwenTarget(gpu, layer_ids=(0, 1), slots=3, context_capacity=256, max_query_tokens=128)
+    target = PersistentQwenTarget(gpu, layer_ids=(0, 1), native_backend=backends.CAPACITY_BACKEND, slots=3,
+                                  context_capacity=256, max_query_tokens=128)
     names = ['a', 'b', 'c']
     for n in names:
         target.add_request(n)

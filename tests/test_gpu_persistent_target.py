@@ -29,8 +29,11 @@ def ids(x):
 
 
 def make_target(gpu, **kw):
-    from qwen3_dspark_amd.hf_hooks import GRAPH_BACKEND, PersistentQwenTarget
-    args = dict(slots=3, context_capacity=256, max_query_tokens=128, graph_backend=GRAPH_BACKEND,
+    from qwen3_dspark_amd import backends
+    from qwen3_dspark_amd.graph import TorchGraphBackend
+    from qwen3_dspark_amd.persistent_target import PersistentQwenTarget
+    args = dict(slots=3, context_capacity=256, max_query_tokens=128, graph_backend=TorchGraphBackend(),
+                native_backend=backends.CAPACITY_BACKEND,
                 max_graph_buckets=1, graph_byte_budget=1 << 30, workspace_byte_budget=1 << 30)
     args.update(kw)
     return PersistentQwenTarget(gpu, layer_ids=(0, 1), **args)
@@ -49,7 +52,7 @@ def test_graph_bucket_replays_match_eager_and_cpu_model():
     target.register_bucket(pre)
     target.release_features(target.prefill({n: ids(p) for n, p in zip(names, prompts)}, bucket=pre))
     step = Bucket((NEW,) * 3, (256 - NEW,) * 3, 'graph verify')
-    target.register_graph_bucket(step, reserve_bytes=1 << 20)
+    target.register_graph_bucket(step, reserve_bytes=256 << 20)
     with pytest.raises(ValueError, match='no capture-on-miss'):
         target.verify({n: ids([1] * NEW) for n in names}, bucket=step)
     say('[graph] capture')
@@ -62,6 +65,8 @@ def test_graph_bucket_replays_match_eager_and_cpu_model():
         chunks = {n: ids(x) for n, x in zip(names, new)}
         g = target.verify(chunks, bucket=step)
         assert g.work['execution_kind'] == 'mi355x_hip_full_model_graph'
+        if rnd == 0:
+            say(f"[graph] private pool {g.work['graph_retained_bytes']} bytes of a 256 MiB reservation")
         g_last, g_ctx = g.last.clone(), g.context.clone()
         g_logits = {r: x.clone() for r, x in target.predict(g).items()}
         with pytest.raises(RuntimeError, match='existing verification transaction'):
@@ -117,9 +122,9 @@ def test_graph_ticket_protocol_and_guards():
     with pytest.raises(ValueError, match='budget'):
         target.register_bucket(Bucket((7, 7), (249, 249), 'too large for 2 MiB'))
     step = Bucket((2, 2), (100, 100), 'graph')
-    target.register_graph_bucket(step, reserve_bytes=4096)
+    target.register_graph_bucket(step, reserve_bytes=256 << 20)
     with pytest.raises(ValueError, match='Duplicate graph bucket'):
-        target.register_graph_bucket(step, reserve_bytes=4096)
+        target.register_graph_bucket(step, reserve_bytes=256 << 20)
     with pytest.raises(ValueError, match='budget'):
         target.register_bucket(Bucket((1,), (10,), 'third bucket beyond max_buckets'))
     target.capture_graph({'a': ids([9, 9]), 'b': ids([8, 8])}, bucket=step)
