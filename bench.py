@@ -61,6 +61,12 @@ def parse():
     ap.add_argument('--warmup', type=int, default=5)
     ap.add_argument('--chunk', type=int, default=None, help='keys per split-K verification work item')
     ap.add_argument('--draft-chunk', type=int, default=None, help='keys per split-K draft work item')
+    ap.add_argument('--draft-persistent', type=int, default=None, choices=(0, 1, 8),
+                    help='draft scheduling: 0 one workgroup per (chunk, KV head), 1 or 8 persistent workgroups '
+                         'taking items from one queue or one queue per KV head (default: the library default)')
+    ap.add_argument('--draft-ab', action='store_true',
+                    help='only compare the draft scheduling modes on one pool (alternating rounds of the '
+                         "workload's 5 draft layers), with outputs checked bitwise equal across modes")
     ap.add_argument('--no-cpu-baseline', action='store_true', help='skip the CPU oracle leg (profiling runs)')
     ap.add_argument('--equal-runs', action='store_true',
                     help='verification plans with equal runs on every XCD (no XCD speed calibration)')
@@ -75,6 +81,10 @@ def parse():
     ap.add_argument('--xcd-ab', action='store_true',
                     help='only compare verification plans with equal runs and with XCD-calibrated runs on one store '
                          '(alternating transactions of 28 layers), and report the measured XCD speeds')
+    ap.add_argument('--timeline', action='store_true',
+                    help='per-workgroup phase timeline of the draft attention on the workload, from the timeline '
+                         'build of the library (clock stamps per segment: start, first loads issued, first stage '
+                         'landed, stream end, merge + write end), summarised per call')
     ap.add_argument('--mfma-probe', action='store_true',
                     help='only run the draft kernels for a rocprofv3 --pmc MfmaUtil MfmaFlopsBF16 pass')
     ap.add_argument('--cpu-verify-layers', type=int, default=VERIFY_LAYERS, help='verify layers in the CPU sample')
@@ -175,6 +185,10 @@ def main():
         return traffic_probe(args)
     if args.mfma_probe:
         return mfma_probe(args)
+    if args.timeline:
+        return timeline_probe(args)
+    if args.draft_ab:
+        return draft_ab(args)
     if args.xcd_ab:
         return xcd_ab(args)
     if args.stream_probe:
@@ -225,7 +239,7 @@ def main():
     qd = torch.randn(DRAFT_LAYERS, nq_d, 16, 128, generator=gen, device=dev).to(torch.bfloat16)
     bkd = torch.randn(DRAFT_LAYERS, nq_d, 8, 128, generator=gen, device=dev).to(torch.bfloat16)
     bvd = torch.randn(DRAFT_LAYERS, nq_d, 8, 128, generator=gen, device=dev).to(torch.bfloat16)
-    draft = HipDraftAttention(dev, chunk=args.draft_chunk or DRAFT_CHUNK)
+    draft = HipDraftAttention(dev, chunk=args.draft_chunk or DRAFT_CHUNK, **draft_modes(args.draft_persistent))
     draft_offsets = [h.index * CAPACITY for h in handles]   # slot * capacity + first position
     torch.cuda.synchronize()
 
@@ -637,6 +651,178 @@ def traffic_probe(args):
                       'context_rows': sum(contexts),
                       'calibration_copy_bytes': 1 << 30,
                       'streaming_reference': streaming_reference(dev, src, dst)}), flush=True)
+
+
+def draft_modes(arg):
+    """HipDraftAttention keyword for the --draft-persistent choice."""
+    return {} if arg is None else {'persistent': None if arg == 0 else arg}
+
+
+def draft_ab(args, rounds=16):
+    """The workload's 5 draft layers per round on one pool, rounds
+    alternating between the scheduling modes (one workgroup per item
+    dispatched by the hardware; persistent workgroups on one queue; on one
+    queue per KV head), event-timed on the launch stream; median per call.
+    Every mode's outputs must be bitwise equal to the first mode's."""
+    import numpy as np
+    import torch
+
+    from qwen3_dspark_amd.draft import DraftBatch, HipDraftAttention
+    from qwen3_dspark_amd.kernels import SCALE
+    from qwen3_dspark_amd.schedule import DRAFT_CHUNK
+    dev = torch.device('cuda:0')
+    torch.cuda.set_device(dev)
+    contexts, anchors, _ = workload(args.warmup + args.steps)
+    gen = torch.Generator(device=dev).manual_seed(SEED)
+    ctx_k = torch.empty(DRAFT_LAYERS, B, 8, CAPACITY, 128, dtype=torch.bfloat16, device=dev)
+    ctx_v = torch.empty_like(ctx_k)
+    for layer in range(DRAFT_LAYERS):
+        ctx_k[layer].normal_(generator=gen)
+        ctx_v[layer].normal_(generator=gen)
+    nq = BLOCK * sum(len(a) for a in anchors)
+    qd = torch.randn(DRAFT_LAYERS, nq, 16, 128, generator=gen, device=dev).to(torch.bfloat16)
+    bk = torch.randn(DRAFT_LAYERS, nq, 8, 128, generator=gen, device=dev).to(torch.bfloat16)
+    bv = torch.randn(DRAFT_LAYERS, nq, 8, 128, generator=gen, device=dev).to(torch.bfloat16)
+    batch = DraftBatch(dev, [i * CAPACITY for i in range(B)], contexts, anchors)
+    modes = {'hardware dispatch': None, 'persistent, one queue': 1, 'persistent, queue per KV head': 8}
+    kernels = {m: HipDraftAttention(dev, chunk=args.draft_chunk or DRAFT_CHUNK, persistent=p)
+               for m, p in modes.items()}
+    times = {m: [] for m in modes}
+    ref = None
+    for r in range(rounds + 2):
+        for m, k in kernels.items():
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record()
+            outs = [k(qd[l], bk[l], bv[l], ctx_k[l], ctx_v[l], batch, scale=SCALE) for l in range(DRAFT_LAYERS)]
+            b.record()
+            b.synchronize()
+            if r >= 2:
+                times[m].append(a.elapsed_time(b) / DRAFT_LAYERS)
+            if ref is None:
+                ref = [o.clone() for o in outs]
+            elif not all(torch.equal(o, x) for o, x in zip(outs, ref)):
+                raise AssertionError(f'draft outputs differ under {m}')
+    d_b = draft_bytes(anchors)
+    res = {}
+    for m, t in times.items():
+        ms = float(np.median(t))
+        res[m] = {'median_ms': round(ms, 5), 'p10_ms': round(float(np.percentile(t, 10)), 5),
+                  'p90_ms': round(float(np.percentile(t, 90)), 5), 'gbs': round(d_b / ms / 1e6, 1),
+                  'frac_of_8tbs': round(d_b / ms / 1e6 / HBM_PEAK_GBS, 4)}
+        log(f'[draft-ab] {m}: {ms * 1e3:.1f} us per call ({res[m]["frac_of_8tbs"]:.3f} of 8 TB/s)')
+    print(json.dumps({'draft_ab': res, 'rounds': rounds, 'calls_per_round': DRAFT_LAYERS,
+                      'outputs_bitwise_equal': True, 'draft_chunk': args.draft_chunk or DRAFT_CHUNK}), flush=True)
+
+
+def timeline_probe(args, calls=5, samples=6):
+    """Per-workgroup timeline of the draft attention (DSPARK_TIMELINE build
+    of the library): the workload's draft layers run back to back, `calls`
+    per sample as in a round; the stamps of a sample's last call are read
+    after it.  Per call: span from the first segment start to the last
+    segment end; per segment the phases start -> first loads issued (record
+    and scalar metadata), -> first stage landed (the ring's first HBM
+    latency), -> stream end, -> half merge and output written; per CU the
+    idle time between one segment's end and the next one's start there, and
+    the tail (time from the median to the last segment end).  Medians over
+    `samples` samples."""
+    os.environ['DSPARK_AMD_TIMELINE'] = '1'
+    import numpy as np
+    import torch
+
+    from qwen3_dspark_amd import _native
+    from qwen3_dspark_amd.draft import DraftBatch, HipDraftAttention
+    from qwen3_dspark_amd.kernels import SCALE
+    from qwen3_dspark_amd.schedule import DRAFT_CHUNK
+    lib = _native.load()
+    dev = torch.device('cuda:0')
+    torch.cuda.set_device(dev)
+    contexts, anchors, _ = workload(args.warmup + args.steps)
+    gen = torch.Generator(device=dev).manual_seed(SEED)
+    ctx_k = torch.empty(DRAFT_LAYERS, B, 8, CAPACITY, 128, dtype=torch.bfloat16, device=dev)
+    ctx_v = torch.empty_like(ctx_k)
+    for layer in range(DRAFT_LAYERS):
+        ctx_k[layer].normal_(generator=gen)
+        ctx_v[layer].normal_(generator=gen)
+    nq = BLOCK * sum(len(a) for a in anchors)
+    qd = torch.randn(nq, 16, 128, generator=gen, device=dev).to(torch.bfloat16)
+    bk = torch.randn(nq, 8, 128, generator=gen, device=dev).to(torch.bfloat16)
+    bv = torch.randn(nq, 8, 128, generator=gen, device=dev).to(torch.bfloat16)
+    draft = HipDraftAttention(dev, chunk=args.draft_chunk or DRAFT_CHUNK, **draft_modes(args.draft_persistent))
+    batch = DraftBatch(dev, [i * CAPACITY for i in range(B)], contexts, anchors)
+    nbytes = int(lib.dspark_timeline_bytes())
+    host = np.zeros(nbytes // 8, dtype=np.uint64)
+    tick_us = 0.01                               # the 100 MHz constant clock
+    rows = []
+    for sample in range(samples + 1):
+        for layer in range(calls):
+            draft(qd, bk, bv, ctx_k[layer], ctx_v[layer], batch, scale=SCALE)
+        _native.call('dspark_timeline_fetch', host.ctypes.data, nbytes)
+        wg = np.zeros(8192 * 4, dtype=np.uint64)
+        _native.call('dspark_timeline_fetch_wg', wg.ctypes.data, wg.nbytes)
+        if sample == 0:
+            continue                             # warm-up
+        rec = host.reshape(-1, 8)
+        slot = np.arange(len(rec)) % 16                     # segment index within its workgroup
+        valid = (rec[:, 5] >> np.uint64(63)) == 1
+        # Every workgroup's first segment of the last call overwrote slot 0;
+        # later slots may still hold segments of earlier calls of the sample.
+        start = rec[valid & (slot == 0), 0].min()
+        rec = rec[valid & (rec[:, 0] >= start)]
+        t = rec[:, :5].astype(np.float64)
+        t0 = t[:, 0].min()
+        t = (t - t0) * tick_us
+        where = (rec[:, 5] & np.uint64(0xffffffff)).astype(np.int64)
+        xcc = ((rec[:, 5] >> np.uint64(32)) & np.uint64(15)).astype(np.int64)
+        cu = xcc * 1000 + ((where >> 8) & 0xff)           # XCC and the CU/SH/SE bits of HW_ID
+        keys = ((rec[:, 6] >> np.uint64(32)) & np.uint64(0xffffffff)).astype(np.int64)
+        span = float(t[:, 4].max())
+        meta, first, stream, merge = (t[:, 1] - t[:, 0], t[:, 2] - t[:, 1], t[:, 3] - t[:, 2], t[:, 4] - t[:, 3])
+        gaps, busy = [], []
+        for c in np.unique(cu):
+            sel = np.argsort(t[cu == c, 0])
+            tc = t[cu == c][sel]
+            gaps += list(tc[1:, 0] - tc[:-1, 4])
+            busy.append(float((tc[:, 4] - tc[:, 0]).sum()))
+        stream_gbs = keys * 2 * 128 * 2 / np.maximum(stream, 1e-3) * 1e-3     # one KV head: K + V rows
+        wg = wg.reshape(-1, 4)
+        wg = wg[(wg[:, 3] >> np.uint64(63)) == 1]
+        persistent = {}
+        if len(wg):
+            w = (wg & np.uint64((1 << 63) - 1)).astype(np.float64)
+            w = (w - t0) * tick_us
+            persistent = dict(wg_entry_min_us=float(w[:, 0].min()), wg_entry_max_us=float(w[:, 0].max()),
+                              first_ticket_p50_us=float(np.median(w[:, 1] - w[:, 0])),
+                              first_ticket_max_us=float((w[:, 1] - w[:, 0]).max()),
+                              loop_left_max_us=float(w[:, 2].max()),
+                              exit_protocol_p50_us=float(np.median(w[:, 3] - w[:, 2])),
+                              exit_protocol_max_us=float((w[:, 3] - w[:, 2]).max()), exit_max_us=float(w[:, 3].max()))
+            log(f'[timeline]   workgroups: entry {persistent["wg_entry_min_us"]:.1f}..{persistent["wg_entry_max_us"]:.1f} us, '
+                f'first ticket p50 {persistent["first_ticket_p50_us"]:.2f} max {persistent["first_ticket_max_us"]:.2f} us, '
+                f'exit protocol p50 {persistent["exit_protocol_p50_us"]:.2f} max {persistent["exit_protocol_max_us"]:.2f} us, '
+                f'last exit {persistent["exit_max_us"]:.1f} us')
+        rows.append(dict(
+            span_us=span, segments=int(len(t)), cus=int(len(np.unique(cu))),
+            segments_per_cu=float(len(t) / len(np.unique(cu))),
+            start_to_issue_us=float(np.median(meta)), issue_to_first_stage_us=float(np.median(first)),
+            stream_us=float(np.median(stream)), merge_write_us=float(np.median(merge)),
+            overhead_per_segment_us=float(np.median(meta + first + merge)),
+            cu_gap_median_us=float(np.median(gaps)) if gaps else 0.0,
+            cu_gap_p90_us=float(np.percentile(gaps, 90)) if gaps else 0.0,
+            cu_busy_frac=float(np.sum(busy) / (span * len(busy))),
+            end_p50_us=float(np.median(t[:, 4])), end_p90_us=float(np.percentile(t[:, 4], 90)),
+            tail_us=float(span - np.percentile(t[:, 4], 90)),
+            first_start_spread_us=float(np.sort(t[:, 0])[min(len(t) - 1, 255)]),
+            stream_gbs_per_workgroup_p50=float(np.median(stream_gbs[keys >= 1024])) if (keys >= 1024).any() else 0.0,
+            **persistent))
+        log(f'[timeline] sample {sample}: span {span:.1f} us, {len(t)} segments on {rows[-1]["cus"]} CUs; '
+            f'per segment: issue {rows[-1]["start_to_issue_us"]:.2f}, first stage {rows[-1]["issue_to_first_stage_us"]:.2f}, '
+            f'merge+write {rows[-1]["merge_write_us"]:.2f} us; CU gap {rows[-1]["cu_gap_median_us"]:.2f} us; '
+            f'busy {rows[-1]["cu_busy_frac"]:.3f}; tail {rows[-1]["tail_us"]:.1f} us')
+    summary = {k: round(float(np.median([r[k] for r in rows])), 3) for k in rows[0] if all(k in r for r in rows)}
+    print(json.dumps({'timeline': 'draft attention', 'workload': '64 requests, contexts log-uniform [256, 8192], '
+                      '1..8 blocks each, 5 draft layers back to back', 'draft_chunk': draft.chunk,
+                      'persistent': draft.persistent,
+                      'samples': samples, 'median': summary, 'per_sample': rows}), flush=True)
 
 
 def stream_probe(gib=16, reps=10):

@@ -24,7 +24,7 @@ extern "C" {
 /* Thread-local message for the last failing call on this thread. */
 const char* dspark_last_error(void);
 
-/* ABI revision of this header (currently 4). */
+/* ABI revision of this header (currently 5). */
 int dspark_abi_version(void);
 
 /*
@@ -198,6 +198,17 @@ int dspark_verify_attn_staged_fwd(const void* q, const void* k_res, const void* 
  * Replaces the cat + index_select + cast + noncausal kernel sequence of
  *   dspark_qwen/packed_draft.py:219-236 (PackedDraft.backbone)
  * with the block_mask semantics of dspark_qwen/model.py:12-19.
+ *
+ * Scheduling: with workgroups = 0 the grid holds one workgroup per (run,
+ * KV head) of the work list (or per fixed chunk without one).  With
+ * workgroups > 0 (a multiple of 8; one per CU fills the chip) the grid is
+ * that many persistent workgroups taking (run, KV head) items, runs in
+ * list order, from ticket counters in `queue`: queues = 1 shares one queue,
+ * queues = 8 gives each KV head its own queue served by workgroups
+ * b = head (mod 8).  queue holds 2 int32 per queue, must be zero before the
+ * first call and is zero again after every call (the last workgroup resets
+ * it); calls sharing one queue buffer must not overlap.  Outputs do not
+ * depend on the mode.
  */
 int dspark_draft_attn_fwd(const void* q, int q_dtype, const void* k_ctx, const void* v_ctx,
                           int k_dtype, const int64_t* ctx_idx, const int64_t* ctx_off,
@@ -206,6 +217,7 @@ int dspark_draft_attn_fwd(const void* q, int q_dtype, const void* k_ctx, const v
                           const int32_t* cu_blocks, const int32_t* anchors,
                           int n_req, int64_t ctx_rows_bound, int max_blocks, float scale, int chunk,
                           const int32_t* work, int n_work, int n_groups,
+                          int workgroups, int queues, int32_t* queue,
                           void* out, void* workspace, int64_t workspace_bytes, void* stream);
 
 /*

@@ -7,7 +7,7 @@ import ctypes
 import os
 import threading
 
-from .build import LIB_PATH
+from .build import LIB_PATH, TIMELINE_LIB_PATH
 
 _lock = threading.Lock()
 _lib = None
@@ -35,7 +35,7 @@ SIGNATURES = {
     'dspark_verify_attn_staged_fwd': (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _L, _L, _L, _L, _I, _F, _I,
                                            _P, _I, _I, _P, _P, _L, _P]),
     'dspark_draft_attn_fwd': (_I, [_P, _I, _P, _P, _I, _P, _P, _P, _L, _L, _P, _P, _P, _P, _I, _L, _I, _F, _I, _P,
-                                   _I, _I, _P, _P, _L, _P]),
+                                   _I, _I, _I, _I, _P, _P, _P, _L, _P]),
     'dspark_txn_metadata': (_I, [_P, _I, _L, _L, _L, _P, _P, _P, _P, _P, _P, _P, _P]),
     'dspark_kv_stage': (_I, [_P, _P, _P, _P, _L, _L, _P]),
     'dspark_kv_commit': (_I, [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _L, _L, _L, _L, _L, _I, _L, _L, _P]),
@@ -59,11 +59,24 @@ SIGNATURES = {
     'dspark_rows_rebuild': (_I, [_PP, _PP, _PP, _I, _I, _L, _L, _L, _P, _L, _P]),
 }
 
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 
 class NativeError(RuntimeError):
     """A C-ABI call returned a non-zero status."""
+
+
+# Extra entry points of the timeline (profiling) build.
+TIMELINE_SIGNATURES = {
+    'dspark_timeline_bytes': (_L, []),
+    'dspark_timeline_fetch': (_I, [_P, _L]),
+    'dspark_timeline_fetch_wg': (_I, [_P, _L]),
+}
+
+
+def timeline_build():
+    """True when this process uses the timeline build (DSPARK_AMD_TIMELINE set)."""
+    return bool(os.environ.get('DSPARK_AMD_TIMELINE'))
 
 
 def load():
@@ -71,11 +84,13 @@ def load():
     global _lib
     with _lock:
         if _lib is None:
-            if not os.path.exists(LIB_PATH):
-                raise RuntimeError(f'HIP extension not built ({LIB_PATH}); run __graft_entry__.build(). '
+            path = TIMELINE_LIB_PATH if timeline_build() else LIB_PATH
+            if not os.path.exists(path):
+                raise RuntimeError(f'HIP extension not built ({path}); run __graft_entry__.build(). '
                                    'There is no CPU or fallback implementation.')
-            lib = ctypes.CDLL(LIB_PATH)
-            for name, (res, args) in SIGNATURES.items():
+            lib = ctypes.CDLL(path)
+            table = dict(SIGNATURES, **(TIMELINE_SIGNATURES if timeline_build() else {}))
+            for name, (res, args) in table.items():
                 fn = getattr(lib, name)
                 fn.restype = res
                 fn.argtypes = args

@@ -12,6 +12,10 @@ CSRC = os.path.join(HERE, 'csrc')
 BUILD_DIR = os.path.join(HERE, '_build')
 LIB_NAME = 'libdspark_amd.so'
 LIB_PATH = os.path.join(BUILD_DIR, LIB_NAME)
+# Profiling build of the same sources with per-workgroup phase stamps in the
+# draft kernel (DSPARK_TIMELINE); loaded instead of LIB_PATH only when the
+# DSPARK_AMD_TIMELINE environment variable is set (bench.py --timeline).
+TIMELINE_LIB_PATH = os.path.join(BUILD_DIR, 'libdspark_amd_timeline.so')
 SOURCES = ('attn.hip', 'kv.hip', 'layout.hip', 'prologue.hip', 'project.hip', 'sample.hip', 'measure.hip',
            'errors.cpp')
 ARCH = 'gfx950'
@@ -27,23 +31,26 @@ def hipcc():
     return path
 
 
-def build(verbose=False):
-    """Compile every source into LIB_PATH (atomically replaced)."""
+def build(verbose=False, timeline=False):
+    """Compile every source into LIB_PATH (or, with timeline, the profiling
+    build into TIMELINE_LIB_PATH), atomically replaced."""
     os.makedirs(BUILD_DIR, exist_ok=True)
-    fd, tmp = tempfile.mkstemp(prefix=LIB_NAME + '.', suffix='.tmp', dir=BUILD_DIR)
+    target = TIMELINE_LIB_PATH if timeline else LIB_PATH
+    fd, tmp = tempfile.mkstemp(prefix=os.path.basename(target) + '.', suffix='.tmp', dir=BUILD_DIR)
     os.close(fd)
-    cmd = [hipcc(), *FLAGS, *(os.path.join(CSRC, s) for s in SOURCES), '-o', tmp]
+    extra = ['-DDSPARK_TIMELINE'] if timeline else []
+    cmd = [hipcc(), *FLAGS, *extra, *(os.path.join(CSRC, s) for s in SOURCES), '-o', tmp]
     try:
         proc = subprocess.run(cmd, capture_output=True, text=True)
         if proc.returncode != 0:
             raise RuntimeError('hipcc failed:\n' + proc.stderr[-8000:])
         if verbose and proc.stderr:
             print(proc.stderr)
-        os.replace(tmp, LIB_PATH)
+        os.replace(tmp, target)
     finally:
         if os.path.exists(tmp):
             os.unlink(tmp)
-    return LIB_PATH
+    return target
 
 
 if __name__ == '__main__':

@@ -650,7 +650,10 @@ struct DraftArgs {
   int64_t tok_stride;
   int64_t head_stride;
   const int32_t* work;      // optional segment list (see the C ABI)
+  int* queue;               // persistent mode: ticket counters (self-resetting; see draft_attn_kernel)
   int n_work;               // segment records in the work list
+  int n_runs;               // runs of the work list (persistent mode: items = 8 * n_runs)
+  int queues;               // persistent mode: 1 (one queue) or 8 (one per XCD, head g on XCD g)
   int n_req;
   int chunk;
   int tmax;                 // max blocks per request (<= 8)
@@ -661,6 +664,29 @@ struct DraftArgs {
 constexpr int BLOCK_ROWS = 7;
 constexpr int MAX_BLOCKS = 8;                        // draft blocks per request
 constexpr int CHUNK_ALIGN = 64;                      // fixed chunks are multiples of this many keys
+
+// Timeline build (compiled with DSPARK_TIMELINE into a separate profiling
+// library; the product library has none of this): lane 0 of wave 0 of every
+// draft workgroup records, per segment it runs, the 100 MHz constant clock
+// at the segment's start, once its first ring loads are issued, once the
+// first context stage (or the own rows) has landed, at the end of the key
+// stream and after the half merge and output write, plus where it ran.  The
+// stamps are held in scalar registers and stored after the segment's write,
+// so the ring's load accounting sees no extra memory operation.
+#ifdef DSPARK_TIMELINE
+constexpr int TL_WGS = 8192;                         // workgroups recorded
+constexpr int TL_ITEMS = 16;                         // segments recorded per workgroup
+constexpr int TL_WORDS = 8;
+__device__ uint64_t tl_stamps[TL_WGS * TL_ITEMS * TL_WORDS];
+// Persistent mode, per workgroup: entry, first ticket known, loop left, exit.
+__device__ uint64_t tl_wg[TL_WGS * 4];
+__device__ __forceinline__ uint64_t tl_now() { return __builtin_amdgcn_s_memrealtime(); }
+#define TL_DECL uint64_t tl_t[5] = {0, 0, 0, 0, 0};
+#define TL_MARK(i) (tl_t[i] = tl_now())
+#else
+#define TL_DECL
+#define TL_MARK(i) ((void)0)
+#endif
 
 // One context segment of one request: keys [k0, k1) of request r (whose
 // blocks are b0 .. b0+nb, largest anchor amax).  The segment ending the
@@ -924,6 +950,16 @@ __device__ __forceinline__ void settle(const T&... x) {
   (settle_one(x), ...);
 }
 
+// atomicAdd whose result is read much later: the address carries an
+// opaque zero offset, so the compiler issues one plain atomic for the
+// calling lanes instead of a wave-aggregated one, whose result it would wait
+// for right away.
+__device__ __forceinline__ int atomic_add_deferred(int* p, int v) {
+  int z;
+  asm volatile("v_mov_b32 %0, 0" : "=v"(z));
+  return atomicAdd(p + z, v);
+}
+
 // Wave w of the workgroup attends blocks 2(w/2) and 2(w/2)+1 of the
 // segment's request over key half w%2 of every stage.  INDEXED: context
 // rows come through a per-request physical index vector (the append-order
@@ -933,11 +969,18 @@ __device__ __forceinline__ void settle(const T&... x) {
 // No early return: every wave reaches the end, so that the caller may place
 // workgroup barriers between items.
 template <bool INDEXED, bool KF32>
-__device__ __forceinline__ void draft_pair_item(const DraftArgs& a, unsigned char* smem, const DraftSeg& sg, int g) {
+__device__ __forceinline__ void draft_pair_item(const DraftArgs& a, unsigned char* smem, const DraftSeg& sg, int g,
+                                                int item, int* ticket_ctr = nullptr, int* ticket_out = nullptr,
+                                                int tid = -1) {
   using R = PairRing<KF32>;
+  TL_DECL
+  TL_MARK(0);
   constexpr int KEL = KF32 ? 4 : 2;                 // bytes per K element
-  const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  // The thread index: threadIdx.x, or a copy the persistent loop makes
+  // opaque per item, so that nothing derived from it is kept live across items.
+  if (tid < 0) tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int pw = wave >> 1;                         // block pair
   const int kh = wave & 1;                          // key half of each stage
   const int hh = lane >> 5;
@@ -1052,6 +1095,14 @@ __device__ __forceinline__ void draft_pair_item(const DraftArgs& a, unsigned cha
   // stores have completed), so it places no vmcnt wait of its own among the
   // ring's direct-to-LDS loads below.
   __builtin_amdgcn_s_waitcnt(0x0f70);   // vmcnt(0)
+  // Persistent mode: the workgroup draws its next ticket after this
+  // segment's stream (a ticket drawn at the start would reserve the next
+  // item for a busy workgroup and undo the longest-first order).  Its value
+  // is read after the merge.
+  int next_ticket = 0;
+  auto draw = [&]() {
+    if (ticket_ctr && threadIdx.x == 0) next_ticket = atomic_add_deferred(ticket_ctr, 1);
+  };
   // bf16 Q rows, issued first: slot row R = 32p + n holds tile row n of
   // pair p (rows with no query read block 0, token 0 and are zeroed later).
   const uint32_t q_lds_row = smem_lds + (uint32_t)(R::Q_OFF + (32 * pw + n) * ROWB);
@@ -1102,9 +1153,11 @@ __device__ __forceinline__ void draft_pair_item(const DraftArgs& a, unsigned cha
   #pragma unroll
   for (int p = 0; p < R::STAGES - 1; ++p)
     if (p < prologue) issue(p);
+  TL_MARK(1);
   if (last) {
     wait_stages(prologue);   // the Q and own rows, issued first, have landed
     asm volatile("s_barrier" ::: "memory");
+    TL_MARK(2);
     if (q_lds) read_q();
     if (active && kh == 0) {
       // Register r of a lane in half hh holds block (r/4)%2 of the pair,
@@ -1133,15 +1186,24 @@ __device__ __forceinline__ void draft_pair_item(const DraftArgs& a, unsigned cha
     // Every thread issues exactly PER_WAVE loads per context stage, so at
     // the top of step s the stages issued after stage s number
     // min(n_steps - 1 - s, STAGES - 2).
-    for (int s = 0; s < n_steps; ++s) {
+    auto step = [&](int s) {
       wait_stages(min(n_steps - 1 - s, R::STAGES - 2));
       asm volatile("s_barrier" ::: "memory");
+#ifdef DSPARK_TIMELINE
+      if (s == 0 && !last) TL_MARK(2);
+#endif
       if (s == 0 && q_lds && !last) read_q();
       if (s + R::STAGES - 1 < n_steps) issue(s + R::STAGES - 1);
       if (active) compute(s);
-    }
+    };
+    for (int s = 0; s < n_steps; ++s) step(s);
   }
+  // The next ticket is drawn when the stream ends, so that its round trip
+  // overlaps the merge below (a draw inside the stream loop, right after the
+  // ring's last stage load, made the compiler spill the loop's registers).
+  draw();
   asm volatile("s_barrier" ::: "memory");   // every wave is done with the ring and the own rows
+  TL_MARK(3);
 
   // The key halves merge: the kh = 1 wave of each pair leaves its state in
   // the drained ring (register-major, lane-minor), the kh = 0 wave folds it
@@ -1204,12 +1266,111 @@ __device__ __forceinline__ void draft_pair_item(const DraftArgs& a, unsigned cha
       }
     }
   }
+  if (ticket_ctr && threadIdx.x == 0) *ticket_out = next_ticket;
+#ifdef DSPARK_TIMELINE
+  TL_MARK(4);
+  if (threadIdx.x == 0 && blockIdx.x < TL_WGS && item < TL_ITEMS) {
+    uint32_t hw, xcc;
+    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_HW_ID)" : "=s"(hw));
+    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
+    uint64_t* t = tl_stamps + ((size_t)blockIdx.x * TL_ITEMS + item) * TL_WORDS;
+    #pragma unroll
+    for (int i = 0; i < 5; ++i) t[i] = tl_t[i];
+    t[5] = (uint64_t)hw | ((uint64_t)(xcc & 15) << 32) | ((uint64_t)1 << 63);
+    t[6] = (uint64_t)(uint32_t)r | ((uint64_t)(uint32_t)(k1 - k0) << 32);
+    t[7] = (uint64_t)(uint32_t)nb | ((uint64_t)(uint32_t)n_steps << 16) | ((uint64_t)(last ? 1 : 0) << 32) |
+           ((uint64_t)(uint32_t)(pslot >= 0) << 33);
+  }
+#else
+  (void)item;
+#endif
 }
 
 // With a work list, workgroup (run w, KV head g) runs the segments of run w
 // (blockIdx.x = 8w + g).  Without one, workgroup (chunk, KV head) runs one
 // fixed chunk of `chunk` context rows, chunks in request order.  Every
 // branch is uniform across the workgroup.
+// One segment record of the work list.
+__device__ __forceinline__ DraftSeg draft_seg(const DraftArgs& a, int i) {
+  int w[WORK_INTS];
+  #pragma unroll
+  for (int j = 0; j < WORK_INTS; ++j) w[j] = ld_const(a.work + WORK_INTS * i + j);
+  return DraftSeg{w[0], w[1], w[2], w[3], w[4], w[5], w[6], w[2] >= w[6], w[7]};
+}
+
+// Persistent mode (a.queue): the grid is a fixed set of workgroups (one per
+// CU) that take items - (run, KV head) pairs of a plan with one segment per
+// run, runs in list order - from device ticket counters, so a CU starts its
+// next item as soon as it is done instead of waiting for the hardware
+// dispatcher.  A workgroup draws its next ticket once the current segment
+// has issued its last ring load (draft_pair_item).  With one queue, ticket t
+// is run t / 8, head t % 8; with a queue per XCD, workgroup b serves head
+// b % 8 (its XCD when workgroups are dealt round-robin) and ticket t of that
+// queue is run t.  Counter layout per queue: {next ticket, workgroups done}.
+// The last workgroup of a queue to finish sets both back to zero, so every
+// launch finds them zero (the caller zeroes them once, at allocation).  The
+// only state carried from item to item is the ticket: the item itself runs
+// at the register limit of two waves per SIMD.
+template <bool INDEXED, bool KF32>
+__device__ __forceinline__ void draft_persistent(const DraftArgs& a, unsigned char* smem) {
+  __shared__ int ticket_sh;
+  const bool per_head = a.queues == 8;
+  int* ctr = a.queue + (per_head ? 2 * (int)(blockIdx.x & 7) : 0);
+#ifdef DSPARK_TIMELINE
+  const uint64_t tl_entry = tl_now();
+#endif
+  if (threadIdx.x == 0) ticket_sh = atomicAdd(ctr, 1);
+  __syncthreads();
+  int t = __builtin_amdgcn_readfirstlane(ticket_sh);
+#ifdef DSPARK_TIMELINE
+  const uint64_t tl_first = tl_now();
+  int item = 0;
+#else
+  constexpr int item = 0;
+#endif
+  while (t < (per_head ? a.n_work : 8 * a.n_work)) {
+    const int run = per_head ? t : t >> 3;
+    const int g = per_head ? (int)(blockIdx.x & 7) : (t & 7);
+    int tid;
+    asm volatile("v_mov_b32 %0, %1" : "=v"(tid) : "v"((int)threadIdx.x));
+    draft_pair_item<INDEXED, KF32>(a, smem, draft_seg(a, run), g, item, ctr, &ticket_sh, tid);
+#ifdef DSPARK_TIMELINE
+    ++item;
+#endif
+    __syncthreads();   // the next segment refills the ring the last one read; publishes ticket_sh
+    t = __builtin_amdgcn_readfirstlane(ticket_sh);
+    __syncthreads();   // every thread has read ticket_sh before it is written again
+  }
+#ifdef DSPARK_TIMELINE
+  const uint64_t tl_left = tl_now();
+#endif
+  if (threadIdx.x == 0) {
+    const int q = per_head ? (int)(blockIdx.x & 7) : 0;
+    const int members = per_head ? (int)(gridDim.x >> 3) + ((int)(gridDim.x & 7) > q ? 1 : 0) : (int)gridDim.x;
+    const int finished = atomicAdd(ctr + 1, 1);
+    if (finished == members - 1) {   // every member has drawn its last ticket: reset for the next launch
+      atomicExch(ctr, 0);
+      atomicExch(ctr + 1, 0);
+    }
+#ifdef DSPARK_TIMELINE
+    if (blockIdx.x < TL_WGS) {
+      uint64_t* w = tl_wg + 4 * (size_t)blockIdx.x;
+      w[0] = tl_entry;
+      w[1] = tl_first;
+      w[2] = tl_left;
+      w[3] = tl_now() | ((uint64_t)1 << 63);
+    }
+#endif
+  }
+}
+
+template <bool INDEXED, bool KF32>
+__global__ __launch_bounds__(DWAVES * WAVE) void draft_attn_persistent_kernel(DraftArgs a) {
+  // 1 KiB alignment: tile offsets are XORed into LDS addresses.
+  __shared__ __attribute__((aligned(1024))) unsigned char smem[PairRing<KF32>::SMEM];
+  draft_persistent<INDEXED, KF32>(a, smem);
+}
+
 template <bool INDEXED, bool KF32>
 __global__ __launch_bounds__(DWAVES * WAVE) void draft_attn_kernel(DraftArgs a) {
   // 1 KiB alignment: tile offsets are XORed into LDS addresses.
@@ -1232,7 +1393,7 @@ __global__ __launch_bounds__(DWAVES * WAVE) void draft_attn_kernel(DraftArgs a) 
         for (int j = 0; j < WORK_INTS; ++j) w[j] = ld_const(a.work + WORK_INTS * i + j);
       }
       const DraftSeg sg{w[0], w[1], w[2], w[3], w[4], w[5], w[6], w[2] >= w[6], w[7]};
-      draft_pair_item<INDEXED, KF32>(a, smem, sg, g);
+      draft_pair_item<INDEXED, KF32>(a, smem, sg, g, i - lo);
       __syncthreads();   // the next segment refills the ring the last one read
     }
     return;
@@ -1249,7 +1410,7 @@ __global__ __launch_bounds__(DWAVES * WAVE) void draft_attn_kernel(DraftArgs a) 
   for (int b = 0; b < nb; ++b) amax = max(amax, a.anchors[b0 + b]);
   const DraftSeg sg{r, c * a.chunk, min(c * a.chunk + a.chunk, ctx), nch > 1 ? first + c : -1, b0, nb, amax,
                     c == nch - 1, 0};
-  draft_pair_item<INDEXED, KF32>(a, smem, sg, g);
+  draft_pair_item<INDEXED, KF32>(a, smem, sg, g, 0);
 }
 
 // ---------------------------------------------------------------------------
@@ -1621,10 +1782,16 @@ extern "C" int dspark_draft_attn_fwd(const void* q, int q_dtype, const void* k_c
                                      const int32_t* cu_blocks, const int32_t* anchors,
                                      int n_req, int64_t ctx_rows_bound, int max_blocks, float scale, int chunk,
                                      const int32_t* work, int n_work, int n_groups,
+                                     int workgroups, int queues, int32_t* queue,
                                      void* out, void* workspace, int64_t workspace_bytes_, void* stream) {
   clear_error();
   DSPARK_REQUIRE(q && k_ctx && v_ctx && ctx_off && ctx_len && k_blk && v_blk && cu_blocks && anchors && out,
                  "null pointer argument");
+  DSPARK_REQUIRE(workgroups == 0 || (work && queue && aligned16(queue) && (queues == 1 || queues == 8) &&
+                                     workgroups >= 8 && workgroups % 8 == 0 && workgroups <= (1 << 16) &&
+                                     n_work == n_groups),
+                 "persistent mode needs a work list of one segment per run, a 16-byte aligned queue buffer, "
+                 "queues 1 or 8 and workgroups a multiple of 8 in [8, 65536]");
   DSPARK_REQUIRE(aligned16(q) && aligned16(k_ctx) && aligned16(v_ctx) && aligned16(k_blk) && aligned16(v_blk) && aligned16(out),
                  "Q/K/V/out must be 16-byte aligned");
   DSPARK_REQUIRE(tok_stride >= HD && tok_stride % 8 == 0 && head_stride >= HD && head_stride % 8 == 0,
@@ -1663,16 +1830,28 @@ extern "C" int dspark_draft_attn_fwd(const void* q, int q_dtype, const void* k_c
   a.tok_stride = tok_stride;
   a.head_stride = head_stride;
   a.work = work;
+  a.queue = workgroups ? queue : nullptr;
   a.n_work = n_work;
+  a.n_runs = n_groups;
+  a.queues = queues;
   a.n_req = n_req;
   a.chunk = chunk;
   a.tmax = max_blocks;
   a.scale_log2 = scale * LOG2E;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  const int64_t grid = work ? (int64_t)n_groups * HKV : n_cl * HKV;
+  const int64_t grid = workgroups ? (int64_t)workgroups : work ? (int64_t)n_groups * HKV : n_cl * HKV;
   DSPARK_REQUIRE(grid <= 0x7fffffffLL, "grid too large");
   const dim3 blocks((unsigned)grid), threads(DWAVES * WAVE);
-  if (ctx_idx && k_dtype)
+  if (workgroups) {
+    if (ctx_idx && k_dtype)
+      hipLaunchKernelGGL((draft_attn_persistent_kernel<true, true>), blocks, threads, 0, s, a);
+    else if (ctx_idx)
+      hipLaunchKernelGGL((draft_attn_persistent_kernel<true, false>), blocks, threads, 0, s, a);
+    else if (k_dtype)
+      hipLaunchKernelGGL((draft_attn_persistent_kernel<false, true>), blocks, threads, 0, s, a);
+    else
+      hipLaunchKernelGGL((draft_attn_persistent_kernel<false, false>), blocks, threads, 0, s, a);
+  } else if (ctx_idx && k_dtype)
     hipLaunchKernelGGL((draft_attn_kernel<true, true>), blocks, threads, 0, s, a);
   else if (ctx_idx)
     hipLaunchKernelGGL((draft_attn_kernel<true, false>), blocks, threads, 0, s, a);
@@ -1686,3 +1865,39 @@ extern "C" int dspark_draft_attn_fwd(const void* q, int q_dtype, const void* k_c
               a.part_o, a.part_ml, a.out, n_req, chunk, max_blocks, 1};
   return launch_merge(m, n_req, max_blocks, s);
 }
+
+#ifdef DSPARK_TIMELINE
+// Timeline build only: copy the per-workgroup draft stamps (TL_WGS x
+// TL_ITEMS records of TL_WORDS words) to host memory, then clear them.
+// Synchronous (waits for the device).  Not part of the product ABI.
+extern "C" int dspark_timeline_fetch(void* host, int64_t bytes) {
+  clear_error();
+  const int64_t have = (int64_t)sizeof(uint64_t) * TL_WGS * TL_ITEMS * TL_WORDS;
+  DSPARK_REQUIRE(host && bytes == have, "need a host buffer of exactly %lld bytes", (long long)have);
+  DSPARK_REQUIRE(hipDeviceSynchronize() == hipSuccess, "device synchronisation failed");
+  DSPARK_REQUIRE(hipMemcpyFromSymbol(host, HIP_SYMBOL(tl_stamps), (size_t)have, 0, hipMemcpyDeviceToHost) == hipSuccess,
+                 "timeline copy failed");
+  void* dev = nullptr;
+  DSPARK_REQUIRE(hipGetSymbolAddress(&dev, HIP_SYMBOL(tl_stamps)) == hipSuccess && dev, "timeline symbol lookup failed");
+  DSPARK_REQUIRE(hipMemset(dev, 0, (size_t)have) == hipSuccess, "timeline clear failed");
+  return OK;
+}
+
+extern "C" int64_t dspark_timeline_bytes(void) {
+  return (int64_t)sizeof(uint64_t) * TL_WGS * TL_ITEMS * TL_WORDS;
+}
+
+// The persistent-mode workgroup stamps (TL_WGS x 4 words), then cleared.
+extern "C" int dspark_timeline_fetch_wg(void* host, int64_t bytes) {
+  clear_error();
+  const int64_t have = (int64_t)sizeof(uint64_t) * TL_WGS * 4;
+  DSPARK_REQUIRE(host && bytes == have, "need a host buffer of exactly %lld bytes", (long long)have);
+  DSPARK_REQUIRE(hipDeviceSynchronize() == hipSuccess, "device synchronisation failed");
+  DSPARK_REQUIRE(hipMemcpyFromSymbol(host, HIP_SYMBOL(tl_wg), (size_t)have, 0, hipMemcpyDeviceToHost) == hipSuccess,
+                 "timeline copy failed");
+  void* dev = nullptr;
+  DSPARK_REQUIRE(hipGetSymbolAddress(&dev, HIP_SYMBOL(tl_wg)) == hipSuccess && dev, "timeline symbol lookup failed");
+  DSPARK_REQUIRE(hipMemset(dev, 0, (size_t)have) == hipSuccess, "timeline clear failed");
+  return OK;
+}
+#endif

@@ -192,15 +192,30 @@ class HipDraftAttention:
     backend_name = backends.DRAFT_BLOCKS_BACKEND
     native_varlen_calls_per_layer = 1
 
-    def __init__(self, device, *, chunk=DRAFT_CHUNK, runs=None):
+    def __init__(self, device, *, chunk=DRAFT_CHUNK, runs=None, persistent=1):
+        """persistent: 1 (the default) or 8 for one persistent workgroup per CU
+        taking (chunk, KV head) items, longest chunks first, from one device
+        queue or from one queue per KV head (head g on XCD g); None for one
+        workgroup per (run, KV head) dispatched by the hardware (the only
+        form for balanced runs).  Outputs are bitwise the same in every
+        mode.  One object's launches must not overlap (they share its ticket
+        counters): use it from one stream."""
         self.device = require_gfx950(device)
         _native.load()
         if chunk % 64:
             raise ValueError('Draft chunk must be a multiple of 64')
         if runs is not None and (type(runs) is not int or runs < 0):
             raise ValueError('runs must be None (fixed chunks) or a nonnegative integer (balanced runs)')
+        if persistent not in (None, 1, 8):
+            raise ValueError('persistent must be None, 1 or 8 (queues)')
+        if runs is not None and persistent is not None:
+            raise ValueError('balanced runs (runs=...) need persistent=None')
         self.chunk = int(chunk)
         self.runs = runs            # None: fixed chunks; else balanced runs per KV head (0: one per CU)
+        self.persistent = persistent
+        # Ticket counters of the persistent mode: zero now, zero again after every launch.
+        self._queue = torch.zeros(16, dtype=torch.int32, device=self.device) if persistent else None
+        self._workgroups = -(-cu_count(self.device) // 8) * 8 if persistent else 0
         self._workspace = Workspace(self.device)
         self._geometry_for = None
         self._geometry = None
@@ -273,6 +288,7 @@ class HipDraftAttention:
                      tok_stride, head_stride, _native.ptr(block_keys), _native.ptr(block_values),
                      _native.ptr(batch.cu_blocks), _native.ptr(batch.anchor_rows), batch.request_count, bound,
                      batch.max_blocks, float(SCALE), self.chunk, _native.ptr(work), n_work, n_runs,
+                     self._workgroups, self.persistent or 0, _native.ptr(self._queue),
                      _native.ptr(out), _native.ptr(ws), ws.numel(), _native.stream_handle(self.device))
         return out
 
