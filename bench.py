@@ -253,6 +253,7 @@ def main():
     def round_(step, timed):
         ctx_now = [pool.length(h) for h in handles]
         batch = DraftBatch(dev, draft_offsets, contexts, anchors)
+        draft.plan(batch, dctx_k[0])      # the round's draft plan, prepared like begin() for verification
         outs = []
         if timed:
             d0, d1 = events()

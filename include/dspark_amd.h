@@ -207,8 +207,11 @@ int dspark_verify_attn_staged_fwd(const void* q, const void* k_res, const void* 
  * queues = 8 gives each KV head its own queue served by workgroups
  * b = head (mod 8).  queue holds 2 int32 per queue, must be zero before the
  * first call and is zero again after every call (the last workgroup resets
- * it); calls sharing one queue buffer must not overlap.  Outputs do not
- * depend on the mode.
+ * it); calls sharing one queue buffer must not overlap.  The persistent
+ * mode needs a work list of one segment per run (n_work == n_groups) and
+ * seg_anchors: 8 int32 per segment record, the anchors of the record's
+ * blocks b0 .. b0+nb-1 then any padding (16-byte aligned; NULL otherwise).
+ * Outputs do not depend on the mode.
  */
 int dspark_draft_attn_fwd(const void* q, int q_dtype, const void* k_ctx, const void* v_ctx,
                           int k_dtype, const int64_t* ctx_idx, const int64_t* ctx_off,
@@ -217,7 +220,7 @@ int dspark_draft_attn_fwd(const void* q, int q_dtype, const void* k_ctx, const v
                           const int32_t* cu_blocks, const int32_t* anchors,
                           int n_req, int64_t ctx_rows_bound, int max_blocks, float scale, int chunk,
                           const int32_t* work, int n_work, int n_groups,
-                          int workgroups, int queues, int32_t* queue,
+                          int workgroups, int queues, int32_t* queue, const int32_t* seg_anchors,
                           void* out, void* workspace, int64_t workspace_bytes, void* stream);
 
 /*

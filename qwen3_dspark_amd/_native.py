@@ -35,7 +35,7 @@ SIGNATURES = {
     'dspark_verify_attn_staged_fwd': (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _L, _L, _L, _L, _I, _F, _I,
                                            _P, _I, _I, _P, _P, _L, _P]),
     'dspark_draft_attn_fwd': (_I, [_P, _I, _P, _P, _I, _P, _P, _P, _L, _L, _P, _P, _P, _P, _I, _L, _I, _F, _I, _P,
-                                   _I, _I, _I, _I, _P, _P, _P, _L, _P]),
+                                   _I, _I, _I, _I, _P, _P, _P, _P, _L, _P]),
     'dspark_txn_metadata': (_I, [_P, _I, _L, _L, _L, _P, _P, _P, _P, _P, _P, _P, _P]),
     'dspark_kv_stage': (_I, [_P, _P, _P, _P, _L, _L, _P]),
     'dspark_kv_commit': (_I, [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _L, _L, _L, _L, _L, _I, _L, _L, _P]),

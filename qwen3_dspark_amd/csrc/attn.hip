@@ -650,7 +650,8 @@ struct DraftArgs {
   int64_t tok_stride;
   int64_t head_stride;
   const int32_t* work;      // optional segment list (see the C ABI)
-  int* queue;               // persistent mode: ticket counters (self-resetting; see draft_attn_kernel)
+  int* queue;               // persistent mode: ticket counters (self-resetting; see draft_persistent)
+  const int32_t* seg_anc;   // persistent mode: 8 anchors per segment record (its blocks', padded)
   int n_work;               // segment records in the work list
   int n_runs;               // runs of the work list (persistent mode: items = 8 * n_runs)
   int queues;               // persistent mode: 1 (one queue) or 8 (one per XCD, head g on XCD g)
@@ -950,6 +951,33 @@ __device__ __forceinline__ void settle(const T&... x) {
   (settle_one(x), ...);
 }
 
+// The persistent loop's next item, staged in LDS: ticket, segment record,
+// 8 anchors.
+constexpr int NXT_REC = 1;
+constexpr int NXT_ANC = 1 + WORK_INTS;
+constexpr int NXT_INTS = 1 + WORK_INTS + 8;
+
+__device__ __forceinline__ int persistent_items(const DraftArgs& a) {
+  return a.queues == 8 ? a.n_work : 8 * a.n_work;
+}
+
+__device__ __forceinline__ int persistent_run(const DraftArgs& a, int t) { return a.queues == 8 ? t : t >> 3; }
+
+// Called by one lane: stage ticket t and, if it names an item, that item's
+// record and anchors (plain vector loads; the lane waits for them).
+__device__ __forceinline__ void stage_next(const DraftArgs& a, int* nxt, int t) {
+  nxt[0] = t;
+  if (t < persistent_items(a)) {
+    const int run = persistent_run(a, t);
+    const int4* rec = reinterpret_cast<const int4*>(a.work + WORK_INTS * run);
+    const int4* anc = reinterpret_cast<const int4*>(a.seg_anc + 8 * run);
+    const int4 r0 = rec[0], r1 = rec[1], a0 = anc[0], a1 = anc[1];
+    const int v[16] = {r0.x, r0.y, r0.z, r0.w, r1.x, r1.y, r1.z, r1.w, a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+    #pragma unroll
+    for (int j = 0; j < 16; ++j) nxt[NXT_REC + j] = v[j];
+  }
+}
+
 // atomicAdd whose result is read much later: the address carries an
 // opaque zero offset, so the compiler issues one plain atomic for the
 // calling lanes instead of a wave-aggregated one, whose result it would wait
@@ -970,7 +998,7 @@ __device__ __forceinline__ int atomic_add_deferred(int* p, int v) {
 // workgroup barriers between items.
 template <bool INDEXED, bool KF32>
 __device__ __forceinline__ void draft_pair_item(const DraftArgs& a, unsigned char* smem, const DraftSeg& sg, int g,
-                                                int item, int* ticket_ctr = nullptr, int* ticket_out = nullptr,
+                                                int item, int* ticket_ctr = nullptr, int* nxt = nullptr,
                                                 int tid = -1) {
   using R = PairRing<KF32>;
   TL_DECL
@@ -1001,8 +1029,12 @@ __device__ __forceinline__ void draft_pair_item(const DraftArgs& a, unsigned cha
   const bool row_ok = blk < nb && tok < BLOCK_ROWS;
   // Context rows visible to each block of the pair (a missing second block
   // copies the first's, so that the pair's limits are the first block's).
-  const int anc0 = active ? min(ld_const(a.anchors + b0 + 2 * pw), k1) : 0;
-  const int anc1 = 2 * pw + 1 < nb ? min(ld_const(a.anchors + b0 + 2 * pw + 1), k1) : anc0;
+  // Persistent mode: the segment's anchors were staged in LDS with its record.
+  auto anchor = [&](int j) {
+    return nxt ? __builtin_amdgcn_readfirstlane(nxt[NXT_ANC + j]) : ld_const(a.anchors + b0 + j);
+  };
+  const int anc0 = active ? min(anchor(2 * pw), k1) : 0;
+  const int anc1 = 2 * pw + 1 < nb ? min(anchor(2 * pw + 1), k1) : anc0;
   const int vis = row_ok ? (bi ? anc1 : anc0) : 0;
   const int pair_hi = max(anc0, anc1);              // keys at or past this are seen by neither block
   const int full_lim = min(min(anc0, anc1), kend);  // keys below this need no mask
@@ -1095,13 +1127,15 @@ __device__ __forceinline__ void draft_pair_item(const DraftArgs& a, unsigned cha
   // stores have completed), so it places no vmcnt wait of its own among the
   // ring's direct-to-LDS loads below.
   __builtin_amdgcn_s_waitcnt(0x0f70);   // vmcnt(0)
-  // Persistent mode: the workgroup draws its next ticket after this
-  // segment's stream (a ticket drawn at the start would reserve the next
-  // item for a busy workgroup and undo the longest-first order).  Its value
-  // is read after the merge.
+  // Persistent mode: lane 0 of wave 1 (a key-half-1 wave, idle once it has
+  // handed its state to the merge) draws the workgroup's next ticket when
+  // this segment's stream ends (a ticket drawn at the start would reserve
+  // the next item for a busy workgroup and undo the longest-first order),
+  // then, during the merge, stages that item's record and anchors in LDS.
+  const bool fetcher = ticket_ctr && tid == WAVE;
   int next_ticket = 0;
   auto draw = [&]() {
-    if (ticket_ctr && threadIdx.x == 0) next_ticket = atomic_add_deferred(ticket_ctr, 1);
+    if (fetcher) next_ticket = atomic_add_deferred(ticket_ctr, 1);
   };
   // bf16 Q rows, issued first: slot row R = 32p + n holds tile row n of
   // pair p (rows with no query read block 0, token 0 and are zeroed later).
@@ -1219,6 +1253,7 @@ __device__ __forceinline__ void draft_pair_item(const DraftArgs& a, unsigned cha
   }
   asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
   __syncthreads();
+  if (fetcher) stage_next(a, nxt, next_ticket);
   if (active && kh == 0) {
     const float m1 = mb[64 * WAVE + lane];
     const float l1 = mb[65 * WAVE + lane];
@@ -1266,7 +1301,6 @@ __device__ __forceinline__ void draft_pair_item(const DraftArgs& a, unsigned cha
       }
     }
   }
-  if (ticket_ctr && threadIdx.x == 0) *ticket_out = next_ticket;
 #ifdef DSPARK_TIMELINE
   TL_MARK(4);
   if (threadIdx.x == 0 && blockIdx.x < TL_WGS && item < TL_ITEMS) {
@@ -1290,56 +1324,56 @@ __device__ __forceinline__ void draft_pair_item(const DraftArgs& a, unsigned cha
 // (blockIdx.x = 8w + g).  Without one, workgroup (chunk, KV head) runs one
 // fixed chunk of `chunk` context rows, chunks in request order.  Every
 // branch is uniform across the workgroup.
-// One segment record of the work list.
-__device__ __forceinline__ DraftSeg draft_seg(const DraftArgs& a, int i) {
-  int w[WORK_INTS];
-  #pragma unroll
-  for (int j = 0; j < WORK_INTS; ++j) w[j] = ld_const(a.work + WORK_INTS * i + j);
-  return DraftSeg{w[0], w[1], w[2], w[3], w[4], w[5], w[6], w[2] >= w[6], w[7]};
-}
 
 // Persistent mode (a.queue): the grid is a fixed set of workgroups (one per
 // CU) that take items - (run, KV head) pairs of a plan with one segment per
 // run, runs in list order - from device ticket counters, so a CU starts its
 // next item as soon as it is done instead of waiting for the hardware
-// dispatcher.  A workgroup draws its next ticket once the current segment
-// has issued its last ring load (draft_pair_item).  With one queue, ticket t
-// is run t / 8, head t % 8; with a queue per XCD, workgroup b serves head
-// b % 8 (its XCD when workgroups are dealt round-robin) and ticket t of that
-// queue is run t.  Counter layout per queue: {next ticket, workgroups done}.
-// The last workgroup of a queue to finish sets both back to zero, so every
-// launch finds them zero (the caller zeroes them once, at allocation).  The
-// only state carried from item to item is the ticket: the item itself runs
-// at the register limit of two waves per SIMD.
+// dispatcher.  A workgroup draws its next ticket when the current segment's
+// stream ends and stages the next item's record and anchors in LDS while
+// the current one merges (draft_pair_item), so an item starts without a
+// memory round trip.  With one queue, ticket t is run t / 8, head t % 8;
+// with a queue per XCD, workgroup b serves head b % 8 (its XCD when
+// workgroups are dealt round-robin) and ticket t of that queue is run t.
+// Counter layout per queue: {next ticket, workgroups done}.  The last
+// workgroup of a queue to finish sets both back to zero, so every launch
+// finds them zero (the caller zeroes them once, at allocation).  Between
+// items the workgroup keeps no state in registers (the item runs at the
+// register limit of two waves per SIMD), and each item gets an opaque copy
+// of the thread index so that nothing derived from it stays live across
+// items.
 template <bool INDEXED, bool KF32>
 __device__ __forceinline__ void draft_persistent(const DraftArgs& a, unsigned char* smem) {
-  __shared__ int ticket_sh;
+  static_assert(WORK_INTS == 8, "the staged record is 8 words");
+  __shared__ int nxt[NXT_INTS];
   const bool per_head = a.queues == 8;
   int* ctr = a.queue + (per_head ? 2 * (int)(blockIdx.x & 7) : 0);
 #ifdef DSPARK_TIMELINE
   const uint64_t tl_entry = tl_now();
 #endif
-  if (threadIdx.x == 0) ticket_sh = atomicAdd(ctr, 1);
+  if (threadIdx.x == WAVE) stage_next(a, nxt, atomicAdd(ctr, 1));
   __syncthreads();
-  int t = __builtin_amdgcn_readfirstlane(ticket_sh);
 #ifdef DSPARK_TIMELINE
   const uint64_t tl_first = tl_now();
   int item = 0;
 #else
   constexpr int item = 0;
 #endif
-  while (t < (per_head ? a.n_work : 8 * a.n_work)) {
-    const int run = per_head ? t : t >> 3;
+  for (;;) {
+    const int t = __builtin_amdgcn_readfirstlane(nxt[0]);
+    if (t >= persistent_items(a)) break;
+    int w[WORK_INTS];
+    #pragma unroll
+    for (int j = 0; j < WORK_INTS; ++j) w[j] = __builtin_amdgcn_readfirstlane(nxt[NXT_REC + j]);
+    const DraftSeg sg{w[0], w[1], w[2], w[3], w[4], w[5], w[6], w[2] >= w[6], w[7]};
     const int g = per_head ? (int)(blockIdx.x & 7) : (t & 7);
     int tid;
     asm volatile("v_mov_b32 %0, %1" : "=v"(tid) : "v"((int)threadIdx.x));
-    draft_pair_item<INDEXED, KF32>(a, smem, draft_seg(a, run), g, item, ctr, &ticket_sh, tid);
+    draft_pair_item<INDEXED, KF32>(a, smem, sg, g, item, ctr, nxt, tid);
 #ifdef DSPARK_TIMELINE
     ++item;
 #endif
-    __syncthreads();   // the next segment refills the ring the last one read; publishes ticket_sh
-    t = __builtin_amdgcn_readfirstlane(ticket_sh);
-    __syncthreads();   // every thread has read ticket_sh before it is written again
+    __syncthreads();   // the next segment refills the ring the last one read; publishes nxt
   }
 #ifdef DSPARK_TIMELINE
   const uint64_t tl_left = tl_now();
@@ -1354,11 +1388,11 @@ __device__ __forceinline__ void draft_persistent(const DraftArgs& a, unsigned ch
     }
 #ifdef DSPARK_TIMELINE
     if (blockIdx.x < TL_WGS) {
-      uint64_t* w = tl_wg + 4 * (size_t)blockIdx.x;
-      w[0] = tl_entry;
-      w[1] = tl_first;
-      w[2] = tl_left;
-      w[3] = tl_now() | ((uint64_t)1 << 63);
+      uint64_t* wg = tl_wg + 4 * (size_t)blockIdx.x;
+      wg[0] = tl_entry;
+      wg[1] = tl_first;
+      wg[2] = tl_left;
+      wg[3] = tl_now() | ((uint64_t)1 << 63);
     }
 #endif
   }
@@ -1782,16 +1816,17 @@ extern "C" int dspark_draft_attn_fwd(const void* q, int q_dtype, const void* k_c
                                      const int32_t* cu_blocks, const int32_t* anchors,
                                      int n_req, int64_t ctx_rows_bound, int max_blocks, float scale, int chunk,
                                      const int32_t* work, int n_work, int n_groups,
-                                     int workgroups, int queues, int32_t* queue,
+                                     int workgroups, int queues, int32_t* queue, const int32_t* seg_anchors,
                                      void* out, void* workspace, int64_t workspace_bytes_, void* stream) {
   clear_error();
   DSPARK_REQUIRE(q && k_ctx && v_ctx && ctx_off && ctx_len && k_blk && v_blk && cu_blocks && anchors && out,
                  "null pointer argument");
-  DSPARK_REQUIRE(workgroups == 0 || (work && queue && aligned16(queue) && (queues == 1 || queues == 8) &&
-                                     workgroups >= 8 && workgroups % 8 == 0 && workgroups <= (1 << 16) &&
-                                     n_work == n_groups),
-                 "persistent mode needs a work list of one segment per run, a 16-byte aligned queue buffer, "
-                 "queues 1 or 8 and workgroups a multiple of 8 in [8, 65536]");
+  DSPARK_REQUIRE(workgroups == 0 || (work && aligned16(work) && queue && aligned16(queue) && seg_anchors &&
+                                     aligned16(seg_anchors) && (queues == 1 || queues == 8) && workgroups >= 8 &&
+                                     workgroups % 8 == 0 && workgroups <= (1 << 16) && n_work == n_groups),
+                 "persistent mode needs a 16-byte aligned work list of one segment per run with its segment "
+                 "anchors, a 16-byte aligned queue buffer, queues 1 or 8 and workgroups a multiple of 8 in "
+                 "[8, 65536]");
   DSPARK_REQUIRE(aligned16(q) && aligned16(k_ctx) && aligned16(v_ctx) && aligned16(k_blk) && aligned16(v_blk) && aligned16(out),
                  "Q/K/V/out must be 16-byte aligned");
   DSPARK_REQUIRE(tok_stride >= HD && tok_stride % 8 == 0 && head_stride >= HD && head_stride % 8 == 0,
@@ -1831,6 +1866,7 @@ extern "C" int dspark_draft_attn_fwd(const void* q, int q_dtype, const void* k_c
   a.head_stride = head_stride;
   a.work = work;
   a.queue = workgroups ? queue : nullptr;
+  a.seg_anc = seg_anchors;
   a.n_work = n_work;
   a.n_runs = n_groups;
   a.queues = queues;

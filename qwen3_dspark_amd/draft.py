@@ -153,11 +153,14 @@ class DraftBatch:
         return self._offsets[capacity]
 
     def work(self, chunk, runs=None, capacity=None):
-        """(device list, segment count, run count) of the draft plan: fixed
-        chunks longest first (runs None), or `runs` balanced runs per KV head
-        (0: one per CU).  With a pool capacity (0: flat rows) the segment
-        records also carry each request's kernel offset.  Uploaded once per
-        plan."""
+        """(device list, segment count, run count, segment anchors) of the
+        draft plan: fixed chunks longest first (runs None), or `runs`
+        balanced runs per KV head (0: one per CU).  With a pool capacity (0:
+        flat rows) the segment records also carry each request's kernel
+        offset.  Segment anchors (fixed-chunk plans, for the persistent
+        kernel): 8 int32 per segment record, the anchors of its request's
+        blocks, zero-padded, in the same upload at a 16-byte boundary (None
+        for balanced runs).  Uploaded once per plan."""
         key = (chunk, runs, capacity)
         if key not in self._work:
             flat = [a for b in self.anchors for a in b]
@@ -168,7 +171,16 @@ class DraftBatch:
                 runs = runs or draft_run_count(sum(max(b) for b in self.anchors), cu_count(self.device))
                 plan = draft_work(self.context_lengths, self.cu_blocks_host, flat, runs, offsets=offs)
             records, n_seg, n_runs = plan
-            self._work[key] = (upload_work(records, self.device), n_seg, n_runs)
+            records = list(records)
+            anchor_at = None
+            if runs is None:
+                records += [0] * (-len(records) % 4)           # the anchor table starts 16-byte aligned
+                anchor_at = len(records)
+                for i in range(n_seg):
+                    b0, nb = records[8 * i + 4], records[8 * i + 5]
+                    records += flat[b0:b0 + nb] + [0] * (8 - nb)
+            dev = upload_work(records, self.device)
+            self._work[key] = (dev, n_seg, n_runs, None if anchor_at is None else dev[anchor_at:])
         return self._work[key]
 
     def index_max(self):
@@ -243,6 +255,23 @@ class HipDraftAttention:
             return cap, HEAD_DIM, cap * HEAD_DIM
         raise ValueError('Context K/V must be [rows,8,128], [slots,8,capacity,128] or [1,8,N,128]')
 
+    def plan(self, batch, context_keys):
+        """Check the batch against the context pool form and upload its plan
+        (kernel offsets, work list, segment anchors) and size the split-K
+        workspace: what a call does before its launch.  Cached per batch and
+        pool shape, so a caller may prepare a round's batch ahead of its
+        draft layers (as begin() prepares a verification transaction)."""
+        key = (batch, context_keys.shape)
+        if self._geometry_for is None or self._geometry_for[0] is not batch or self._geometry_for[1] != key[1]:
+            self._geometry = self._context_geometry(context_keys, batch)
+            self._geometry_for = key
+        capacity, tok_stride, head_stride = self._geometry
+        offsets = batch.device_offsets(capacity)
+        work, n_work, n_runs, seg_anchors = batch.work(self.chunk, self.runs, capacity)
+        need = _native.load().dspark_attn_workspace_bytes(n_work, 0, batch.max_blocks, self.chunk)
+        ws = self._workspace.get(need)
+        return capacity, tok_stride, head_stride, offsets, work, n_work, n_runs, seg_anchors, ws
+
     def __call__(self, query, block_keys, block_values, context_keys, context_values, batch, *, scale):
         """Q [7*blocks, 16, 128], block K/V [7*blocks, 8, 128], context K/V in
         one of the pool forms of the module docstring.  V is bf16.  Q and K
@@ -270,18 +299,10 @@ class HipDraftAttention:
             raise ValueError('Context K (bf16 or fp32) and V (bf16) must be matching contiguous tensors on the GPU')
         if block_keys.dtype != context_keys.dtype:
             raise ValueError('Backbone/cache precision mismatch')
-        # The batch is immutable: its pool bounds are checked once per pool shape.
-        key = (batch, context_keys.shape)
-        if self._geometry_for is None or self._geometry_for[0] is not batch or self._geometry_for[1] != key[1]:
-            self._geometry = self._context_geometry(context_keys, batch)
-            self._geometry_for = key
-        capacity, tok_stride, head_stride = self._geometry
-        offsets = batch.device_offsets(capacity)
+        capacity, tok_stride, head_stride, offsets, work, n_work, n_runs, seg_anchors, ws = self.plan(batch,
+                                                                                                      context_keys)
         out = torch.empty(query.shape, dtype=torch.bfloat16, device=self.device)
         bound = max(batch.context_rows, 1)
-        work, n_work, n_runs = batch.work(self.chunk, self.runs, capacity)
-        need = _native.load().dspark_attn_workspace_bytes(n_work, 0, batch.max_blocks, self.chunk)
-        ws = self._workspace.get(need)
         _native.call('dspark_draft_attn_fwd', _native.ptr(query), int(query.dtype == torch.float32),
                      _native.ptr(context_keys), _native.ptr(context_values), int(context_keys.dtype == torch.float32),
                      _native.ptr(batch.context_indices), _native.ptr(offsets), _native.ptr(batch.ctx_len),
@@ -289,6 +310,7 @@ class HipDraftAttention:
                      _native.ptr(batch.cu_blocks), _native.ptr(batch.anchor_rows), batch.request_count, bound,
                      batch.max_blocks, float(SCALE), self.chunk, _native.ptr(work), n_work, n_runs,
                      self._workgroups, self.persistent or 0, _native.ptr(self._queue),
+                     _native.ptr(seg_anchors) if self.persistent else None,
                      _native.ptr(out), _native.ptr(ws), ws.numel(), _native.stream_handle(self.device))
         return out
 

@@ -97,15 +97,16 @@ def test_invalid_sizes_are_rejected_before_any_launch():
                                     1 << 20, None)
     assert rc == -1 and 'multiple of 8' in lib.dspark_last_error().decode()
     rc = lib.dspark_draft_attn_fwd(fake, 0, fake, fake, 0, None, fake, fake, 1024, 128, fake, fake, fake, fake,
-                                   2, 100, 9, 0.088, 512, None, 0, 0, 0, 1, None, fake, fake, 1 << 24, None)
+                                   2, 100, 9, 0.088, 512, None, 0, 0, 0, 1, None, None, fake, fake, 1 << 24, None)
     assert rc == -1 and 'max_blocks' in lib.dspark_last_error().decode()
     rc = lib.dspark_draft_attn_fwd(fake, 0, fake, fake, 2, None, fake, fake, 1024, 128, fake, fake, fake, fake,
-                                   2, 100, 8, 0.088, 512, None, 0, 0, 0, 1, None, fake, fake, 1 << 24, None)
+                                   2, 100, 8, 0.088, 512, None, 0, 0, 0, 1, None, None, fake, fake, 1 << 24, None)
     assert rc == -1 and 'k_dtype' in lib.dspark_last_error().decode()
-    for wgs, queues, queue in ((256, 1, None), (256, 3, fake), (250, 8, fake)):
+    for wgs, queues, queue, anc in ((256, 1, None, fake), (256, 3, fake, fake), (250, 8, fake, fake),
+                                    (256, 1, fake, None)):
         rc = lib.dspark_draft_attn_fwd(fake, 0, fake, fake, 0, None, fake, fake, 1024, 128, fake, fake, fake, fake,
-                                       2, 100, 8, 0.088, 512, fake, 2, 2, wgs, queues, queue, fake, fake, 1 << 24,
-                                       None)
+                                       2, 100, 8, 0.088, 512, fake, 2, 2, wgs, queues, queue, anc, fake, fake,
+                                       1 << 24, None)
         assert rc == -1 and 'persistent mode' in lib.dspark_last_error().decode()
     rc = lib.dspark_verify_attn_fwd(fake, fake, fake, fake, fake, fake, fake, fake, 2, 1 << 20, 100, 128, 1000, 7,
                                     0.088, 512, None, 0, 0, fake, fake, 1 << 24, None)
