@@ -47,7 +47,6 @@ VERIFY_LAYERS, DRAFT_LAYERS, BLOCK = 28, 5, 7
 ROW_BYTES = 8 * 128 * 2            # one K (or V) token row, all 8 KV heads
 Q_ROW_BYTES = 16 * 128 * 2         # one Q (or O) token row, all 16 query heads
 HBM_PEAK_GBS = 8000.0              # MI355X HBM3E, published
-CPU_THREADS_CAP = 16               # host CPU share of one GPU on the box
 
 
 def log(msg):
@@ -72,6 +71,9 @@ def parse():
                     help='verification plans with equal runs on every XCD (no XCD speed calibration)')
     ap.add_argument('--traffic-summary', nargs=2, metavar=('FETCH_DIR', 'WRITE_DIR'),
                     help='turn the FETCH_SIZE and WRITE_SIZE passes of --traffic-probe into profiles/*_traffic.json')
+    ap.add_argument('--trace-summary', nargs='+', metavar='DIR:LOG',
+                    help='turn rocprofv3 --kernel-trace runs of the plain bench command (each a trace directory and '
+                         'the bench line its process printed) into profiles/attn_64req_kernel_trace.json')
     ap.add_argument('--traffic-probe', action='store_true',
                     help='untimed run for hardware-counter passes: 3 verification-attention and 3 draft-attention '
                          'layers of the workload, then a 1 GiB device-to-device copy as the counter calibration')
@@ -85,6 +87,9 @@ def parse():
                     help='per-workgroup phase timeline of the draft attention on the workload, from the timeline '
                          'build of the library (clock stamps per segment: start, first loads issued, first stage '
                          'landed, stream end, merge + write end), summarised per call')
+    ap.add_argument('--graph-ab', action='store_true',
+                    help='only compare the captured 28-layer verification round with the same 28 eager calls on one '
+                         'store: alternating blocks, each behind the same queued GPU work, outputs bitwise equal')
     ap.add_argument('--mfma-probe', action='store_true',
                     help='only run the draft kernels for a rocprofv3 --pmc MfmaUtil MfmaFlopsBF16 pass')
     ap.add_argument('--cpu-verify-layers', type=int, default=VERIFY_LAYERS, help='verify layers in the CPU sample')
@@ -112,6 +117,122 @@ def verify_bytes(contexts):
     """Algorithmic HBM bytes of one verification-attention layer: every key
     row (committed + staged) read once, Q read once, O written once."""
     return sum(c + Q_LEN for c in contexts) * 2 * ROW_BYTES + 2 * B * Q_LEN * Q_ROW_BYTES
+
+
+def verify_store(args, dev, layers=VERIFY_LAYERS, calibrate=True):
+    """The workload's resident store (seeded N(0,1) K/V, every request at
+    its context length), its bucket and the round's Q and new K/V rows."""
+    import torch
+
+    from qwen3_dspark_amd.persistent_kv import Bucket, PersistentTargetKV
+    contexts, _, _ = workload(args.warmup + args.steps)
+    gen = torch.Generator(device=dev).manual_seed(SEED)
+    pool = PersistentTargetKV(layers=layers, slots=B, context_capacity=CAPACITY, max_query_tokens=B * Q_LEN,
+                              heads=8, dim=128, device=dev)
+    handles = [pool.add_request(f'req{i}') for i in range(B)]
+    for layer in range(layers):
+        pool.keys[layer].normal_(generator=gen)
+        pool.values[layer].normal_(generator=gen)
+    for h, c in zip(handles, contexts):
+        pool.load_prefix(h, pool.keys[:, h.index, :c], pool.values[:, h.index, :c])
+    bucket = Bucket((Q_LEN,) * B, (CAPACITY - Q_LEN,) * B, '64-request stress shape')
+    pool.register_bucket(bucket)
+    if calibrate and not args.equal_runs:
+        pool.calibrate_xcd()
+    qv = torch.randn(layers, B * Q_LEN, 16, 128, generator=gen, device=dev).to(torch.bfloat16)
+    kn = torch.randn(layers, B * Q_LEN, 8, 128, generator=gen, device=dev).to(torch.bfloat16)
+    vn = torch.randn(layers, B * Q_LEN, 8, 128, generator=gen, device=dev).to(torch.bfloat16)
+    return pool, handles, bucket, contexts, qv, kn, vn
+
+
+def plan_ab(pool, handles, bucket, qv, kn, vn, speed, rounds=8):
+    """Verification calls planned with equal runs and with the XCD-calibrated
+    runs the timed rounds use, on the same store, alternating rounds of 28
+    calls; median per call (the calibrated plan is what `roofline` reports)."""
+    import numpy as np
+    import torch
+    if speed is None:
+        return None
+    out = torch.empty_like(qv)
+    plans = {'equal_runs': None, 'xcd_calibrated': speed}
+    times = {n: [] for n in plans}
+    for r in range(rounds + 1):
+        for name in (('equal_runs', 'xcd_calibrated') if r % 2 == 0 else ('xcd_calibrated', 'equal_runs')):
+            pool.set_xcd_speed(plans[name])
+            tx = pool.begin(handles, bucket)
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for layer in range(VERIFY_LAYERS):
+                pool.attend(tx, layer, qv[layer], keys=kn[layer], values=vn[layer], out=out[layer])
+            e1.record()
+            pool.abort(tx)
+            if r >= 1:
+                times[name].append((e0, e1))
+    torch.cuda.synchronize()
+    pool.set_xcd_speed(speed)
+    return {n + '_call_ms': round(float(np.median([a.elapsed_time(b) for a, b in t])) / VERIFY_LAYERS, 5)
+            for n, t in times.items()}
+
+
+def graph_vs_eager(pool, handles, bucket, contexts, qv, kn, vn, rounds=14):
+    """The captured verification round (VerificationGraph: 28 fused layers in
+    one HIP graph) against the same 28 eager calls on one store and one
+    transaction plan: blocks alternate, each behind the same queued GPU work
+    (a 64 MiB copy, so the host's submission never shows), event-timed on
+    the launch stream; median per layer.  Replay outputs must equal the
+    eager outputs bit for bit."""
+    import numpy as np
+    import torch
+
+    from qwen3_dspark_amd.graph import VerificationGraph
+    dev = pool.device
+    graph = VerificationGraph(pool, bucket).capture()
+    graph.query.copy_(qv)
+    graph.keys.copy_(kn)
+    graph.values.copy_(vn)
+    out = torch.empty_like(qv)
+    pad = torch.empty(64 << 20, dtype=torch.uint8, device=dev)
+    pad_src = torch.empty_like(pad)
+    times = {'eager': [], 'graph': []}
+    same = True
+    for r in range(rounds + 2):
+        for kind in (('eager', 'graph') if r % 2 == 0 else ('graph', 'eager')):
+            tx = pool.begin(handles, bucket)
+            pad.copy_(pad_src)
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            if kind == 'eager':
+                for layer in range(VERIFY_LAYERS):
+                    pool.attend(tx, layer, qv[layer], keys=kn[layer], values=vn[layer], out=out[layer])
+                e1.record()
+                e1.synchronize()
+            else:
+                done = graph.submit(tx)
+                e1.record()
+                graph.wait(done)
+                same = same and torch.equal(graph.output, out)
+            pool.abort(tx)
+            if r >= 2:
+                times[kind].append(e0.elapsed_time(e1) / VERIFY_LAYERS)
+    res = {'layers': VERIFY_LAYERS, 'rounds': rounds, 'bit_identical_to_eager': bool(same)}
+    for kind, t in times.items():
+        ms = float(np.median(t))
+        res[kind] = {'per_layer_ms': round(ms, 5), 'p10_ms': round(float(np.percentile(t, 10)), 5),
+                     'p90_ms': round(float(np.percentile(t, 90)), 5),
+                     'gbs': round(verify_bytes(contexts) / ms / 1e6, 1)}
+        log(f'[graph-ab] {kind}: {ms * 1e3:.1f} us per layer')
+    res['replay_over_eager'] = round(res['graph']['per_layer_ms'] / res['eager']['per_layer_ms'], 4)
+    return res
+
+
+def graph_ab(args):
+    """--graph-ab: graph_vs_eager on the workload's first round (run it
+    under a kernel trace to compare the kernels' durations and gaps)."""
+    import torch
+    dev = torch.device('cuda:0')
+    torch.cuda.set_device(dev)
+    pool, handles, bucket, contexts, qv, kn, vn = verify_store(args, dev)
+    print(json.dumps({'graph_ab': graph_vs_eager(pool, handles, bucket, contexts, qv, kn, vn)}), flush=True)
 
 
 def xcd_ab(args, rounds=14):
@@ -181,6 +302,8 @@ def main():
         sys.exit(2)
     if args.traffic_summary:
         return traffic_summary(*args.traffic_summary)
+    if args.trace_summary:
+        return trace_summary(args.trace_summary)
     if args.traffic_probe:
         return traffic_probe(args)
     if args.mfma_probe:
@@ -189,6 +312,8 @@ def main():
         return timeline_probe(args)
     if args.draft_ab:
         return draft_ab(args)
+    if args.graph_ab:
+        return graph_ab(args)
     if args.xcd_ab:
         return xcd_ab(args)
     if args.stream_probe:
@@ -334,6 +459,16 @@ def main():
             return None, None, 'stale: measured on other kernel sources'
         return tj.get('hbm_bytes_per_launch'), tj.get('ratio'), tj.get('algorithmic_bytes_per_launch')
     traffic, traffic_ratio, traffic_round = counted('verify_attn_traffic.json')
+    profiled = None
+    tpath = os.path.join(ROOT, 'profiles', 'attn_64req_kernel_trace.json')
+    if os.path.exists(tpath):
+        with open(tpath) as f:
+            tj = json.load(f)
+        profiled = ({'source': 'profiles/attn_64req_kernel_trace.json', 'processes': len(tj['processes']),
+                     'verify_frac_from_kernels_range': tj['verify_frac_from_kernels_range'],
+                     'draft_frac_from_kernels_range': tj['draft_frac_from_kernels_range']}
+                    if tj.get('kernel_source_sha256') == kernel_source_hash()
+                    else 'stale: traced on other kernel sources')
     d_traffic, d_traffic_ratio, d_traffic_round = counted('draft_attn_traffic.json')
 
     result = {
@@ -355,6 +490,7 @@ def main():
             'traffic_round_algorithmic_bytes': traffic_round,
             'kernel': 'fused verification attention: varlen_attn_kernel<true> + merge_kernel',
             'avg_launch_ms': round(v_avg_ms, 5), 'algorithmic_bytes_per_launch': int(v_avg_bytes),
+            'profiled': profiled,
         },
         'breakdown': {
             'verify_layer_ms': round(v_avg_ms, 5), 'verify_call_ms': pct(v_ms, VERIFY_LAYERS), 'verify_gbs': round(v_gbs, 1),
@@ -370,11 +506,14 @@ def main():
         },
     }
 
-    result['next'] = {'verify_graph': verify_graph_leg(pool, bucket, handles, qv, kn, vn, verify_bytes),
+    result['breakdown']['verify_plans'] = plan_ab(pool, handles, bucket, qv, kn, vn, xcd_speed)
+    result['next'] = {'verify_graph': graph_vs_eager(pool, handles, bucket, [pool.length(h) for h in handles],
+                                                     qv, kn, vn),
                       'qkv_prologue': prologue_leg(dev, B * Q_LEN),
                       'draft_context_projection': [draft_projection_leg(dev, B, Q_LEN),
                                                    draft_projection_leg(dev, 16, None)],
                       'lm_head_and_verification': sampling_leg(dev, args.no_cpu_baseline)}
+    result['gpu_configs'] = gpu_configs(dev)
 
     if not args.no_cpu_baseline:
         result['cpu_baseline'], result['parity'] = cpu_leg(args, pool, bucket, handles, contexts, anchors, qv, qd,
@@ -433,50 +572,6 @@ def prologue_leg(dev, tokens, reps=50):
     flops = 2 * tokens * 1024 * 4096
     return {'tokens': tokens, 'median_ms': round(ms, 5), 'bytes': nbytes, 'gbs': round(nbytes / ms / 1e6, 1),
             'tflops': round(flops / ms / 1e9, 2)}
-
-
-def verify_graph_leg(pool, bucket, handles, qv, kn, vn, bytes_of, reps=10):
-    """The 28 verification-attention layers of a round captured in one HIP
-    graph (VerificationGraph) and replayed per transaction, the metadata of
-    begin() outside the graph.  Median replay span (events on the stream
-    around the replay, with GPU work queued ahead so that the host's graph
-    submission does not show) over `reps` transactions at the current
-    lengths, each aborted after its replay; the replay's outputs are
-    compared bit for bit with eager calls on the same transaction."""
-    import numpy as np
-    import torch
-
-    from qwen3_dspark_amd.graph import VerificationGraph
-    graph = VerificationGraph(pool, bucket).capture()
-    graph.query.copy_(qv)
-    graph.keys.copy_(kn)
-    graph.values.copy_(vn)
-    ctx = [pool.length(h) for h in handles]
-    # A ~1 ms copy queued ahead keeps the GPU busy while the host submits
-    # the graph, so the span is the replay's execution, not host latency.
-    pad = torch.empty(1 << 30, dtype=torch.uint8, device=pool.device)
-    pad_src = torch.empty_like(pad)
-    spans = []
-    for i in range(reps + 2):
-        tx = pool.begin(handles, bucket)
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        for _ in range(4):
-            pad.copy_(pad_src)
-        e0.record()
-        done = graph.submit(tx)
-        e1.record()
-        graph.wait(done)
-        pool.abort(tx)
-        if i >= 2:
-            spans.append(e0.elapsed_time(e1))
-    tx = pool.begin(handles, bucket)
-    same = all(torch.equal(pool.attend(tx, l, qv[l], keys=kn[l], values=vn[l]), graph.output[l])
-               for l in range(VERIFY_LAYERS))
-    pool.abort(tx)
-    ms = float(np.median(spans))
-    return {'layers': VERIFY_LAYERS, 'replay_ms': round(ms, 4), 'per_layer_ms': round(ms / VERIFY_LAYERS, 5),
-            'gbs': round(bytes_of(ctx) * VERIFY_LAYERS / ms / 1e6, 1), 'replays': reps,
-            'bit_identical_to_eager': bool(same)}
 
 
 def sampling_leg(dev, skip_cpu, reps=10):
@@ -914,7 +1009,7 @@ def traffic_summary(fetch_dir, write_dir):
             if 'varlen_attn_kernel' in name:
                 phase = 'verify'
                 out['verify_chunk'].append(value)
-            elif 'draft_attn_kernel' in name:
+            elif 'draft_attn' in name:          # draft_attn_kernel or draft_attn_persistent_kernel
                 phase = 'draft'
                 out['draft_chunk'].append(value)
             elif 'merge_kernel' in name and phase:
@@ -950,6 +1045,78 @@ def traffic_summary(fetch_dir, write_dir):
                                                      'write_kib')}}))
 
 
+def trace_summary(pairs):
+    """profiles/attn_64req_kernel_trace.json from kernel traces of the plain
+    bench command, one process each: per process, the mean duration of the
+    verification chunk kernel and its merge over the timed rounds'
+    (warmup + steps) x 28 launches, the same for the draft chunk kernel and
+    its merge (x 5), beside the per-call event figures and algorithmic bytes
+    that process's bench line reported; stamped with the kernel sources'
+    sha256."""
+    import sqlite3
+
+    import numpy as np
+    procs = []
+    for pair in pairs:
+        trace_dir, log_path = pair.split(':', 1)
+        db = [os.path.join(d, f) for d, _, fs in os.walk(trace_dir) for f in fs if f.endswith('_results.db')]
+        if len(db) != 1:
+            raise SystemExit(f'expected one results database under {trace_dir}, found {db}')
+        with open(log_path) as f:
+            line = json.loads([x for x in f.read().splitlines() if x.startswith('{"metric"')][-1])
+        rounds = line['steps'] + line['warmup']
+        con = sqlite3.connect(db[0])
+        names = [r[0] for r in con.execute('select name, start, end from kernels order by start')]
+        spans = [(r[1], r[2]) for r in con.execute('select name, start, end from kernels order by start')]
+        got = {'verify_chunk': [], 'verify_merge': [], 'draft_chunk': [], 'draft_merge': []}
+        phase = None
+        for name, (t0, t1) in zip(names, spans):
+            if 'varlen_attn_kernel' in name:
+                phase = 'verify'
+                got['verify_chunk'].append((t1 - t0) * 1e-3)
+            elif 'draft_attn' in name:
+                phase = 'draft'
+                got['draft_chunk'].append((t1 - t0) * 1e-3)
+            elif 'merge_kernel' in name and phase:
+                got[phase + '_merge'].append((t1 - t0) * 1e-3)
+        calls = {'verify': VERIFY_LAYERS * rounds, 'draft': DRAFT_LAYERS * rounds}
+        row = {'bench_value_tokens_per_s': line['value'], 'ms_per_step': line['ms_per_step']}
+        for kind, n in calls.items():
+            chunk, merge = got[kind + '_chunk'][:n], got[kind + '_merge'][:n]
+            if len(chunk) < n or len(merge) < n:
+                raise SystemExit(f'{db[0]}: fewer {kind} launches than the timed rounds hold')
+            b = line['breakdown']
+            event_ms = b[kind + '_layer_ms']
+            algorithmic = (line['roofline']['algorithmic_bytes_per_launch'] if kind == 'verify'
+                           else b['draft_algorithmic_bytes_per_launch'])
+            kernel_us = float(np.mean(chunk)) + float(np.mean(merge))
+            row[kind] = dict(chunk_us=round(float(np.mean(chunk)), 2), merge_us=round(float(np.mean(merge)), 2),
+                             chunk_plus_merge_us=round(kernel_us, 2), event_us_per_call=round(event_ms * 1e3, 2),
+                             algorithmic_bytes_per_launch=int(algorithmic),
+                             frac_from_kernels=round(algorithmic / (kernel_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+                             frac_from_events=round(algorithmic / (event_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4))
+        procs.append(row)
+    doc = {'what': 'kernel traces of `python bench.py --no-cpu-baseline`, one process each', 'processes': procs,
+           'kernel_source_sha256': kernel_source_hash()}
+    for kind in ('verify', 'draft'):
+        fr = [p[kind]['frac_from_kernels'] for p in procs]
+        doc[kind + '_frac_from_kernels_range'] = [min(fr), max(fr)]
+    with open(os.path.join(ROOT, 'profiles', 'attn_64req_kernel_trace.json'), 'w') as f:
+        json.dump(doc, f, indent=1)
+    print(json.dumps(doc))
+
+
+def cpu_threads():
+    """(threads, reason): the host threads the CPU baseline uses - the
+    process's OpenMP share when OMP_NUM_THREADS is set (the GPU box sets it
+    to its CPU share per GPU, 16), else every core os.cpu_count() reports."""
+    n = os.cpu_count() or 1
+    env = os.environ.get('OMP_NUM_THREADS', '')
+    if env.isdigit() and int(env) >= 1:
+        return min(int(env), n), f'OMP_NUM_THREADS={env} (the host CPU share of this process; os.cpu_count()={n})'
+    return n, f'os.cpu_count()={n}'
+
+
 def cpu_model():
     """The host CPU's model name (/proc/cpuinfo), for the CPU baseline."""
     try:
@@ -971,9 +1138,9 @@ def cpu_configs(threads):
          4 blocks each at anchors U[0, c];
       4. verification of 28 layers, 32 requests, contexts U[256, 2048].
     Inputs are seeded N(0,1) draws rounded to bf16 (the oracle computes in
-    FP32).  Per call: median of 5 reps (3 at 28 layers' scale, 1 for the
-    2-thread 28-layer case); layers of one config are identical in cost, so
-    a round is `layers` calls."""
+    FP32).  Every layer of a config is executed (one call per layer, on the
+    config's inputs), nothing is scaled: round time = median over `reps`
+    rounds."""
     import numpy as np
     import torch
 
@@ -996,10 +1163,13 @@ def cpu_configs(threads):
 
     def report(call, rows, layers, reps):
         row = {'query_rows': rows, 'layers': layers}
-        for th, n in ((threads, reps), (2, max(1, reps if reps >= 5 else 1))):
-            t = median_s(lambda: call(th), n)
-            row[f'{th}_threads'] = {'call_ms': round(1e3 * t, 3), 'round_ms': round(1e3 * t * layers, 2),
-                                    'tokens_per_s': round(rows / (t * layers), 1), 'reps': n}
+        for th in (threads, 2):
+            def one_round():
+                for _ in range(layers):
+                    call(th)
+            t = median_s(one_round, reps)
+            row[f'{th}_threads'] = {'round_ms': round(1e3 * t, 2), 'call_ms': round(1e3 * t / layers, 3),
+                                    'tokens_per_s': round(rows / t, 1), 'rounds': reps, 'layers_executed': layers}
         return row
 
     def draft_case(contexts, anchors, layers, reps):
@@ -1026,10 +1196,110 @@ def cpu_configs(threads):
         '2_verify_4_requests_1_layer': verify_case([int(x) for x in rng.integers(64, 513, size=4)], 1, 5),
         '3_draft_5_layers_16_requests_4_blocks': draft_case(
             c3, [[int(a) for a in rng.integers(0, c + 1, size=4)] for c in c3], 5, 5),
-        '4_verify_28_layers_32_requests': verify_case([int(x) for x in rng.integers(256, 2049, size=32)], 28, 3),
+        '4_verify_28_layers_32_requests': verify_case([int(x) for x in rng.integers(256, 2049, size=32)], 28, 5),
     }
-    return {'cpu': cpu_model(), 'threads': [threads, 2], 'kind': 'port (oracle/attn_ref.c, FP32, OpenMP)',
-            'configs': configs}
+    return {'cpu': cpu_model(), 'threads': [threads, 2], 'threads_reason': cpu_threads()[1],
+            'kind': 'port (oracle/attn_ref.c, FP32, OpenMP)', 'configs': configs}
+
+
+def gpu_configs(dev, blocks=12, per_block=10):
+    """The four smaller workloads on the GPU, each call of the attention
+    path timed as in the round: blocks of `per_block` back-to-back calls
+    queued behind GPU work (so host launch latency never shows), one event
+    pair per block; per-call latency median / p10 / p90 over `blocks` blocks
+    (after two warm-up blocks), algorithmic bytes per call, GB/s, fraction
+    of 8 TB/s.
+      1. draft, 2 requests, contexts 128 / 96, one 7-row block each at its
+         context length (fp32 Q and K, bf16 V: the kernel's fp32 form);
+      2. verification, 1 layer, 4 requests, contexts U[64, 512], 7 new
+         rows staged beforehand (a timed call is the attention launch over
+         resident + staged rows: the round's fused launch without its copy
+         of the new rows into scratch, since a layer stages once per
+         transaction);
+      3. draft, 5 layers, 16 requests, contexts U[128, 1024], 4 blocks each
+         (one at c, three at U[0, c]);
+      4. verification, 28 layers, 32 requests, contexts U[256, 2048], timed
+         like 2 (a call is one layer; a round is 28)."""
+    import numpy as np
+    import torch
+
+    from qwen3_dspark_amd.draft import DraftBatch, HipDraftAttention
+    from qwen3_dspark_amd.kernels import SCALE
+    from qwen3_dspark_amd.persistent_kv import Bucket, PersistentTargetKV
+    rng = np.random.default_rng(SEED + 41)
+    gen = torch.Generator(device=dev).manual_seed(SEED + 41)
+
+    def rnd(*shape, dtype=torch.bfloat16):
+        return torch.randn(*shape, generator=gen, device=dev).to(dtype)
+
+    def timed(call, layers, nbytes, rows):
+        for _ in range(2):
+            for i in range(per_block):
+                call(i % layers)
+        times = []
+        for _ in range(blocks):
+            queue_ahead(dev, copies=2)
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record()
+            for i in range(per_block):
+                call(i % layers)
+            b.record()
+            b.synchronize()
+            times.append(a.elapsed_time(b) / per_block)
+        ms = float(np.median(times))
+        return {'call_us': {'median': round(ms * 1e3, 2), 'p10': round(float(np.percentile(times, 10)) * 1e3, 2),
+                            'p90': round(float(np.percentile(times, 90)) * 1e3, 2)},
+                'layers': layers, 'round_us': round(ms * 1e3 * layers, 1), 'query_rows': rows,
+                'attn_tokens_per_s': round(rows / (ms * 1e-3), 1), 'algorithmic_bytes_per_call': int(nbytes),
+                'gbs': round(nbytes / ms / 1e6, 1), 'frac_of_8tbs': round(nbytes / ms / 1e6 / HBM_PEAK_GBS, 4),
+                'blocks': blocks, 'calls_per_block': per_block}
+
+    def draft_config(contexts, anchors, layers, kdtype):
+        n = sum(len(a) for a in anchors)
+        ctx_k, ctx_v = rnd(layers, sum(contexts), 8, 128, dtype=kdtype), rnd(layers, sum(contexts), 8, 128)
+        q, bk, bv = rnd(layers, 7 * n, 16, 128, dtype=kdtype), rnd(layers, 7 * n, 8, 128, dtype=kdtype), \
+            rnd(layers, 7 * n, 8, 128)
+        offs = [int(x) for x in np.concatenate([[0], np.cumsum(contexts)[:-1]])]
+        batch = DraftBatch(dev, offs, contexts, anchors)
+        kernel = HipDraftAttention(dev)
+        kernel.plan(batch, ctx_k[0])
+        return timed(lambda l: kernel(q[l], bk[l], bv[l], ctx_k[l], ctx_v[l], batch, scale=SCALE), layers,
+                     draft_bytes(anchors), 7 * n)
+
+    def verify_config(contexts, layers):
+        n, cap = len(contexts), max(contexts) + 2 * Q_LEN
+        pool = PersistentTargetKV(layers=layers, slots=n, context_capacity=cap, max_query_tokens=n * Q_LEN,
+                                  heads=8, dim=128, device=dev)
+        hs = [pool.add_request(f'c{i}') for i in range(n)]
+        for layer in range(layers):
+            pool.keys[layer].normal_(generator=gen)
+            pool.values[layer].normal_(generator=gen)
+        for h, c in zip(hs, contexts):
+            pool.load_prefix(h, pool.keys[:, h.index, :c], pool.values[:, h.index, :c])
+        bucket = Bucket((Q_LEN,) * n, (cap - Q_LEN,) * n, 'config')
+        pool.register_bucket(bucket)
+        q, kn, vn = rnd(layers, n * Q_LEN, 16, 128), rnd(layers, n * Q_LEN, 8, 128), rnd(layers, n * Q_LEN, 8, 128)
+        out = torch.empty_like(q)
+        tx = pool.begin(hs, bucket)
+        for layer in range(layers):           # staged once; the timed calls attend over resident + staged rows
+            pool.stage_layer(tx, layer, kn[layer], vn[layer])
+        nbytes = sum(c + Q_LEN for c in contexts) * 2 * ROW_BYTES + 2 * n * Q_LEN * Q_ROW_BYTES
+        res = timed(lambda l: pool.attend(tx, l, q[l], out=out[l]), layers, nbytes, n * Q_LEN)
+        pool.abort(tx)
+        del pool
+        return res
+
+    c3 = [int(x) for x in rng.integers(128, 1025, size=16)]
+    a3 = [[c] + sorted(int(x) for x in rng.integers(0, c + 1, size=3)) for c in c3]
+    out = {
+        '1_draft_2_requests_fp32qk': draft_config([128, 96], [[128], [96]], 1, torch.float32),
+        '2_verify_4_requests_1_layer': verify_config([int(x) for x in rng.integers(64, 513, size=4)], 1),
+        '3_draft_5_layers_16_requests_4_blocks': draft_config(c3, a3, 5, torch.bfloat16),
+        '4_verify_28_layers_32_requests': verify_config([int(x) for x in rng.integers(256, 2049, size=32)], 28),
+    }
+    for name, r in out.items():
+        log(f'[gpu-configs] {name}: {r["call_us"]["median"]} us per call, {r["gbs"]} GB/s')
+    return out
 
 
 def draft_pairs(anchors):
@@ -1108,7 +1378,7 @@ def cpu_leg(args, pool, bucket, handles, contexts, anchors, qv, qd, bkd, bvd, dc
     from qwen3_dspark_amd.draft import DraftBatch
     from qwen3_dspark_amd.kernels import SCALE
 
-    threads = max(1, min(CPU_THREADS_CAP, os.cpu_count() or 1))
+    threads, reason = cpu_threads()
     dev = pool.device
     n_verify = max(1, min(VERIFY_LAYERS, args.cpu_verify_layers))
     n_draft = max(1, min(DRAFT_LAYERS, args.cpu_draft_layers))
@@ -1133,7 +1403,7 @@ def cpu_leg(args, pool, bucket, handles, contexts, anchors, qv, qd, bkd, bvd, dc
     slots = [h.index for h in handles]
     cmax = max(ctx)
     t_verify = 0.0
-    two = {}      # per-layer seconds at 2 threads (layer 0 of each kind)
+    two = {'verify': 0.0, 'draft': 0.0}      # the same layers at 2 threads
     for layer in range(n_verify):
         kn = torch.randn(B * Q_LEN, 8, 128, generator=gen, device=dev).to(torch.bfloat16)
         vn = torch.randn(B * Q_LEN, 8, 128, generator=gen, device=dev).to(torch.bfloat16)
@@ -1146,10 +1416,9 @@ def cpu_leg(args, pool, bucket, handles, contexts, anchors, qv, qd, bkd, bvd, dc
         ref = cref.verify_attention(q, kres, vres, ks, vs, slots, ctx, cu_q, scale=SCALE, threads=threads)
         t_verify += time.perf_counter() - t0
         gate(out, ref, 'verify')
-        if layer == 0:
-            t0 = time.perf_counter()
-            cref.verify_attention(q, kres, vres, ks, vs, slots, ctx, cu_q, scale=SCALE, threads=2)
-            two['verify'] = time.perf_counter() - t0
+        t0 = time.perf_counter()
+        cref.verify_attention(q, kres, vres, ks, vs, slots, ctx, cu_q, scale=SCALE, threads=2)
+        two['verify'] += time.perf_counter() - t0
         del kres, vres
     pool.abort(tx)
 
@@ -1172,27 +1441,27 @@ def cpu_leg(args, pool, bucket, handles, contexts, anchors, qv, qd, bkd, bvd, dc
                                     bits(bvd[layer]), cu_b, flat, scale=SCALE, threads=threads)
         t_draft += time.perf_counter() - t0
         gate(dout, dref, 'draft')
-        if layer == 0:
-            t0 = time.perf_counter()
-            cref.draft_attention(bits(qd[layer]), ck, cv, offs_host, contexts, bits(bkd[layer]), bits(bvd[layer]),
-                                 cu_b, flat, scale=SCALE, threads=2)
-            two['draft'] = time.perf_counter() - t0
+        t0 = time.perf_counter()
+        cref.draft_attention(bits(qd[layer]), ck, cv, offs_host, contexts, bits(bkd[layer]), bits(bvd[layer]),
+                             cu_b, flat, scale=SCALE, threads=2)
+        two['draft'] += time.perf_counter() - t0
     stats['within_tolerance'] = bool(stats['verify_max_abs'] <= 2e-2 and stats['verify_mean_abs'] <= 2e-3
                                      and stats['draft_max_abs'] <= 2e-2 and stats['draft_mean_abs'] <= 2e-3)
     stats['checked_layers'] = {'verify': n_verify, 'draft': n_draft}
+    full = (n_verify, n_draft) == (VERIFY_LAYERS, DRAFT_LAYERS)
     round_s = VERIFY_LAYERS * t_verify / n_verify + DRAFT_LAYERS * t_draft / n_draft
-    scaled = '' if (n_verify, n_draft) == (VERIFY_LAYERS, DRAFT_LAYERS) else ', scaled to 28 + 5 layers'
-    round_2 = VERIFY_LAYERS * two['verify'] + DRAFT_LAYERS * two['draft']
+    round_2 = VERIFY_LAYERS * two['verify'] / n_verify + DRAFT_LAYERS * two['draft'] / n_draft
+    scaled = '' if full else ', scaled to 28 + 5 layers (a reduced --cpu-*-layers sample)'
     cpu = {
         'value': round(B * Q_LEN / round_s, 3), 'unit': 'tokens/s', 'cores': threads, 'kind': 'port',
+        'threads_reason': reason, 'cpu': cpu_model(), 'layers_executed': {'verify': n_verify, 'draft': n_draft},
         'sample': f'C oracle (oracle/attn_ref.c, FP32, OpenMP, {threads} threads) over one round of the same '
                   f'64-request workload: {n_verify} verification layers ({t_verify:.2f} s) and {n_draft} draft '
                   f'layers ({t_draft:.2f} s){scaled}; round time {round_s:.2f} s; host CPU {cpu_model()}',
         'two_threads': {'value': round(B * Q_LEN / round_2, 3), 'unit': 'tokens/s', 'cores': 2,
-                        'sample': f'the same C oracle at 2 threads (the reference CI thread count) on the first '
-                                  f'verification layer ({two["verify"]:.2f} s) and the first draft layer '
-                                  f'({two["draft"]:.2f} s) of that round, scaled to 28 + 5 layers: '
-                                  f'{round_2:.2f} s per round'},
+                        'sample': f'the same C oracle at 2 threads (the reference CI thread count) on the same '
+                                  f'{n_verify} verification layers ({two["verify"]:.2f} s) and {n_draft} draft '
+                                  f'layers ({two["draft"]:.2f} s){scaled}: {round_2:.2f} s per round'},
     }
     return cpu, stats
 

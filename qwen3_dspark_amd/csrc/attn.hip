@@ -963,6 +963,13 @@ __device__ __forceinline__ int persistent_items(const DraftArgs& a) {
 
 __device__ __forceinline__ int persistent_run(const DraftArgs& a, int t) { return a.queues == 8 ? t : t >> 3; }
 
+// Workgroups serving one queue (the grid is a multiple of 8).  Member i of
+// a queue takes ticket i first without drawing; drawn tickets start after
+// the members'.
+__device__ __forceinline__ int persistent_members(const DraftArgs& a) {
+  return a.queues == 8 ? (int)(gridDim.x >> 3) : (int)gridDim.x;
+}
+
 // Called by one lane: stage ticket t and, if it names an item, that item's
 // record and anchors (plain vector loads; the lane waits for them).
 __device__ __forceinline__ void stage_next(const DraftArgs& a, int* nxt, int t) {
@@ -1125,7 +1132,10 @@ __device__ __forceinline__ void draft_pair_item(const DraftArgs& a, unsigned cha
 
   // Nothing of the compiler's is in flight from here on (a previous item's
   // stores have completed), so it places no vmcnt wait of its own among the
-  // ring's direct-to-LDS loads below.
+  // ring's direct-to-LDS loads below.  (Without this wait a persistent
+  // workgroup gains nothing: the compiler then waits for the previous item's
+  // output stores itself, where their data registers are reused, which
+  // falls among this item's first ring loads.)
   __builtin_amdgcn_s_waitcnt(0x0f70);   // vmcnt(0)
   // Persistent mode: lane 0 of wave 1 (a key-half-1 wave, idle once it has
   // handed its state to the merge) draws the workgroup's next ticket when
@@ -1135,7 +1145,7 @@ __device__ __forceinline__ void draft_pair_item(const DraftArgs& a, unsigned cha
   const bool fetcher = ticket_ctr && tid == WAVE;
   int next_ticket = 0;
   auto draw = [&]() {
-    if (fetcher) next_ticket = atomic_add_deferred(ticket_ctr, 1);
+    if (fetcher) next_ticket = atomic_add_deferred(ticket_ctr, 1) + persistent_members(a);
   };
   // bf16 Q rows, issued first: slot row R = 32p + n holds tile row n of
   // pair p (rows with no query read block 0, token 0 and are zeroed later).
@@ -1329,13 +1339,14 @@ __device__ __forceinline__ void draft_pair_item(const DraftArgs& a, unsigned cha
 // CU) that take items - (run, KV head) pairs of a plan with one segment per
 // run, runs in list order - from device ticket counters, so a CU starts its
 // next item as soon as it is done instead of waiting for the hardware
-// dispatcher.  A workgroup draws its next ticket when the current segment's
-// stream ends and stages the next item's record and anchors in LDS while
-// the current one merges (draft_pair_item), so an item starts without a
-// memory round trip.  With one queue, ticket t is run t / 8, head t % 8;
+// dispatcher.  Member i of a queue starts with ticket i without drawing;
+// later tickets are drawn (counter + members) when the current segment's
+// stream ends, and the next item's record and anchors are staged in LDS
+// while the current one merges (draft_pair_item), so an item starts without
+// a memory round trip.  With one queue, ticket t is run t / 8, head t % 8;
 // with a queue per XCD, workgroup b serves head b % 8 (its XCD when
 // workgroups are dealt round-robin) and ticket t of that queue is run t.
-// Counter layout per queue: {next ticket, workgroups done}.  The last
+// Counter layout per queue: {tickets drawn, workgroups done}.  The last
 // workgroup of a queue to finish sets both back to zero, so every launch
 // finds them zero (the caller zeroes them once, at allocation).  Between
 // items the workgroup keeps no state in registers (the item runs at the
@@ -1351,7 +1362,7 @@ __device__ __forceinline__ void draft_persistent(const DraftArgs& a, unsigned ch
 #ifdef DSPARK_TIMELINE
   const uint64_t tl_entry = tl_now();
 #endif
-  if (threadIdx.x == WAVE) stage_next(a, nxt, atomicAdd(ctr, 1));
+  if (threadIdx.x == WAVE) stage_next(a, nxt, per_head ? (int)(blockIdx.x >> 3) : (int)blockIdx.x);
   __syncthreads();
 #ifdef DSPARK_TIMELINE
   const uint64_t tl_first = tl_now();
@@ -1379,8 +1390,7 @@ __device__ __forceinline__ void draft_persistent(const DraftArgs& a, unsigned ch
   const uint64_t tl_left = tl_now();
 #endif
   if (threadIdx.x == 0) {
-    const int q = per_head ? (int)(blockIdx.x & 7) : 0;
-    const int members = per_head ? (int)(gridDim.x >> 3) + ((int)(gridDim.x & 7) > q ? 1 : 0) : (int)gridDim.x;
+    const int members = persistent_members(a);
     const int finished = atomicAdd(ctr + 1, 1);
     if (finished == members - 1) {   // every member has drawn its last ticket: reset for the next launch
       atomicExch(ctr, 0);
