@@ -544,8 +544,11 @@ def queue_ahead(dev, copies=8):
 def prologue_leg(dev, tokens, reps=50):
     """The verify-layer prologue (q/k/v projection + q/k RMSNorm + RoPE, K/V
     written token-major as into scratch) for one layer of the round's
-    tokens, Qwen3-0.6B sizes (hidden 1024), random-init weights.  Median of
-    `reps` event-timed launches, queued back to back behind GPU work."""
+    tokens, Qwen3-0.6B sizes (hidden 1024), random-init weights, fed the
+    transaction's rotary table as PersistentTargetKV.stage_projected does
+    (one dspark_rope_table launch per transaction, shared by the 28 layers;
+    timed on its own).  Medians of `reps` event-timed launches, queued back
+    to back behind GPU work."""
     import numpy as np
     import torch
 
@@ -556,22 +559,28 @@ def prologue_leg(dev, tokens, reps=50):
     pro = QKVPrologue(*w, *norms)
     x = torch.randn(tokens, 1024, generator=g, device=dev).to(torch.bfloat16)
     pos = torch.arange(tokens, device=dev, dtype=torch.long) * 13
+    table = pro.rope_table(pos)
     for _ in range(5):
-        pro(x, pos)
-    times = []
-    queue_ahead(dev)
-    for _ in range(reps):
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record()
-        pro(x, pos)
-        e1.record()
-        times.append((e0, e1))
-    torch.cuda.synchronize()
-    ms = float(np.median([a.elapsed_time(b) for a, b in times]))
+        pro(x, pos, rope=table)
+
+    def timed(fn):
+        times = []
+        queue_ahead(dev)
+        for _ in range(reps):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            fn()
+            e1.record()
+            times.append((e0, e1))
+        torch.cuda.synchronize()
+        return float(np.median([a.elapsed_time(b) for a, b in times]))
+
+    ms = timed(lambda: pro(x, pos, rope=table))
+    table_ms = timed(lambda: pro.rope_table(pos))
     nbytes = (4096 * 1024 + tokens * 1024 + tokens * 4096) * 2
     flops = 2 * tokens * 1024 * 4096
     return {'tokens': tokens, 'median_ms': round(ms, 5), 'bytes': nbytes, 'gbs': round(nbytes / ms / 1e6, 1),
-            'tflops': round(flops / ms / 1e9, 2)}
+            'tflops': round(flops / ms / 1e9, 2), 'rope_table_ms_per_transaction': round(table_ms, 5)}
 
 
 def sampling_leg(dev, skip_cpu, reps=10):

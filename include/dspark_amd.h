@@ -24,7 +24,7 @@ extern "C" {
 /* Thread-local message for the last failing call on this thread. */
 const char* dspark_last_error(void);
 
-/* ABI revision of this header (currently 5). */
+/* ABI revision of this header (currently 6). */
 int dspark_abi_version(void);
 
 /*
@@ -230,16 +230,31 @@ int dspark_draft_attn_fwd(const void* q, int q_dtype, const void* k_ctx, const v
  *   q = RoPE(RMSNorm(x Wq^T, q_norm)), k = RoPE(RMSNorm(x Wk^T, k_norm)), v = x Wv^T
  * per 128-dim head; W* in nn.Linear layout ([16*128 | 8*128, hidden]),
  * RMSNorm y = w x / sqrt(mean(x^2) + eps), RoPE rotate-half with angle
- * positions[t] * inv_freq[d] (float32 table of 64 entries).  q_out
- * [tokens, 16, 128]; k_out/v_out token rows of 8*128 elements,
- * kv_row_stride apart (1024 writes a [tokens, 8, 128] tensor, e.g. the
- * transaction scratch layer, replacing stage_layer's copy).  hidden must be
- * a multiple of 128.  FP32 accumulation, bf16 outputs.
+ * positions[t] * inv_freq[d] (float32 table of 64 entries).  rope
+ * (optional, NULL forms the angles in the kernel): the rows' cos/sin table
+ * written by dspark_rope_table for these positions and inv_freq - the same
+ * bits, without the per-layer sincos.  q_out [tokens, 16, 128];
+ * k_out/v_out token rows of 8*128 elements, kv_row_stride apart (1024
+ * writes a [tokens, 8, 128] tensor, e.g. the transaction scratch layer,
+ * replacing stage_layer's copy).  hidden must be a multiple of 128.  x, the
+ * weights, outputs, inv_freq and rope 16-byte aligned, q_norm/k_norm 8-byte
+ * aligned.  FP32 accumulation, bf16 outputs.
  */
 int dspark_qkv_prologue(const void* x, const void* wq, const void* wk, const void* wv,
                         const void* q_norm, const void* k_norm, const float* inv_freq,
-                        const int64_t* positions, int tokens, int hidden, float eps,
+                        const int64_t* positions, const float* rope, int tokens, int hidden, float eps,
                         void* q_out, void* k_out, void* v_out, int64_t kv_row_stride, void* stream);
+
+/*
+ * Rotary table of a set of rows: table[t][d] = cos(positions[t] * inv_freq[d]),
+ * table[t][64 + d] = sin(...), d < 64, the angle formed in FP32 (float32
+ * [tokens][128]).  Computed once per verification transaction and shared by
+ * the prologues of all layers, as the model computes its position
+ * embeddings once per forward (transformers' Qwen3RotaryEmbedding, called by
+ * Qwen3Model.forward; the reference keeps them in the model dtype, this
+ * table in float32).
+ */
+int dspark_rope_table(const float* inv_freq, const int64_t* positions, int tokens, float* table, void* stream);
 
 /*
  * Draft context K/V projection: what DSpark's draft does to newly committed

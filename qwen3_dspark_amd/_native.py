@@ -44,7 +44,8 @@ SIGNATURES = {
     'dspark_layout_build': (_I, [_P, _P, _L, _P, _P, _L, _I, _P, _P, _P, _P, _P, _L, _P]),
     'dspark_pool_gather': (_I, [_P, _P, _L, _L, _L, _I, _L, _P, _L, _P, _P, _P]),
     'dspark_pool_append': (_I, [_P, _P, _L, _L, _L, _L, _L, _I, _L, _I, _I, _PP, _PP, _L, _L, _L, _P, _I, _P, _P]),
-    'dspark_qkv_prologue': (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _F, _P, _P, _P, _L, _P]),
+    'dspark_qkv_prologue': (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _F, _P, _P, _P, _L, _P]),
+    'dspark_rope_table': (_I, [_P, _P, _I, _P, _P]),
     'dspark_draft_kv_project': (_I, [_P, _I, _I, _P, _P, _I, _P, _P, _I, _F, _F, _P, _P, _L, _L, _L, _P, _P]),
     'dspark_draft_kv_epilogue': (_I, [_P, _L, _P, _I, _I, _I, _P, _I, _P, _P, _I, _F, _F, _P, _P, _L, _L, _L, _P,
                                       _P]),
@@ -59,7 +60,7 @@ SIGNATURES = {
     'dspark_rows_rebuild': (_I, [_PP, _PP, _PP, _I, _I, _L, _L, _L, _P, _L, _P]),
 }
 
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 
 class NativeError(RuntimeError):

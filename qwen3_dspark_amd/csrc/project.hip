@@ -19,7 +19,7 @@
 // is rounded to bf16 once.
 //
 // Work: one workgroup per (layer, K or V, KV head) x 64-token tile (the
-// shared head_tile_gemm), XCD-aware so that the token tiles of one weight
+// shared 32x32x16 MFMA tile of head_gemm.h), XCD-aware so that the token tiles of one weight
 // slice share an L2.  Token t belongs to the request whose record
 // (slot, first position, first token, count) covers it; its row goes to
 // (slot, position) of every layer's pool.  A non-finite output sets *flag
@@ -51,34 +51,33 @@ struct DraftProjArgs {
 __global__ __launch_bounds__(HG_WAVES * WAVE) void draft_kv_project_kernel(DraftProjArgs a) {
   __shared__ __attribute__((aligned(16))) unsigned char smem[HG_SMEM];
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
-  const int col = lane & 15;
-  const int grp = lane >> 4;
   const int tiles = (a.tokens + HG_TOKENS - 1) / HG_TOKENS;
   const int xcd = blockIdx.x & 7;
   const int slot_id = blockIdx.x >> 3;
   const int job = xcd + 8 * (slot_id / tiles);        // layer * 16 + (V ? 8 : 0) + head
   const int t0 = (slot_id % tiles) * HG_TOKENS;
   const int layer = job >> 4;
-  const bool is_v = (job & 8) != 0;
+  const bool is_v = (job & 8) != 0;                   // workgroup-uniform
   const int head = job & 7;
   const bf16* w = a.w + ((size_t)(2 * layer + (is_v ? 1 : 0)) * KV_ROW + (size_t)head * HD) * a.hidden;
 
-  f32x4 acc[8];
+  const HeadLane L;
+  const int row = t0 + L.token();
+  const int tok = min(row, a.tokens - 1);
+  HeadNormW nw;
+  float v[2][8];
   float ss;
-  head_tile_gemm<true>(w, a.x, a.tokens, a.hidden, t0, smem, acc, ss);
-  if (wave >= 4) return;        // the second column half; no barrier follows
-  const int tw = t0 + 16 * wave;
-  if (tw >= a.tokens) return;   // wave-uniform; no barrier follows
-  const int tok = min(tw + col, a.tokens - 1);
+  head_tile_gemm<true>(w, a.x, a.tokens, a.hidden, t0, smem, v, ss, [&]() {
+    if (!is_v) nw.load(a.k_norm + (size_t)layer * HD);
+  });
 
-  // Context norm: this token's row sum of squares (its 4 lane groups each
-  // saw a quarter of the row), applied as one scale of the FP32 result.
-  ss += __shfl_xor(ss, 16);
-  ss += __shfl_xor(ss, 32);
+  // Context norm: the token row's sum of squares, applied as one scale of
+  // the FP32 result.
   const float r = rsqrtf(ss / (float)a.hidden + a.eps_ctx);
   #pragma unroll
-  for (int mt = 0; mt < 8; ++mt) acc[mt] *= r;
+  for (int i = 0; i < 2; ++i)
+    #pragma unroll
+    for (int e = 0; e < 8; ++e) v[i][e] *= r;
 
   // The request holding this token: the last record whose first token <= tok.
   int lo = 0, hi = a.n_req - 1;
@@ -90,23 +89,23 @@ __global__ __launch_bounds__(HG_WAVES * WAVE) void draft_kv_project_kernel(Draft
   const int32_t* rq = a.req + 4 * lo;
   const int pos = rq[1] + (tok - rq[2]);
   if (!is_v) {
-    head_rms_norm(acc, a.k_norm + (size_t)layer * HD, a.eps_k, grp);
-    head_rope(acc, a.inv_freq, (float)pos, grp);
+    head_rms_norm(v, nw, a.eps_k, head_row_sumsq(v, smem));
+    HeadRope rope;
+    rope.compute(a.inv_freq, (float)pos);
+    head_rope(v, rope);
   }
-  const bool valid = tw + col < a.tokens;
+  const bool valid = row < a.tokens;
   if (a.flag) {
     bool bad = false;
     #pragma unroll
-    for (int mt = 0; mt < 8; ++mt)
+    for (int i = 0; i < 2; ++i)
       #pragma unroll
-      for (int e = 0; e < 4; ++e) bad |= !__builtin_isfinite(acc[mt][e]);
+      for (int e = 0; e < 8; ++e) bad |= !__builtin_isfinite(v[i][e]);
     if (__builtin_amdgcn_ballot_w64(bad && valid) && lane == 0) *a.flag = 1;   // idempotent vector store
   }
-  if (valid) {
-    bf16* out = (is_v ? a.v_pool : a.k_pool) + (size_t)layer * a.layer_stride + (size_t)rq[0] * a.slot_stride +
-                (size_t)head * a.head_stride + (size_t)pos * HD;
-    head_store(acc, out, grp);
-  }
+  bf16* out = (is_v ? a.v_pool : a.k_pool) + (size_t)layer * a.layer_stride + (size_t)rq[0] * a.slot_stride +
+              (size_t)head * a.head_stride + (size_t)pos * HD;
+  head_store(v, out, valid);
 }
 
 }  // namespace dspark
@@ -127,8 +126,9 @@ extern "C" int dspark_draft_kv_project(const void* x, int tokens, int hidden, co
   DSPARK_REQUIRE(layer_stride >= 0 && slot_stride >= 0 && head_stride >= HD && head_stride % 8 == 0 &&
                      slot_stride % 8 == 0 && layer_stride % 8 == 0,
                  "pool strides must be multiples of 8 elements (head stride >= 128)");
-  const uintptr_t any = (uintptr_t)x | (uintptr_t)w | (uintptr_t)k_pool | (uintptr_t)v_pool;
+  const uintptr_t any = (uintptr_t)x | (uintptr_t)w | (uintptr_t)k_pool | (uintptr_t)v_pool | (uintptr_t)inv_freq;
   DSPARK_REQUIRE(any % 16 == 0, "tensors must be 16-byte aligned");
+  DSPARK_REQUIRE((uintptr_t)k_norm % 8 == 0, "k_norm must be 8-byte aligned");
   const int64_t tiles = (tokens + HG_TOKENS - 1) / HG_TOKENS;
   DSPARK_REQUIRE(tiles * layers * 2 * HKV <= 0x7fffffffLL, "too many tokens");
   DraftProjArgs a{static_cast<const bf16*>(x), static_cast<const bf16*>(w), static_cast<const bf16*>(k_norm), inv_freq,

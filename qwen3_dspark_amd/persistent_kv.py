@@ -302,6 +302,7 @@ class PersistentTargetKV:
         self._tx_generation = None
         self._staged = set()
         self._tx_rows = 0
+        self._rope = {}                  # theta -> rotary table of the open transaction's rows
         self._receipt = None             # (ExternalWrite, completion event) while one is live
 
     # -- phase ------------------------------------------------------------
@@ -582,6 +583,7 @@ class PersistentTargetKV:
         tx = Transaction(self._transactions, handles, contexts, bucket, query_lengths)
         self._phase, self._tx, self._tx_generation = nxt, tx, self._ledger.generation
         self._staged, self._tx_rows, self._receipt = set(), sum(query_lengths), None
+        self._rope = {}                  # theta -> rotary table of this transaction's rows
         return tx
 
     @torch.no_grad()
@@ -605,7 +607,11 @@ class PersistentTargetKV:
         self._check_fused_storage('The fused prologue')
         if not isinstance(hidden, torch.Tensor) or hidden.ndim != 2 or hidden.shape[0] != self._tx_rows:
             raise ValueError('Hidden states must be [sum Q, hidden] for the transaction')
-        queries, _, _ = prologue(hidden, ws.positions, k_out=self.scratch_keys[layer], v_out=self.scratch_values[layer])
+        rope = self._rope.get(prologue.theta)
+        if rope is None:                 # once per transaction: every layer's rows sit at the same positions
+            rope = self._rope[prologue.theta] = prologue.rope_table(ws.positions)
+        queries, _, _ = prologue(hidden, ws.positions, k_out=self.scratch_keys[layer], v_out=self.scratch_values[layer],
+                                 rope=rope)
         self._staged.add(layer)
         return queries
 

@@ -7,6 +7,10 @@ dspark_qwen/persistent_qwen_target.py:45-95, RoPE as dspark_qwen/model.py:22-24)
 in one HIP launch per layer (dspark_qkv_prologue).  K/V can be written
 straight into a PersistentTargetKV transaction's scratch
 (PersistentTargetKV.stage_projected), which replaces stage_layer's copy.
+The rows' rotary cos/sin can be computed once (QKVPrologue.rope_table) and
+shared by every layer, as the model computes its position embeddings once
+per forward; the prologue then gives the same bits without its per-layer
+sincos.
 """
 import torch
 
@@ -42,6 +46,7 @@ class QKVPrologue:
             raise ValueError('eps and theta must be positive')
         self.hidden = hidden
         self.eps = float(eps)
+        self.theta = float(theta)
         self.weights = tuple(t.detach().contiguous() for t in (q_proj, k_proj, v_proj, q_norm, k_norm))
         self.inv_freq = rope_inv_freq(theta).to(self.device)
 
@@ -54,17 +59,39 @@ class QKVPrologue:
         return cls(attn.q_proj.weight, attn.k_proj.weight, attn.v_proj.weight, attn.q_norm.weight,
                    attn.k_norm.weight, eps=cfg.rms_norm_eps, theta=theta)
 
-    def __call__(self, hidden, positions, *, k_out=None, v_out=None):
+    def _positions(self, positions, t):
+        if (not isinstance(positions, torch.Tensor) or positions.dtype != torch.long or positions.shape != (t,)
+                or positions.device != self.device or not positions.is_contiguous()):
+            raise ValueError('Positions must be a contiguous int64 [T] device tensor')
+
+    def rope_table(self, positions):
+        """The rows' rotary table [T, 128] float32: cos(positions[t] *
+        inv_freq[d]) for d < 64, then the sines (one dspark_rope_table
+        launch).  Valid for every prologue of the same theta on these
+        positions."""
+        t = positions.shape[0] if isinstance(positions, torch.Tensor) and positions.ndim == 1 else 0
+        if t < 1:
+            raise ValueError('Positions must be a contiguous int64 [T] device tensor')
+        self._positions(positions, t)
+        table = torch.empty((t, HEAD_DIM), dtype=torch.float32, device=self.device)
+        _native.call('dspark_rope_table', self.inv_freq.data_ptr(), positions.data_ptr(), t, table.data_ptr(),
+                     _native.stream_handle(self.device))
+        return table
+
+    def __call__(self, hidden, positions, *, k_out=None, v_out=None, rope=None):
         """hidden [T, H] bf16, positions [T] int64 (device) -> (q [T,16,128],
         k, v [T,8,128]).  k_out/v_out: optional destinations whose token rows
-        are 8*128 elements apart (e.g. a scratch layer); they are returned."""
+        are 8*128 elements apart (e.g. a scratch layer); they are returned.
+        rope: optional rope_table(positions) of a prologue with this theta."""
         t = hidden.shape[0] if isinstance(hidden, torch.Tensor) and hidden.ndim == 2 else 0
         if (t < 1 or hidden.shape[1] != self.hidden or hidden.dtype != torch.bfloat16
                 or hidden.device != self.device or not hidden.is_contiguous()):
             raise ValueError('Hidden states must be contiguous bf16 [T, hidden] on the prologue device')
-        if (not isinstance(positions, torch.Tensor) or positions.dtype != torch.long or positions.shape != (t,)
-                or positions.device != self.device or not positions.is_contiguous()):
-            raise ValueError('Positions must be a contiguous int64 [T] device tensor')
+        self._positions(positions, t)
+        if rope is not None and (not isinstance(rope, torch.Tensor) or rope.dtype != torch.float32
+                                 or tuple(rope.shape) != (t, HEAD_DIM) or rope.device != self.device
+                                 or not rope.is_contiguous()):
+            raise ValueError('Rotary table must be a contiguous float32 [T, 128] device tensor (rope_table)')
         q = torch.empty((t, Q_HEADS, HEAD_DIM), dtype=torch.bfloat16, device=self.device)
         outs = []
         for o in (k_out, v_out):
@@ -77,7 +104,7 @@ class QKVPrologue:
             outs.append(o)
         wq, wk, wv, qn, kn = self.weights
         _native.call('dspark_qkv_prologue', hidden.data_ptr(), wq.data_ptr(), wk.data_ptr(), wv.data_ptr(),
-                     qn.data_ptr(), kn.data_ptr(), self.inv_freq.data_ptr(), positions.data_ptr(), t, self.hidden,
-                     self.eps, q.data_ptr(), outs[0].data_ptr(), outs[1].data_ptr(), KV_HEADS * HEAD_DIM,
-                     _native.stream_handle(self.device))
+                     qn.data_ptr(), kn.data_ptr(), self.inv_freq.data_ptr(), positions.data_ptr(),
+                     rope.data_ptr() if rope is not None else None, t, self.hidden, self.eps, q.data_ptr(),
+                     outs[0].data_ptr(), outs[1].data_ptr(), KV_HEADS * HEAD_DIM, _native.stream_handle(self.device))
         return q, outs[0], outs[1]

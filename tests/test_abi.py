@@ -63,7 +63,7 @@ def test_workspace_size_formula():
                                   'dspark_draft_attn_fwd',
                                   'dspark_txn_metadata', 'dspark_kv_stage', 'dspark_kv_commit', 'dspark_kv_gather',
                                   'dspark_layout_build', 'dspark_pool_gather', 'dspark_pool_append',
-                                  'dspark_crop_plan', 'dspark_rows_rebuild', 'dspark_qkv_prologue',
+                                  'dspark_crop_plan', 'dspark_rows_rebuild', 'dspark_qkv_prologue', 'dspark_rope_table',
                                   'dspark_draft_kv_project', 'dspark_draft_kv_epilogue', 'dspark_logit_row_stats',
                                   'dspark_spec_verify',
                                   'dspark_logits_to_probs', 'dspark_sample_rows'])

@@ -51,6 +51,30 @@ def test_prologue_against_oracle(tokens):
     say(f'[prologue] T={tokens} max-abs q/k/v {errs}')
 
 
+@pytest.mark.parametrize('tokens', [448, 5])
+def test_rope_table_gives_the_same_bits(tokens):
+    """rope_table: cos/sin of the float32 angle positions * inv_freq to
+    float32 accuracy, and the prologue fed with it writes the same bits as
+    the prologue forming the angles itself."""
+    from qwen3_dspark_amd.prologue import QKVPrologue
+    gen = torch.Generator().manual_seed(SEED + 31 + tokens)
+    pro = QKVPrologue(*(t.to(DEV) for t in weights(gen)), eps=1e-6, theta=1e6)
+    x = randn_bf16(gen, tokens, HIDDEN).to(DEV)
+    pos = torch.randint(0, 40000, (tokens,), generator=gen)
+    table = pro.rope_table(pos.to(DEV))
+    plain = pro(x, pos.to(DEV))
+    fed = pro(x, pos.to(DEV), rope=table)
+    torch.cuda.synchronize()
+    angle = (pos.numpy().astype(np.float32)[:, None] * pro.inv_freq.cpu().numpy()[None, :]).astype(np.float64)
+    ref = np.concatenate([np.cos(angle), np.sin(angle)], axis=1)
+    assert np.abs(table.cpu().numpy().astype(np.float64) - ref).max() <= 2e-6
+    for a, b in zip(plain, fed):
+        assert torch.equal(a, b)
+    with pytest.raises(ValueError, match='Rotary table'):
+        pro(x, pos.to(DEV), rope=table[:, :64].contiguous())
+    say(f'[prologue] T={tokens} rope table bit-identical')
+
+
 def test_prologue_writes_scratch_and_feeds_attention():
     """stage_projected writes exactly the prologue's K/V into scratch (bit
     for bit), at the transaction's absolute positions, and the fused
