@@ -882,12 +882,18 @@ def timeline_probe(args, calls=5, samples=6):
         keys = ((rec[:, 6] >> np.uint64(32)) & np.uint64(0xffffffff)).astype(np.int64)
         span = float(t[:, 4].max())
         meta, first, stream, merge = (t[:, 1] - t[:, 0], t[:, 2] - t[:, 1], t[:, 3] - t[:, 2], t[:, 4] - t[:, 3])
-        gaps, busy = [], []
+        gaps, busy, stream_gaps = [], [], []
         for c in np.unique(cu):
             sel = np.argsort(t[cu == c, 0])
             tc = t[cu == c][sel]
             gaps += list(tc[1:, 0] - tc[:-1, 4])
-            busy.append(float((tc[:, 4] - tc[:, 0]).sum()))
+            # between streams: one segment's stream end to the next one's first stage landed
+            stream_gaps += list(tc[1:, 2] - tc[:-1, 3])
+            covered, end = 0.0, -np.inf          # union of the CU's [start, written] intervals (they may overlap)
+            for a0, a1 in zip(tc[:, 0], tc[:, 4]):
+                covered += max(0.0, a1 - max(a0, end))
+                end = max(end, a1)
+            busy.append(float(covered))
         stream_gbs = keys * 2 * 128 * 2 / np.maximum(stream, 1e-3) * 1e-3     # one KV head: K + V rows
         wg = wg.reshape(-1, 4)
         wg = wg[(wg[:, 3] >> np.uint64(63)) == 1]
@@ -912,6 +918,8 @@ def timeline_probe(args, calls=5, samples=6):
             stream_us=float(np.median(stream)), merge_write_us=float(np.median(merge)),
             overhead_per_segment_us=float(np.median(meta + first + merge)),
             cu_gap_median_us=float(np.median(gaps)) if gaps else 0.0,
+            stream_gap_median_us=float(np.median(stream_gaps)) if stream_gaps else 0.0,
+            stream_gap_p90_us=float(np.percentile(stream_gaps, 90)) if stream_gaps else 0.0,
             cu_gap_p90_us=float(np.percentile(gaps, 90)) if gaps else 0.0,
             cu_busy_frac=float(np.sum(busy) / (span * len(busy))),
             end_p50_us=float(np.median(t[:, 4])), end_p90_us=float(np.percentile(t[:, 4], 90)),
@@ -922,6 +930,7 @@ def timeline_probe(args, calls=5, samples=6):
         log(f'[timeline] sample {sample}: span {span:.1f} us, {len(t)} segments on {rows[-1]["cus"]} CUs; '
             f'per segment: issue {rows[-1]["start_to_issue_us"]:.2f}, first stage {rows[-1]["issue_to_first_stage_us"]:.2f}, '
             f'merge+write {rows[-1]["merge_write_us"]:.2f} us; CU gap {rows[-1]["cu_gap_median_us"]:.2f} us; '
+            f'stream end to next first stage {rows[-1]["stream_gap_median_us"]:.2f} us; '
             f'busy {rows[-1]["cu_busy_frac"]:.3f}; tail {rows[-1]["tail_us"]:.1f} us')
     summary = {k: round(float(np.median([r[k] for r in rows])), 3) for k in rows[0] if all(k in r for r in rows)}
     print(json.dumps({'timeline': 'draft attention', 'workload': '64 requests, contexts log-uniform [256, 8192], '
