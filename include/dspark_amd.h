@@ -24,7 +24,7 @@ extern "C" {
 /* Thread-local message for the last failing call on this thread. */
 const char* dspark_last_error(void);
 
-/* ABI revision of this header (currently 6). */
+/* ABI revision of this header (currently 7). */
 int dspark_abi_version(void);
 
 /*
@@ -285,15 +285,18 @@ int dspark_draft_kv_project(const void* x, int tokens, int hidden, const void* w
 
 /*
  * The same projection after a library GEMM, for large appends: y [tokens,
- * y_stride] bf16 holds x Wfold^T (columns [layer][K, V][head][128], the
- * folded weights of dspark_draft_kv_project as one [layers*2*1024, hidden]
- * matrix); this applies the context-norm factor of x's rows, k_norm and
- * RoPE on K, and stores K/V into the pool exactly as dspark_draft_kv_project
- * does.  Row i of y and x is token token0 + i of the records, so a long
- * append can be projected in chunks.  Same flag convention.
+ * y_stride] holds x Wfold^T (columns [layer][K, V][head][128], the folded
+ * weights of dspark_draft_kv_project as one [layers*2*1024, hidden]
+ * matrix), FP32 (y_dtype 1: the GEMM's accumulator, so that every output is
+ * rounded to bf16 once, as dspark_draft_kv_project rounds it) or bf16
+ * (y_dtype 0: the reference's autocast rounding of k_proj / v_proj); this
+ * applies the context-norm factor of x's rows, k_norm and RoPE on K, and
+ * stores K/V into the pool exactly as dspark_draft_kv_project does.  Row i
+ * of y and x is token token0 + i of the records, so a long append can be
+ * projected in chunks.  Same flag convention.
  * Replaces the same reference code as dspark_draft_kv_project.
  */
-int dspark_draft_kv_epilogue(const void* y, int64_t y_stride, const void* x, int tokens, int token0,
+int dspark_draft_kv_epilogue(const void* y, int y_dtype, int64_t y_stride, const void* x, int tokens, int token0,
                              int hidden, const void* k_norm, int layers, const float* inv_freq,
                              const int32_t* req, int n_req, float eps_ctx, float eps_k, void* k_pool,
                              void* v_pool, int64_t layer_stride, int64_t slot_stride, int64_t head_stride,

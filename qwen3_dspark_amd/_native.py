@@ -47,8 +47,8 @@ SIGNATURES = {
     'dspark_qkv_prologue': (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _F, _P, _P, _P, _L, _P]),
     'dspark_rope_table': (_I, [_P, _P, _I, _P, _P]),
     'dspark_draft_kv_project': (_I, [_P, _I, _I, _P, _P, _I, _P, _P, _I, _F, _F, _P, _P, _L, _L, _L, _P, _P]),
-    'dspark_draft_kv_epilogue': (_I, [_P, _L, _P, _I, _I, _I, _P, _I, _P, _P, _I, _F, _F, _P, _P, _L, _L, _L, _P,
-                                      _P]),
+    'dspark_draft_kv_epilogue': (_I, [_P, _I, _L, _P, _I, _I, _I, _P, _I, _P, _P, _I, _F, _F, _P, _P, _L, _L, _L,
+                                      _P, _P]),
     'dspark_row_stats_bytes': (_L, [_I, _I]),
     'dspark_logit_row_stats': (_I, [_P, _I, _I, _I, _L, _D, _P, _P, _P]),
     'dspark_draw_workspace_bytes': (_L, [_I]),
@@ -60,7 +60,7 @@ SIGNATURES = {
     'dspark_rows_rebuild': (_I, [_PP, _PP, _PP, _I, _I, _L, _L, _L, _P, _L, _P]),
 }
 
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 
 class NativeError(RuntimeError):

@@ -36,4 +36,4 @@ int launch_status(const char* what) {
 
 extern "C" const char* dspark_last_error(void) { return g_error.c_str(); }
 
-extern "C" int dspark_abi_version(void) { return 6; }
+extern "C" int dspark_abi_version(void) { return 7; }

@@ -145,13 +145,13 @@ extern "C" int dspark_draft_kv_project(const void* x, int tokens, int hidden, co
 // From a few thousand tokens on, the projection is a plain GEMM-bound
 // problem (T x hidden by hidden x layers*2*1024) that hipBLASLt runs at a
 // much higher MFMA rate than the fused 64-token tiles above.  The host then
-// computes y = f Wfold^T (bf16, the folded weights as one
-// [layers*2*1024, hidden] matrix) and this kernel applies everything else:
-// the context-norm factor 1/sqrt(mean(f^2) + eps) of each token, k_norm and
-// RoPE on the K heads, and the store into each request's pool slot, with
-// the same finiteness flag.  y is rounded to bf16 once more than in the
-// fused kernel (at the GEMM output, where the reference's autocast rounds
-// k_proj / v_proj too).
+// computes y = f Wfold^T (the folded weights as one [layers*2*1024, hidden]
+// matrix) and this kernel applies everything else: the context-norm factor
+// 1/sqrt(mean(f^2) + eps) of each token, k_norm and RoPE on the K heads, and
+// the store into each request's pool slot, with the same finiteness flag.
+// y may be FP32 (the GEMM's accumulator, as the fused kernel keeps it: the
+// outputs are then rounded to bf16 once, at the same point) or bf16 (the
+// reference's autocast rounding of k_proj / v_proj).
 //
 // Work: 16 tokens per workgroup, one per 16-lane group; lane c of a group
 // holds dims 8c .. 8c+7 of a head, so each (token, head) is one coalesced
@@ -162,7 +162,7 @@ extern "C" int dspark_draft_kv_project(const void* x, int tokens, int hidden, co
 namespace dspark {
 
 struct DraftEpiArgs {
-  const bf16* y;             // [T, y_stride]: columns [layer][K or V][head][128]
+  const void* y;             // [T, y_stride] bf16 or FP32: columns [layer][K or V][head][128]
   const bf16* x;             // [T, hidden] fc output (for the context-norm factor)
   const bf16* k_norm;        // [layers][128]
   const float* inv_freq;     // [64]
@@ -183,6 +183,23 @@ struct DraftEpiArgs {
   float eps_k;
 };
 
+// Eight consecutive values of a y row as FP32.
+__device__ __forceinline__ void load_y8(const bf16* p, float (&v)[8]) {
+  const bf16x8 b = ld8(p);
+  #pragma unroll
+  for (int e = 0; e < 8; ++e) v[e] = (float)b[e];
+}
+__device__ __forceinline__ void load_y8(const float* p, float (&v)[8]) {
+  const f32x4 lo = *reinterpret_cast<const f32x4*>(p);
+  const f32x4 hi = *reinterpret_cast<const f32x4*>(p + 4);
+  #pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    v[e] = lo[e];
+    v[4 + e] = hi[e];
+  }
+}
+
+template <typename YT>
 __global__ __launch_bounds__(256) void draft_kv_epilogue_kernel(DraftEpiArgs a) {
   const int lane = threadIdx.x & 63;
   const int c = threadIdx.x & 15;                      // 8-dim chunk of a head
@@ -225,18 +242,18 @@ __global__ __launch_bounds__(256) void draft_kv_epilogue_kernel(DraftEpiArgs a) 
     float kw[8];
     #pragma unroll
     for (int e = 0; e < 8; ++e) kw[e] = (float)a.k_norm[(size_t)layer * HD + 8 * c + e];
-    const bf16* yl = a.y + (size_t)t * a.y_stride + (size_t)layer * 2 * KV_ROW;
+    const YT* yl = static_cast<const YT*>(a.y) + (size_t)t * a.y_stride + (size_t)layer * 2 * KV_ROW;
     bf16* kout = a.k_pool + (size_t)layer * a.layer_stride + (size_t)rq[0] * a.slot_stride + (size_t)pos * HD + 8 * c;
     bf16* vout = a.v_pool + (size_t)layer * a.layer_stride + (size_t)rq[0] * a.slot_stride + (size_t)pos * HD + 8 * c;
     #pragma unroll 2
     for (int h = 0; h < HKV; ++h) {
       // K head h: norm factor, k_norm, RoPE
-      const bf16x8 kv = ld8(yl + (size_t)h * HD + 8 * c);
       float k[8];
+      load_y8(yl + (size_t)h * HD + 8 * c, k);
       float kss = 0.f;
       #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        k[e] = (float)kv[e] * r;
+        k[e] *= r;
         kss += k[e] * k[e];
       }
       #pragma unroll
@@ -254,11 +271,12 @@ __global__ __launch_bounds__(256) void draft_kv_epilogue_kernel(DraftEpiArgs a) 
         ko[e] = (bf16)o;
       }
       // V head h: the norm factor only
-      const bf16x8 vv = ld8(yl + KV_ROW + (size_t)h * HD + 8 * c);
+      float vv[8];
+      load_y8(yl + KV_ROW + (size_t)h * HD + 8 * c, vv);
       bf16x8 vo;
       #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        const float o = (float)vv[e] * r;
+        const float o = vv[e] * r;
         bad |= !__builtin_isfinite(o);
         vo[e] = (bf16)o;
       }
@@ -273,13 +291,14 @@ __global__ __launch_bounds__(256) void draft_kv_epilogue_kernel(DraftEpiArgs a) 
 
 }  // namespace dspark
 
-extern "C" int dspark_draft_kv_epilogue(const void* y, int64_t y_stride, const void* x, int tokens, int token0,
+extern "C" int dspark_draft_kv_epilogue(const void* y, int y_dtype, int64_t y_stride, const void* x, int tokens, int token0,
                                         int hidden, const void* k_norm, int layers, const float* inv_freq,
                                         const int32_t* req, int n_req, float eps_ctx, float eps_k, void* k_pool,
                                         void* v_pool, int64_t layer_stride, int64_t slot_stride, int64_t head_stride,
                                         int32_t* flag, void* stream) {
   clear_error();
   DSPARK_REQUIRE(y && x && k_norm && inv_freq && req && k_pool && v_pool, "null pointer argument");
+  DSPARK_REQUIRE(y_dtype == 0 || y_dtype == 1, "y_dtype must be 0 (bf16) or 1 (fp32)");
   DSPARK_REQUIRE(tokens >= 1 && token0 >= 0 && hidden >= 128 && hidden % 128 == 0,
                  "need tokens >= 1, token0 >= 0 and hidden a multiple of 128");
   DSPARK_REQUIRE(layers >= 1 && layers <= 64, "layers must be in [1, 64] (got %d)", layers);
@@ -292,10 +311,14 @@ extern "C" int dspark_draft_kv_epilogue(const void* y, int64_t y_stride, const v
                  "pool strides must be multiples of 8 elements (head stride >= 128)");
   const uintptr_t any = (uintptr_t)y | (uintptr_t)x | (uintptr_t)k_pool | (uintptr_t)v_pool;
   DSPARK_REQUIRE(any % 16 == 0, "tensors must be 16-byte aligned");
-  DraftEpiArgs a{static_cast<const bf16*>(y), static_cast<const bf16*>(x), static_cast<const bf16*>(k_norm), inv_freq,
+  DraftEpiArgs a{y, static_cast<const bf16*>(x), static_cast<const bf16*>(k_norm), inv_freq,
                  req, static_cast<bf16*>(k_pool), static_cast<bf16*>(v_pool), y_stride, layer_stride, slot_stride,
                  head_stride, flag, tokens, token0, hidden, layers, n_req, eps_ctx, eps_k};
-  hipLaunchKernelGGL(draft_kv_epilogue_kernel, dim3((unsigned)((tokens + 15) / 16)), dim3(256), 0,
-                     static_cast<hipStream_t>(stream), a);
+  if (y_dtype)
+    hipLaunchKernelGGL(draft_kv_epilogue_kernel<float>, dim3((unsigned)((tokens + 15) / 16)), dim3(256), 0,
+                       static_cast<hipStream_t>(stream), a);
+  else
+    hipLaunchKernelGGL(draft_kv_epilogue_kernel<bf16>, dim3((unsigned)((tokens + 15) / 16)), dim3(256), 0,
+                       static_cast<hipStream_t>(stream), a);
   return launch_status("draft_kv_epilogue_kernel");
 }

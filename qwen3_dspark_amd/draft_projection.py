@@ -17,8 +17,11 @@ Two launches for all draft layers and requests:
 From GEMM_MIN_TOKENS appended tokens on, the k/v projection itself is a
 plain GEMM that hipBLASLt runs faster than the fused tiles: it then runs as
 one library GEMM per GEMM_CHUNK tokens (all layers' folded weights as one
-matrix) followed by dspark_draft_kv_epilogue (norm factor, k_norm, RoPE,
-pool store, flag).
+matrix, bf16 operands, FP32 output) followed by dspark_draft_kv_epilogue
+(norm factor, k_norm, RoPE, pool store, flag).  Both paths keep the
+projection in FP32 through the norms and RoPE and round every output to
+bf16 once, so the path a given append length takes changes only the
+accumulation order.
 """
 import torch
 
@@ -28,7 +31,7 @@ from .prologue import rope_inv_freq
 
 
 GEMM_MIN_TOKENS = 2048   # appends at least this long take the GEMM + epilogue path
-GEMM_CHUNK = 16384       # tokens per library GEMM (bounds its bf16 output)
+GEMM_CHUNK = 16384       # tokens per library GEMM (bounds its FP32 output: 640 MiB at 5 layers)
 PATHS = ('fused', 'gemm')
 
 
@@ -68,6 +71,8 @@ class DraftContextProjector:
         wc = context_norm.detach().float()
         folded = [torch.stack((kp.detach().float() * wc, vp.detach().float() * wc)) for kp, _, vp in layers]
         self.w = torch.stack(folded).to(torch.bfloat16).contiguous()          # [layers, 2, 1024, hidden]
+        # The GEMM path's right operand, stored transposed once: [hidden, layers*2*1024].
+        self.w_t = self.w.view(-1, self.w.shape[-1]).t().contiguous()
         self.k_norm = torch.stack([kn.detach() for _, kn, _ in layers]).contiguous()   # [layers, 128]
         self.inv_freq = rope_inv_freq(theta).to(self.device)
 
@@ -105,11 +110,10 @@ class DraftContextProjector:
                          self.k_norm.data_ptr(), self.layers, self.inv_freq.data_ptr(), records.data_ptr(), n_req,
                          self.eps, self.eps, keys.data_ptr(), values.data_ptr(), s[0], s[1], s[2], flag_ptr, stream)
             return
-        w = self.w.view(-1, self.hidden)
         for c0 in range(0, t, GEMM_CHUNK):
             x = fc_out[c0:c0 + GEMM_CHUNK]
-            y = torch.nn.functional.linear(x, w)              # hipBLASLt, [rows, layers*2*1024] bf16
-            _native.call('dspark_draft_kv_epilogue', y.data_ptr(), y.stride(0), x.data_ptr(), x.shape[0], c0,
+            y = torch.mm(x, self.w_t, out_dtype=torch.float32)   # hipBLASLt, [rows, layers*2*1024] FP32
+            _native.call('dspark_draft_kv_epilogue', y.data_ptr(), 1, y.stride(0), x.data_ptr(), x.shape[0], c0,
                          self.hidden, self.k_norm.data_ptr(), self.layers, self.inv_freq.data_ptr(),
                          records.data_ptr(), n_req, self.eps, self.eps, keys.data_ptr(), values.data_ptr(), s[0],
                          s[1], s[2], flag_ptr, stream)
