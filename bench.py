@@ -1236,6 +1236,8 @@ def gpu_configs(dev, blocks=12, per_block=10):
          transaction);
       3. draft, 5 layers, 16 requests, contexts U[128, 1024], 4 blocks each
          (one at c, three at U[0, c]);
+    The draft workloads run with the default, batch-sized chunk and, for
+    comparison, with the fixed 4096-row chunk of the stress workload.
       4. verification, 28 layers, 32 requests, contexts U[256, 2048], timed
          like 2 (a call is one layer; a round is 28)."""
     import numpy as np
@@ -1244,6 +1246,7 @@ def gpu_configs(dev, blocks=12, per_block=10):
     from qwen3_dspark_amd.draft import DraftBatch, HipDraftAttention
     from qwen3_dspark_amd.kernels import SCALE
     from qwen3_dspark_amd.persistent_kv import Bucket, PersistentTargetKV
+    from qwen3_dspark_amd.schedule import DRAFT_CHUNK
     rng = np.random.default_rng(SEED + 41)
     gen = torch.Generator(device=dev).manual_seed(SEED + 41)
 
@@ -1279,10 +1282,17 @@ def gpu_configs(dev, blocks=12, per_block=10):
             rnd(layers, 7 * n, 8, 128)
         offs = [int(x) for x in np.concatenate([[0], np.cumsum(contexts)[:-1]])]
         batch = DraftBatch(dev, offs, contexts, anchors)
-        kernel = HipDraftAttention(dev)
+        kernel = HipDraftAttention(dev)          # the default: draft chunk sized to the batch
         kernel.plan(batch, ctx_k[0])
-        return timed(lambda l: kernel(q[l], bk[l], bv[l], ctx_k[l], ctx_v[l], batch, scale=SCALE), layers,
-                     draft_bytes(anchors), 7 * n)
+        res = timed(lambda l: kernel(q[l], bk[l], bv[l], ctx_k[l], ctx_v[l], batch, scale=SCALE), layers,
+                    draft_bytes(anchors), 7 * n)
+        res['draft_chunk'] = kernel.chunk_for(batch)
+        # the same calls with the stress workload's fixed 4096-row chunk, for comparison
+        fixed = HipDraftAttention(dev, chunk=DRAFT_CHUNK)
+        fixed.plan(batch, ctx_k[0])
+        res['fixed_4096_call_us'] = timed(lambda l: fixed(q[l], bk[l], bv[l], ctx_k[l], ctx_v[l], batch, scale=SCALE),
+                                          layers, draft_bytes(anchors), 7 * n)['call_us']
+        return res
 
     def verify_config(contexts, layers):
         n, cap = len(contexts), max(contexts) + 2 * Q_LEN

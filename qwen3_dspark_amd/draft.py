@@ -24,7 +24,7 @@ import torch
 from . import _native, backends
 from ._device import Workspace, cu_count, require_gfx950, upload
 from .kernels import HEAD_DIM, KV_HEADS, Q_HEADS, SCALE, _check_scale
-from .schedule import DRAFT_CHUNK, draft_run_count, draft_work, upload_work
+from .schedule import draft_chunk_for, draft_run_count, draft_work, upload_work
 
 BLOCK_SIZE = 7
 MAX_BLOCKS = 8
@@ -108,6 +108,7 @@ class DraftBatch:
         self.anchor_rows = meta[2 * n + 1:]
         self._offsets = {}
         self._work = {}
+        self._chunk = None            # the batch-sized draft chunk, once computed
         self._index_max = None
         self.physical_context_rows = self.context_rows
 
@@ -204,8 +205,11 @@ class HipDraftAttention:
     backend_name = backends.DRAFT_BLOCKS_BACKEND
     native_varlen_calls_per_layer = 1
 
-    def __init__(self, device, *, chunk=DRAFT_CHUNK, runs=None, persistent=1):
-        """persistent: 1 (the default) or 8 for one persistent workgroup per CU
+    def __init__(self, device, *, chunk=None, runs=None, persistent=1):
+        """chunk: rows per (chunk, KV head) item of the fixed-chunk plan, a
+        multiple of 64; None (the default) sizes it to each batch
+        (schedule.draft_chunk_for: about one item per CU, at most 4096 rows).
+        persistent: 1 (the default) or 8 for one persistent workgroup per CU
         taking (chunk, KV head) items, longest chunks first, from one device
         queue or from one queue per KV head (head g on XCD g); None for one
         workgroup per (run, KV head) dispatched by the hardware (the only
@@ -214,15 +218,15 @@ class HipDraftAttention:
         counters): use it from one stream."""
         self.device = require_gfx950(device)
         _native.load()
-        if chunk % 64:
-            raise ValueError('Draft chunk must be a multiple of 64')
+        if chunk is not None and (type(chunk) is not int or chunk <= 0 or chunk % 64):
+            raise ValueError('Draft chunk must be None or a positive multiple of 64')
         if runs is not None and (type(runs) is not int or runs < 0):
             raise ValueError('runs must be None (fixed chunks) or a nonnegative integer (balanced runs)')
         if persistent not in (None, 1, 8):
             raise ValueError('persistent must be None, 1 or 8 (queues)')
         if runs is not None and persistent is not None:
             raise ValueError('balanced runs (runs=...) need persistent=None')
-        self.chunk = int(chunk)
+        self.chunk = chunk          # None: sized to each batch
         self.runs = runs            # None: fixed chunks; else balanced runs per KV head (0: one per CU)
         self.persistent = persistent
         # Ticket counters of the persistent mode: zero now, zero again after every launch.
@@ -267,10 +271,20 @@ class HipDraftAttention:
             self._geometry_for = key
         capacity, tok_stride, head_stride = self._geometry
         offsets = batch.device_offsets(capacity)
-        work, n_work, n_runs, seg_anchors = batch.work(self.chunk, self.runs, capacity)
-        need = _native.load().dspark_attn_workspace_bytes(n_work, 0, batch.max_blocks, self.chunk)
+        chunk = self.chunk_for(batch)
+        work, n_work, n_runs, seg_anchors = batch.work(chunk, self.runs, capacity)
+        need = _native.load().dspark_attn_workspace_bytes(n_work, 0, batch.max_blocks, chunk)
         ws = self._workspace.get(need)
-        return capacity, tok_stride, head_stride, offsets, work, n_work, n_runs, seg_anchors, ws
+        return capacity, tok_stride, head_stride, offsets, work, n_work, n_runs, seg_anchors, ws, chunk
+
+    def chunk_for(self, batch):
+        """The fixed chunk the plan of `batch` uses: the constructor's, or
+        sized to the batch's visible context rows."""
+        if self.chunk is not None:
+            return self.chunk
+        if batch._chunk is None:
+            batch._chunk = draft_chunk_for(sum(max(b) for b in batch.anchors), cu_count(self.device))
+        return batch._chunk
 
     def __call__(self, query, block_keys, block_values, context_keys, context_values, batch, *, scale):
         """Q [7*blocks, 16, 128], block K/V [7*blocks, 8, 128], context K/V in
@@ -299,8 +313,8 @@ class HipDraftAttention:
             raise ValueError('Context K (bf16 or fp32) and V (bf16) must be matching contiguous tensors on the GPU')
         if block_keys.dtype != context_keys.dtype:
             raise ValueError('Backbone/cache precision mismatch')
-        capacity, tok_stride, head_stride, offsets, work, n_work, n_runs, seg_anchors, ws = self.plan(batch,
-                                                                                                      context_keys)
+        capacity, tok_stride, head_stride, offsets, work, n_work, n_runs, seg_anchors, ws, chunk = self.plan(
+            batch, context_keys)
         out = torch.empty(query.shape, dtype=torch.bfloat16, device=self.device)
         bound = max(batch.context_rows, 1)
         _native.call('dspark_draft_attn_fwd', _native.ptr(query), int(query.dtype == torch.float32),
@@ -308,7 +322,7 @@ class HipDraftAttention:
                      _native.ptr(batch.context_indices), _native.ptr(offsets), _native.ptr(batch.ctx_len),
                      tok_stride, head_stride, _native.ptr(block_keys), _native.ptr(block_values),
                      _native.ptr(batch.cu_blocks), _native.ptr(batch.anchor_rows), batch.request_count, bound,
-                     batch.max_blocks, float(SCALE), self.chunk, _native.ptr(work), n_work, n_runs,
+                     batch.max_blocks, float(SCALE), chunk, _native.ptr(work), n_work, n_runs,
                      self._workgroups, self.persistent or 0, _native.ptr(self._queue),
                      _native.ptr(seg_anchors) if self.persistent else None,
                      _native.ptr(out), _native.ptr(ws), ws.numel(), _native.stream_handle(self.device))
@@ -379,7 +393,7 @@ class DraftKVPool:
     GROW_ALIGN = 256
 
     def __init__(self, *, layers, slots, capacity, heads=KV_HEADS, dim=HEAD_DIM, dtype=torch.bfloat16,
-                 key_dtype=None, value_dtype=None, device='cuda', chunk=DRAFT_CHUNK, projector=None,
+                 key_dtype=None, value_dtype=None, device='cuda', chunk=None, projector=None,
                  growable=False):
         if any(type(n) is not int or n < 1 for n in (layers, slots, capacity, heads, dim)):
             raise ValueError('All pool sizes must be positive integers')

@@ -28,7 +28,6 @@ from ._device import require_gfx950
 from .draft import BLOCK_SIZE, MAX_BLOCKS, DraftKVPool
 from .draft_projection import DraftContextProjector
 from .kernels import HEAD_DIM, KV_HEADS, Q_HEADS
-from .schedule import DRAFT_CHUNK
 
 
 def _rotate(x, cos, sin):
@@ -87,7 +86,7 @@ class PackedDraft:
     INITIAL_CAPACITY = 1024
 
     def __init__(self, draft, *, native_backend=None, test_kernel=None, slots=None, capacity=None,
-                 chunk=DRAFT_CHUNK):
+                 chunk=None):
         if draft.training:
             raise ValueError('Packed draft is inference-only; call eval first')
         if test_kernel is not None:

@@ -46,6 +46,7 @@ MIN_DRAFT_SEGMENT = 1024      # fewest context rows a draft run is given
 # Fixed draft chunks when no list is given (a chunk carries up to 8 blocks
 # of FP32 partials, so draft chunks are coarser).
 DRAFT_CHUNK = 4096
+MIN_DRAFT_CHUNK = 256         # the batch-sized draft chunk never falls below this many rows
 WORK_INTS = 8
 REQ_INTS = 4
 
@@ -314,6 +315,19 @@ def draft_work(context_lengths, cu_blocks, anchors, groups=None, *, chunk=None, 
                     lambda r, k0, k1, slot: (r, k0, k1, slot, cu_blocks[r], cu_blocks[r + 1] - cu_blocks[r], amax[r],
                                              off1[r]),
                     lambda r, first, count: (first, count, cu_blocks[r], cu_blocks[r + 1] - cu_blocks[r]))
+
+
+def draft_chunk_for(visible_rows, n_cu):
+    """Fixed draft chunk sized to a batch: its visible context rows (each
+    request's largest anchor, summed) cut into about one (chunk, KV head)
+    item per CU, in multiples of DRAFT_TILE rows, between MIN_DRAFT_CHUNK
+    and DRAFT_CHUNK.  A batch that fills the CUs at DRAFT_CHUNK keeps it; a
+    small one is cut finer, so that its few requests still spread over every
+    CU (at the price of split-K partials and their merge)."""
+    per_head = max(1, int(n_cu) // 8)
+    rows = -(-max(1, int(visible_rows)) // per_head)
+    rows = -(-rows // DRAFT_TILE) * DRAFT_TILE
+    return max(MIN_DRAFT_CHUNK, min(DRAFT_CHUNK, rows))
 
 
 def draft_run_count(total_rows, n_cu):

@@ -228,3 +228,21 @@ def test_xcd_speeds_size_the_runs_of_each_xcd():
         varlen_work([7] * 64, kl, list(range(64)), groups)
     with pytest.raises(ValueError, match='8 positive'):
         varlen_work([7] * 64, kl, list(range(64)), groups, xcd_speed=[1.0] * 7)
+
+
+def test_batch_sized_draft_chunk():
+    """About one (chunk, KV head) item per CU, multiples of 64 rows, clamped
+    to [256, 4096]: the 64-request stress batch keeps 4096, a 16-request
+    batch of short contexts is cut finer."""
+    from qwen3_dspark_amd.schedule import DRAFT_CHUNK, MIN_DRAFT_CHUNK, draft_chunk_for
+    assert draft_chunk_for(157046, 256) == DRAFT_CHUNK
+    assert draft_chunk_for(9216, 256) == 320                  # 9216 rows over 32 CUs per KV head: 288 -> 320
+    assert draft_chunk_for(224, 256) == MIN_DRAFT_CHUNK
+    assert draft_chunk_for(0, 256) == MIN_DRAFT_CHUNK
+    for rows in (1, 63, 64, 65, 5000, 70000, 10 ** 7):
+        for cus in (8, 80, 256, 304):
+            c = draft_chunk_for(rows, cus)
+            assert c % 64 == 0 and MIN_DRAFT_CHUNK <= c <= DRAFT_CHUNK
+            # at or above the floor and below the cap, chunks of this size give at most one item per CU per head
+            if MIN_DRAFT_CHUNK < c < DRAFT_CHUNK:
+                assert -(-rows // c) <= max(1, cus // 8)
