@@ -64,8 +64,17 @@ class DraftBatch:
 
     context_offsets[r]: see the module docstring for each pool form.
     context_lengths[r]: committed context rows c_r.
-    anchors[r]: sequence of block anchors, each in [0, c_r], 1..8 blocks.
+    anchors[r]: sequence of block anchors, each in [0, c_r], one or more.
     context_indices: optional int64 device tensor of physical pool rows.
+
+    The kernel attends at most MAX_BLOCKS blocks of a request per pass over
+    its context: a request with more blocks is planned as consecutive views
+    of at most MAX_BLOCKS blocks over the same context (each view streams
+    the context once).  Output rows stay block-major in the given order.
+    The per-request attributes below (context_offsets, context_lengths,
+    anchors, request_count, ...) describe these views, which is what the
+    kernel and the work counters see; `views[i]` names view i's request and
+    first block, and `requests` is the number of requests given.
     """
 
     def __init__(self, device, context_offsets, context_lengths, anchors, *, context_indices=None):
@@ -77,10 +86,16 @@ class DraftBatch:
             raise ValueError('One offset, context length and anchor list per request required')
         if any(c < 0 for c in lens) or any(o < 0 for o in offs):
             raise ValueError('Context offsets and lengths must be nonnegative')
-        if any(not 1 <= len(b) <= MAX_BLOCKS for b in blocks):
-            raise ValueError(f'Each request needs 1..{MAX_BLOCKS} draft blocks')
+        if any(not b for b in blocks):
+            raise ValueError('Each request needs at least one draft block')
         if any(not 0 <= a <= c for b, c in zip(blocks, lens) for a in b):
             raise ValueError('Every anchor must lie in [0, context length]')
+        self.requests = len(blocks)
+        views = [(r, j) for r, b in enumerate(blocks) for j in range(0, len(b), MAX_BLOCKS)]
+        self.views = tuple(views)
+        offs = [offs[r] for r, _ in views]
+        lens = [lens[r] for r, _ in views]
+        blocks = [blocks[r][j:j + MAX_BLOCKS] for r, j in views]
         if context_indices is not None:
             if (not isinstance(context_indices, torch.Tensor) or context_indices.dtype != torch.long
                     or context_indices.ndim != 1 or context_indices.device != self.device
@@ -643,7 +658,7 @@ class DraftKVPool:
 
     def batch(self, anchors):
         """DraftBatch over this pool for an ordered {request: anchors}
-        mapping (1..8 anchors in [0, length] each)."""
+        mapping (one or more anchors in [0, length] each)."""
         if not anchors:
             raise ValueError('Require active anchor requests')
         names = list(anchors)

@@ -25,7 +25,7 @@ import torch
 
 from . import backends
 from ._device import require_gfx950
-from .draft import BLOCK_SIZE, MAX_BLOCKS, DraftKVPool
+from .draft import BLOCK_SIZE, DraftKVPool
 from .draft_projection import DraftContextProjector
 from .kernels import HEAD_DIM, KV_HEADS, Q_HEADS
 
@@ -70,7 +70,7 @@ class PackedDraft:
       * native_backend must name this build's multi-block draft kernel
         (backends.DRAFT_BLOCKS_BACKEND); a CPU test_kernel is refused with
         the reference's message, since every draft here is on the GPU;
-      * backbone_blocks adds 1..8 blocks per request at any anchors
+      * backbone_blocks adds one or more blocks per request at any anchors
         (DSparkDraft.backbone's multi-anchor form, model.py:101-119);
         backbone is its one-block form at anchor = committed length.
     Draft weights in float32 (the reference's autocast form) are snapshotted
@@ -168,7 +168,7 @@ class PackedDraft:
 
     @torch.no_grad()
     def backbone_blocks(self, blocks):
-        """1..8 blocks per request: {request: (anchor tokens [1, n] long,
+        """One or more blocks per request: {request: (anchor tokens [1, n] long,
         n anchor positions in [0, length])}.  Block b holds its anchor token
         and MASK tokens at positions anchor_b .. anchor_b + block_size - 1 and
         sees context positions j < anchor_b plus its own rows
@@ -192,10 +192,10 @@ class PackedDraft:
             where = tuple(int(a) for a in where)
             n = len(where)
             if (not isinstance(anchor, torch.Tensor) or anchor.shape != (1, n) or anchor.dtype != torch.long
-                    or anchor.device != self.device or not 1 <= n <= MAX_BLOCKS
+                    or anchor.device != self.device or n < 1
                     or not bool(((anchor >= 0) & (anchor < vocab)).all())):
                 raise ValueError('Require one valid [1,1] long anchor per active request' if one_block else
-                                 f'Require [1, n] long anchor tokens for 1..{MAX_BLOCKS} blocks per request')
+                                 'Require [1, n] long anchor tokens for n >= 1 blocks per request')
             if any(not 0 <= a <= length for a in where):
                 raise ValueError('Every anchor must lie in [0, committed length]')
             block = anchor.new_full((n, size), self.mask_token_id)

@@ -82,6 +82,28 @@ def test_multi_block_against_oracle(dev, name, contexts, blocks):
         assert torch.equal(run(dev, kernel, c2), 2 * out)
 
 
+def test_more_than_eight_blocks_per_request(dev):
+    """A request with more blocks than one pass of the kernel holds (8) is
+    planned as consecutive views over the same context (DSparkDraft.backbone
+    takes any number of anchors, model.py:101-119): 11 + 3 blocks meet the
+    oracle, and equal bit for bit the same blocks given as separate requests
+    of at most 8 blocks over the same context rows."""
+    from qwen3_dspark_amd.draft import DraftBatch, HipDraftAttention
+    say('[draft] 11 + 3 blocks')
+    rng = np.random.default_rng(SEED + 811)
+    gen = torch.Generator().manual_seed(SEED + 811)
+    c = draft_case(gen, rng, [3000, 200], [11, 3])
+    ref, cu_b = oracle(c)
+    batch = DraftBatch(dev, c['offs'], c['lens'], c['anchors'])
+    assert batch.requests == 2 and batch.views == ((0, 0), (0, 8), (1, 0)) and batch.max_blocks == 8
+    split = dict(c, offs=[c['offs'][0], c['offs'][0], c['offs'][1]], lens=[3000, 3000, 200],
+                 anchors=[c['anchors'][0][:8], c['anchors'][0][8:], c['anchors'][1]])
+    for kernel in (HipDraftAttention(dev), HipDraftAttention(dev, chunk=1024)):
+        out = run(dev, kernel, c)
+        attention_gate(f64(out), ref, [(7 * cu_b[i], 7 * cu_b[i + 1]) for i in range(len(cu_b) - 1)])
+        assert torch.equal(run(dev, kernel, split), out)
+
+
 def test_single_block_equals_packed_noncausal_path(dev):
     """One block per request at anchor = c: the fused kernel and the packed
     noncausal varlen kernel over ctx ++ block both meet the oracle."""
@@ -185,7 +207,7 @@ def test_poison_isolation_and_contract(dev):
     with pytest.raises(ValueError):
         DraftBatch(dev, [0], [5], [[6]])
     with pytest.raises(ValueError):
-        DraftBatch(dev, [0], [5], [[1] * 9])
+        DraftBatch(dev, [0], [5], [[]])            # a request needs a block (more than 8 are fine)
     batch = DraftBatch(dev, c['offs'], c['lens'], c['anchors'])
     with pytest.raises(ValueError):
         kernel(c['q'].to(dev)[:7], c['bk'].to(dev), c['bv'].to(dev), c['ctx_k'].to(dev), c['ctx_v'].to(dev), batch, scale=SCALE)
