@@ -28,6 +28,7 @@ from .schedule import draft_chunk_for, draft_run_count, draft_work, upload_work
 
 BLOCK_SIZE = 7
 MAX_BLOCKS = 8
+APPEND_LAYERS = 16            # layers per dspark_pool_append launch (its pointer arrays)
 _QK_DTYPES = (torch.bfloat16, torch.float32)
 
 
@@ -416,8 +417,6 @@ class DraftKVPool:
         value_dtype = dtype if value_dtype is None else value_dtype
         if any(d not in (torch.bfloat16, torch.float32) for d in (dtype, key_dtype, value_dtype)):
             raise ValueError('Draft pool dtype must be bfloat16 or float32')
-        if layers > 16:
-            raise ValueError('At most 16 draft layers per pool')
         self.device = require_gfx950(device)
         _native.load()
         self.layers, self.slot_capacity, self.capacity, self.heads, self.dim = layers, slots, capacity, heads, dim
@@ -573,18 +572,24 @@ class DraftKVPool:
         else:
             parts = [(self.keys, None, ks, None, self._elems[0], strides[0]),
                      (None, self.values, None, vs, self._elems[1], strides[1])]
+        launches = 0
         for kp, vp, ksrc, vsrc, e, st in parts:
-            _native.call('dspark_pool_append', _native.ptr(kp), _native.ptr(vp),
-                         self.slot_capacity * H * C * D * e, H * C * D * e, C * D * e, D * e, C, H, D * e, e,
-                         self.layers, None if ksrc is None else _native.pointer_array(ksrc),
-                         None if vsrc is None else _native.pointer_array(vsrc), st[0], st[1], rows,
-                         dev_req.data_ptr(), len(order), self._flag.data_ptr() if check_finite else None,
-                         _native.stream_handle(self.device))
+            # one launch takes the source pointers of up to APPEND_LAYERS layers
+            for l0 in range(0, self.layers, APPEND_LAYERS):
+                l1 = min(self.layers, l0 + APPEND_LAYERS)
+                _native.call('dspark_pool_append', None if kp is None else _native.ptr(kp[l0]),
+                             None if vp is None else _native.ptr(vp[l0]),
+                             self.slot_capacity * H * C * D * e, H * C * D * e, C * D * e, D * e, C, H, D * e, e,
+                             l1 - l0, None if ksrc is None else _native.pointer_array(ksrc[l0:l1]),
+                             None if vsrc is None else _native.pointer_array(vsrc[l0:l1]), st[0], st[1], rows,
+                             dev_req.data_ptr(), len(order), self._flag.data_ptr() if check_finite else None,
+                             _native.stream_handle(self.device))
+                launches += 1
         if check_finite and int(self._flag.item()):
             raise RuntimeError('Nonfinite projected draft context')
         for request, n in order:
             self._lengths[request] += n
-        self.last_append_work = dict(requests=len(order), new_context_tokens=rows, append_launches=len(parts),
+        self.last_append_work = dict(requests=len(order), new_context_tokens=rows, append_launches=launches,
                                      appended_kv_bytes=self.layers * rows * H * D * sum(self._elems),
                                      cache_concatenation_kv_bytes=0)
         return self.last_append_work

@@ -170,3 +170,29 @@ def test_pool_attention_against_oracle(dev):
         ref = cref.draft_attention(bits(q), ck, cv, offs, list(lengths.values()), bits(bk), bits(bv), cu_b,
                                    [x for a in anchors.values() for x in a], scale=SCALE)
         attention_gate(out.float().cpu().numpy(), ref)
+
+
+def test_more_than_sixteen_layers_append_in_groups(dev):
+    """A pool of 20 layers (more than one append launch's 16 pointer slots):
+    the append runs per group of 16 layers, and every layer's rows land bit
+    for bit, for K and V in one launch and for an fp32-K pool (separate K
+    and V launches)."""
+    from qwen3_dspark_amd.draft import DraftKVPool
+    gen = torch.Generator().manual_seed(SEED + 20)
+    for key_dtype, launches in ((torch.bfloat16, 2), (torch.float32, 4)):
+        pool = DraftKVPool(layers=20, slots=3, capacity=64, device=dev, key_dtype=key_dtype,
+                           value_dtype=torch.bfloat16)
+        for r in ('a', 'b'):
+            pool.add_request(r)
+        rows = {'a': 5, 'b': 9}
+        proj = [(randn_bf16(gen, 14, 8, 128).to(key_dtype), randn_bf16(gen, 14, 8, 128)) for _ in range(20)]
+        work = pool.append_projected(rows, [(k.to(dev), v.to(dev)) for k, v in proj])
+        torch.cuda.synchronize()
+        assert work['append_launches'] == launches
+        assert pool.lengths == rows
+        kv = {r: pool.request_kv(r) for r in rows}
+        for layer, (k, v) in enumerate(proj):
+            for r, lo, hi in (('a', 0, 5), ('b', 5, 14)):
+                gk, gv = kv[r][layer]
+                assert torch.equal(gk[0].transpose(0, 1).cpu(), k[lo:hi])
+                assert torch.equal(gv[0].transpose(0, 1).cpu(), v[lo:hi])
