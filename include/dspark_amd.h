@@ -188,7 +188,8 @@ int dspark_verify_attn_staged_fwd(const void* q, const void* k_res, const void* 
  *   phys = ctx_idx ? ctx_idx[ctx_off[r] + j] : ctx_off[r] + j,
  * so both a slotted pool ([slots*cap, 8, 128]) and the append-order pool of
  * dspark_qwen/packed_draft.py ([1, 8, N, 128] with gather indices) are read
- * in place.  q/out [7*n_blocks,16,128]; k_blk/v_blk [7*n_blocks,8,128].
+ * in place.  Every ctx_idx entry a request addresses lies in [0, 2^31): the
+ * kernel reads the low 32 bits.  q/out [7*n_blocks,16,128]; k_blk/v_blk [7*n_blocks,8,128].
  * V (context and block) and out are bf16.  q_dtype / k_dtype select bf16 (0)
  * or fp32 (1) for Q and for K (context and block K share one type, with the
  * same element strides as V): fp32 values are rounded to bf16 (nearest even)

@@ -718,6 +718,7 @@ struct DraftSeg {
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef __attribute__((address_space(3))) bf16x8 lds_bf16x8;
 typedef __attribute__((address_space(3))) f32x4 lds_f32x4;
+typedef __attribute__((address_space(3))) int lds_i32;
 
 constexpr int DWAVES = 8;                            // waves per workgroup: 4 pairs x 2 key halves
 constexpr int DSTEP = 64;                            // context keys per ring stage
@@ -751,11 +752,16 @@ struct PairRing {
   static constexpr int Q_OFF = STAGES * STAGE_BYTES;
   static constexpr int Q_BYTES = KF32 ? 0 : 4 * 32 * ROWB;
   static constexpr int SMEM = Q_OFF + Q_BYTES;
+  // Indexed context only: per ring slot, each wave's copy of the stage's
+  // DSTEP physical row indices (32-bit), after the ring and Q.
+  static constexpr int IDX_OFF = SMEM;
+  static constexpr int IDX_BYTES = STAGES * DWAVES * DSTEP * 4;
   static constexpr int OWN_SLOT = (STAGES - 1) * STAGE_BYTES;
   static constexpr int MERGE_FLOATS = 64 + 2;              // per lane: O^T, max, sum
   static constexpr int MERGE_BYTES = MERGE_FLOATS * WAVE * 4;
   static_assert(PER_WAVE * DWAVES * 1024 == STAGE_BYTES, "stage pieces must divide evenly over the waves");
-  static_assert(SMEM <= 160 * 1024, "ring exceeds the LDS of a CU");
+  static_assert(SMEM + IDX_BYTES <= 158 * 1024, "ring exceeds the LDS of a CU");
+  static_assert(DSTEP == WAVE, "a stage's indices are one word per lane");
   static_assert(Q_BYTES == 0 || Q_BYTES == PER_WAVE * DWAVES * 1024, "a Q load is one piece round");
   // The half merge may reach into the own-row slot: a barrier separates
   // the own-block reads from the merge writes also when no context stage runs.
@@ -1062,13 +1068,17 @@ __device__ __forceinline__ void draft_pair_item(const DraftArgs& a, unsigned cha
         hi[ks] = *reinterpret_cast<const f32x4*>(qp + 16 * ks + 4);
       }
       #pragma unroll
-      for (int ks = 0; ks < 8; ++ks) qf[ks] = row_ok ? to_bf16x8(lo[ks], hi[ks]) : zero8();
+      for (int ks = 0; ks < 8; ++ks) qf[ks] = to_bf16x8(lo[ks], hi[ks]);
     } else {
       #pragma unroll
       for (int ks = 0; ks < 8; ++ks) qf[ks] = ld8(static_cast<const bf16*>(a.q) + qe + 16 * ks);
-      #pragma unroll
-      for (int ks = 0; ks < 8; ++ks) qf[ks] = row_ok ? qf[ks] : zero8();
     }
+    // Both forms complete here, before the row select: a select on a branch
+    // that skipped the loads would leave registers with loads possibly in
+    // flight, and the compiler would wait for them among the ring's loads.
+    settle(qf[0], qf[1], qf[2], qf[3], qf[4], qf[5], qf[6], qf[7]);
+    #pragma unroll
+    for (int ks = 0; ks < 8; ++ks) qf[ks] = row_ok ? qf[ks] : zero8();
     settle(qf[0], qf[1], qf[2], qf[3], qf[4], qf[5], qf[6], qf[7]);
   }
   const int off1 = __builtin_amdgcn_readfirstlane(sg.off1);
@@ -1076,11 +1086,11 @@ __device__ __forceinline__ void draft_pair_item(const DraftArgs& a, unsigned cha
 
   const char* kbase = static_cast<const char*>(a.k_ctx) + (size_t)g * a.head_stride * KEL;
   const char* vbase = reinterpret_cast<const char*>(a.v_ctx) + (size_t)g * a.head_stride * 2;
-  // Context row kk of this request (clamped into range) as a byte address.
+  // Consecutive context: row kk of this request (clamped into range) as a
+  // byte address.
   auto ctx_row = [&](const char* base, int el, int kk) -> const char* {
     kk = min(kk, kend - 1);
-    const int64_t phys = INDEXED ? a.ctx_idx[coff + kk] : coff + kk;
-    return base + (size_t)phys * (size_t)a.tok_stride * el;
+    return base + (size_t)(coff + kk) * (size_t)a.tok_stride * el;
   };
   // Own row `row` (0..63: pair row/16, block 2(row/16) + (row%16)/8, token
   // min(row%8, 6), clamped to the request's blocks) as an element index.
@@ -1089,6 +1099,17 @@ __device__ __forceinline__ void draft_pair_item(const DraftArgs& a, unsigned cha
     return (size_t)(BLOCK_ROWS * (b0 + b) + min(row & 7, BLOCK_ROWS - 1)) * KV_ROW + (size_t)g * HD;
   };
   const uint32_t smem_lds = lds_address(smem);
+  // Indexed context: the physical rows of stage s come through LDS.  Each
+  // wave loads its own copy of the stage's DSTEP indices (their low words;
+  // the indices lie below 2^31), clamped into range like ctx_row, together
+  // with the ring stage s - 2, so that they have landed when stage s issues
+  // and no compiler-visible load falls among the ring's loads.
+  const uint32_t idx_base = smem_lds + (uint32_t)(R::IDX_OFF + wave * DSTEP * 4);
+  auto idx_slot = [&](int step) { return idx_base + (uint32_t)((step % R::STAGES) * DWAVES * DSTEP * 4); };
+  auto issue_idx = [&](int step) {
+    const int kk = min(k0 + step * DSTEP + lane, kend - 1);
+    lds_dma4(a.ctx_idx + coff + kk, __builtin_amdgcn_readfirstlane(idx_slot(step)));
+  };
   // One slot of pieces of 1 KiB; wave w issues pieces PER_WAVE*w ..
   // +PER_WAVE-1 (the K/V choice is uniform per piece).
   //  * bf16 K / V piece: rows 4*pr .. +3; lane L fetches row 4*pr + L/16,
@@ -1117,10 +1138,22 @@ __device__ __forceinline__ void draft_pair_item(const DraftArgs& a, unsigned cha
       lds_dma16_nt(src, __builtin_amdgcn_readfirstlane(slot + (uint32_t)(piece * 1024)));
     }
   };
+  // Stage `step` of the context: with indices, the indices of stage
+  // step + STAGES - 1 load first (into the slot that stage step - 1 has
+  // finished with), then the stage's rows at the addresses read from LDS.
   auto issue = [&](int step) {
-    const int ks = k0 + step * DSTEP;
-    fill(smem_lds + (uint32_t)((step % R::STAGES) * R::STAGE_BYTES),
-         [&](int k) { return ctx_row(kbase, KEL, ks + k); }, [&](int k) { return ctx_row(vbase, 2, ks + k); }, 63);
+    const uint32_t slot = smem_lds + (uint32_t)((step % R::STAGES) * R::STAGE_BYTES);
+    if constexpr (INDEXED) {
+      issue_idx(step + R::STAGES - 1);
+      const uint32_t ix = idx_slot(step);
+      auto phys = [&](int k) { return (size_t)(uint32_t)*(const lds_i32*)(uintptr_t)(ix + 4 * k); };
+      fill(slot, [&](int k) { return kbase + phys(k) * (size_t)a.tok_stride * KEL; },
+           [&](int k) { return vbase + phys(k) * (size_t)a.tok_stride * 2; }, 63);
+    } else {
+      const int ks = k0 + step * DSTEP;
+      fill(slot, [&](int k) { return ctx_row(kbase, KEL, ks + k); }, [&](int k) { return ctx_row(vbase, 2, ks + k); },
+           63);
+    }
   };
 
   PairState st;
@@ -1130,13 +1163,11 @@ __device__ __forceinline__ void draft_pair_item(const DraftArgs& a, unsigned cha
   for (int D = 0; D < 4; ++D) st.o[D] = f32x16{};
   const int n_steps = kend > k0 ? (kend - k0 + DSTEP - 1) / DSTEP : 0;
 
-  // Nothing of the compiler's is in flight from here on (a previous item's
-  // stores have completed), so it places no vmcnt wait of its own among the
-  // ring's direct-to-LDS loads below.  (Without this wait a persistent
-  // workgroup gains nothing: the compiler then waits for the previous item's
-  // output stores itself, where their data registers are reused, which
-  // falls among this item's first ring loads.)
-  __builtin_amdgcn_s_waitcnt(0x0f70);   // vmcnt(0)
+  // No drain here: a previous item's output stores may still be in flight
+  // when this item's ring loads issue.  The ring's counted waits stay exact
+  // with them: loads complete in order among themselves, so an older store
+  // still pending only lengthens a vmcnt(N) wait, and the compiler's own Q
+  // loads above have completed before the first ring load.
   // Persistent mode: lane 0 of wave 1 (a key-half-1 wave, idle once it has
   // handed its state to the merge) draws the workgroup's next ticket when
   // this segment's stream ends (a ticket drawn at the start would reserve
@@ -1147,6 +1178,13 @@ __device__ __forceinline__ void draft_pair_item(const DraftArgs& a, unsigned cha
   auto draw = [&]() {
     if (fetcher) next_ticket = atomic_add_deferred(ticket_ctr, 1) + persistent_members(a);
   };
+  // Indexed: the first two stages' indices load first of all.
+  if constexpr (INDEXED) {
+    if (n_steps > 0) {
+      issue_idx(0);
+      issue_idx(1);
+    }
+  }
   // bf16 Q rows, issued first: slot row R = 32p + n holds tile row n of
   // pair p (rows with no query read block 0, token 0 and are zeroed later).
   const uint32_t q_lds_row = smem_lds + (uint32_t)(R::Q_OFF + (32 * pw + n) * ROWB);
@@ -1185,15 +1223,28 @@ __device__ __forceinline__ void draft_pair_item(const DraftArgs& a, unsigned cha
   }
   // Only stages that hold context are loaded, so the number of ring loads
   // still in flight behind a given one is known: all but the newest
-  // `behind` stages of PER_WAVE loads each have landed after wait_stages.
+  // `behind` stages of LPS loads each (PER_WAVE pieces, and with indices
+  // one index load) have landed after wait_stages.
+  constexpr int LPS = R::PER_WAVE + (INDEXED ? 1 : 0);
   auto wait_stages = [](int behind) {
     if (behind <= 0) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    else if (behind == 1) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(R::PER_WAVE) : "memory");
-    else if (behind == 2 || R::STAGES < 4) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * R::PER_WAVE) : "memory");
-    else asm volatile("s_waitcnt vmcnt(%0)" ::"n"(3 * R::PER_WAVE) : "memory");
+    else if (behind == 1) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(LPS) : "memory");
+    else if (behind == 2 || R::STAGES < 4) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * LPS) : "memory");
+    else asm volatile("s_waitcnt vmcnt(%0)" ::"n"(3 * LPS) : "memory");
   };
   static_assert(R::STAGES <= 4, "wait_stages covers at most three stages in flight");
+  static_assert(R::STAGES == 3 || !INDEXED, "the index prologue loads two stages");
   const int prologue = min(R::STAGES - 1, n_steps);
+  if constexpr (INDEXED) {
+    // The first two stages' indices have landed once at most the Q and own
+    // row loads issued after them are in flight.
+    if (n_steps > 0) {
+      const int after = (q_lds ? R::PER_WAVE : 0) + (last ? R::PER_WAVE : 0);
+      if (after == 0) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      else if (after == R::PER_WAVE) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(R::PER_WAVE) : "memory");
+      else asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * R::PER_WAVE) : "memory");
+    }
+  }
   #pragma unroll
   for (int p = 0; p < R::STAGES - 1; ++p)
     if (p < prologue) issue(p);
@@ -1411,14 +1462,14 @@ __device__ __forceinline__ void draft_persistent(const DraftArgs& a, unsigned ch
 template <bool INDEXED, bool KF32>
 __global__ __launch_bounds__(DWAVES * WAVE) void draft_attn_persistent_kernel(DraftArgs a) {
   // 1 KiB alignment: tile offsets are XORed into LDS addresses.
-  __shared__ __attribute__((aligned(1024))) unsigned char smem[PairRing<KF32>::SMEM];
+  __shared__ __attribute__((aligned(1024))) unsigned char smem[PairRing<KF32>::SMEM + (INDEXED ? PairRing<KF32>::IDX_BYTES : 0)];
   draft_persistent<INDEXED, KF32>(a, smem);
 }
 
 template <bool INDEXED, bool KF32>
 __global__ __launch_bounds__(DWAVES * WAVE) void draft_attn_kernel(DraftArgs a) {
   // 1 KiB alignment: tile offsets are XORed into LDS addresses.
-  __shared__ __attribute__((aligned(1024))) unsigned char smem[PairRing<KF32>::SMEM];
+  __shared__ __attribute__((aligned(1024))) unsigned char smem[PairRing<KF32>::SMEM + (INDEXED ? PairRing<KF32>::IDX_BYTES : 0)];
   const int g = blockIdx.x & 7;
   if (a.work) {
     // The run's range and (speculatively) record number `run`, which is the

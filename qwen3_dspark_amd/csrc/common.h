@@ -127,6 +127,12 @@ __device__ __forceinline__ void lds_dma16_nt(const void* gptr, uint32_t lds) {
   asm volatile("global_load_lds_dwordx4 %0, off nt" ::"v"(gptr), "{m0}"(lds) : "memory");
 }
 
+// Direct global->LDS load of 4 bytes per lane: lane L's word lands at LDS
+// byte address `lds` + 4*L; ordered like lds_dma16.
+__device__ __forceinline__ void lds_dma4(const void* gptr, uint32_t lds) {
+  asm volatile("global_load_lds_dword %0, off" ::"v"(gptr), "{m0}"(lds) : "memory");
+}
+
 __device__ __forceinline__ uint32_t lds_address(const void* p) {
   return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
 }

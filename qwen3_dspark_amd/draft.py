@@ -210,6 +210,8 @@ class DraftBatch:
                 if int(cat.min()) < 0:
                     raise ValueError('Negative context index')
                 self._index_max = int(cat.max())
+                if self._index_max >= 2 ** 31:
+                    raise ValueError('Context indices must lie below 2^31 (the kernel reads their low words)')
             else:
                 self._index_max = -1
         return self._index_max

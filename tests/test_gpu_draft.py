@@ -176,6 +176,50 @@ def test_pool_forms_are_bit_identical(dev):
     assert torch.equal(out, rows_out)
 
 
+def test_indexed_pool_long_contexts_every_mode(dev):
+    """The append-order pool [1,8,N,128] read through gather indices over
+    many ring stages (contexts up to 4100 rows, split-K chunks, an empty and
+    a one-row context), with NaN in every pool row no index addresses, for
+    a bf16 and an fp32 K pool and every scheduling mode: bit for bit the
+    row store's output under the same kernel settings, which meets the
+    oracle."""
+    from qwen3_dspark_amd.draft import HipDraftAttention
+    say('[draft] indexed pool, long contexts, every mode')
+    rng = np.random.default_rng(SEED + 41)
+    gen = torch.Generator().manual_seed(SEED + 41)
+    contexts, blocks = [3100, 700, 4100, 1, 0], [5, 8, 3, 1, 2]
+    c = draft_case(gen, rng, contexts, blocks, spare=0)
+    ref, cu_b = oracle(c)
+    n = sum(contexts) + 777
+    perm = rng.permutation(n)
+    indices, offs, cursor = [], [], 0
+    pool_k = torch.full((1, 8, n, 128), float('nan'), dtype=torch.bfloat16)
+    pool_v = torch.full_like(pool_k, float('nan'))
+    for o, l in zip(c['offs'], c['lens']):
+        offs.append(len(indices))
+        idx = perm[cursor:cursor + l]
+        cursor += l
+        indices += [int(x) for x in idx]
+        pool_k[0, :, idx] = c['ctx_k'][o:o + l].transpose(0, 1)
+        pool_v[0, :, idx] = c['ctx_v'][o:o + l].transpose(0, 1)
+    idx_t = torch.tensor(indices, dtype=torch.long, device=dev)
+    kernels = (HipDraftAttention(dev), HipDraftAttention(dev, chunk=1024), HipDraftAttention(dev, persistent=None),
+               HipDraftAttention(dev, persistent=8))
+    for kernel in kernels:
+        rows_out = run(dev, kernel, c)
+        attention_gate(f64(rows_out), ref, [(7 * cu_b[i], 7 * cu_b[i + 1]) for i in range(len(cu_b) - 1)])
+        for key_pool in (pool_k, pool_k.float()):
+            # an fp32 K pool takes fp32 block K (its values here are bf16-exact)
+            cc = dict(c, bk=c['bk'].to(key_pool.dtype))
+            out = run(dev, kernel, cc, ctx_k=key_pool, ctx_v=pool_v, indices=idx_t, offs=offs)
+            assert torch.equal(out, rows_out), (key_pool.dtype, kernel.persistent, kernel.chunk)
+    # The kernel reads 32-bit indices: a larger one is refused before launch.
+    bad = idx_t.clone()
+    bad[0] = 2 ** 31
+    with pytest.raises(ValueError, match='below 2'):
+        run(dev, kernels[0], c, ctx_k=pool_k, ctx_v=pool_v, indices=bad, offs=offs)
+
+
 def test_poison_isolation_and_contract(dev):
     from qwen3_dspark_amd.draft import DraftBatch, HipDraftAttention
     say('[draft] poison isolation')
