@@ -90,6 +90,10 @@ def parse():
                     help='per-workgroup phase timeline of the draft attention on the workload, from the timeline '
                          'build of the library (clock stamps per segment: start, first loads issued, first stage '
                          'landed, stream end, merge + write end), summarised per call')
+    ap.add_argument('--verify-timeline', action='store_true',
+                    help='per-workgroup start and end of the verification attention on the workload (timeline '
+                         'build), for the XCD-calibrated and the equal-run plan: the spread of workgroup end times '
+                         'that bounds the call, per XCD and per workgroup stream rate')
     ap.add_argument('--graph-ab', action='store_true',
                     help='only compare the captured 28-layer verification round with the same 28 eager calls on one '
                          'store: alternating blocks, each behind the same queued GPU work, outputs bitwise equal')
@@ -149,19 +153,24 @@ def verify_store(args, dev, layers=VERIFY_LAYERS, calibrate=True):
 
 
 def plan_ab(pool, handles, bucket, qv, kn, vn, speed, rounds=8):
-    """Verification calls planned with equal runs and with the XCD-calibrated
-    runs the timed rounds use, on the same store, alternating rounds of 28
-    calls; median per call (the calibrated plan is what `roofline` reports)."""
+    """Verification calls under three plans on the same store, alternating
+    rounds of 28 calls; median per call.  The timed rounds use
+    `xcd_calibrated` (what `roofline` reports): runs sized to the calibrated
+    XCD speeds, the second resident workgroup of each CU given
+    schedule.SECOND_SLOT_SHARE of a run's cost.  `equal_runs` drops the XCD
+    speeds, `no_slot_share` the second-slot share."""
     import numpy as np
     import torch
-    if speed is None:
-        return None
     out = torch.empty_like(qv)
-    plans = {'equal_runs': None, 'xcd_calibrated': speed}
+    plans = {'equal_runs': (None, True), 'xcd_calibrated': (speed, True), 'no_slot_share': (speed, False)}
+    if speed is None:
+        plans = {'xcd_calibrated': (None, True), 'no_slot_share': (None, False)}
     times = {n: [] for n in plans}
+    names = list(plans)
     for r in range(rounds + 1):
-        for name in (('equal_runs', 'xcd_calibrated') if r % 2 == 0 else ('xcd_calibrated', 'equal_runs')):
-            pool.set_xcd_speed(plans[name])
+        for name in (names if r % 2 == 0 else names[::-1]):
+            pool.set_xcd_speed(plans[name][0])
+            pool.set_slot_balance(plans[name][1])
             tx = pool.begin(handles, bucket)
             e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
             e0.record()
@@ -173,6 +182,7 @@ def plan_ab(pool, handles, bucket, qv, kn, vn, speed, rounds=8):
                 times[name].append((e0, e1))
     torch.cuda.synchronize()
     pool.set_xcd_speed(speed)
+    pool.set_slot_balance(True)
     return {n + '_call_ms': round(float(np.median([a.elapsed_time(b) for a, b in t])) / VERIFY_LAYERS, 5)
             for n, t in times.items()}
 
@@ -315,6 +325,8 @@ def main():
         return mfma_probe(args)
     if args.timeline:
         return timeline_probe(args)
+    if args.verify_timeline:
+        return verify_timeline_probe(args)
     if args.draft_ab:
         return draft_ab(args)
     if args.graph_ab:
@@ -944,6 +956,105 @@ def timeline_probe(args, calls=5, samples=6):
                       'samples': samples, 'median': summary, 'per_sample': rows}), flush=True)
 
 
+def verify_timeline_probe(args, samples=6):
+    """Per-workgroup timeline of the verification attention (DSPARK_TIMELINE
+    build): transactions of the workload's 28 layers on one store, rotating
+    over the plans of plan_ab (XCD-calibrated with the second-slot share,
+    without that share, equal runs with it); after each, the start and end
+    stamps of the last layer's workgroups.  Per call: span from the first
+    start to the last end, workgroup end times (p10, p50, p90, last), the
+    mean end of the workgroups dispatched first and second onto their CUs
+    (blockIdx.x below / at or above the CU count) and per XCD, the
+    per-workgroup stream rate (keys x 512 B over its own start-to-end time)
+    and `balanced_us`, the span a perfect balance of the same work at each
+    workgroup's own rate would give.  Medians over `samples` samples per
+    plan."""
+    os.environ['DSPARK_AMD_TIMELINE'] = '1'
+    import numpy as np
+    import torch
+
+    from qwen3_dspark_amd import _native
+    from qwen3_dspark_amd._device import cu_count
+    _native.load()
+    dev = torch.device('cuda:0')
+    torch.cuda.set_device(dev)
+    n_cu = cu_count(dev)
+    pool, handles, bucket, contexts, qv, kn, vn = verify_store(args, dev)
+    speed = pool.xcd_speed
+    out = torch.empty_like(qv)
+    host = np.zeros(8192 * 4, dtype=np.uint64)
+    tick_us = 0.01
+    plans = {'xcd_calibrated': (speed, True), 'no_slot_share': (speed, False), 'equal_runs': (None, True)}
+    rows = {n: [] for n in plans}
+    last = {}                 # per plan: the previous sample's rates by workgroup id and by CU
+    names = list(plans)
+    for sample in range(len(names) * (samples + 1)):
+        name = names[sample % len(names)]
+        pool.set_xcd_speed(plans[name][0])
+        pool.set_slot_balance(plans[name][1])
+        tx = pool.begin(handles, bucket)
+        for layer in range(VERIFY_LAYERS):
+            pool.attend(tx, layer, qv[layer], keys=kn[layer], values=vn[layer], out=out[layer])
+        pool.abort(tx)
+        _native.call('dspark_timeline_fetch_verify', host.ctypes.data, host.nbytes)
+        if sample < len(names):
+            continue                             # warm-up, one per plan
+        rec = host.reshape(-1, 4)
+        wid = np.nonzero((rec[:, 2] >> np.uint64(63)) == 1)[0]
+        rec = rec[wid]
+        t0 = float(rec[:, 0].min())
+        start = (rec[:, 0].astype(np.float64) - t0) * tick_us
+        end = (rec[:, 1].astype(np.float64) - t0) * tick_us
+        xcc = ((rec[:, 2] >> np.uint64(32)) & np.uint64(15)).astype(np.int64)
+        hw = (rec[:, 2] & np.uint64(0xffffffff)).astype(np.int64)
+        cu = xcc * 1000 + ((hw >> 8) & 0xff)
+        keys = (rec[:, 3] & np.uint64(0xffffffff)).astype(np.float64)
+        rate = keys * 512 / np.maximum(end - start, 1e-3) * 1e-3          # GB/s: K + V rows of one KV head
+        # Perfect balance at the measured per-workgroup rates: every
+        # workgroup busy until the same instant.
+        balanced = float(keys.sum() * 512 / (rate.sum() * 1e3)) + float(np.median(start))
+        # Is a workgroup's rate a property of its work (the same blockIdx
+        # each call) or of the CU it lands on?  Correlation with the previous
+        # sample of the same plan, matched by workgroup id and by CU.
+        by_wid = dict(zip(wid.tolist(), rate.tolist()))
+        by_cu = {}
+        for c, x in zip(cu.tolist(), rate.tolist()):
+            by_cu.setdefault(c, []).append(x)
+        by_cu = {c: float(np.mean(v)) for c, v in by_cu.items()}
+
+        def corr(a, b):
+            common = sorted(set(a) & set(b))
+            return float(np.corrcoef([a[k] for k in common], [b[k] for k in common])[0, 1]) if len(common) > 2 else 0.0
+        prev = last.get(name)
+        last[name] = (by_wid, by_cu)
+        rows[name].append(dict(
+            span_us=float(end.max()), workgroups=int(len(rec)), cus=int(len(np.unique(cu))),
+            start_max_us=float(start.max()), end_p10_us=float(np.percentile(end, 10)),
+            end_p50_us=float(np.median(end)), end_p90_us=float(np.percentile(end, 90)),
+            end_mean_us=float(end.mean()), balanced_us=balanced,
+            rate_p10_gbs=float(np.percentile(rate, 10)), rate_p50_gbs=float(np.median(rate)),
+            rate_p90_gbs=float(np.percentile(rate, 90)),
+            keys_min=int(keys.min()), keys_max=int(keys.max()),
+            rate_corr_by_workgroup=corr(prev[0], by_wid) if prev else float('nan'),
+            rate_corr_by_cu=corr(prev[1], by_cu) if prev else float('nan'),
+            cus_with_one_of_each=int(sum(1 for c in np.unique(cu)
+                                         if ((cu == c) & (wid < n_cu)).sum() == 1 and ((cu == c) & (wid >= n_cu)).sum() == 1)),
+            first_slot_end_mean_us=float(end[wid < n_cu].mean()) if (wid < n_cu).any() else 0.0,
+            second_slot_end_mean_us=float(end[wid >= n_cu].mean()) if (wid >= n_cu).any() else 0.0,
+            **{f'xcd{x}_end_mean_us': float(end[xcc == x].mean()) for x in range(8) if (xcc == x).any()}))
+        r = rows[name][-1]
+        log(f'[verify-timeline] {name}: span {r["span_us"]:.1f} us, ends p10/p50/p90 {r["end_p10_us"]:.1f}/'
+            f'{r["end_p50_us"]:.1f}/{r["end_p90_us"]:.1f} us, first/second slot mean end '
+            f'{r["first_slot_end_mean_us"]:.1f}/{r["second_slot_end_mean_us"]:.1f} us, balanced {balanced:.1f} us, '
+            f'rate p10/p50/p90 {r["rate_p10_gbs"]:.1f}/{r["rate_p50_gbs"]:.1f}/{r["rate_p90_gbs"]:.1f} GB/s')
+    pool.set_xcd_speed(speed)
+    pool.set_slot_balance(True)
+    summary = {n: {k: round(float(np.nanmedian([r[k] for r in v])), 3) for k in v[0]} for n, v in rows.items()}
+    print(json.dumps({'timeline': 'verification attention', 'workload': '64 requests, contexts log-uniform '
+                      '[256, 8192], 7 new rows each, last layer of 28', 'xcd_speed': speed, 'samples': samples,
+                      'median': summary, 'per_sample': rows}), flush=True)
+
+
 def stream_probe(gib=16, reps=10):
     """The streaming-read ceiling: dspark_stream_read over a `gib` GiB
     buffer (far beyond the last-level cache), each workgroup streaming its
@@ -1003,13 +1114,32 @@ def streaming_reference(dev, src, dst, reps=10):
 
 
 def kernel_source_hash():
-    """sha256 of the attention kernels' sources: stamps the traffic figures
-    measured with them."""
+    """sha256 of the attention kernels' product code: stamps the traffic and
+    trace figures measured with them.  Comments, blank lines and the
+    timeline build's `#ifdef DSPARK_TIMELINE` parts (kept up to their
+    `#else`) are left out, so that only a change to what the product library
+    compiles moves the stamp."""
     import hashlib
+    import re
     h = hashlib.sha256()
     for name in ('attn.hip', 'common.h'):
-        with open(os.path.join(ROOT, 'qwen3_dspark_amd', 'csrc', name), 'rb') as f:
-            h.update(f.read())
+        with open(os.path.join(ROOT, 'qwen3_dspark_amd', 'csrc', name)) as f:
+            text = f.read()
+        text = re.sub(r'/\*.*?\*/', '', text, flags=re.S)
+        skip = False
+        for line in text.splitlines():
+            code = line.split('//', 1)[0].strip()
+            if code.startswith('#ifdef DSPARK_TIMELINE'):
+                skip = True
+                continue
+            if skip and code.startswith('#else'):
+                skip = False
+                continue
+            if skip and code.startswith('#endif'):
+                skip = False
+                continue
+            if code and not skip:
+                h.update(code.encode() + b'\n')
     return h.hexdigest()
 
 

@@ -72,6 +72,7 @@ TIMELINE_SIGNATURES = {
     'dspark_timeline_bytes': (_L, []),
     'dspark_timeline_fetch': (_I, [_P, _L]),
     'dspark_timeline_fetch_wg': (_I, [_P, _L]),
+    'dspark_timeline_fetch_verify': (_I, [_P, _L]),
 }
 
 

@@ -599,6 +599,33 @@ __device__ __forceinline__ void varlen_run(const VarlenArgs& a, unsigned char* s
   }
 }
 
+// Timeline build (compiled with DSPARK_TIMELINE into a separate profiling
+// library; the product library has none of this): lane 0 of wave 0 of every
+// draft workgroup records, per segment it runs, the 100 MHz constant clock
+// at the segment's start, once its first ring loads are issued, once the
+// first context stage (or the own rows) has landed, at the end of the key
+// stream and after the half merge and output write, plus where it ran.  The
+// stamps are held in scalar registers and stored after the segment's write,
+// so the ring's load accounting sees no extra memory operation.  Every
+// verification workgroup of a work-list launch records its start and end.
+#ifdef DSPARK_TIMELINE
+constexpr int TL_WGS = 8192;                         // workgroups recorded
+constexpr int TL_ITEMS = 16;                         // segments recorded per workgroup
+constexpr int TL_WORDS = 8;
+__device__ uint64_t tl_stamps[TL_WGS * TL_ITEMS * TL_WORDS];
+// Persistent mode, per workgroup: entry, first ticket known, loop left, exit.
+__device__ uint64_t tl_wg[TL_WGS * 4];
+// Verification with a work list, per workgroup: start, end, where (HW_ID,
+// XCC_ID << 32, bit 63 set), keys streamed | segments << 32.
+__device__ uint64_t tl_vwg[TL_WGS * 4];
+__device__ __forceinline__ uint64_t tl_now() { return __builtin_amdgcn_s_memrealtime(); }
+#define TL_DECL uint64_t tl_t[5] = {0, 0, 0, 0, 0};
+#define TL_MARK(i) (tl_t[i] = tl_now())
+#else
+#define TL_DECL
+#define TL_MARK(i) ((void)0)
+#endif
+
 // With a work list, the 8 workgroups of run w (one per KV head g) all run
 // on XCD w mod 8: workgroups are dealt round-robin over the 8 XCDs, so
 // blockIdx.x = 8 (8 (w / 8) + g) + w mod 8 (the run count is a multiple of
@@ -616,12 +643,33 @@ __global__ __launch_bounds__(256, 2) void varlen_attn_kernel(VarlenArgs a) {
     const int32_t* range = a.work + WORK_INTS * a.n_work + run;
     const int b = min(max(range[0], 0), a.n_work);      // clamped: never past the records
     const int e = min(max(range[1], b), a.n_work);
+#ifdef DSPARK_TIMELINE
+    const uint64_t tl_start = tl_now();
+    int tl_keys = 0;
+#endif
     varlen_run<VERIFY>(a, smem, g, blockIdx.y, [&](int n, Segment& sg) {
       if (b + n >= e) return false;
       const int32_t* w = a.work + WORK_INTS * (b + n);
       sg = Segment{w[0], w[1], w[2], w[3], w[4], w[5], w[6], w[7]};
+#ifdef DSPARK_TIMELINE
+      tl_keys += sg.k1 - sg.k0;
+#endif
       return true;
     });
+#ifdef DSPARK_TIMELINE
+    const uint64_t tl_end = tl_now();
+    const int wid = blockIdx.x + gridDim.x * blockIdx.y;
+    if (threadIdx.x == 0 && wid < TL_WGS) {
+      uint32_t hw, xcc;
+      asm volatile("s_getreg_b32 %0, hwreg(HW_REG_HW_ID)" : "=s"(hw));
+      asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
+      uint64_t* t = tl_vwg + 4 * (size_t)wid;
+      t[0] = tl_start;
+      t[1] = tl_end;
+      t[2] = (uint64_t)hw | ((uint64_t)(xcc & 15) << 32) | ((uint64_t)1 << 63);
+      t[3] = (uint64_t)(uint32_t)tl_keys | ((uint64_t)(uint32_t)(e - b) << 32);
+    }
+#endif
     return;
   }
   varlen_run<VERIFY>(a, smem, g, blockIdx.y, [&](int n, Segment& sg) {
@@ -665,29 +713,6 @@ struct DraftArgs {
 constexpr int BLOCK_ROWS = 7;
 constexpr int MAX_BLOCKS = 8;                        // draft blocks per request
 constexpr int CHUNK_ALIGN = 64;                      // fixed chunks are multiples of this many keys
-
-// Timeline build (compiled with DSPARK_TIMELINE into a separate profiling
-// library; the product library has none of this): lane 0 of wave 0 of every
-// draft workgroup records, per segment it runs, the 100 MHz constant clock
-// at the segment's start, once its first ring loads are issued, once the
-// first context stage (or the own rows) has landed, at the end of the key
-// stream and after the half merge and output write, plus where it ran.  The
-// stamps are held in scalar registers and stored after the segment's write,
-// so the ring's load accounting sees no extra memory operation.
-#ifdef DSPARK_TIMELINE
-constexpr int TL_WGS = 8192;                         // workgroups recorded
-constexpr int TL_ITEMS = 16;                         // segments recorded per workgroup
-constexpr int TL_WORDS = 8;
-__device__ uint64_t tl_stamps[TL_WGS * TL_ITEMS * TL_WORDS];
-// Persistent mode, per workgroup: entry, first ticket known, loop left, exit.
-__device__ uint64_t tl_wg[TL_WGS * 4];
-__device__ __forceinline__ uint64_t tl_now() { return __builtin_amdgcn_s_memrealtime(); }
-#define TL_DECL uint64_t tl_t[5] = {0, 0, 0, 0, 0};
-#define TL_MARK(i) (tl_t[i] = tl_now())
-#else
-#define TL_DECL
-#define TL_MARK(i) ((void)0)
-#endif
 
 // One context segment of one request: keys [k0, k1) of request r (whose
 // blocks are b0 .. b0+nb, largest anchor amax).  The segment ending the
@@ -1982,6 +2007,20 @@ extern "C" int dspark_timeline_fetch(void* host, int64_t bytes) {
 
 extern "C" int64_t dspark_timeline_bytes(void) {
   return (int64_t)sizeof(uint64_t) * TL_WGS * TL_ITEMS * TL_WORDS;
+}
+
+// The verification workgroup stamps (TL_WGS x 4 words), then cleared.
+extern "C" int dspark_timeline_fetch_verify(void* host, int64_t bytes) {
+  clear_error();
+  const int64_t have = (int64_t)sizeof(uint64_t) * TL_WGS * 4;
+  DSPARK_REQUIRE(host && bytes == have, "need a host buffer of exactly %lld bytes", (long long)have);
+  DSPARK_REQUIRE(hipDeviceSynchronize() == hipSuccess, "device synchronisation failed");
+  DSPARK_REQUIRE(hipMemcpyFromSymbol(host, HIP_SYMBOL(tl_vwg), (size_t)have, 0, hipMemcpyDeviceToHost) == hipSuccess,
+                 "timeline copy failed");
+  void* dev = nullptr;
+  DSPARK_REQUIRE(hipGetSymbolAddress(&dev, HIP_SYMBOL(tl_vwg)) == hipSuccess && dev, "timeline symbol lookup failed");
+  DSPARK_REQUIRE(hipMemset(dev, 0, (size_t)have) == hipSuccess, "timeline clear failed");
+  return OK;
 }
 
 // The persistent-mode workgroup stamps (TL_WGS x 4 words), then cleared.

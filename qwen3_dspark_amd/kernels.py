@@ -101,9 +101,10 @@ class HipVarlenKernel:
             for k in layout.key_lengths:
                 starts.append(acc)
                 acc += k
-            runs = run_count(acc, cu_count(self.device), tiles)
+            n_cu = cu_count(self.device)
+            runs = run_count(acc, n_cu, tiles)
             records, n_segments, runs = segment_plan(self.split, layout.query_lengths, layout.key_lengths, starts,
-                                                     runs, self.chunk)
+                                                     runs, self.chunk, n_cu=n_cu)
             self._work = (upload_work(records, self.device), n_segments, runs)
             self._work_for = key
         return self._work

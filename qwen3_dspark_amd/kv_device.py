@@ -99,6 +99,7 @@ class HipKVDevice:
         self.max_rows, self.heads, self.dim, self.dtype = max_query_tokens, heads, dim, dtype
         self.chunk, self.split = chunk, split
         self.xcd_speed = None          # relative speed of each XCD for balanced plans (None: equal runs)
+        self.slot_balance = True       # balanced plans give second-resident workgroups SECOND_SLOT_SHARE
         self.elem = torch.empty((), dtype=dtype).element_size()
         self._keys = torch.zeros((layers, slots, heads, context_capacity, dim), dtype=dtype, device=self.device)
         self._values = torch.zeros_like(self._keys)
@@ -173,9 +174,11 @@ class HipKVDevice:
         the seven metadata arrays in one launch.  Raises before anything is
         published if the list does not fit or a launch fails."""
         key_lengths = [c + q for c, q in zip(contexts, query_lengths)]
-        runs = run_count(sum(key_lengths), cu_count(self.device), (shape.maximum_query_length + 7) // 8)
+        n_cu = cu_count(self.device)
+        runs = run_count(sum(key_lengths), n_cu, (shape.maximum_query_length + 7) // 8)
         records, _, _ = segment_plan(self.split, query_lengths, key_lengths, slots, runs, self.chunk,
-                                     self.launch_shape(shape), xcd_speed=self.xcd_speed)
+                                     self.launch_shape(shape), xcd_speed=self.xcd_speed,
+                                     n_cu=n_cu if self.slot_balance else None)
         if len(records) > ws.work.numel():
             raise ValueError('Work list exceeds the bucket workspace')
         r = len(slots)

@@ -436,6 +436,20 @@ class PersistentTargetKV:
         self._permit('admin')
         self.kv_device.xcd_speed = normalised(speed)
 
+    @property
+    def slot_balance(self):
+        """Whether later balanced plans give the runs whose workgroups are the
+        second resident on their CUs a smaller share of the cost
+        (schedule.SECOND_SLOT_SHARE; on by default)."""
+        return self.kv_device.slot_balance
+
+    def set_slot_balance(self, enabled):
+        """Switch the second-slot share of later balanced plans on or off."""
+        self._permit('admin')
+        if not isinstance(enabled, bool):
+            raise ValueError('slot balance must be True or False')
+        self.kv_device.slot_balance = enabled
+
     def calibrate_xcd(self, *, workgroups=1024, passes=2, clip=0.25):
         """Measure the read bandwidth each XCD gets from this store's resident
         K/V and size the runs of later balanced plans to it, so that the

@@ -23,6 +23,8 @@ the merge.
 
 With measured per-XCD speeds (xcd_speed), run w's share of the cost is
 proportional to the speed of its XCD, so that the XCDs finish together.
+With two resident workgroups per CU, the runs dispatched second onto their
+CUs get SECOND_SLOT_SHARE of that share (run_shares).
 
 Draft attention: the same balanced segments over the context rows each
 request streams (up to its largest anchor), one run per (workgroup, KV
@@ -39,6 +41,11 @@ MIN_SEGMENT = 256             # fewest keys a run is given (tiny calls use fewer
 RESIDENT_PER_CU = 2           # varlen/verify workgroups resident per CU (register budget)
 XCDS = 8                      # MI355X: workgroup b runs on XCD b mod 8; varlen runs come in whole rounds of 8
 SEGMENT_COST = 96             # keys' worth of fixed work per segment in balanced varlen plans (measured)
+# Cost share of a balanced varlen run whose workgroups are dispatched after
+# every CU already holds one: two resident workgroups share a CU, and the
+# later one's waves lose issue arbitration to the older ones, so it streams
+# ~15 % slower (measured; 0.6-0.9 all gain about the same).
+SECOND_SLOT_SHARE = 0.75
 DRAFT_TILE = 64               # draft cuts fall on multiples of the ring stage
 DRAFT_SEGMENT_COST = 512      # balanced draft plans: fixed cost of a segment, in context rows (measured)
 DRAFT_BLOCK_WEIGHT = 0.055    # balanced draft plans: extra cost of a row per block beyond the first (measured)
@@ -200,18 +207,45 @@ def xcd_shares(groups, xcd_speed):
     return [speed[w % XCDS] for w in range(int(groups))]
 
 
-def varlen_work(query_lengths, key_lengths, starts, groups, seg_cost=None, xcd_speed=None):
+def second_slot_runs(groups, n_cu):
+    """Runs whose workgroups are the second resident on their CUs, or an
+    empty set.  Run w's workgroups are blockIdx.x = 8 (8 (w / 8) + g) + w mod
+    8 (g = KV head); the dispatcher deals ids 0 .. n_cu - 1 one per CU first,
+    so with exactly RESIDENT_PER_CU = 2 workgroups per CU (8 groups = 2 n_cu)
+    and n_cu a multiple of 64 the runs w >= n_cu / 8 are the second ones.
+    Any other launch shape gets no distinction."""
+    groups = int(groups)
+    if n_cu is None or int(n_cu) % 64 or 8 * groups != RESIDENT_PER_CU * int(n_cu):
+        return frozenset()
+    return frozenset(range(int(n_cu) // 8, groups))
+
+
+def run_shares(groups, xcd_speed=None, n_cu=None):
+    """Cost share of each of `groups` runs: its XCD's speed (xcd_shares;
+    equal without xcd_speed), times SECOND_SLOT_SHARE for the runs of
+    second_slot_runs(groups, n_cu); None when every share is equal."""
+    shares = xcd_shares(groups, xcd_speed)
+    second = second_slot_runs(groups, n_cu)
+    if not second:
+        return shares
+    shares = shares or [1.0] * int(groups)
+    return [x * (SECOND_SLOT_SHARE if w in second else 1.0) for w, x in enumerate(shares)]
+
+
+def varlen_work(query_lengths, key_lengths, starts, groups, seg_cost=None, xcd_speed=None, n_cu=None):
     """Balanced plan: (flat int32 list, segment count, run count) for varlen (starts =
     first key row of each request) or verify (starts = resident slot of each
     request); groups = number of runs (workgroups per KV head); seg_cost
     (default SEGMENT_COST) the fixed cost of a segment in keys; xcd_speed
-    (8 relative speeds) weights each run by the speed of its XCD.  The cut
-    points depend on every request's length (and on xcd_speed), so a
-    request's output can differ in the last bits between batches;
-    request_work keeps them apart."""
+    (8 relative speeds) weights each run by the speed of its XCD; n_cu (the
+    device's CU count) gives the second resident workgroups of each CU
+    SECOND_SLOT_SHARE of a run's cost (run_shares).  The cut points depend
+    on every request's length (and on xcd_speed), so a request's output can
+    differ in the last bits between batches; request_work keeps them
+    apart."""
     cost = SEGMENT_COST if seg_cost is None else seg_cost
     return _segment_list(query_lengths, key_lengths, starts,
-                         _balanced_runs(key_lengths, groups, TILE, cost, shares=xcd_shares(groups, xcd_speed)))
+                         _balanced_runs(key_lengths, groups, TILE, cost, shares=run_shares(groups, xcd_speed, n_cu)))
 
 
 def request_work(query_lengths, key_lengths, starts, chunk, groups):
@@ -250,17 +284,18 @@ def varlen_list_bound(n_req, groups, rows_bound=0, chunk=None):
 SPLITS = ('balanced', 'request')
 
 
-def segment_plan(split, query_lengths, key_lengths, starts, groups, chunk, capacity=None, xcd_speed=None):
+def segment_plan(split, query_lengths, key_lengths, starts, groups, chunk, capacity=None, xcd_speed=None,
+                 n_cu=None):
     """(flat int32 list, segment count, run count) of the named plan; the
-    launch must pass the returned counts (n_work, n_groups).  xcd_speed:
-    see varlen_work (balanced plans only).
+    launch must pass the returned counts (n_work, n_groups).  xcd_speed,
+    n_cu: see varlen_work (balanced plans only).
 
     capacity = (segments, runs) lays the list out in regions of fixed size:
     the records padded to `segments`, the run ranges to `runs` (trailing runs
     empty).  Every transaction of a bucket then launches with the same
     arguments and grid, which a captured graph replays."""
     if split == 'balanced':
-        out, n_seg, runs = varlen_work(query_lengths, key_lengths, starts, groups, xcd_speed=xcd_speed)
+        out, n_seg, runs = varlen_work(query_lengths, key_lengths, starts, groups, xcd_speed=xcd_speed, n_cu=n_cu)
     elif split == 'request':
         out, n_seg, runs = request_work(query_lengths, key_lengths, starts, chunk, groups)
     else:

@@ -24,6 +24,7 @@ class CpuKVDevice:
         self.calls = []            # device-call names, in order
         self.fail = None           # name of a device call to fail once (injected fault)
         self.xcd_speed = None      # relative XCD speeds for balanced plans (the device half holds them)
+        self.slot_balance = True   # second-slot share of balanced plans (the device half holds it)
 
     def measure_xcd_speed(self, workgroups=1024, passes=2):
         self._enter('measure_xcd_speed')

@@ -20,9 +20,10 @@ def decode(out, n_seg, groups, n_req):
     return rec, ranges, reqs
 
 
-def check(query_lengths, key_lengths, starts, groups, chunk=None, seg_cost=None, xcd_speed=None):
+def check(query_lengths, key_lengths, starts, groups, chunk=None, seg_cost=None, xcd_speed=None, n_cu=None):
     if chunk is None:
-        out, n_seg, runs = varlen_work(query_lengths, key_lengths, starts, groups, seg_cost, xcd_speed=xcd_speed)
+        out, n_seg, runs = varlen_work(query_lengths, key_lengths, starts, groups, seg_cost, xcd_speed=xcd_speed,
+                                       n_cu=n_cu)
         assert runs == groups
     else:
         out, n_seg, runs = request_work(query_lengths, key_lengths, starts, chunk, groups)
@@ -246,3 +247,36 @@ def test_batch_sized_draft_chunk():
             # at or above the floor and below the cap, chunks of this size give at most one item per CU per head
             if MIN_DRAFT_CHUNK < c < DRAFT_CHUNK:
                 assert -(-rows // c) <= max(1, cus // 8)
+
+
+def test_second_slot_runs_get_a_smaller_share():
+    """With two resident workgroups per CU (8 x 64 runs on 256 CUs), the
+    runs whose workgroups are dispatched after every CU holds one (w >= 32:
+    blockIdx.x = 8 (8 (w / 8) + g) + w mod 8 >= 256 for every KV head g)
+    carry SECOND_SLOT_SHARE of the cost of the others; any other shape, or
+    no CU count, leaves the plan as it was."""
+    from qwen3_dspark_amd.schedule import (SECOND_SLOT_SHARE, run_shares, second_slot_runs, varlen_work,
+                                           xcd_shares)
+    second = second_slot_runs(64, 256)
+    assert second == frozenset(range(32, 64))
+    for w in range(64):
+        ids = [8 * (8 * (w // 8) + g) + w % 8 for g in range(8)]
+        assert all((i >= 256) == (w in second) for i in ids)
+    assert second_slot_runs(32, 256) == frozenset()          # one workgroup per CU
+    assert second_slot_runs(64, None) == frozenset()
+    assert second_slot_runs(8, 32) == frozenset()            # 32 CUs: not a multiple of 64
+    speed = [1.05, 0.95, 1.03, 0.97, 1.04, 0.96, 1.02, 0.98]
+    shares = run_shares(64, speed, 256)
+    base = xcd_shares(64, speed)
+    assert shares == [x * (SECOND_SLOT_SHARE if w >= 32 else 1.0) for w, x in enumerate(base)]
+    assert run_shares(64, None, None) is None and run_shares(64, speed, None) == base
+    # the plan: per-run cost (keys + SEGMENT_COST per segment) follows the shares
+    rng = np.random.default_rng(3)
+    kl = [int(x) for x in np.exp(rng.uniform(np.log(263), np.log(8199), size=64))]
+    loads, _ = check([7] * 64, kl, list(range(64)), 64, xcd_speed=speed, n_cu=256)
+    cost = [k + SEGMENT_COST * n for k, n in zip(loads, check.starts)]
+    total, norm = sum(cost), sum(shares)
+    for w in range(64):
+        assert abs(cost[w] - total * shares[w] / norm) <= 2 * (TILE + SEGMENT_COST)
+    assert sum(loads) == sum(kl)
+    assert varlen_work([7] * 64, kl, list(range(64)), 32, n_cu=256) == varlen_work([7] * 64, kl, list(range(64)), 32)

@@ -217,7 +217,15 @@ def test_xcd_speeds_are_validated_normalised_clipped_and_admin_only():
         pool.set_xcd_speed(None)
     with pytest.raises(RuntimeError, match='Outstanding verification transaction'):
         pool.calibrate_xcd()
+    with pytest.raises(RuntimeError, match='Outstanding verification transaction'):
+        pool.set_slot_balance(False)
     pool.abort(tx)
+    # the second-slot share: on by default, a bool, admin-only
+    assert pool.slot_balance is True
+    pool.set_slot_balance(False)
+    assert pool.slot_balance is False and pool.kv_device.slot_balance is False
+    with pytest.raises(ValueError, match='True or False'):
+        pool.set_slot_balance(1)
 
 
 def test_attention_staging_matches_independent_variable_prefix_sdpa():
