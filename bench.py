@@ -90,6 +90,9 @@ def parse():
                     help='per-workgroup phase timeline of the draft attention on the workload, from the timeline '
                          'build of the library (clock stamps per segment: start, first loads issued, first stage '
                          'landed, stream end, merge + write end), summarised per call')
+    ap.add_argument('--skew-sweep', action='store_true',
+                    help='only time the draft attention of the workload with V placed at increasing distances '
+                         'after K in one allocation (the kv_pair skew), alternating rounds on one pool')
     ap.add_argument('--verify-timeline', action='store_true',
                     help='per-workgroup start and end of the verification attention on the workload (timeline '
                          'build), for the XCD-calibrated and the equal-run plan: the spread of workgroup end times '
@@ -327,6 +330,8 @@ def main():
         return timeline_probe(args)
     if args.verify_timeline:
         return verify_timeline_probe(args)
+    if args.skew_sweep:
+        return skew_sweep(args)
     if args.draft_ab:
         return draft_ab(args)
     if args.graph_ab:
@@ -372,8 +377,9 @@ def main():
     kn = torch.randn(VERIFY_LAYERS, B * Q_LEN, 8, 128, generator=gen, device=dev).to(torch.bfloat16)
     vn = torch.randn(VERIFY_LAYERS, B * Q_LEN, 8, 128, generator=gen, device=dev).to(torch.bfloat16)
     # -- draft: head-major slotted context pool [5, 64, 8, 8192, 128] ----
-    dctx_k = torch.empty(DRAFT_LAYERS, B, 8, CAPACITY, 128, dtype=torch.bfloat16, device=dev)
-    dctx_v = torch.empty_like(dctx_k)
+    from qwen3_dspark_amd._device import kv_pair
+    # one allocation, V 32 MiB after K, as DraftKVPool lays its pool out (kv_pair)
+    dctx_k, dctx_v = kv_pair((DRAFT_LAYERS, B, 8, CAPACITY, 128), torch.bfloat16, torch.bfloat16, dev)
     for layer in range(DRAFT_LAYERS):
         dctx_k[layer].normal_(generator=gen)
         dctx_v[layer].normal_(generator=gen)
@@ -754,8 +760,8 @@ def traffic_probe(args):
     pool.abort(tx)
     torch.cuda.synchronize()
     del pool
-    ctx_k = torch.zeros(B, 8, CAPACITY, 128, dtype=torch.bfloat16, device=dev)
-    ctx_v = torch.zeros_like(ctx_k)
+    from qwen3_dspark_amd._device import kv_pair
+    ctx_k, ctx_v = kv_pair((B, 8, CAPACITY, 128), torch.bfloat16, torch.bfloat16, dev)
     n_rows = BLOCK * sum(len(a) for a in anchors)
     qd = torch.zeros(n_rows, 16, 128, dtype=torch.bfloat16, device=dev)
     kd = torch.zeros(n_rows, 8, 128, dtype=torch.bfloat16, device=dev)
@@ -796,8 +802,9 @@ def draft_ab(args, rounds=16):
     torch.cuda.set_device(dev)
     contexts, anchors, _ = workload(args.warmup + args.steps)
     gen = torch.Generator(device=dev).manual_seed(SEED)
-    ctx_k = torch.empty(DRAFT_LAYERS, B, 8, CAPACITY, 128, dtype=torch.bfloat16, device=dev)
-    ctx_v = torch.empty_like(ctx_k)
+    from qwen3_dspark_amd._device import kv_pair
+    # one allocation, V 32 MiB after K, as DraftKVPool lays its pool out (kv_pair)
+    ctx_k, ctx_v = kv_pair((DRAFT_LAYERS, B, 8, CAPACITY, 128), torch.bfloat16, torch.bfloat16, dev)
     for layer in range(DRAFT_LAYERS):
         ctx_k[layer].normal_(generator=gen)
         ctx_v[layer].normal_(generator=gen)
@@ -860,8 +867,9 @@ def timeline_probe(args, calls=5, samples=6):
     torch.cuda.set_device(dev)
     contexts, anchors, _ = workload(args.warmup + args.steps)
     gen = torch.Generator(device=dev).manual_seed(SEED)
-    ctx_k = torch.empty(DRAFT_LAYERS, B, 8, CAPACITY, 128, dtype=torch.bfloat16, device=dev)
-    ctx_v = torch.empty_like(ctx_k)
+    from qwen3_dspark_amd._device import kv_pair
+    # one allocation, V 32 MiB after K, as DraftKVPool lays its pool out (kv_pair)
+    ctx_k, ctx_v = kv_pair((DRAFT_LAYERS, B, 8, CAPACITY, 128), torch.bfloat16, torch.bfloat16, dev)
     for layer in range(DRAFT_LAYERS):
         ctx_k[layer].normal_(generator=gen)
         ctx_v[layer].normal_(generator=gen)
@@ -954,6 +962,59 @@ def timeline_probe(args, calls=5, samples=6):
                       '1..8 blocks each, 5 draft layers back to back', 'draft_chunk': draft.chunk,
                       'persistent': draft.persistent,
                       'samples': samples, 'median': summary, 'per_sample': rows}), flush=True)
+
+
+def skew_sweep(args, rounds=14, skews_mib=(0, 2, 4, 6, 8, 12, 16, 20, 24, 28, 32, 40, 48, 64, 96)):
+    """Draft attention of the workload (one layer's [64, 8, 8192, 128]
+    pool, 5 calls per round) with K fixed at the start of one allocation and
+    V placed `skew` MiB after K's end, every skew on the same allocation
+    (V rewritten before each skew's calls), rounds alternating in order;
+    median per call.  The outputs must be bitwise equal for every skew."""
+    import numpy as np
+    import torch
+
+    from qwen3_dspark_amd.draft import DraftBatch, HipDraftAttention
+    from qwen3_dspark_amd.kernels import SCALE
+    dev = torch.device('cuda:0')
+    torch.cuda.set_device(dev)
+    contexts, anchors, _ = workload(args.warmup + args.steps)
+    shape = (B, 8, CAPACITY, 128)
+    n = B * 8 * CAPACITY * 128
+    mib = 1 << 19                                        # bf16 elements per MiB
+    gen = torch.Generator(device=dev).manual_seed(SEED)
+    flat = torch.empty(2 * n + (max(skews_mib) + 2) * mib, dtype=torch.bfloat16, device=dev)
+    k = flat[:n].view(shape)
+    k.normal_(generator=gen)
+    src_v = torch.empty(shape, dtype=torch.bfloat16, device=dev)
+    src_v.normal_(generator=gen)
+    nq = BLOCK * sum(len(a) for a in anchors)
+    qd = torch.randn(nq, 16, 128, generator=gen, device=dev).to(torch.bfloat16)
+    bk = torch.randn(nq, 8, 128, generator=gen, device=dev).to(torch.bfloat16)
+    bv = torch.randn(nq, 8, 128, generator=gen, device=dev).to(torch.bfloat16)
+    batch = DraftBatch(dev, [i * CAPACITY for i in range(B)], contexts, anchors)
+    kernel = HipDraftAttention(dev)
+    times = {m: [] for m in skews_mib}
+    ref = None
+    for r in range(rounds):
+        for m in (skews_mib if r % 2 == 0 else skews_mib[::-1]):
+            v = flat[n + m * mib:2 * n + m * mib].view(shape)
+            v.copy_(src_v)
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for _ in range(DRAFT_LAYERS):
+                out = kernel(qd, bk, bv, k, v, batch, scale=SCALE)
+            e1.record()
+            e1.synchronize()
+            if ref is None:
+                ref = out.clone()
+            elif not torch.equal(out, ref):
+                raise AssertionError(f'draft output differs at skew {m} MiB')
+            if r >= 2:
+                times[m].append(e0.elapsed_time(e1) / DRAFT_LAYERS * 1e3)
+    res = {f'{m}_mib_us': round(float(np.median(t)), 2) for m, t in times.items()}
+    log('[skew-sweep] ' + ', '.join(f'{m} MiB {res[f"{m}_mib_us"]:.1f}' for m in skews_mib))
+    print(json.dumps({'skew_sweep': res, 'rounds': rounds - 2, 'calls_per_round': DRAFT_LAYERS,
+                      'k_base_mod_1gib': int(flat.data_ptr() % (1 << 30))}), flush=True)
 
 
 def verify_timeline_probe(args, samples=6):
@@ -1515,8 +1576,8 @@ def mfma_probe(args):
     contexts, anchors, _ = workload(args.warmup + args.steps)
     long_ctx = [CAPACITY] * B
     long_anchors = [[CAPACITY * (j + 1) // 8 for j in range(8)] for _ in range(B)]
-    ctx_k = torch.zeros(B, 8, CAPACITY, 128, dtype=torch.bfloat16, device=dev)
-    ctx_v = torch.zeros_like(ctx_k)
+    from qwen3_dspark_amd._device import kv_pair
+    ctx_k, ctx_v = kv_pair((B, 8, CAPACITY, 128), torch.bfloat16, torch.bfloat16, dev)
     draft = HipDraftAttention(dev)
     cases = {}
     for name, ctx, anc in (('draft_8_blocks_8192', long_ctx, long_anchors), ('draft_workload', contexts, anchors)):

@@ -22,7 +22,7 @@ The context K/V of one draft layer may live in
 import torch
 
 from . import _native, backends
-from ._device import Workspace, cu_count, require_gfx950, upload
+from ._device import Workspace, cu_count, kv_pair, require_gfx950, upload
 from .kernels import HEAD_DIM, KV_HEADS, Q_HEADS, SCALE, _check_scale
 from .schedule import draft_chunk_for, draft_run_count, draft_work, upload_work
 
@@ -428,8 +428,7 @@ class DraftKVPool:
                        torch.empty((), dtype=value_dtype).element_size())
         if any((dim * e) % 16 for e in self._elems):
             raise ValueError('A KV head row must be a multiple of 16 bytes')
-        self.keys = torch.zeros((layers, slots, heads, capacity, dim), dtype=key_dtype, device=self.device)
-        self.values = torch.zeros((layers, slots, heads, capacity, dim), dtype=value_dtype, device=self.device)
+        self.keys, self.values = kv_pair((layers, slots, heads, capacity, dim), key_dtype, value_dtype, self.device)
         self.growable = bool(growable)
         self.resizes = 0
         self._lengths = {}
@@ -476,8 +475,7 @@ class DraftKVPool:
         copy every slot's committed rows to the same slot and positions."""
         old_k, old_v, old_s, old_c = self.keys, self.values, self.slot_capacity, self.capacity
         shape = (self.layers, slots, self.heads, capacity, self.dim)
-        keys = torch.zeros(shape, dtype=self.key_dtype, device=self.device)
-        values = torch.zeros(shape, dtype=self.value_dtype, device=self.device)
+        keys, values = kv_pair(shape, self.key_dtype, self.value_dtype, self.device)
         used = max(self._lengths.values(), default=0)
         if used:
             keys[:, :old_s, :, :used].copy_(old_k[:, :, :, :used])

@@ -21,7 +21,7 @@ bucket, so a captured launch replays for every later transaction of it.
 import torch
 
 from . import _native
-from ._device import cu_count, require_gfx950, upload
+from ._device import KV_PAIR_SKEW, cu_count, kv_pair, require_gfx950, upload
 from .kernels import HEAD_DIM, KV_HEADS, SCALE
 from .schedule import REQ_INTS, WORK_INTS, run_count, segment_plan, varlen_list_bound
 
@@ -89,7 +89,7 @@ class HipKVDevice:
     """Resident and scratch KV in HBM plus the store's launches on gfx950."""
 
     def __init__(self, *, layers, slots, context_capacity, max_query_tokens, heads, dim, dtype, device, chunk,
-                 split):
+                 split, kv_skew=KV_PAIR_SKEW):
         # the copy kernels move 16-byte pieces of a head row
         if (dim * torch.empty((), dtype=dtype).element_size()) % 16:
             raise ValueError('A KV head row (dim * element size) must be a multiple of 16 bytes')
@@ -101,8 +101,9 @@ class HipKVDevice:
         self.xcd_speed = None          # relative speed of each XCD for balanced plans (None: equal runs)
         self.slot_balance = True       # balanced plans give second-resident workgroups SECOND_SLOT_SHARE
         self.elem = torch.empty((), dtype=dtype).element_size()
-        self._keys = torch.zeros((layers, slots, heads, context_capacity, dim), dtype=dtype, device=self.device)
-        self._values = torch.zeros_like(self._keys)
+        # K and V in one allocation, V kv_skew bytes after K (kv_pair)
+        self._keys, self._values = kv_pair((layers, slots, heads, context_capacity, dim), dtype, dtype, self.device,
+                                           kv_skew)
         self.keys = self._keys.permute(0, 1, 3, 2, 4)
         self.values = self._values.permute(0, 1, 3, 2, 4)
         self.scratch_keys = torch.zeros((layers, max_query_tokens, heads, dim), dtype=dtype, device=self.device)
