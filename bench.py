@@ -72,8 +72,8 @@ def parse():
     ap.add_argument('--traffic-summary', nargs=2, metavar=('FETCH_DIR', 'WRITE_DIR'),
                     help='turn the FETCH_SIZE and WRITE_SIZE passes of --traffic-probe into profiles/*_traffic.json')
     ap.add_argument('--trace-merge', nargs='+', metavar='JSON',
-                    help='merge --trace-summary outputs taken on different boxes (same kernel sources) into '
-                         'profiles/attn_64req_kernel_trace.json, each process tagged with its box')
+                    help='merge --trace-summary outputs of separate sets of processes (same kernel sources) into '
+                         'profiles/attn_64req_kernel_trace.json, each process tagged with its set')
     ap.add_argument('--trace-summary', nargs='+', metavar='DIR:LOG',
                     help='turn rocprofv3 --kernel-trace runs of the plain bench command (each a trace directory and '
                          'the bench line its process printed) into profiles/attn_64req_kernel_trace.json')
@@ -1322,18 +1322,19 @@ def trace_summary(pairs):
 
 def trace_merge(paths):
     """One profiles/attn_64req_kernel_trace.json from --trace-summary outputs
-    made on several boxes: the processes of output i are tagged box i + 1,
-    the ranges cover all of them; every output must carry the sha256 of the
+    of separate sets of processes (each set run back to back, the sets at
+    different times): the processes of output i are tagged set i + 1, the
+    ranges cover all of them; every output must carry the sha256 of the
     current kernel sources."""
     procs, want = [], kernel_source_hash()
-    for box, path in enumerate(paths, 1):
+    for n, path in enumerate(paths, 1):
         with open(path) as f:
             doc = json.load(f)
         if doc['kernel_source_sha256'] != want:
             raise SystemExit(f'{path} was measured on other kernel sources')
-        procs += [dict(p, box=box) for p in doc['processes']]
-    out = {'what': 'kernel traces of `python bench.py --no-cpu-baseline`, one process each, on '
-                   f'{len(paths)} boxes', 'processes': procs, 'kernel_source_sha256': want}
+        procs += [dict(p, set=n) for p in doc['processes']]
+    out = {'what': 'kernel traces of `python bench.py --no-cpu-baseline`, one process each, in '
+                   f'{len(paths)} sets', 'processes': procs, 'kernel_source_sha256': want}
     for kind in ('verify', 'draft'):
         fr = [p[kind]['frac_from_kernels'] for p in procs]
         out[kind + '_frac_from_kernels_range'] = [min(fr), max(fr)]
