@@ -84,24 +84,43 @@ class HostStaging:
     hot path (work lists, offsets, transaction requests, accepted counts).
 
     The pinned buffer is allocated once.  Each upload writes the next
-    256-byte-aligned region, enqueues an asynchronous copy on the current
-    stream and records an event for the region; a region is rewritten only
-    after its event has completed.  Steady state therefore performs no
-    pinned allocation (which can stall the host for milliseconds) and never
-    synchronises the device.  One instance per device, guarded by a lock.
+    256-byte-aligned region and enqueues an asynchronous copy on the current
+    stream.  Regions are retired in groups: the copies issued since the last
+    event form an open span, and one event is recorded after the span's
+    last copy once the span reaches MARK_BYTES, the stream changes, or a new
+    upload would reuse a byte of it.  A region is rewritten only after the
+    event of its span has completed.  An event per upload would put a
+    marker between every metadata copy and the next kernel (≈5-6 us each on
+    the launch stream); a round's handful of uploads now share one.  Steady
+    state performs no pinned allocation (which can stall the host for
+    milliseconds) and never synchronises the device.  One instance per
+    device, guarded by a lock.
     """
+
+    MARK_BYTES = 64 << 10
 
     def __init__(self, device, nbytes=1 << 20):
         self.device = device
         self._buf = torch.empty(nbytes, dtype=torch.uint8, pin_memory=True)
         self._head = 0
-        self._inflight = collections.deque()    # (start, end, event), oldest first
+        self._inflight = collections.deque()    # (start, end, event) per closed span, oldest first
+        self._open = None                       # [start, end, stream] of the copies since the last event
         self._events = []
         self._lock = threading.Lock()
 
+    def _close(self):
+        # One event after the open span's last copy, on the span's stream.
+        if self._open is None:
+            return
+        start, end, stream = self._open
+        ev = self._events.pop() if self._events else torch.cuda.Event()
+        ev.record(stream)
+        self._inflight.append((start, end, ev))
+        self._open = None
+
     def _retire(self, start, end):
-        # Uploads on one stream complete in order: drop finished ones first,
-        # then wait only for a still-pending region that the new one reuses.
+        # Spans on one stream complete in order: drop finished ones first,
+        # then wait only for a still-pending span that the new region reuses.
         q = self._inflight
         while q and q[0][2].query():
             self._events.append(q.popleft()[2])
@@ -127,8 +146,10 @@ class HostStaging:
         if n == 0:
             return out
         with self._lock:
+            stream = torch.cuda.current_stream(self.device)
             span = (n + 255) & ~255
             if span > self._buf.numel():
+                self._close()
                 for _, _, ev in self._inflight:
                     ev.synchronize()
                 self._inflight.clear()
@@ -137,14 +158,20 @@ class HostStaging:
             if self._head + span > self._buf.numel():
                 self._head = 0
             start, end = self._head, self._head + span
+            if self._open is not None and (self._open[2].cuda_stream != stream.cuda_stream
+                                           or (self._open[0] < end and start < self._open[1])):
+                self._close()
             self._retire(start, end)
             self._head = end
             host = self._buf[start:start + n].view(dtype)
             host.copy_(torch.from_numpy(arr))
             out.copy_(host, non_blocking=True)
-            ev = self._events.pop() if self._events else torch.cuda.Event()
-            ev.record(torch.cuda.current_stream(self.device))
-            self._inflight.append((start, end, ev))
+            if self._open is None:
+                self._open = [start, end, stream]
+            else:
+                self._open[0], self._open[1] = min(self._open[0], start), max(self._open[1], end)
+            if self._open[1] - self._open[0] >= self.MARK_BYTES:
+                self._close()
         return out
 
 
