@@ -19,6 +19,7 @@ The context K/V of one draft layer may live in
     physical indices (PackedLayout.gather_indices order): off_r indexes the
     index vector.
 """
+import numpy as np
 import torch
 
 from . import _native, backends
@@ -117,16 +118,37 @@ class DraftBatch:
         for b in blocks:
             cu_b.append(cu_b[-1] + len(b))
         self.cu_blocks_host = tuple(cu_b)
-        meta = upload(self.device, lens + cu_b + [a for b in blocks for a in b])
-        n = self.request_count
-        self.ctx_len = meta[:n]
-        self.cu_blocks = meta[n:2 * n + 1]
-        self.anchor_rows = meta[2 * n + 1:]
+        # Device metadata (lengths, block offsets, anchors) is uploaded on
+        # first use, together with a plan's offsets and work list when
+        # prepare() comes first (one copy instead of three).
+        self._meta_host = lens + cu_b + [a for b in blocks for a in b]
+        self._meta = None
         self._offsets = {}
         self._work = {}
         self._chunk = None            # the batch-sized draft chunk, once computed
         self._index_max = None
         self.physical_context_rows = self.context_rows
+
+    def _device_meta(self):
+        if self._meta is None:
+            self._meta = upload(self.device, self._meta_host)
+        return self._meta
+
+    @property
+    def ctx_len(self):
+        """[n] int32 device: committed context rows per (view of a) request."""
+        return self._device_meta()[:self.request_count]
+
+    @property
+    def cu_blocks(self):
+        """[n+1] int32 device: block offsets."""
+        n = self.request_count
+        return self._device_meta()[n:2 * n + 1]
+
+    @property
+    def anchor_rows(self):
+        """[blocks] int32 device: context rows visible to each block."""
+        return self._device_meta()[2 * self.request_count + 1:]
 
     @classmethod
     def from_packed_layout(cls, layout, *, block_size=BLOCK_SIZE):
@@ -169,6 +191,33 @@ class DraftBatch:
             self._offsets[capacity] = upload(self.device, self.kernel_offsets(capacity), torch.int64)
         return self._offsets[capacity]
 
+    def prepare(self, chunk, runs=None, capacity=None):
+        """(device_offsets(capacity), work(chunk, runs, capacity)), with the
+        batch metadata, the offsets and the work list that are not on the
+        device yet uploaded in one copy: int32 [metadata | int64 offsets |
+        work list], each part 16-byte aligned."""
+        key = (chunk, runs, capacity)
+        missing = (self._meta is None) + (capacity not in self._offsets) + (key not in self._work)
+        if missing >= 2:
+            meta = self._meta_host if self._meta is None else []
+            offs = (np.asarray(self.kernel_offsets(capacity), dtype=np.int64).view(np.int32).tolist()
+                    if capacity not in self._offsets else [])
+            plan = self._work_host(chunk, runs, capacity) if key not in self._work else None
+            parts, at = [], []
+            for part in (meta, offs, plan[0] if plan else []):
+                at.append(sum(len(p) for p in parts))
+                parts.append(list(part) + [0] * (-len(part) % 4))
+            dev = upload(self.device, [x for p in parts for x in p])
+            if meta:
+                self._meta = dev[at[0]:at[0] + len(meta)]
+            if offs:
+                self._offsets[capacity] = dev[at[1]:at[1] + len(offs)].view(torch.int64)
+            if plan:
+                records, n_seg, n_runs, anchor_at = plan
+                w = dev[at[2]:at[2] + len(records)]
+                self._work[key] = (w, n_seg, n_runs, None if anchor_at is None else w[anchor_at:])
+        return self.device_offsets(capacity), self.work(chunk, runs, capacity)
+
     def work(self, chunk, runs=None, capacity=None):
         """(device list, segment count, run count, segment anchors) of the
         draft plan: fixed chunks longest first (runs None), or `runs`
@@ -180,25 +229,31 @@ class DraftBatch:
         for balanced runs).  Uploaded once per plan."""
         key = (chunk, runs, capacity)
         if key not in self._work:
-            flat = [a for b in self.anchors for a in b]
-            offs = None if capacity is None else self.kernel_offsets(capacity)
-            if runs is None:
-                plan = draft_work(self.context_lengths, self.cu_blocks_host, flat, chunk=chunk, offsets=offs)
-            else:
-                runs = runs or draft_run_count(sum(max(b) for b in self.anchors), cu_count(self.device))
-                plan = draft_work(self.context_lengths, self.cu_blocks_host, flat, runs, offsets=offs)
-            records, n_seg, n_runs = plan
-            records = list(records)
-            anchor_at = None
-            if runs is None:
-                records += [0] * (-len(records) % 4)           # the anchor table starts 16-byte aligned
-                anchor_at = len(records)
-                for i in range(n_seg):
-                    b0, nb = records[8 * i + 4], records[8 * i + 5]
-                    records += flat[b0:b0 + nb] + [0] * (8 - nb)
+            records, n_seg, n_runs, anchor_at = self._work_host(chunk, runs, capacity)
             dev = upload_work(records, self.device)
             self._work[key] = (dev, n_seg, n_runs, None if anchor_at is None else dev[anchor_at:])
         return self._work[key]
+
+    def _work_host(self, chunk, runs, capacity):
+        """The host side of work(): (records, segment count, run count,
+        index of the segment anchor table or None)."""
+        flat = [a for b in self.anchors for a in b]
+        offs = None if capacity is None else self.kernel_offsets(capacity)
+        if runs is None:
+            plan = draft_work(self.context_lengths, self.cu_blocks_host, flat, chunk=chunk, offsets=offs)
+        else:
+            runs = runs or draft_run_count(sum(max(b) for b in self.anchors), cu_count(self.device))
+            plan = draft_work(self.context_lengths, self.cu_blocks_host, flat, runs, offsets=offs)
+        records, n_seg, n_runs = plan
+        records = list(records)
+        anchor_at = None
+        if runs is None:
+            records += [0] * (-len(records) % 4)           # the anchor table starts 16-byte aligned
+            anchor_at = len(records)
+            for i in range(n_seg):
+                b0, nb = records[8 * i + 4], records[8 * i + 5]
+                records += flat[b0:b0 + nb] + [0] * (8 - nb)
+        return records, n_seg, n_runs, anchor_at
 
     def index_max(self):
         """Largest physical index addressed through context_indices (one
@@ -288,9 +343,8 @@ class HipDraftAttention:
             self._geometry = self._context_geometry(context_keys, batch)
             self._geometry_for = key
         capacity, tok_stride, head_stride = self._geometry
-        offsets = batch.device_offsets(capacity)
         chunk = self.chunk_for(batch)
-        work, n_work, n_runs, seg_anchors = batch.work(chunk, self.runs, capacity)
+        offsets, (work, n_work, n_runs, seg_anchors) = batch.prepare(chunk, self.runs, capacity)
         need = _native.load().dspark_attn_workspace_bytes(n_work, 0, batch.max_blocks, chunk)
         ws = self._workspace.get(need)
         return capacity, tok_stride, head_stride, offsets, work, n_work, n_runs, seg_anchors, ws, chunk
