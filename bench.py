@@ -1276,11 +1276,12 @@ def traffic_summary(fetch_dir, write_dir):
 def trace_summary(pairs):
     """profiles/attn_64req_kernel_trace.json from kernel traces of the plain
     bench command, one process each: per process, the mean duration of the
-    verification chunk kernel and its merge over the timed rounds'
-    (warmup + steps) x 28 launches, the same for the draft chunk kernel and
-    its merge (x 5), beside the per-call event figures and algorithmic bytes
-    that process's bench line reported; stamped with the kernel sources'
-    sha256."""
+    verification chunk kernel and its merge over the launches of the
+    instrumented rounds (the steps x 28 after the warmup + steps plain
+    rounds), the same for the draft chunk kernel and its merge (x 5): the
+    very calls behind the per-call event figures and algorithmic bytes that
+    the process's bench line reports, which are set beside them; stamped
+    with the kernel sources' sha256."""
     import sqlite3
 
     import numpy as np
@@ -1292,7 +1293,7 @@ def trace_summary(pairs):
             raise SystemExit(f'expected one results database under {trace_dir}, found {db}')
         with open(log_path) as f:
             line = json.loads([x for x in f.read().splitlines() if x.startswith('{"metric"')][-1])
-        rounds = line['steps'] + line['warmup']
+        plain, instrumented = line['steps'] + line['warmup'], line['steps']
         con = sqlite3.connect(db[0])
         names = [r[0] for r in con.execute('select name, start, end from kernels order by start')]
         spans = [(r[1], r[2]) for r in con.execute('select name, start, end from kernels order by start')]
@@ -1307,12 +1308,13 @@ def trace_summary(pairs):
                 got['draft_chunk'].append((t1 - t0) * 1e-3)
             elif 'merge_kernel' in name and phase:
                 got[phase + '_merge'].append((t1 - t0) * 1e-3)
-        calls = {'verify': VERIFY_LAYERS * rounds, 'draft': DRAFT_LAYERS * rounds}
+        per_round = {'verify': VERIFY_LAYERS, 'draft': DRAFT_LAYERS}
         row = {'bench_value_tokens_per_s': line['value'], 'ms_per_step': line['ms_per_step']}
-        for kind, n in calls.items():
-            chunk, merge = got[kind + '_chunk'][:n], got[kind + '_merge'][:n]
-            if len(chunk) < n or len(merge) < n:
-                raise SystemExit(f'{db[0]}: fewer {kind} launches than the timed rounds hold')
+        for kind, k in per_round.items():
+            lo, hi = k * plain, k * (plain + instrumented)
+            chunk, merge = got[kind + '_chunk'][lo:hi], got[kind + '_merge'][lo:hi]
+            if len(chunk) < hi - lo or len(merge) < hi - lo:
+                raise SystemExit(f'{db[0]}: fewer {kind} launches than the rounds hold')
             b = line['breakdown']
             event_ms = b[kind + '_layer_ms']
             algorithmic = (line['roofline']['algorithmic_bytes_per_launch'] if kind == 'verify'
