@@ -123,6 +123,12 @@ def workload(steps_total):
     return [int(c) for c in contexts], anchors, accepted
 
 
+def grown_contexts(contexts, accepted):
+    """Context lengths after every round of `accepted` has committed: those
+    the instrumented rounds (and so the per-call figures) run at."""
+    return [int(c) + int(n) for c, n in zip(contexts, accepted.sum(axis=0))]
+
+
 def verify_bytes(contexts):
     """Algorithmic HBM bytes of one verification-attention layer: every key
     row (committed + staged) read once, Q read once, O written once."""
@@ -317,7 +323,7 @@ def main():
                                    'exchange (requests would shard across GPUs); run with --gpus 1'}))
         sys.exit(2)
     if args.traffic_summary:
-        return traffic_summary(*args.traffic_summary)
+        return traffic_summary(args, *args.traffic_summary)
     if args.trace_summary:
         return trace_summary(args.trace_summary)
     if args.trace_merge:
@@ -744,9 +750,11 @@ def draft_projection_leg(dev, n_req, per_request, reps=20):
 
 def traffic_probe(args):
     """Kernels for `rocprofv3 --pmc FETCH_SIZE` / `--pmc WRITE_SIZE` passes:
-    3 verification-attention launches of the workload, staging fused in as
-    in the timed rounds, then 3 draft-attention launches (store and pool
-    contents are irrelevant to the bytes moved, so they stay zero-filled),
+    3 verification-attention launches of the workload at the contexts of the
+    instrumented rounds (after the warm-up and timed rounds' commits),
+    staging fused in as in the rounds, then 3 draft-attention launches
+    (store and pool contents are irrelevant to the bytes moved, so they stay
+    zero-filled),
     then a plain copy of exactly 2**30 bytes whose counter reading
     calibrates the counters to bytes."""
     import torch
@@ -756,11 +764,12 @@ def traffic_probe(args):
     from qwen3_dspark_amd.persistent_kv import Bucket, PersistentTargetKV
 
     dev = torch.device('cuda:0')
-    contexts, anchors, _ = workload(args.warmup + args.steps)
+    contexts, anchors, accepted = workload(args.warmup + args.steps)
+    grown = grown_contexts(contexts, accepted)
     pool = PersistentTargetKV(layers=3, slots=B, context_capacity=CAPACITY, max_query_tokens=B * Q_LEN,
                               heads=8, dim=128, device=dev, chunk=args.chunk or DEFAULT_CHUNK)
     handles = [pool.add_request(f'req{i}') for i in range(B)]
-    for h, c in zip(handles, contexts):
+    for h, c in zip(handles, grown):
         pool.load_prefix(h, pool.keys[:, h.index, :c], pool.values[:, h.index, :c])
     bucket = Bucket((Q_LEN,) * B, (CAPACITY - Q_LEN,) * B, '64-request stress shape')
     pool.register_bucket(bucket)
@@ -788,9 +797,9 @@ def traffic_probe(args):
     dst.copy_(src)
     torch.cuda.synchronize()
     del ctx_k, ctx_v
-    print(json.dumps({'traffic_probe': 'done', 'verify_algorithmic_bytes_per_launch': verify_bytes(contexts),
+    print(json.dumps({'traffic_probe': 'done', 'verify_algorithmic_bytes_per_launch': verify_bytes(grown),
                       'draft_algorithmic_bytes_per_launch': draft_bytes(anchors),
-                      'context_rows': sum(contexts),
+                      'context_rows': sum(grown),
                       'calibration_copy_bytes': 1 << 30,
                       'streaming_reference': streaming_reference(dev, src, dst)}), flush=True)
 
@@ -1218,7 +1227,7 @@ def kernel_source_hash():
     return h.hexdigest()
 
 
-def traffic_summary(fetch_dir, write_dir):
+def traffic_summary(args, fetch_dir, write_dir):
     """profiles/{verify,draft}_attn_traffic.json from the counter CSVs of
     `rocprofv3 --pmc FETCH_SIZE` and `--pmc WRITE_SIZE` runs of
     --traffic-probe.  Dispatches in order: 3 x (verification chunk kernel,
@@ -1251,9 +1260,10 @@ def traffic_summary(fetch_dir, write_dir):
     fetch, write = read(fetch_dir, 'FETCH_SIZE'), read(write_dir, 'WRITE_SIZE')
     copy_bytes = 1 << 30
     f_factor, w_factor = fetch['copy'] * 1024 / copy_bytes, write['copy'] * 1024 / copy_bytes
-    contexts, anchors, _ = workload(1)
+    contexts, anchors, accepted = workload(args.warmup + args.steps)
+    grown = grown_contexts(contexts, accepted)
     source = kernel_source_hash()
-    for kind, algorithmic in (('verify', verify_bytes(contexts)), ('draft', draft_bytes(anchors))):
+    for kind, algorithmic in (('verify', verify_bytes(grown)), ('draft', draft_bytes(anchors))):
         read_b = (fetch[kind + '_chunk'] + fetch[kind + '_merge']) * 1024 / f_factor
         write_b = (write[kind + '_chunk'] + write[kind + '_merge']) * 1024 / w_factor
         total = read_b + write_b
@@ -1264,7 +1274,9 @@ def traffic_summary(fetch_dir, write_dir):
                               'calibration_copy': fetch['copy']},
                    write_kib={'chunk': write[kind + '_chunk'], 'merge': write[kind + '_merge'],
                               'calibration_copy': write['copy']},
-                   context_rows=sum(contexts), workload_round='first round of the bench workload',
+                   context_rows=sum(grown) if kind == 'verify' else sum(contexts),
+                   workload_round=('contexts after the warm-up and timed rounds, those of the instrumented rounds'
+                                   if kind == 'verify' else 'the draft contexts of every round'),
                    kernel_source_sha256=source)
         with open(os.path.join(ROOT, 'profiles', f'{kind}_attn_traffic.json'), 'w') as f:
             json.dump(doc, f, indent=1)
