@@ -77,6 +77,9 @@ def parse():
     ap.add_argument('--trace-summary', nargs='+', metavar='DIR:LOG',
                     help='turn rocprofv3 --kernel-trace runs of the plain bench command (each a trace directory and '
                          'the bench line its process printed) into profiles/attn_64req_kernel_trace.json')
+    ap.add_argument('--layer-summary', nargs='+', metavar='DIR:LOG',
+                    help='per-layer verification kernel durations from rocprofv3 --kernel-trace runs of the plain '
+                         'bench command (each a trace directory and the bench line its process printed)')
     ap.add_argument('--traffic-probe', action='store_true',
                     help='untimed run for hardware-counter passes: 3 verification-attention and 3 draft-attention '
                          'layers of the workload, then a 1 GiB device-to-device copy as the counter calibration')
@@ -328,6 +331,8 @@ def main():
         return trace_summary(args.trace_summary)
     if args.trace_merge:
         return trace_merge(args.trace_merge)
+    if args.layer_summary:
+        return layer_summary(args.layer_summary)
     if args.traffic_probe:
         return traffic_probe(args)
     if args.mfma_probe:
@@ -1285,6 +1290,56 @@ def traffic_summary(args, fetch_dir, write_dir):
                                                      'write_kib')}}))
 
 
+def traced_launches(trace_dir):
+    """The results database under `trace_dir` and, in launch order, the
+    durations (us) of the verification and draft chunk kernels and of the
+    merge launch that follows each kind."""
+    import sqlite3
+    db = [os.path.join(d, f) for d, _, fs in os.walk(trace_dir) for f in fs if f.endswith('_results.db')]
+    if len(db) != 1:
+        raise SystemExit(f'expected one results database under {trace_dir}, found {db}')
+    con = sqlite3.connect(db[0])
+    got = {'verify_chunk': [], 'verify_merge': [], 'draft_chunk': [], 'draft_merge': []}
+    phase = None
+    for name, t0, t1 in con.execute('select name, start, end from kernels order by start'):
+        if 'varlen_attn_kernel' in name:
+            phase = 'verify'
+            got['verify_chunk'].append((t1 - t0) * 1e-3)
+        elif 'draft_attn' in name:
+            phase = 'draft'
+            got['draft_chunk'].append((t1 - t0) * 1e-3)
+        elif 'merge_kernel' in name and phase:
+            got[phase + '_merge'].append((t1 - t0) * 1e-3)
+    return db[0], got
+
+
+def layer_summary(pairs):
+    """Per model layer, from kernel traces of the plain bench command (each
+    a trace directory and the bench line its process printed): the mean
+    duration of the verification chunk kernel over the instrumented rounds,
+    and the means of each run of four consecutive layers (one layer's K, and
+    its V, is 1 GiB of the store)."""
+    import numpy as np
+    out = []
+    for pair in pairs:
+        trace_dir, log_path = pair.split(':', 1)
+        db, got = traced_launches(trace_dir)
+        with open(log_path) as f:
+            line = json.loads([x for x in f.read().splitlines() if x.startswith('{"metric"')][-1])
+        plain, instrumented = line['steps'] + line['warmup'], line['steps']
+        v = got['verify_chunk'][VERIFY_LAYERS * plain:VERIFY_LAYERS * (plain + instrumented)]
+        if len(v) < VERIFY_LAYERS * instrumented:
+            raise SystemExit(f'{db}: fewer verification launches than the rounds hold')
+        per_round = np.array(v).reshape(instrumented, VERIFY_LAYERS)
+        per_layer = per_round.mean(axis=0)
+        out.append({'bench_value_tokens_per_s': line['value'], 'mean_us': round(float(per_layer.mean()), 2),
+                    'per_layer_us': [round(float(x), 2) for x in per_layer],
+                    'per_4_layers_us': [round(float(x), 2) for x in per_layer.reshape(-1, 4).mean(axis=1)],
+                    'sd_over_rounds_us': round(float(per_round.std(axis=0).mean()), 2)})
+    print(json.dumps({'what': 'verification chunk kernel per layer, instrumented rounds', 'processes': out,
+                      'kernel_source_sha256': kernel_source_hash()}))
+
+
 def trace_summary(pairs):
     """profiles/attn_64req_kernel_trace.json from kernel traces of the plain
     bench command, one process each: per process, the mean duration of the
@@ -1294,39 +1349,21 @@ def trace_summary(pairs):
     very calls behind the per-call event figures and algorithmic bytes that
     the process's bench line reports, which are set beside them; stamped
     with the kernel sources' sha256."""
-    import sqlite3
-
     import numpy as np
     procs = []
     for pair in pairs:
         trace_dir, log_path = pair.split(':', 1)
-        db = [os.path.join(d, f) for d, _, fs in os.walk(trace_dir) for f in fs if f.endswith('_results.db')]
-        if len(db) != 1:
-            raise SystemExit(f'expected one results database under {trace_dir}, found {db}')
+        db, got = traced_launches(trace_dir)
         with open(log_path) as f:
             line = json.loads([x for x in f.read().splitlines() if x.startswith('{"metric"')][-1])
         plain, instrumented = line['steps'] + line['warmup'], line['steps']
-        con = sqlite3.connect(db[0])
-        names = [r[0] for r in con.execute('select name, start, end from kernels order by start')]
-        spans = [(r[1], r[2]) for r in con.execute('select name, start, end from kernels order by start')]
-        got = {'verify_chunk': [], 'verify_merge': [], 'draft_chunk': [], 'draft_merge': []}
-        phase = None
-        for name, (t0, t1) in zip(names, spans):
-            if 'varlen_attn_kernel' in name:
-                phase = 'verify'
-                got['verify_chunk'].append((t1 - t0) * 1e-3)
-            elif 'draft_attn' in name:
-                phase = 'draft'
-                got['draft_chunk'].append((t1 - t0) * 1e-3)
-            elif 'merge_kernel' in name and phase:
-                got[phase + '_merge'].append((t1 - t0) * 1e-3)
         per_round = {'verify': VERIFY_LAYERS, 'draft': DRAFT_LAYERS}
         row = {'bench_value_tokens_per_s': line['value'], 'ms_per_step': line['ms_per_step']}
         for kind, k in per_round.items():
             lo, hi = k * plain, k * (plain + instrumented)
             chunk, merge = got[kind + '_chunk'][lo:hi], got[kind + '_merge'][lo:hi]
             if len(chunk) < hi - lo or len(merge) < hi - lo:
-                raise SystemExit(f'{db[0]}: fewer {kind} launches than the rounds hold')
+                raise SystemExit(f'{db}: fewer {kind} launches than the rounds hold')
             b = line['breakdown']
             event_ms = b[kind + '_layer_ms']
             algorithmic = (line['roofline']['algorithmic_bytes_per_launch'] if kind == 'verify'
