@@ -1410,8 +1410,9 @@ def trace_merge(paths):
 
 def cpu_threads():
     """(threads, reason): the host threads the CPU baseline uses - the
-    process's OpenMP share when OMP_NUM_THREADS is set (the GPU box sets it
-    to its CPU share per GPU, 16), else every core os.cpu_count() reports."""
+    process's OpenMP share when OMP_NUM_THREADS is set (a shared host sets
+    it to its CPU share per GPU, e.g. 16), else every core os.cpu_count()
+    reports."""
     n = os.cpu_count() or 1
     env = os.environ.get('OMP_NUM_THREADS', '')
     if env.isdigit() and int(env) >= 1:
